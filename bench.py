@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""Route benchmark on one MI355X.
+
+Headline workload: MLA latent-centroid route, 1,000,000 nodes x 288 fp32
+(unit-norm Gaussian), one query per call, top-3; the bank and the query are
+resident in HBM before timing.  Each step is one route call through the C
+ABI (kernel + top-k + device->host copy of the k results).  Reported:
+
+* value      p50 wall latency per call (ms) over --steps calls
+* roofline   HBM roofline of the route kernel: algorithmic bytes per launch
+             (N*D*4 row bytes + N*4 norm bytes) / mean kernel time from HIP
+             events recorded on the library's route stream
+* gqa        the ragged GQA route (512 nodes, lengths U[16,512], 4 layers x 8
+             kv heads x 128, bf16, 32 query heads, top-3): p50/p99 and its
+             roofline (sum(L_i) * 32 * 128 * 2 bytes)
+* cpu_baseline  the oracle's fp64 route law on the same 1M bank, timed on
+             this host's cores for a bounded number of queries
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def pct(xs, p):
+    return float(np.percentile(np.asarray(xs, dtype=np.float64), p))
+
+
+def bench_mla(steps: int, warmup: int):
+    from graftrepository_amd import MlaNodeBank, workloads as wl
+    from graftrepository_amd.mla_probe import HipProbe
+
+    cfg = wl.MLA_HEADLINE
+    n, d, k = cfg["nodes"], cfg["dim"], cfg["topk"]
+    t0 = time.time()
+    rows = wl.mla_rows(n, d, seed=cfg["seed"])
+    q = wl.mla_queries(1, d, seed=cfg["seed"])
+    log(f"[mla] generated {n}x{d} bank in {time.time() - t0:.1f}s")
+    bank = MlaNodeBank(rows)
+    probe = HipProbe()
+    dq = probe.upload_queries(q)
+    for _ in range(warmup):
+        bank.route(dq, k, on_device=True, query_count=1)
+    walls, devs = [], []
+    for _ in range(steps):
+        r = bank.route(dq, k, on_device=True, query_count=1)
+        walls.append(r.wall_ms)
+        devs.append(r.device_ms)
+    ids = r.ids[0].copy()
+    scores = r.scores[0].copy()
+    dq.close()
+    bank.close()
+    bytes_per_launch = n * d * 4 + n * 4
+    mean_dev = float(np.mean(devs))
+    achieved = bytes_per_launch / (mean_dev * 1e-3) / 1e9
+    log(f"[mla] p50 {pct(walls, 50):.4f} ms  p99 {pct(walls, 99):.4f} ms  "
+        f"kernel {mean_dev:.4f} ms  {achieved:.0f} GB/s")
+    return dict(rows=rows, q=q, ids=ids, scores=scores, walls=walls,
+                devs=devs, bytes=bytes_per_launch, achieved=achieved,
+                mean_dev=mean_dev, cfg=cfg)
+
+
+def bench_gqa(steps: int, warmup: int):
+    from graftrepository_amd import GqaNodeBank, workloads as wl
+    from graftrepository_amd.gqa_probe import HipProbe
+
+    cfg = wl.GQA_RAGGED
+    kv = cfg["layers"] * cfg["kv_heads"]
+    H = cfg["layers"] * cfg["heads"]
+    hd = cfg["head_dim"]
+    lens = wl.gqa_lengths(cfg["nodes"], cfg["seed"], lo=cfg["lo"], hi=cfg["hi"])
+    keys, offs = wl.gqa_bank(lens, kv, hd, cfg["seed"])
+    q = wl.gqa_queries(1, H, cfg["tokens"], hd, cfg["seed"])
+    bank = GqaNodeBank(keys, offs, kv_heads=kv, head_dim=hd, dtype="bf16")
+    probe = HipProbe()
+    dq = probe.upload_queries(q.view(np.float32))  # bf16 bits, uploaded raw
+    shape = q.shape
+    for _ in range(warmup):
+        bank.route(dq, cfg["topk"], on_device=True, query_dtype="bf16",
+                   query_shape=shape)
+    walls, devs = [], []
+    for _ in range(steps):
+        r = bank.route(dq, cfg["topk"], on_device=True, query_dtype="bf16",
+                       query_shape=shape)
+        walls.append(r.wall_ms)
+        devs.append(r.device_ms)
+    dq.close()
+    bank.close()
+    sum_l = int(offs[-1])
+    bytes_per_call = sum_l * kv * hd * 2
+    mean_dev = float(np.mean(devs))
+    achieved = bytes_per_call / (mean_dev * 1e-3) / 1e9
+    log(f"[gqa] sumL {sum_l}  p50 {pct(walls, 50):.4f} ms  p99 {pct(walls, 99):.4f} ms"
+        f"  device {mean_dev:.4f} ms  {achieved:.0f} GB/s")
+    return dict(keys=keys, offs=offs, q=q, ids=r.ids[0].copy(),
+                scores=r.scores[0].copy(), walls=walls, devs=devs,
+                bytes=bytes_per_call, achieved=achieved, mean_dev=mean_dev,
+                sum_l=sum_l, cfg=cfg, kv=kv, H=H)
+
+
+def cpu_baseline_mla(m, seconds: float):
+    """Oracle fp64 route on the host cores, bounded to about `seconds`."""
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rows, q, k = m["rows"], m["q"], m["cfg"]["topk"]
+    times = []
+    ids = sc = None
+    t_end = time.time() + seconds
+    while time.time() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        ids, sc, _ = oracle.mla_route(rows, q, k, threads=threads)
+        times.append((time.perf_counter() - t0) * 1e3)
+        if len(times) >= 50:
+            break
+    match = bool(np.array_equal(ids[0], m["ids"])) and bool(
+        np.array_equal(sc[0].view(np.uint32), m["scores"].view(np.uint32)))
+    log(f"[cpu] oracle MLA route p50 {pct(times, 50):.1f} ms on {threads} threads "
+        f"({len(times)} calls); ids/scores match GPU: {match}")
+    return dict(value=pct(times, 50), unit="ms", cores=threads, kind="port",
+                sample=f"{len(times)} single-query routes of the 1,000,000 x 288 "
+                       f"bank (fp64 law, OpenMP), p50",
+                parity_with_gpu=match)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--gqa-steps", type=int, default=300)
+    ap.add_argument("--only", choices=["all", "mla", "gqa"], default="all")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures the route on one GPU only; --gpus {args.gpus} "
+              f"(WORLD_SIZE {world}) is not supported: the route runs on one "
+              "GPU's bank and multi-GPU sharding is not part of this build.",
+              file=sys.stderr)
+        return 2
+
+    out = {}
+    m = g = None
+    if args.only in ("all", "mla"):
+        m = bench_mla(args.steps, args.warmup)
+    if args.only in ("all", "gqa"):
+        g = bench_gqa(args.gqa_steps, min(args.warmup, 20))
+    cpu = None
+    if m is not None and not args.skip_cpu:
+        cpu = cpu_baseline_mla(m, args.cpu_seconds)
+
+    if m is not None:
+        cfg = m["cfg"]
+        out = {
+            "metric": "p50 route latency (ms) @1M MLA nodes + achieved HBM GB/s; ragged GQA p50",
+            "value": round(pct(m["walls"], 50), 5),
+            "unit": "ms",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(float(np.mean(m["walls"])), 5),
+            "higher_is_better": False,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "f64",
+            "data": "synthetic (unit-norm Gaussian centroids, seeded)",
+            "config": {"workload": "mla_route", "nodes": cfg["nodes"],
+                       "dim": cfg["dim"], "bank_dtype": "f32", "topk": cfg["topk"],
+                       "queries_per_call": 1, "query_resident": "hbm"},
+            "p99_ms": round(pct(m["walls"], 99), 5),
+            "kernel_ms_mean": round(m["mean_dev"], 5),
+            "roofline": {"bound": "hbm", "achieved": round(m["achieved"], 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(m["achieved"] / HBM_PEAK_GBS, 4),
+                         "traffic": None,
+                         "kernel": "mla_route_kernel<f32>",
+                         "bytes_per_launch": m["bytes"]},
+        }
+    if g is not None:
+        gq = {
+            "workload": "gqa_ragged_route", "nodes": g["cfg"]["nodes"],
+            "sum_tokens": g["sum_l"], "kv_heads_stacked": g["kv"],
+            "query_heads_stacked": g["H"], "head_dim": g["cfg"]["head_dim"],
+            "bank_dtype": "bf16", "topk": g["cfg"]["topk"],
+            "steps": args.gqa_steps,
+            "p50_ms": round(pct(g["walls"], 50), 5),
+            "p99_ms": round(pct(g["walls"], 99), 5),
+            "device_ms_mean": round(g["mean_dev"], 5),
+            "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),
+                         "bytes_per_call": g["bytes"]},
+        }
+        if out:
+            out["gqa"] = gq
+        else:
+            out = {"metric": "ragged GQA p50 route latency (ms)",
+                   "value": gq["p50_ms"], "unit": "ms", "n_gpus": 1,
+                   "steps": args.gqa_steps, "warmup": args.warmup,
+                   "ms_per_step": round(float(np.mean(g["walls"])), 5),
+                   "higher_is_better": False, "scaling": "weak",
+                   "vs_baseline": None, "dtype": "f64",
+                   "data": "synthetic", "config": gq}
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,191 @@
+// grm_common.hpp -- shared pieces of the gfx950 GRM route library:
+// error plumbing, the ranked-candidate type, the tie law, and the wave-wide
+// top-k list every route kernel uses.
+//
+// Tie law (cpp/grm_runtime.cpp:75-82, score_node_better): higher score first,
+// equal scores by lower node id; non-finite scores never enter a ranking
+// (scripts/grm_mla_cuda_probe.py:136-152).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace grm {
+
+constexpr int kWave = 64;
+constexpr int kMaxTopK = 16;
+constexpr uint64_t kNoId = ~0ull;
+constexpr uint32_t kNoSlot = 0xffffffffu;
+
+enum Dtype : int { kF32 = 0, kBF16 = 1, kF16 = 2, kI8 = 3 };
+
+// ------------------------------------------------------------------ errors
+
+void set_error(const std::string& msg);
+void clear_error();
+
+inline int hip_code(hipError_t rc) {
+  return rc == hipSuccess ? 0 : 1000 + static_cast<int>(rc);
+}
+
+int fail(int code, const char* what);
+int fail_hip(hipError_t rc, const char* what);
+
+#define GRM_HIP_CHECK(expr)                                       \
+  do {                                                            \
+    hipError_t grm_rc_ = (expr);                                  \
+    if (grm_rc_ != hipSuccess) return ::grm::fail_hip(grm_rc_, #expr); \
+  } while (0)
+
+#define GRM_CHECK_RC(expr)                \
+  do {                                    \
+    int grm_rc2_ = (expr);                \
+    if (grm_rc2_ != 0) return grm_rc2_;   \
+  } while (0)
+
+// ------------------------------------------------------------- candidates
+
+// One ranked entry: score, bank slot, node id (16 bytes).
+struct Cand {
+  float score;
+  uint32_t slot;
+  uint64_t id;
+};
+static_assert(sizeof(Cand) == 16, "Cand must stay 16 bytes");
+
+__host__ __device__ inline bool better(float s, uint64_t id, float ts,
+                                       uint64_t tid) {
+  return s > ts || (s == ts && id < tid);
+}
+
+__device__ inline float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// --------------------------------------------------------- wave top-k list
+//
+// A sorted list of `k` entries distributed over one wavefront: lane j < k
+// holds entry j (best first).  `th_*` caches entry k-1, the bar a new
+// candidate must beat; it is wave-uniform.
+struct WaveList {
+  float s;
+  uint32_t slot;
+  uint64_t id;
+  float th_s;
+  uint64_t th_id;
+};
+
+__device__ inline void wl_init(WaveList& L) {
+  L.s = -INFINITY;
+  L.slot = kNoSlot;
+  L.id = kNoId;
+  L.th_s = -INFINITY;
+  L.th_id = kNoId;
+}
+
+__device__ inline void wl_refresh(WaveList& L, int k) {
+  L.th_s = __shfl(L.s, k - 1);
+  L.th_id = __shfl(L.id, k - 1);
+}
+
+// Offer one candidate per lane (`valid` lanes only) and keep the best k of
+// list + candidates.  Each iteration extracts the best remaining candidate
+// with a butterfly arg-max and inserts it, so the loop runs at most k times
+// and not at all once no lane beats the bar.
+__device__ inline void wl_consume(WaveList& L, int k, float s, uint64_t id,
+                                  uint32_t slot, bool valid) {
+  const int lane = __lane_id();
+  bool cand = valid && better(s, id, L.th_s, L.th_id);
+  while (__ballot(cand) != 0ull) {
+    float bs = cand ? s : -INFINITY;
+    uint64_t bid = cand ? id : kNoId;
+    uint32_t bslot = slot;
+    int bl = cand ? lane : kWave;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const float os = __shfl_xor(bs, off);
+      const uint64_t oid = __shfl_xor(bid, off);
+      const uint32_t oslot = __shfl_xor(bslot, off);
+      const int ol = __shfl_xor(bl, off);
+      const bool take =
+          better(os, oid, bs, bid) || (os == bs && oid == bid && ol < bl);
+      if (take) {
+        bs = os;
+        bid = oid;
+        bslot = oslot;
+        bl = ol;
+      }
+    }
+    // Entries ahead of the winner form a prefix of the sorted list.
+    const bool ahead = lane < k && better(L.s, L.id, bs, bid);
+    const int pos = __popcll(__ballot(ahead));
+    const float ps = __shfl_up(L.s, 1);
+    const uint64_t pid = __shfl_up(L.id, 1);
+    const uint32_t pslot = __shfl_up(L.slot, 1);
+    if (lane == pos) {
+      L.s = bs;
+      L.id = bid;
+      L.slot = bslot;
+    } else if (lane > pos && lane < k) {
+      L.s = ps;
+      L.id = pid;
+      L.slot = pslot;
+    }
+    wl_refresh(L, k);
+    if (lane == bl) cand = false;
+    cand = cand && better(s, id, L.th_s, L.th_id);
+  }
+}
+
+__device__ inline Cand wl_entry(const WaveList& L) {
+  Cand c;
+  c.score = L.s;
+  c.slot = L.slot;
+  c.id = L.id;
+  return c;
+}
+
+// Merge the per-wave lists of a block (written to `lists[wave][0..k)`) into
+// wave 0's list.  Caller synchronises the block before and reads the result
+// from wave 0 after.
+template <int NW>
+__device__ inline void block_merge(Cand (*lists)[kMaxTopK], int k,
+                                   WaveList& out) {
+  const int lane = __lane_id();
+  wl_init(out);
+  for (int base = 0; base < NW * k; base += kWave) {
+    const int i = base + lane;
+    const bool v = i < NW * k;
+    Cand c;
+    c.score = -INFINITY;
+    c.slot = kNoSlot;
+    c.id = kNoId;
+    if (v) c = lists[i / k][i % k];
+    wl_consume(out, k, c.score, c.id, c.slot, v && isfinite(c.score));
+  }
+}
+
+// Consume `count` candidates from global memory into the list (one wave,
+// strided by `stride_waves` waves starting at wave index `w`).
+__device__ inline void wl_consume_global(WaveList& L, int k,
+                                         const Cand* __restrict__ src,
+                                         uint32_t count, uint32_t w,
+                                         uint32_t stride_waves) {
+  const int lane = __lane_id();
+  for (uint32_t base = w * kWave; base < count; base += stride_waves * kWave) {
+    const uint32_t i = base + lane;
+    const bool v = i < count;
+    Cand c;
+    c.score = -INFINITY;
+    c.slot = kNoSlot;
+    c.id = kNoId;
+    if (v) c = src[i];
+    wl_consume(L, k, c.score, c.id, c.slot, v && isfinite(c.score));
+  }
+}
+
+}  // namespace grm

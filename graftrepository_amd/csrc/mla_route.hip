@@ -1,0 +1,780 @@
+// mla_route.hip -- MLA latent-centroid route on gfx950.
+//
+// Law (cpp/grm_runtime.cpp:3518-3545 exact_mla_entry_score, :4299-4361
+// route_mla_arena, row norms :3232-3241):
+//   score(node) = float( dot / (qnorm * (double)norm_f + 1e-8) )
+//   dot   = sum_d (double)q_d * (double)r_d, sequential in d
+//   qnorm = sqrt(sum_d (double)q_d^2)        norm_f = float(sqrt(sum (double)r_d^2))
+// Every node is scored with exactly these fp64 operations in this order, so
+// scores are bit-identical to the reference's CPU router and the ranking
+// needs no re-check.  fp64 costs nothing here: the kernel streams 4 bytes
+// (fp32 bank) or 2 bytes (bf16 bank) per multiply-add and is bound by HBM.
+//
+// Bank layout in HBM ("lane-interleaved tiles"): slots are grouped in tiles
+// of 64; a tile stores its rows chunk-major, each 16-byte chunk (4 fp32 or
+// 8 bf16 values of one row) at [tile][chunk][lane].  Lane l of a wavefront
+// owns slot tile*64+l, walks its row in d order (the law's order) and every
+// load instruction of the wave reads 1 KiB of contiguous memory.
+//
+// Top-k is fused: each wave keeps a distributed top-k list (grm_common.hpp),
+// blocks merge their waves' lists in LDS, and the last block to finish
+// merges the per-block lists -- the score vector never leaves registers.
+#include "grm_common.hpp"
+#include "grm_hip_router.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <set>
+#include <unordered_map>
+#include <vector>
+
+namespace grm {
+namespace mla {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kMaxDim = 4096;
+constexpr int kRouteWaves = 4;           // waves per route block
+constexpr uint32_t kStageRows = 1u << 16;  // rows per attach staging batch
+
+// ------------------------------------------------------------------ kernels
+
+template <int DT>
+__device__ inline double chunk_dot(u32x4 v, const double* __restrict__ q,
+                                   double acc) {
+  // fma(r, q, acc) == acc + r*q exactly: r*q has <= 48 significant bits.
+  if constexpr (DT == kF32) {
+    acc = fma(static_cast<double>(__uint_as_float(v.x)), q[0], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.y)), q[1], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.z)), q[2], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.w)), q[3], acc);
+  } else {
+    acc = fma(static_cast<double>(__uint_as_float(v.x << 16)), q[0], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.x & 0xffff0000u)), q[1], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.y << 16)), q[2], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.y & 0xffff0000u)), q[3], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.z << 16)), q[4], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.z & 0xffff0000u)), q[5], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.w << 16)), q[6], acc);
+    acc = fma(static_cast<double>(__uint_as_float(v.w & 0xffff0000u)), q[7], acc);
+  }
+  return acc;
+}
+
+// Dot product of this lane's row with the query, d ascending.
+template <int DT>
+__device__ inline double tile_dot(const u32x4* __restrict__ p, uint32_t chunks,
+                                  const double* __restrict__ qd) {
+  constexpr int EPC = DT == kF32 ? 4 : 8;
+  constexpr uint32_t kBatch = 8;
+  double acc = 0.0;
+  uint32_t c = 0;
+  for (; c + kBatch <= chunks; c += kBatch) {
+    u32x4 v[kBatch];
+#pragma unroll
+    for (uint32_t j = 0; j < kBatch; ++j) {
+      v[j] = __builtin_nontemporal_load(p + static_cast<size_t>(c + j) * kWave);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kBatch; ++j) {
+      acc = chunk_dot<DT>(v[j], qd + (c + j) * EPC, acc);
+    }
+  }
+  for (; c < chunks; ++c) {
+    acc = chunk_dot<DT>(__builtin_nontemporal_load(p + static_cast<size_t>(c) * kWave),
+                        qd + c * EPC, acc);
+  }
+  return acc;
+}
+
+// One query against every slot; writes the query's top-k to `out[0..k)`.
+// Requires gridDim.x * k entries of `block_out` and a zeroed `ticket`; the
+// last block re-zeroes the ticket.
+template <int DT, int NW>
+__global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
+    const u32x4* __restrict__ tiles, const float* __restrict__ norms,
+    const uint64_t* __restrict__ ids, uint32_t num_tiles, uint32_t chunks,
+    uint32_t dim, uint32_t dim_pad, const void* __restrict__ query,
+    int query_dtype, int k, Cand* __restrict__ block_out,
+    unsigned* __restrict__ ticket, Cand* __restrict__ out) {
+  extern __shared__ double qd[];
+  __shared__ double s_qnorm;
+  __shared__ Cand s_lists[NW][kMaxTopK];
+  __shared__ int s_last;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+
+  for (uint32_t d = tid; d < dim_pad; d += NW * kWave) {
+    double v = 0.0;
+    if (d < dim) {
+      v = query_dtype == kBF16
+              ? static_cast<double>(bf16_to_f32(static_cast<const uint16_t*>(query)[d]))
+              : static_cast<double>(static_cast<const float*>(query)[d]);
+    }
+    qd[d] = v;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double acc = 0.0;  // cpp/grm_runtime.cpp:4310-4314, sequential
+    for (uint32_t d = 0; d < dim; ++d) acc = fma(qd[d], qd[d], acc);
+    s_qnorm = sqrt(acc);
+  }
+  __syncthreads();
+  const double qnorm = s_qnorm;
+
+  WaveList L;
+  wl_init(L);
+  for (uint32_t t = blockIdx.x * NW + wave; t < num_tiles; t += gridDim.x * NW) {
+    const double dot = tile_dot<DT>(
+        tiles + static_cast<size_t>(t) * chunks * kWave + lane, chunks, qd);
+    const uint32_t slot = t * kWave + lane;
+    const float nrm = norms[slot];  // NaN marks an empty or evicted slot
+    const double den = qnorm * static_cast<double>(nrm) + 1.0e-8;
+    const float s = static_cast<float>(dot / den);
+    const bool need = isfinite(s) && s >= L.th_s;
+    uint64_t id = kNoId;
+    if (need) id = ids[slot];
+    wl_consume(L, k, s, id, slot, need);
+  }
+
+  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(L);
+  __syncthreads();
+  if (wave == 0) {
+    WaveList B;
+    block_merge<NW>(s_lists, k, B);
+    if (lane < k) block_out[static_cast<size_t>(blockIdx.x) * k + lane] = wl_entry(B);
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = (atomicAdd(ticket, 1u) == gridDim.x - 1) ? 1 : 0;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  WaveList G;
+  wl_init(G);
+  wl_consume_global(G, k, block_out, gridDim.x * static_cast<uint32_t>(k),
+                    static_cast<uint32_t>(wave), NW);
+  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(G);
+  __syncthreads();
+  if (wave == 0) {
+    WaveList B;
+    block_merge<NW>(s_lists, k, B);
+    if (lane < k) out[lane] = wl_entry(B);
+    if (lane == 0) atomicExch(ticket, 0u);
+  }
+}
+
+// Place staged row-major rows into their tile slots and compute row norms
+// (cpp/grm_runtime.cpp:3232-3241).  rows: [count][dim] of DT; slots/ids may be
+// null (contiguous slots from slot0 / ids = slot).
+template <int DT>
+__global__ void mla_place_rows_kernel(const void* __restrict__ rows,
+                                      uint64_t count, uint32_t dim,
+                                      uint32_t chunks,
+                                      const uint64_t* __restrict__ slots,
+                                      const uint64_t* __restrict__ ids,
+                                      uint64_t slot0, u32x4* __restrict__ tiles,
+                                      float* __restrict__ norms,
+                                      uint64_t* __restrict__ slot_ids) {
+  constexpr int EPC = DT == kF32 ? 4 : 8;
+  for (uint64_t r = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+       r < count; r += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+    const uint64_t slot = slots ? slots[r] : slot0 + r;
+    const uint64_t tile = slot / kWave;
+    const uint32_t lane = static_cast<uint32_t>(slot % kWave);
+    u32x4* dst = tiles + tile * chunks * kWave + lane;
+    double acc = 0.0;
+    for (uint32_t c = 0; c < chunks; ++c) {
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+      for (int e = 0; e < EPC; ++e) {
+        const uint32_t d = c * EPC + e;
+        float f = 0.0f;
+        uint32_t bits = 0u;
+        if (d < dim) {
+          if constexpr (DT == kF32) {
+            f = static_cast<const float*>(rows)[r * dim + d];
+            bits = __float_as_uint(f);
+          } else {
+            bits = static_cast<const uint16_t*>(rows)[r * dim + d];
+            f = bf16_to_f32(bits);
+          }
+          acc = fma(static_cast<double>(f), static_cast<double>(f), acc);
+        }
+        if constexpr (DT == kF32) {
+          w[e] = bits;
+        } else {
+          w[e / 2] |= (e & 1) ? (bits << 16) : bits;
+        }
+      }
+      u32x4 v;
+      v.x = w[0];
+      v.y = w[1];
+      v.z = w[2];
+      v.w = w[3];
+      dst[static_cast<size_t>(c) * kWave] = v;
+    }
+    norms[slot] = static_cast<float>(sqrt(acc));
+    slot_ids[slot] = ids ? ids[r] : slot;
+  }
+}
+
+__global__ void mla_evict_kernel(const uint64_t* __restrict__ slots,
+                                 uint64_t count, float* __restrict__ norms,
+                                 uint64_t* __restrict__ slot_ids) {
+  for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+       i < count; i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+    const uint64_t s = slots[i];
+    norms[s] = __uint_as_float(0xffffffffu);
+    slot_ids[s] = kNoId;
+  }
+}
+
+}  // namespace mla
+}  // namespace grm
+
+using grm::Cand;
+using grm::kBF16;
+using grm::kF32;
+using grm::kNoId;
+using grm::mla::u32x4;
+
+// ------------------------------------------------------------------ host side
+
+struct MlaDeviceArena {
+  int device = 0;
+  int dtype = kF32;
+  uint32_t dim = 0;
+  uint32_t dim_pad = 0;
+  uint32_t epc = 4;
+  uint32_t chunks = 0;
+  uint64_t capacity = 0;    // slots, multiple of 64
+  uint64_t high_water = 0;  // slots [0, high_water) may hold live rows
+  uint64_t live = 0;
+  uint64_t epoch = 0;
+  u32x4* d_tiles = nullptr;
+  float* d_norms = nullptr;
+  uint64_t* d_ids = nullptr;
+  std::vector<uint64_t> slot_id;  // kNoId when free
+  std::unordered_map<uint64_t, uint64_t> slot_of;
+  std::set<uint64_t> free_slots;  // freed slots below high_water
+  void* d_queries = nullptr;
+  size_t d_queries_bytes = 0;
+  Cand* d_block = nullptr;
+  size_t d_block_count = 0;
+  Cand* d_out = nullptr;
+  size_t d_out_count = 0;
+  Cand* h_out = nullptr;
+  size_t h_out_count = 0;
+  unsigned* d_ticket = nullptr;
+  void* h_stage = nullptr;
+  size_t h_stage_bytes = 0;
+  void* d_stage = nullptr;
+  size_t d_stage_bytes = 0;
+  hipStream_t stream = nullptr;
+  hipStream_t side = nullptr;
+  hipEvent_t ev_start = nullptr;
+  hipEvent_t ev_stop = nullptr;
+  hipEvent_t ev_mut = nullptr;
+  bool mut_pending = false;
+  uint32_t max_blocks = 1024;
+};
+
+namespace {
+
+size_t elem_size(int dtype) { return dtype == kF32 ? 4 : 2; }
+
+void destroy_arena(MlaDeviceArena* a) {
+  if (!a) return;
+  (void)hipSetDevice(a->device);
+  if (a->stream) (void)hipStreamSynchronize(a->stream);
+  if (a->side) (void)hipStreamSynchronize(a->side);
+  if (a->d_tiles) (void)hipFree(a->d_tiles);
+  if (a->d_norms) (void)hipFree(a->d_norms);
+  if (a->d_ids) (void)hipFree(a->d_ids);
+  if (a->d_queries) (void)hipFree(a->d_queries);
+  if (a->d_block) (void)hipFree(a->d_block);
+  if (a->d_out) (void)hipFree(a->d_out);
+  if (a->d_ticket) (void)hipFree(a->d_ticket);
+  if (a->d_stage) (void)hipFree(a->d_stage);
+  if (a->h_out) (void)hipHostFree(a->h_out);
+  if (a->h_stage) (void)hipHostFree(a->h_stage);
+  if (a->ev_start) (void)hipEventDestroy(a->ev_start);
+  if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
+  if (a->ev_mut) (void)hipEventDestroy(a->ev_mut);
+  if (a->stream) (void)hipStreamDestroy(a->stream);
+  if (a->side) (void)hipStreamDestroy(a->side);
+  delete a;
+}
+
+template <typename T>
+int reserve_device(T** ptr, size_t* have, size_t want) {
+  if (want <= *have && *ptr) return 0;
+  if (*ptr) {
+    GRM_HIP_CHECK(hipFree(*ptr));
+    *ptr = nullptr;
+    *have = 0;
+  }
+  GRM_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(ptr), want * sizeof(T)));
+  *have = want;
+  return 0;
+}
+
+template <typename T>
+int reserve_pinned(T** ptr, size_t* have, size_t want) {
+  if (want <= *have && *ptr) return 0;
+  if (*ptr) {
+    GRM_HIP_CHECK(hipHostFree(*ptr));
+    *ptr = nullptr;
+    *have = 0;
+  }
+  GRM_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(ptr), want * sizeof(T),
+                              hipHostMallocDefault));
+  *have = want;
+  return 0;
+}
+
+int wait_mutations(MlaDeviceArena* a) {
+  if (a->mut_pending) {
+    GRM_HIP_CHECK(hipEventSynchronize(a->ev_mut));
+    a->mut_pending = false;
+  }
+  return 0;
+}
+
+// Launch the placement kernel over `count` staged rows on `stream`.
+int launch_place(MlaDeviceArena* a, const void* d_rows, uint64_t count,
+                 const uint64_t* d_slots, const uint64_t* d_ids, uint64_t slot0,
+                 hipStream_t stream) {
+  if (count == 0) return 0;
+  const unsigned threads = 256;
+  const unsigned blocks = static_cast<unsigned>(
+      std::min<uint64_t>((count + threads - 1) / threads, 4096));
+  if (a->dtype == kF32) {
+    grm::mla::mla_place_rows_kernel<kF32><<<blocks, threads, 0, stream>>>(
+        d_rows, count, a->dim, a->chunks, d_slots, d_ids, slot0, a->d_tiles,
+        a->d_norms, a->d_ids);
+  } else {
+    grm::mla::mla_place_rows_kernel<kBF16><<<blocks, threads, 0, stream>>>(
+        d_rows, count, a->dim, a->chunks, d_slots, d_ids, slot0, a->d_tiles,
+        a->d_norms, a->d_ids);
+  }
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
+int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
+                 const uint64_t* node_ids, uint64_t capacity,
+                 MlaDeviceArena** out) {
+  if (!out) return grm::fail(-1, "null output arena pointer");
+  *out = nullptr;
+  if (dim <= 0 || static_cast<uint32_t>(dim) > grm::mla::kMaxDim) {
+    return grm::fail(-1, "dim must be in [1, 4096]");
+  }
+  if (dtype != kF32 && dtype != kBF16) {
+    return grm::fail(-1, "MLA bank dtype must be F32 or BF16");
+  }
+  if (nodes > 0 && !rows) return grm::fail(-1, "null rows with nonzero nodes");
+  if (capacity < nodes) capacity = nodes;
+  if (capacity == 0) return grm::fail(-1, "bank needs nodes or capacity");
+  if (capacity > (1ull << 31)) return grm::fail(-1, "capacity above 2^31 slots");
+  auto* a = new MlaDeviceArena();
+  int rc = 0;
+  auto bail = [&](int code) {
+    destroy_arena(a);
+    return code;
+  };
+  if (hipGetDevice(&a->device) != hipSuccess) a->device = 0;
+  a->dtype = dtype;
+  a->dim = static_cast<uint32_t>(dim);
+  a->epc = dtype == kF32 ? 4 : 8;
+  a->dim_pad = (a->dim + a->epc - 1) / a->epc * a->epc;
+  a->chunks = a->dim_pad / a->epc;
+  a->capacity = (capacity + grm::kWave - 1) / grm::kWave * grm::kWave;
+  if (const char* env = getenv("GRM_HIP_MLA_BLOCKS")) {
+    const long v = strtol(env, nullptr, 10);
+    if (v >= 1 && v <= 65536) a->max_blocks = static_cast<uint32_t>(v);
+  }
+  a->slot_id.assign(a->capacity, kNoId);
+  if (node_ids) {
+    a->slot_of.reserve(nodes * 2);
+    for (uint64_t i = 0; i < nodes; ++i) {
+      if (!a->slot_of.emplace(node_ids[i], i).second) {
+        return bail(grm::fail(-1, "duplicate node id"));
+      }
+      a->slot_id[i] = node_ids[i];
+    }
+  } else {
+    a->slot_of.reserve(nodes * 2);
+    for (uint64_t i = 0; i < nodes; ++i) {
+      a->slot_of.emplace(i, i);
+      a->slot_id[i] = i;
+    }
+  }
+  const size_t tile_bytes = static_cast<size_t>(a->chunks) * grm::kWave * 16;
+  const size_t tiles = a->capacity / grm::kWave;
+#define BAIL_HIP(expr)                                  \
+  do {                                                  \
+    hipError_t e_ = (expr);                             \
+    if (e_ != hipSuccess) return bail(grm::fail_hip(e_, #expr)); \
+  } while (0)
+  BAIL_HIP(hipStreamCreateWithFlags(&a->stream, hipStreamDefault));
+  BAIL_HIP(hipStreamCreateWithFlags(&a->side, hipStreamNonBlocking));
+  BAIL_HIP(hipEventCreate(&a->ev_start));
+  BAIL_HIP(hipEventCreate(&a->ev_stop));
+  BAIL_HIP(hipEventCreateWithFlags(&a->ev_mut, hipEventDisableTiming));
+  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_tiles), tiles * tile_bytes));
+  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_norms), a->capacity * sizeof(float)));
+  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_ids), a->capacity * sizeof(uint64_t)));
+  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_ticket), sizeof(unsigned)));
+  BAIL_HIP(hipMemsetAsync(a->d_tiles, 0, tiles * tile_bytes, a->stream));
+  BAIL_HIP(hipMemsetAsync(a->d_norms, 0xff, a->capacity * sizeof(float), a->stream));
+  BAIL_HIP(hipMemsetAsync(a->d_ids, 0xff, a->capacity * sizeof(uint64_t), a->stream));
+  BAIL_HIP(hipMemsetAsync(a->d_ticket, 0, sizeof(unsigned), a->stream));
+  if (nodes > 0) {
+    const size_t row_bytes = static_cast<size_t>(a->dim) * elem_size(dtype);
+    const uint64_t batch = std::min<uint64_t>(nodes, grm::mla::kStageRows);
+    rc = reserve_device(reinterpret_cast<unsigned char**>(&a->d_stage),
+                        &a->d_stage_bytes,
+                        batch * (row_bytes + sizeof(uint64_t)));
+    if (rc) return bail(rc);
+    for (uint64_t r0 = 0; r0 < nodes; r0 += batch) {
+      const uint64_t n = std::min<uint64_t>(batch, nodes - r0);
+      unsigned char* d_rows = static_cast<unsigned char*>(a->d_stage);
+      uint64_t* d_idbuf = reinterpret_cast<uint64_t*>(d_rows + batch * row_bytes);
+      BAIL_HIP(hipMemcpyAsync(d_rows,
+                              static_cast<const unsigned char*>(rows) + r0 * row_bytes,
+                              n * row_bytes, hipMemcpyHostToDevice, a->stream));
+      if (node_ids) {
+        BAIL_HIP(hipMemcpyAsync(d_idbuf, node_ids + r0, n * sizeof(uint64_t),
+                                hipMemcpyHostToDevice, a->stream));
+      }
+      rc = launch_place(a, d_rows, n, nullptr, node_ids ? d_idbuf : nullptr,
+                        r0, a->stream);
+      if (rc) return bail(rc);
+      // The staging buffer is reused by the next batch.
+      BAIL_HIP(hipStreamSynchronize(a->stream));
+    }
+  }
+  BAIL_HIP(hipStreamSynchronize(a->stream));
+#undef BAIL_HIP
+  a->high_water = nodes;
+  a->live = nodes;
+  *out = a;
+  grm::clear_error();
+  return 0;
+}
+
+int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
+               bool on_device, int q_count, int dim, int warmup, int topk,
+               uint64_t* out_ids, float* out_scores, float* elapsed_ms) {
+  if (!a || !queries || !out_ids) return grm::fail(-1, "null argument");
+  if (dim != static_cast<int>(a->dim)) return grm::fail(-1, "query dim does not match bank");
+  if (q_dtype != kF32 && q_dtype != kBF16) return grm::fail(-1, "query dtype must be F32 or BF16");
+  if (q_count <= 0 || warmup < 0 || warmup >= q_count) {
+    return grm::fail(-1, "need query_count > 0 and 0 <= warmup < query_count");
+  }
+  if (topk <= 0 || topk > grm::kMaxTopK || static_cast<uint64_t>(topk) > a->live) {
+    return grm::fail(-1, "topk must be in [1, 16] and <= live nodes");
+  }
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  const size_t qbytes = static_cast<size_t>(q_count) * a->dim * elem_size(q_dtype);
+  const uint32_t num_tiles = static_cast<uint32_t>((a->high_water + grm::kWave - 1) / grm::kWave);
+  const uint32_t want_blocks = (num_tiles + grm::mla::kRouteWaves - 1) / grm::mla::kRouteWaves;
+  const uint32_t blocks = std::max<uint32_t>(1, std::min(want_blocks, a->max_blocks));
+  GRM_CHECK_RC(reserve_device(&a->d_block, &a->d_block_count,
+                              static_cast<size_t>(blocks) * grm::kMaxTopK));
+  GRM_CHECK_RC(reserve_device(&a->d_out, &a->d_out_count,
+                              static_cast<size_t>(q_count) * topk));
+  GRM_CHECK_RC(reserve_pinned(&a->h_out, &a->h_out_count,
+                              static_cast<size_t>(q_count) * topk));
+  const unsigned char* qbase = static_cast<const unsigned char*>(queries);
+  if (!on_device) {
+    GRM_CHECK_RC(reserve_device(reinterpret_cast<unsigned char**>(&a->d_queries),
+                                &a->d_queries_bytes, qbytes));
+    GRM_HIP_CHECK(hipMemcpyAsync(a->d_queries, queries, qbytes,
+                                 hipMemcpyHostToDevice, a->stream));
+    qbase = static_cast<const unsigned char*>(a->d_queries);
+  }
+  if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
+  const size_t qstride = static_cast<size_t>(a->dim) * elem_size(q_dtype);
+  const size_t lds = static_cast<size_t>(a->dim_pad) * sizeof(double);
+  for (int qi = 0; qi < q_count; ++qi) {
+    if (qi == warmup) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+    const void* q = qbase + qi * qstride;
+    Cand* out = a->d_out + static_cast<size_t>(qi) * topk;
+    if (a->dtype == kF32) {
+      grm::mla::mla_route_kernel<kF32, grm::mla::kRouteWaves>
+          <<<blocks, grm::mla::kRouteWaves * grm::kWave, lds, a->stream>>>(
+              a->d_tiles, a->d_norms, a->d_ids, num_tiles, a->chunks, a->dim,
+              a->dim_pad, q, q_dtype, topk, a->d_block, a->d_ticket, out);
+    } else {
+      grm::mla::mla_route_kernel<kBF16, grm::mla::kRouteWaves>
+          <<<blocks, grm::mla::kRouteWaves * grm::kWave, lds, a->stream>>>(
+              a->d_tiles, a->d_norms, a->d_ids, num_tiles, a->chunks, a->dim,
+              a->dim_pad, q, q_dtype, topk, a->d_block, a->d_ticket, out);
+    }
+    GRM_HIP_CHECK(hipGetLastError());
+  }
+  GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
+  GRM_HIP_CHECK(hipMemcpyAsync(a->h_out, a->d_out,
+                               static_cast<size_t>(q_count) * topk * sizeof(Cand),
+                               hipMemcpyDeviceToHost, a->stream));
+  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
+  for (size_t i = 0; i < static_cast<size_t>(q_count) * topk; ++i) {
+    const Cand& c = a->h_out[i];
+    const bool ok = isfinite(c.score) && c.id != kNoId;
+    out_ids[i] = ok ? c.id : kNoId;
+    if (out_scores) out_scores[i] = ok ? c.score : __builtin_nanf("");
+  }
+  grm::clear_error();
+  return 0;
+}
+
+int stage_upload(MlaDeviceArena* a, size_t bytes, void** host, void** dev) {
+  GRM_CHECK_RC(wait_mutations(a));
+  GRM_CHECK_RC(reserve_pinned(reinterpret_cast<unsigned char**>(&a->h_stage),
+                              &a->h_stage_bytes, bytes));
+  GRM_CHECK_RC(reserve_device(reinterpret_cast<unsigned char**>(&a->d_stage),
+                              &a->d_stage_bytes, bytes));
+  *host = a->h_stage;
+  *dev = a->d_stage;
+  return 0;
+}
+
+}  // namespace
+
+// ============================================================ reference ABI
+
+extern "C" int grm_mla_cuda_arena_create(const float* rows_host, int nodes,
+                                         int dim, MlaDeviceArena** out_arena) {
+  if (!rows_host || !out_arena || nodes <= 0 || dim <= 0) {
+    return grm::fail(-1, "invalid MLA arena arguments");
+  }
+  return create_arena(rows_host, kF32, static_cast<uint64_t>(nodes), dim,
+                      nullptr, static_cast<uint64_t>(nodes), out_arena);
+}
+
+extern "C" int grm_mla_cuda_arena_route(MlaDeviceArena* arena,
+                                        const float* queries_host,
+                                        int query_count, int dim, int warmup,
+                                        int topk, uint64_t* out_topk_host,
+                                        float* elapsed_ms_host) {
+  if (!arena || !queries_host || query_count <= 0 || dim <= 0 ||
+      !elapsed_ms_host) {
+    return grm::fail(-1, "invalid MLA route arguments");
+  }
+  return route_impl(arena, queries_host, kF32, false, query_count, dim, warmup,
+                    topk, out_topk_host, nullptr, elapsed_ms_host);
+}
+
+extern "C" int grm_mla_cuda_arena_route_device(MlaDeviceArena* arena,
+                                               const float* d_queries,
+                                               int query_count, int dim,
+                                               int warmup, int topk,
+                                               uint64_t* out_topk_host,
+                                               float* elapsed_ms_host) {
+  if (!arena || !elapsed_ms_host) return grm::fail(-1, "invalid MLA route arguments");
+  return route_impl(arena, d_queries, kF32, true, query_count, dim, warmup,
+                    topk, out_topk_host, nullptr, elapsed_ms_host);
+}
+
+extern "C" int grm_mla_cuda_upload_queries(const float* host_buf,
+                                           size_t num_floats,
+                                           float** out_device_ptr) {
+  if (!host_buf || !out_device_ptr || num_floats == 0) {
+    return grm::fail(-1, "invalid upload arguments");
+  }
+  *out_device_ptr = nullptr;
+  float* d = nullptr;
+  GRM_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&d), num_floats * sizeof(float)));
+  hipError_t rc = hipMemcpy(d, host_buf, num_floats * sizeof(float), hipMemcpyHostToDevice);
+  if (rc != hipSuccess) {
+    (void)hipFree(d);
+    return grm::fail_hip(rc, "hipMemcpy");
+  }
+  *out_device_ptr = d;
+  return 0;
+}
+
+extern "C" int grm_mla_cuda_free_device_ptr(float* device_ptr) {
+  if (!device_ptr) return 0;
+  GRM_HIP_CHECK(hipFree(device_ptr));
+  return 0;
+}
+
+extern "C" int grm_mla_cuda_arena_destroy(MlaDeviceArena* arena) {
+  destroy_arena(arena);
+  return 0;
+}
+
+extern "C" int grm_mla_cublas_route(const float* rows_host,
+                                    const float* queries_host, int nodes,
+                                    int dim, int query_count, int warmup,
+                                    int topk, uint64_t* out_topk_host,
+                                    float* elapsed_ms_host) {
+  MlaDeviceArena* arena = nullptr;
+  int rc = grm_mla_cuda_arena_create(rows_host, nodes, dim, &arena);
+  if (rc != 0) return rc;
+  rc = grm_mla_cuda_arena_route(arena, queries_host, query_count, dim, warmup,
+                                topk, out_topk_host, elapsed_ms_host);
+  const int drc = grm_mla_cuda_arena_destroy(arena);
+  return rc != 0 ? rc : drc;
+}
+
+// =============================================================== extensions
+
+extern "C" int grm_mla_hip_bank_create(const void* rows_host, int row_dtype,
+                                       uint64_t nodes, int dim,
+                                       const uint64_t* node_ids,
+                                       uint64_t capacity,
+                                       MlaDeviceArena** out_arena) {
+  return create_arena(rows_host, row_dtype, nodes, dim, node_ids, capacity,
+                      out_arena);
+}
+
+extern "C" int grm_mla_hip_route(MlaDeviceArena* arena, const void* queries,
+                                 int query_dtype, int queries_on_device,
+                                 int query_count, int dim, int warmup,
+                                 int topk, uint64_t* out_ids_host,
+                                 float* out_scores_host,
+                                 float* elapsed_ms_host) {
+  return route_impl(arena, queries, query_dtype, queries_on_device != 0,
+                    query_count, dim, warmup, topk, out_ids_host,
+                    out_scores_host, elapsed_ms_host);
+}
+
+extern "C" int grm_mla_hip_append(MlaDeviceArena* a, const void* rows_host,
+                                  int row_dtype, uint64_t count,
+                                  const uint64_t* node_ids,
+                                  uint64_t* out_epoch) {
+  if (!a || (count > 0 && (!rows_host || !node_ids))) {
+    return grm::fail(-1, "invalid append arguments");
+  }
+  if (row_dtype != a->dtype) return grm::fail(-1, "append dtype differs from bank");
+  if (count == 0) {
+    if (out_epoch) *out_epoch = a->epoch;
+    return 0;
+  }
+  {
+    std::unordered_map<uint64_t, int> seen;
+    seen.reserve(count * 2);
+    for (uint64_t i = 0; i < count; ++i) {
+      if (a->slot_of.count(node_ids[i]) || !seen.emplace(node_ids[i], 1).second) {
+        return grm::fail(-1, "append id already live or repeated");
+      }
+      if (node_ids[i] == kNoId) return grm::fail(-1, "node id UINT64_MAX is reserved");
+    }
+  }
+  const uint64_t room = a->free_slots.size() + (a->capacity - a->high_water);
+  if (count > room) return grm::fail(-3, "MLA bank capacity exceeded");
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  const size_t row_bytes = static_cast<size_t>(a->dim) * elem_size(a->dtype);
+  const size_t bytes = count * (2 * sizeof(uint64_t) + row_bytes);
+  void* h = nullptr;
+  void* d = nullptr;
+  GRM_CHECK_RC(stage_upload(a, bytes, &h, &d));
+  uint64_t* h_slots = static_cast<uint64_t*>(h);
+  uint64_t* h_ids = h_slots + count;
+  unsigned char* h_rows = reinterpret_cast<unsigned char*>(h_ids + count);
+  std::vector<uint64_t> taken;
+  taken.reserve(count);
+  for (uint64_t i = 0; i < count; ++i) {
+    uint64_t slot;
+    if (!a->free_slots.empty()) {
+      slot = *a->free_slots.begin();
+      a->free_slots.erase(a->free_slots.begin());
+    } else {
+      slot = a->high_water++;
+    }
+    h_slots[i] = slot;
+    h_ids[i] = node_ids[i];
+    a->slot_id[slot] = node_ids[i];
+    a->slot_of[node_ids[i]] = slot;
+  }
+  memcpy(h_rows, rows_host, count * row_bytes);
+  uint64_t* d_slots = static_cast<uint64_t*>(d);
+  uint64_t* d_ids = d_slots + count;
+  unsigned char* d_rows = reinterpret_cast<unsigned char*>(d_ids + count);
+  GRM_HIP_CHECK(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, a->side));
+  GRM_CHECK_RC(launch_place(a, d_rows, count, d_slots, d_ids, 0, a->side));
+  GRM_HIP_CHECK(hipEventRecord(a->ev_mut, a->side));
+  a->mut_pending = true;
+  a->live += count;
+  a->epoch += 1;
+  if (out_epoch) *out_epoch = a->epoch;
+  grm::clear_error();
+  return 0;
+}
+
+extern "C" int grm_mla_hip_evict(MlaDeviceArena* a, const uint64_t* node_ids,
+                                 uint64_t count, uint64_t* out_epoch) {
+  if (!a || (count > 0 && !node_ids)) return grm::fail(-1, "invalid evict arguments");
+  if (count == 0) {
+    if (out_epoch) *out_epoch = a->epoch;
+    return 0;
+  }
+  std::vector<uint64_t> slots;
+  slots.reserve(count);
+  {
+    std::unordered_map<uint64_t, int> seen;
+    seen.reserve(count * 2);
+    for (uint64_t i = 0; i < count; ++i) {
+      auto it = a->slot_of.find(node_ids[i]);
+      if (it == a->slot_of.end() || !seen.emplace(node_ids[i], 1).second) {
+        return grm::fail(-1, "evict id not live or repeated");
+      }
+      slots.push_back(it->second);
+    }
+  }
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  const size_t bytes = count * sizeof(uint64_t);
+  void* h = nullptr;
+  void* d = nullptr;
+  GRM_CHECK_RC(stage_upload(a, bytes, &h, &d));
+  memcpy(h, slots.data(), bytes);
+  GRM_HIP_CHECK(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, a->side));
+  const unsigned threads = 256;
+  const unsigned blocks = static_cast<unsigned>(std::min<uint64_t>((count + threads - 1) / threads, 1024));
+  grm::mla::mla_evict_kernel<<<blocks, threads, 0, a->side>>>(
+      static_cast<const uint64_t*>(d), count, a->d_norms, a->d_ids);
+  GRM_HIP_CHECK(hipGetLastError());
+  GRM_HIP_CHECK(hipEventRecord(a->ev_mut, a->side));
+  a->mut_pending = true;
+  for (uint64_t s : slots) {
+    a->slot_of.erase(a->slot_id[s]);
+    a->slot_id[s] = kNoId;
+    a->free_slots.insert(s);
+  }
+  // Trailing free slots shrink the scanned range.
+  while (a->high_water > 0 && a->slot_id[a->high_water - 1] == kNoId) {
+    a->free_slots.erase(a->high_water - 1);
+    a->high_water -= 1;
+  }
+  a->live -= count;
+  a->epoch += 1;
+  if (out_epoch) *out_epoch = a->epoch;
+  grm::clear_error();
+  return 0;
+}
+
+extern "C" int grm_mla_hip_sync(MlaDeviceArena* a) {
+  if (!a) return grm::fail(-1, "null arena");
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  return wait_mutations(a);
+}
+
+extern "C" int grm_mla_hip_bank_info(MlaDeviceArena* a, uint64_t* out6) {
+  if (!a || !out6) return grm::fail(-1, "null argument");
+  out6[0] = a->live;
+  out6[1] = a->capacity;
+  out6[2] = a->high_water;
+  out6[3] = a->epoch;
+  out6[4] = a->dim;
+  out6[5] = static_cast<uint64_t>(a->dtype);
+  return 0;
+}

@@ -1,0 +1,226 @@
+/*
+ * grm_hip_router.h -- C ABI of libgrm_hip_router.so, the MI355X (gfx950)
+ * GRM graft route library.
+ *
+ * Part 1 keeps the reference sidecar ABI symbol-for-symbol, so the
+ * reference's ctypes bindings load this library unchanged:
+ *   MLA: scripts/grm_mla_cuda_probe.py:286-547 (C source), :575-626 (ctypes)
+ *   GQA: scripts/grm_gqa_cuda_probe.py:297-606 (C source), :634-697 (ctypes)
+ * Part 2 adds the entry points the reference has no counterpart for (node
+ * ids and scores out, bf16/fp16/int8 storage, ragged CSR banks, device-side
+ * append/evict); their comments say so.
+ *
+ * Conventions (both parts, as the reference, scripts/grm_mla_cuda_probe.py:60-66):
+ *   return 0 on success, -1 on invalid arguments, 1000 + hipError_t on a HIP
+ *   runtime error, -3 when a bank's capacity would be exceeded.
+ *   grm_hip_last_error() returns a message for the calling thread's last
+ *   failure.
+ *   Top-k order: score descending, node id ascending; non-finite scores are
+ *   never ranked; unfilled result slots hold UINT64_MAX (ids) / NaN (scores).
+ *   topk must satisfy 1 <= topk <= 16 and topk <= live nodes.
+ *   Every call is synchronous with respect to its outputs; calls on one bank
+ *   must not overlap (one bank per thread, as the reference).
+ */
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct MlaDeviceArena MlaDeviceArena;
+typedef struct GqaDeviceArena GqaDeviceArena;
+
+/* Element types of banks and queries (extension). */
+enum {
+  GRM_DTYPE_F32 = 0,
+  GRM_DTYPE_BF16 = 1,
+  GRM_DTYPE_F16 = 2,
+  GRM_DTYPE_I8 = 3
+};
+
+/* ======================================================= reference MLA ABI */
+
+/* Replaces grm_mla_cuda_arena_create, scripts/grm_mla_cuda_probe.py:286-336.
+ * rows_host [nodes][dim] fp32; node id of row i is i. */
+int grm_mla_cuda_arena_create(const float* rows_host, int nodes, int dim,
+                              MlaDeviceArena** out_arena);
+
+/* Replaces grm_mla_cuda_arena_route, scripts/grm_mla_cuda_probe.py:437-464.
+ * queries_host [query_count][dim] fp32; out_topk_host [query_count][topk]
+ * row ids; elapsed_ms_host = device time of queries [warmup, query_count). */
+int grm_mla_cuda_arena_route(MlaDeviceArena* arena, const float* queries_host,
+                             int query_count, int dim, int warmup, int topk,
+                             uint64_t* out_topk_host, float* elapsed_ms_host);
+
+/* Replaces grm_mla_cuda_arena_route_device, scripts/grm_mla_cuda_probe.py:473-488.
+ * d_queries is a device pointer to [query_count][dim] fp32. */
+int grm_mla_cuda_arena_route_device(MlaDeviceArena* arena,
+                                    const float* d_queries, int query_count,
+                                    int dim, int warmup, int topk,
+                                    uint64_t* out_topk_host,
+                                    float* elapsed_ms_host);
+
+/* Replaces grm_mla_cuda_upload_queries, scripts/grm_mla_cuda_probe.py:493-514. */
+int grm_mla_cuda_upload_queries(const float* host_buf, size_t num_floats,
+                                float** out_device_ptr);
+
+/* Replaces grm_mla_cuda_free_device_ptr, scripts/grm_mla_cuda_probe.py:515-520. */
+int grm_mla_cuda_free_device_ptr(float* device_ptr);
+
+/* Replaces grm_mla_cuda_arena_destroy, scripts/grm_mla_cuda_probe.py:522-525. */
+int grm_mla_cuda_arena_destroy(MlaDeviceArena* arena);
+
+/* Replaces grm_mla_cublas_route (one-shot create/route/destroy),
+ * scripts/grm_mla_cuda_probe.py:527-547.  No BLAS library is involved. */
+int grm_mla_cublas_route(const float* rows_host, const float* queries_host,
+                         int nodes, int dim, int query_count, int warmup,
+                         int topk, uint64_t* out_topk_host,
+                         float* elapsed_ms_host);
+
+/* ======================================================= reference GQA ABI */
+
+/* Replaces grm_gqa_cuda_arena_create, scripts/grm_gqa_cuda_probe.py:297-365.
+ * keys_host [nodes][kv_heads][key_tokens][head_dim] fp32 (zero-padded dense
+ * bank); node id of node i is i. */
+int grm_gqa_cuda_arena_create(const float* keys_host, int nodes, int kv_heads,
+                              int key_tokens, int head_dim,
+                              GqaDeviceArena** out_arena);
+
+/* Replaces grm_gqa_cuda_arena_route, scripts/grm_gqa_cuda_probe.py:484-514.
+ * queries_host [query_count][query_heads][query_tokens][head_dim] fp32. */
+int grm_gqa_cuda_arena_route(GqaDeviceArena* arena, const float* queries_host,
+                             int query_count, int query_heads,
+                             int query_tokens, int warmup, int topk,
+                             uint64_t* out_topk_host, float* elapsed_ms_host);
+
+/* Replaces grm_gqa_cuda_arena_route_device, scripts/grm_gqa_cuda_probe.py:525-536. */
+int grm_gqa_cuda_arena_route_device(GqaDeviceArena* arena,
+                                    const float* d_queries, int query_count,
+                                    int query_heads, int query_tokens,
+                                    int warmup, int topk,
+                                    uint64_t* out_topk_host,
+                                    float* elapsed_ms_host);
+
+/* Replaces grm_gqa_cuda_upload_queries, scripts/grm_gqa_cuda_probe.py:547-567. */
+int grm_gqa_cuda_upload_queries(const float* host_buf, size_t num_floats,
+                                float** out_device_ptr);
+
+/* Replaces grm_gqa_cuda_free_device_ptr, scripts/grm_gqa_cuda_probe.py:569-574. */
+int grm_gqa_cuda_free_device_ptr(float* device_ptr);
+
+/* Replaces grm_gqa_cuda_arena_destroy, scripts/grm_gqa_cuda_probe.py:576-579. */
+int grm_gqa_cuda_arena_destroy(GqaDeviceArena* arena);
+
+/* Replaces grm_gqa_cublas_route, scripts/grm_gqa_cuda_probe.py:581-606. */
+int grm_gqa_cublas_route(const float* keys_host, const float* queries_host,
+                         int nodes, int kv_heads, int key_tokens,
+                         int query_count, int query_heads, int query_tokens,
+                         int head_dim, int warmup, int topk,
+                         uint64_t* out_topk_host, float* elapsed_ms_host);
+
+/* ============================================= extensions (no counterpart) */
+
+/* Message for the calling thread's most recent failure ("" if none).
+ * No counterpart: the reference sidecar reports codes only. */
+const char* grm_hip_last_error(void);
+
+/* Library/device description: writes a short JSON object (device name,
+ * compute units, library version) into out.  No counterpart. */
+int grm_hip_runtime_info(char* out, size_t out_cap);
+
+/* MLA node bank (no counterpart: the reference rebuilds and re-uploads the
+ * whole bank on every mutation, core/graft_arena.py:1164-1198).
+ * rows_host [nodes][dim] of row_dtype (GRM_DTYPE_F32 or GRM_DTYPE_BF16 as
+ * uint16 bit patterns); node_ids [nodes] or NULL (0..nodes-1); capacity is
+ * the slot count to reserve (>= nodes; 0 means nodes). */
+int grm_mla_hip_bank_create(const void* rows_host, int row_dtype,
+                            uint64_t nodes, int dim, const uint64_t* node_ids,
+                            uint64_t capacity, MlaDeviceArena** out_arena);
+
+/* MLA route returning node ids and scores (no counterpart: the reference
+ * returns row ids only).  queries [query_count][dim] of query_dtype
+ * (F32 or BF16 bits); queries_on_device selects a device pointer.
+ * out_ids_host / out_scores_host are [query_count][topk]; scores may be NULL. */
+int grm_mla_hip_route(MlaDeviceArena* arena, const void* queries,
+                      int query_dtype, int queries_on_device, int query_count,
+                      int dim, int warmup, int topk, uint64_t* out_ids_host,
+                      float* out_scores_host, float* elapsed_ms_host);
+
+/* Append `count` rows with node ids (no counterpart).  The upload and the
+ * device-side placement run on the bank's side stream; the next route waits
+ * for them.  out_epoch (may be NULL) receives the bank epoch after the call.
+ * Appending an id that is already live returns -1. */
+int grm_mla_hip_append(MlaDeviceArena* arena, const void* rows_host,
+                       int row_dtype, uint64_t count, const uint64_t* node_ids,
+                       uint64_t* out_epoch);
+
+/* Evict live node ids (tombstone: the slot stops ranking at once and is
+ * reused by later appends).  Unknown ids return -1 and evict nothing.
+ * No counterpart. */
+int grm_mla_hip_evict(MlaDeviceArena* arena, const uint64_t* node_ids,
+                      uint64_t count, uint64_t* out_epoch);
+
+/* Wait for pending side-stream mutations.  No counterpart. */
+int grm_mla_hip_sync(MlaDeviceArena* arena);
+
+/* Bank description: [live, capacity, slots in use, epoch, dim, dtype].
+ * No counterpart. */
+int grm_mla_hip_bank_info(MlaDeviceArena* arena, uint64_t* out6);
+
+/* Ragged GQA node bank over CSR token offsets (no counterpart: the reference
+ * zero-pads every node to the longest, core/graft_arena.py:2979-3042).
+ * keys_host: node i's block [kv_heads][L_i][head_dim] starts at value
+ * offset tok_offsets[i] * kv_heads * head_dim, L_i = tok_offsets[i+1] -
+ * tok_offsets[i]; key_dtype F32, BF16, F16 (bit patterns) or I8.
+ * For I8, scales_host holds one scale per (kv head, token, group of
+ * group_size values) in the same node-major order, scale_dtype F32 or F16;
+ * values dequantise as fp16(code * scale) (core/graft_quant.py:136-144).
+ * capacity_nodes / capacity_tokens reserve room for appends (0 = exact). */
+int grm_gqa_hip_bank_create(const void* keys_host, int key_dtype,
+                            const void* scales_host, int scale_dtype,
+                            int group_size, const uint64_t* tok_offsets,
+                            uint64_t nodes, int kv_heads, int head_dim,
+                            const uint64_t* node_ids, uint64_t capacity_nodes,
+                            uint64_t capacity_tokens,
+                            GqaDeviceArena** out_arena);
+
+/* GQA route returning node ids and scores (no counterpart).  queries
+ * [query_count][query_heads][query_tokens][head_dim] of query_dtype
+ * (F32 or BF16 bits).  Stacked routing layers are expressed by folding the
+ * layer axis into the head axes of both bank and query. */
+int grm_gqa_hip_route(GqaDeviceArena* arena, const void* queries,
+                      int query_dtype, int queries_on_device, int query_count,
+                      int query_heads, int query_tokens, int warmup, int topk,
+                      uint64_t* out_ids_host, float* out_scores_host,
+                      float* elapsed_ms_host);
+
+/* Append `count` nodes; node j has tok_counts[j] tokens and its blocks are
+ * consecutive in keys_host (and scales_host for I8).  Side-stream upload as
+ * grm_mla_hip_append.  No counterpart. */
+int grm_gqa_hip_append(GqaDeviceArena* arena, const void* keys_host,
+                       const void* scales_host, const uint64_t* tok_counts,
+                       uint64_t count, const uint64_t* node_ids,
+                       uint64_t* out_epoch);
+
+/* Evict live node ids (tombstone; token space is reclaimed by
+ * grm_gqa_hip_compact).  No counterpart. */
+int grm_gqa_hip_evict(GqaDeviceArena* arena, const uint64_t* node_ids,
+                      uint64_t count, uint64_t* out_epoch);
+
+/* Compact the token arena on the device (drops evicted nodes' tokens).
+ * No counterpart. */
+int grm_gqa_hip_compact(GqaDeviceArena* arena);
+
+/* Wait for pending side-stream mutations.  No counterpart. */
+int grm_gqa_hip_sync(GqaDeviceArena* arena);
+
+/* Bank description: [live nodes, node capacity, tokens in use, token
+ * capacity, epoch, kv_heads, head_dim, key dtype].  No counterpart. */
+int grm_gqa_hip_bank_info(GqaDeviceArena* arena, uint64_t* out8);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,291 @@
+"""CPU oracle for the GRM graft route -- TEST INFRASTRUCTURE ONLY.
+
+This package is the checker the HIP route library is compared against.  Only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import it; the product package ``graftrepository_amd`` never does.
+
+``grm_oracle.c`` restates the reference's fp64 route laws (citations in that
+file's header).  This module binds it with ctypes and adds the numpy-level
+storage laws the tests need:
+
+* bf16 rounding of fp32 values (round to nearest even, the conversion every
+  bf16 bank/query goes through before the law is applied);
+* the INT8 symmetric quantiser of ``core/graft_quant.py:93-131`` (group-32,
+  fp32 scales) generalised to any group size and fp16 scales, and its
+  dequant law ``core/graft_quant.py:136-144``.
+
+Pinning (which check fixes which function) is listed in ``PINNING`` below and
+exercised by ``tests/test_oracle_pinning.py``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libgrm_oracle.so"
+REF_LIB_PATH = HERE / "_ref" / "libgrm_runtime.so"
+
+F32, BF16, F16, I8 = 0, 1, 2, 3
+
+# function -> the checks that pin it (see tests/test_oracle_pinning.py)
+PINNING = {
+    "mla_route": "reference C++ grm_store_route goldens (tests/golden) + "
+                 "orthonormal closed form + duplicate-row tie blocks + NaN rows",
+    "mla_row_norms": "closed form (unit vectors, Pythagorean triples) + "
+                     "reference goldens via route order",
+    "gqa_route": "reference C++ grm_store_route_gqa goldens on its fp64 path "
+                 "(tests/golden) + hand cases [1,2,0], ties [0,1,2], multi-key",
+    "f16 conversion": "exhaustive agreement with numpy astype(float16)",
+    "bf16 rounding": "agreement with torch.bfloat16 conversion",
+    "int8 quantise/dequant": "round-trip invariants of "
+                             "tests/test_graft_quant_format.py:54-78 + numpy law",
+}
+
+_lib = None
+
+
+def build(force: bool = False) -> Path:
+    """Compile libgrm_oracle.so with the committed Makefile."""
+    if force or not LIB_PATH.exists():
+        subprocess.run(["make", "-s", "-C", str(HERE), "all"], check=True)
+    return LIB_PATH
+
+
+def build_ref() -> Path | None:
+    """Compile the reference CPU router into oracle/_ref when its sources exist."""
+    src = Path(os.environ.get("GRM_REFERENCE_CPP", "/root/reference/cpp"))
+    if not (src / "grm_runtime.cpp").exists():
+        return REF_LIB_PATH if REF_LIB_PATH.exists() else None
+    subprocess.run(["make", "-s", "-C", str(HERE), "ref", f"REF_DIR={src}"],
+                   check=True)
+    return REF_LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        u64, vp, i32 = ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
+        L.grm_oracle_mla_row_norms.argtypes = [vp, u64, u64, vp, i32]
+        L.grm_oracle_mla_row_norms.restype = None
+        L.grm_oracle_mla_qnorm.argtypes = [vp, u64]
+        L.grm_oracle_mla_qnorm.restype = ctypes.c_double
+        L.grm_oracle_mla_scores.argtypes = [vp, u64, u64, vp, vp, u64, vp, i32]
+        L.grm_oracle_mla_scores.restype = None
+        L.grm_oracle_mla_route.argtypes = [
+            vp, u64, u64, vp, vp, vp, u64, u64, i32, vp, vp, vp]
+        L.grm_oracle_mla_route.restype = i32
+        L.grm_oracle_gqa_scores.argtypes = [
+            vp, i32, vp, i32, u64, vp, u64, u64, u64, vp, u64, u64, u64, vp,
+            i32]
+        L.grm_oracle_gqa_scores.restype = i32
+        L.grm_oracle_gqa_route.argtypes = [
+            vp, i32, vp, i32, u64, vp, u64, u64, u64, vp, vp, vp, u64, u64,
+            u64, u64, i32, vp, vp, vp]
+        L.grm_oracle_gqa_route.restype = i32
+        L.grm_oracle_select_topk.argtypes = [vp, vp, vp, u64, u64, vp, vp, vp]
+        L.grm_oracle_select_topk.restype = None
+        L.grm_oracle_f16_from_f32.argtypes = [vp, u64, vp]
+        L.grm_oracle_f16_from_f32.restype = None
+        L.grm_oracle_f32_from_f16.argtypes = [vp, u64, vp]
+        L.grm_oracle_f32_from_f16.restype = None
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+# ------------------------------------------------------------------ storage laws
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even; NaN stays a quiet NaN."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    rounded = u + (np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1)))
+    out = (rounded >> np.uint32(16)).astype(np.uint16)
+    nan = np.isnan(np.ascontiguousarray(x, dtype=np.float32))
+    if np.any(nan):
+        out[nan] = ((u[nan] >> np.uint32(16)) | np.uint32(0x40)).astype(np.uint16)
+    return out
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    return (b.astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 values rounded to the nearest bf16 value (returned as fp32)."""
+    return bf16_to_f32(bf16_bits(x)).reshape(np.shape(x))
+
+
+def f16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16 bit patterns via the oracle's own RNE conversion."""
+    xs = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(xs.shape, dtype=np.uint16)
+    lib().grm_oracle_f16_from_f32(_p(xs), xs.size, _p(out))
+    return out
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(b.shape, dtype=np.float32)
+    lib().grm_oracle_f32_from_f16(_p(b), b.size, _p(out))
+    return out
+
+
+def quantize_int8(x: np.ndarray, group_size: int, scale_dtype: str = "f32"):
+    """Symmetric INT8 quantiser, core/graft_quant.py:93-131 (bits=8).
+
+    ``scale = max|g| / 127`` in fp32 (0 -> 1.0); for ``scale_dtype='f16'`` the
+    scale is rounded to fp16 first and the codes are computed against the
+    rounded scale.  ``codes = clip(round_half_even(g / scale), -128, 127)``.
+    Returns (codes int8 [..., D], scales [..., D/group] as f32 or f16 bits).
+    """
+    xf = np.ascontiguousarray(x, dtype=np.float32)
+    d = xf.shape[-1]
+    if d % group_size:
+        raise ValueError("last axis not divisible by group_size")
+    g = xf.reshape(*xf.shape[:-1], d // group_size, group_size)
+    scale = np.abs(g).max(axis=-1, keepdims=True) / np.float32(127.0)
+    scale = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
+    if scale_dtype == "f16":
+        sbits = f16_bits(scale)
+        scale = f16_to_f32(sbits)
+        scale = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
+        sbits = f16_bits(scale)
+        stored = sbits.reshape(*xf.shape[:-1], d // group_size)
+    elif scale_dtype == "f32":
+        stored = scale.reshape(*xf.shape[:-1], d // group_size)
+    else:
+        raise ValueError("scale_dtype must be 'f32' or 'f16'")
+    codes = np.clip(np.round(g / scale), -128, 127).astype(np.int8)
+    return codes.reshape(xf.shape), stored
+
+
+def dequantize_int8(codes: np.ndarray, scales: np.ndarray, group_size: int,
+                    scale_dtype: str = "f32") -> np.ndarray:
+    """Dequant law core/graft_quant.py:136-144, returned as fp32 values."""
+    c = np.ascontiguousarray(codes, dtype=np.int8)
+    d = c.shape[-1]
+    s = (f16_to_f32(scales) if scale_dtype == "f16"
+         else np.ascontiguousarray(scales, dtype=np.float32))
+    s = s.reshape(*c.shape[:-1], d // group_size, 1)
+    g = c.reshape(*c.shape[:-1], d // group_size, group_size)
+    prod = (g.astype(np.float32) * s).reshape(c.shape)
+    return f16_to_f32(f16_bits(prod))
+
+
+# ------------------------------------------------------------------ MLA
+
+def mla_row_norms(rows: np.ndarray, threads: int = 0) -> np.ndarray:
+    r = np.ascontiguousarray(rows, dtype=np.float32)
+    out = np.empty(r.shape[0], dtype=np.float32)
+    lib().grm_oracle_mla_row_norms(_p(r), r.shape[0], r.shape[1], _p(out),
+                                   threads)
+    return out
+
+
+def mla_qnorm(q: np.ndarray) -> float:
+    qq = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+    return float(lib().grm_oracle_mla_qnorm(_p(qq), qq.size))
+
+
+def mla_scores(rows: np.ndarray, queries: np.ndarray, threads: int = 0):
+    r = np.ascontiguousarray(rows, dtype=np.float32)
+    q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, r.shape[1])
+    norms = mla_row_norms(r, threads)
+    out = np.empty((q.shape[0], r.shape[0]), dtype=np.float32)
+    lib().grm_oracle_mla_scores(_p(r), r.shape[0], r.shape[1], _p(norms),
+                                _p(q), q.shape[0], _p(out), threads)
+    return out
+
+
+def mla_route(rows: np.ndarray, queries: np.ndarray, topk: int, *,
+              node_ids: np.ndarray | None = None,
+              live: np.ndarray | None = None, threads: int = 0):
+    """fp64 MLA law route; returns (ids [Q,k] uint64, scores [Q,k] f32, counts)."""
+    r = np.ascontiguousarray(rows, dtype=np.float32)
+    q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, r.shape[1])
+    ids = None if node_ids is None else np.ascontiguousarray(node_ids, np.uint64)
+    lv = None if live is None else np.ascontiguousarray(live, np.uint8)
+    out_ids = np.empty((q.shape[0], topk), dtype=np.uint64)
+    out_scores = np.empty((q.shape[0], topk), dtype=np.float32)
+    counts = np.empty(q.shape[0], dtype=np.uint64)
+    rc = lib().grm_oracle_mla_route(
+        _p(r), r.shape[0], r.shape[1], _p(ids), _p(lv), _p(q), q.shape[0],
+        topk, threads, _p(out_ids), _p(out_scores), _p(counts))
+    if rc != 0:
+        raise RuntimeError(f"oracle mla_route failed: {rc}")
+    return out_ids, out_scores, counts
+
+
+# ------------------------------------------------------------------ GQA
+
+def _gqa_args(keys, key_dtype, scales, scale_dtype):
+    k = np.ascontiguousarray(keys)
+    s = None if scales is None else np.ascontiguousarray(scales)
+    sd = F16 if scale_dtype == "f16" else F32
+    return k, s, sd
+
+
+def gqa_scores(keys, key_dtype: int, tok_offsets, kv_heads: int, head_dim: int,
+               queries, *, scales=None, scale_dtype: str = "f32",
+               group_size: int = 0, threads: int = 0) -> np.ndarray:
+    """Exact GQA scores [Q, N] (fp64 law) over a CSR key bank."""
+    k, s, sd = _gqa_args(keys, key_dtype, scales, scale_dtype)
+    offs = np.ascontiguousarray(tok_offsets, dtype=np.uint64)
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    if q.ndim == 3:
+        q = q[None]
+    n = offs.size - 1
+    out = np.empty((q.shape[0], n), dtype=np.float32)
+    rc = lib().grm_oracle_gqa_scores(
+        _p(k), key_dtype, _p(s), sd, group_size, _p(offs), n, kv_heads,
+        head_dim, _p(q), q.shape[0], q.shape[1], q.shape[2], _p(out), threads)
+    if rc != 0:
+        raise RuntimeError(f"oracle gqa_scores failed: {rc}")
+    return out
+
+
+def gqa_route(keys, key_dtype: int, tok_offsets, kv_heads: int, head_dim: int,
+              queries, topk: int, *, scales=None, scale_dtype: str = "f32",
+              group_size: int = 0, node_ids=None, live=None, threads: int = 0):
+    k, s, sd = _gqa_args(keys, key_dtype, scales, scale_dtype)
+    offs = np.ascontiguousarray(tok_offsets, dtype=np.uint64)
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    if q.ndim == 3:
+        q = q[None]
+    n = offs.size - 1
+    ids = None if node_ids is None else np.ascontiguousarray(node_ids, np.uint64)
+    lv = None if live is None else np.ascontiguousarray(live, np.uint8)
+    out_ids = np.empty((q.shape[0], topk), dtype=np.uint64)
+    out_scores = np.empty((q.shape[0], topk), dtype=np.float32)
+    counts = np.empty(q.shape[0], dtype=np.uint64)
+    rc = lib().grm_oracle_gqa_route(
+        _p(k), key_dtype, _p(s), sd, group_size, _p(offs), n, kv_heads,
+        head_dim, _p(ids), _p(lv), _p(q), q.shape[0], q.shape[1], q.shape[2],
+        topk, threads, _p(out_ids), _p(out_scores), _p(counts))
+    if rc != 0:
+        raise RuntimeError(f"oracle gqa_route failed: {rc}")
+    return out_ids, out_scores, counts
+
+
+def select_topk(scores, topk: int, node_ids=None, live=None):
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    ids = None if node_ids is None else np.ascontiguousarray(node_ids, np.uint64)
+    lv = None if live is None else np.ascontiguousarray(live, np.uint8)
+    out_ids = np.empty(topk, dtype=np.uint64)
+    out_scores = np.empty(topk, dtype=np.float32)
+    count = np.zeros(1, dtype=np.uint64)
+    lib().grm_oracle_select_topk(_p(s), _p(ids), _p(lv), s.size, topk,
+                                 _p(out_ids), _p(out_scores), _p(count))
+    return out_ids, out_scores, int(count[0])

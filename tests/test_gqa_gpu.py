@@ -1,0 +1,201 @@
+"""Ragged GQA route parity on the GPU: the HIP library against the fp64 oracle.
+
+Bar: node ids bit-exact (ties to the lowest node id), scores bit-exact (the
+kernels evaluate gqa_raw_score, cpp/grm_runtime.cpp:2980-3029, in its
+order).  Hand cases come from the reference tests:
+tests/test_gqa_ragged_cuda_bank.py:213-229 ([1, 2, 0]) and :441-454 (ties
+[0, 1, 2]).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from graftrepository_amd import GqaNodeBank, workloads as wl
+from graftrepository_amd.gqa_probe import HipProbe
+from graftrepository_amd.grm_hip_router import CudaGQARouteSidecar
+from graftrepository_amd.node_bank import bf16_bits_to_f32
+
+pytestmark = pytest.mark.gpu
+NO_ID = np.iinfo(np.uint64).max
+
+
+def assert_same(res, want_ids, want_scores):
+    np.testing.assert_array_equal(res.ids, want_ids)
+    filled = want_ids != NO_ID
+    assert np.all(np.isnan(res.scores[~filled]))
+    np.testing.assert_array_equal(res.scores[filled].view(np.uint32),
+                                  want_scores[filled].view(np.uint32))
+
+
+def ragged(rng, n, kv, hd, lo, hi):
+    lens = rng.integers(lo, hi + 1, size=n).astype(np.uint64)
+    offs = np.zeros(n + 1, np.uint64)
+    offs[1:] = np.cumsum(lens)
+    keys = rng.standard_normal(int(offs[-1]) * kv * hd).astype(np.float32)
+    return keys, offs
+
+
+@pytest.mark.parametrize("kv,H,Qt,hd", [(1, 1, 1, 8), (2, 8, 2, 16),
+                                        (8, 32, 1, 128), (4, 16, 4, 64),
+                                        (8, 8, 3, 32)])
+def test_f32_ragged_parity(hip_lib, kv, H, Qt, hd):
+    rng = np.random.default_rng(kv * 100 + H + Qt + hd)
+    keys, offs = ragged(rng, 150, kv, hd, 0, 150)
+    qs = rng.standard_normal((3, H, Qt, hd)).astype(np.float32)
+    with GqaNodeBank(keys, offs, kv_heads=kv, head_dim=hd) as bank:
+        res = bank.route(qs, 6)
+    ids, sc, _ = oracle.gqa_route(keys, oracle.F32, offs, kv, hd, qs, 6)
+    assert_same(res, ids, sc)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_half_banks_parity(hip_lib, dtype):
+    lens = wl.gqa_lengths(300, seed=7, lo=1, hi=200)
+    keys, offs = wl.gqa_bank(lens, 8, 128, seed=7, dtype=dtype)
+    qs = wl.gqa_queries(2, 32, 1, 128, seed=7, dtype="bf16")
+    with GqaNodeBank(keys, offs, kv_heads=8, head_dim=128, dtype=dtype) as bank:
+        res = bank.route(qs, 5, query_dtype="bf16")
+    code = oracle.BF16 if dtype == "bf16" else oracle.F16
+    ids, sc, _ = oracle.gqa_route(keys, code, offs, 8, 128,
+                                  bf16_bits_to_f32(qs).reshape(qs.shape), 5)
+    assert_same(res, ids, sc)
+
+
+@pytest.mark.parametrize("group,scale_dtype", [(32, "f32"), (128, "f16"),
+                                               (64, "f32")])
+def test_int8_bank_parity(hip_lib, group, scale_dtype):
+    rng = np.random.default_rng(group)
+    keys, offs = ragged(rng, 200, 8, 128, 1, 120)
+    codes, scales = oracle.quantize_int8(keys.reshape(-1, 128), group,
+                                         scale_dtype)
+    qs = rng.standard_normal((2, 32, 1, 128)).astype(np.float32)
+    with GqaNodeBank(codes, offs, kv_heads=8, head_dim=128, dtype="i8",
+                     scales=scales, scale_dtype=scale_dtype,
+                     group_size=group) as bank:
+        res = bank.route(qs, 5)
+    sd = "f16" if scale_dtype == "f16" else "f32"
+    ids, sc, _ = oracle.gqa_route(codes, oracle.I8, offs, 8, 128, qs, 5,
+                                  scales=scales, scale_dtype=sd,
+                                  group_size=group)
+    assert_same(res, ids, sc)
+
+
+def test_reference_hand_cases(hip_lib):
+    # tests/test_gqa_ragged_cuda_bank.py:213-229
+    rows = [np.asarray([[[0.05, 0.0]]], np.float32),
+            np.asarray([[[0.1, 0.0], [2.0, 0.0], [0.3, 0.0]]], np.float32),
+            np.asarray([[[0.4, 0.0], [0.2, 0.0]]], np.float32)]
+    q = np.asarray([[[1.0, 0.0]]], np.float32)
+    # head_dim 2 is below the 16-byte row granule; pad with zero dims, which
+    # leaves every dot product unchanged.
+    pad = lambda a: np.concatenate([a, np.zeros(a.shape[:-1] + (2,), np.float32)], -1)
+    keys = np.concatenate([pad(r).reshape(-1) for r in rows])
+    offs = np.asarray([0, 1, 4, 6], np.uint64)
+    with GqaNodeBank(keys, offs, kv_heads=1, head_dim=4) as bank:
+        assert bank.route(pad(q), 3).ids[0].tolist() == [1, 2, 0]
+        assert bank.route(pad(q), 2).ids[0].tolist() == [1, 2]
+    # :441-454 identical rows tie to the lowest id
+    row = pad(np.asarray([[[1.0, 0.0], [0.0, 0.5]]], np.float32))
+    keys = np.concatenate([row.reshape(-1)] * 3)
+    offs = np.asarray([0, 2, 4, 6], np.uint64)
+    with GqaNodeBank(keys, offs, kv_heads=1, head_dim=4) as bank:
+        assert bank.route(pad(q), 3).ids[0].tolist() == [0, 1, 2]
+
+
+def test_empty_nodes_nonfinite_keys_and_query(hip_lib):
+    rng = np.random.default_rng(3)
+    kv, hd, H = 2, 16, 4
+    lens = np.asarray([3, 0, 5, 2, 0, 4], np.uint64)
+    offs = np.zeros(lens.size + 1, np.uint64)
+    offs[1:] = np.cumsum(lens)
+    keys = rng.standard_normal(int(offs[-1]) * kv * hd).astype(np.float32)
+    # poison node 3
+    keys[int(offs[3]) * kv * hd + 5] = np.nan
+    q = rng.standard_normal((1, H, 1, hd)).astype(np.float32)
+    with GqaNodeBank(keys, offs, kv_heads=kv, head_dim=hd) as bank:
+        res = bank.route(q, 5)
+        ids, sc, _ = oracle.gqa_route(keys, oracle.F32, offs, kv, hd, q, 5)
+        assert_same(res, ids, sc)
+        assert 3 not in res.ids[0].tolist()
+        assert {1, 4} <= set(res.ids[0].tolist())  # empty nodes score 0.0
+        bad = q.copy()
+        bad[0, 1, 0, 2] = np.inf
+        res = bank.route(bad, 5)
+        ids, sc, _ = oracle.gqa_route(keys, oracle.F32, offs, kv, hd, bad, 5)
+        assert_same(res, ids, sc)
+        assert sorted(res.ids[0][:2].tolist()) == [1, 4]
+
+
+def test_dense_reference_surface(hip_lib):
+    rng = np.random.default_rng(12)
+    bank_np = rng.standard_normal((64, 4, 32, 64)).astype(np.float32)
+    bank_np[:, :, 20:, :] = 0.0  # zero-padded tails
+    qs = rng.standard_normal((4, 16, 2, 64)).astype(np.float32)
+    node_ids = np.arange(64, dtype=np.uint64) * 7
+    sidecar = CudaGQARouteSidecar.build()
+    bank = sidecar.create_bank(bank_np, node_ids)
+    mapped, receipt = bank.route_topk(qs, topk=4, warmup=1)
+    offs = np.arange(65, dtype=np.uint64) * 32
+    want, _, _ = oracle.gqa_route(bank_np.reshape(-1), oracle.F32, offs, 4, 64,
+                                  qs, 4)
+    np.testing.assert_array_equal(mapped, node_ids[want])
+    assert receipt.measured_queries == 3
+    probe = HipProbe()
+    dq = probe.upload_queries(qs)
+    mapped_d, _ = bank.route_topk_device(dq, topk=4)
+    np.testing.assert_array_equal(mapped_d, mapped)
+    dq.close()
+    bank.close()
+
+
+def test_append_evict_compact(hip_lib):
+    rng = np.random.default_rng(77)
+    kv, hd, H = 4, 32, 8
+    keys, offs = ragged(rng, 80, kv, hd, 1, 60)
+    ids0 = np.arange(80, dtype=np.uint64) + 1
+    q = rng.standard_normal((2, H, 1, hd)).astype(np.float32)
+    blocks = {int(i): keys[int(offs[j]) * kv * hd:int(offs[j + 1]) * kv * hd]
+              for j, i in enumerate(ids0)}
+    with GqaNodeBank(keys, offs, kv_heads=kv, head_dim=hd, node_ids=ids0,
+                     capacity_nodes=200, capacity_tokens=20000) as bank:
+        for step in range(3):
+            ev = rng.choice(sorted(blocks), size=10, replace=False)
+            bank.evict(ev)
+            for i in ev.tolist():
+                del blocks[i]
+            lens = rng.integers(0, 70, size=12)
+            new = [rng.standard_normal(int(L) * kv * hd).astype(np.float32)
+                   for L in lens]
+            nid = np.arange(12, dtype=np.uint64) + 1000 + 100 * step
+            bank.append(np.concatenate(new), lens, nid)
+            for i, b in zip(nid.tolist(), new):
+                blocks[i] = b
+            if step == 1:
+                bank.compact()
+            order = sorted(blocks)
+            cat = np.concatenate([blocks[i] for i in order])
+            lens_now = [blocks[i].size // (kv * hd) for i in order]
+            o = np.zeros(len(order) + 1, np.uint64)
+            o[1:] = np.cumsum(lens_now)
+            res = bank.route(q, 7)
+            want, wsc, _ = oracle.gqa_route(cat, oracle.F32, o, kv, hd, q, 7,
+                                            node_ids=np.asarray(order, np.uint64))
+            assert_same(res, want, wsc)
+        assert bank.info()["live"] == len(blocks)
+
+
+def test_ragged_config_parity(hip_lib):
+    cfg = wl.GQA_RAGGED
+    kv = cfg["layers"] * cfg["kv_heads"]
+    H = cfg["layers"] * cfg["heads"]
+    lens = wl.gqa_lengths(cfg["nodes"], cfg["seed"], lo=cfg["lo"], hi=cfg["hi"])
+    keys, offs = wl.gqa_bank(lens, kv, cfg["head_dim"], cfg["seed"])
+    qs = wl.gqa_queries(2, H, cfg["tokens"], cfg["head_dim"], cfg["seed"])
+    with GqaNodeBank(keys, offs, kv_heads=kv, head_dim=cfg["head_dim"],
+                     dtype="bf16") as bank:
+        res = bank.route(qs, cfg["topk"], query_dtype="bf16")
+    ids, sc, _ = oracle.gqa_route(keys, oracle.BF16, offs, kv, cfg["head_dim"],
+                                  bf16_bits_to_f32(qs).reshape(qs.shape),
+                                  cfg["topk"])
+    assert_same(res, ids, sc)

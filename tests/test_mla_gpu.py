@@ -1,0 +1,196 @@
+"""MLA route parity on the GPU: the HIP library against the fp64 oracle.
+
+Bar: node ids bit-exact (ties to the lowest node id) and scores bit-exact
+(the kernel evaluates the reference's fp64 law in the reference's order,
+cpp/grm_runtime.cpp:3518-3545).  Cases follow the reference's gates and
+tests: orthonormal / duplicate-row tie blocks and NaN rows
+(scripts/grm_mla_cuda_route_gate.py:73-86), NaN query -> unfilled slots
+(core/grm_cuda_router.py:460-475), row ids through the sidecar surface.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from graftrepository_amd import MlaNodeBank, workloads as wl
+from graftrepository_amd.grm_hip_router import CudaMLARouteSidecar
+from graftrepository_amd.mla_probe import HipProbe
+from graftrepository_amd.node_bank import bf16_bits_to_f32
+
+pytestmark = pytest.mark.gpu
+NO_ID = np.iinfo(np.uint64).max
+
+
+def assert_same(res_ids, res_scores, want_ids, want_scores):
+    np.testing.assert_array_equal(res_ids, want_ids)
+    filled = want_ids != NO_ID
+    assert np.all(np.isnan(res_scores[~filled]))
+    np.testing.assert_array_equal(res_scores[filled].view(np.uint32),
+                                  want_scores[filled].view(np.uint32))
+
+
+def test_small_config_parity(hip_lib):
+    rows = wl.mla_rows(10_000, 288, seed=11)
+    qs = wl.mla_queries(16, 288, seed=11)
+    with MlaNodeBank(rows) as bank:
+        for k in (1, 3, 16):
+            res = bank.route(qs, k)
+            ids, sc, _ = oracle.mla_route(rows, qs, k)
+            assert_same(res.ids, res.scores, ids, sc)
+
+
+@pytest.mark.parametrize("dim", [1, 3, 4, 5, 64, 127, 128, 256, 288, 300, 1000])
+def test_dims_and_ragged_tiles(hip_lib, dim):
+    rng = np.random.default_rng(dim)
+    n = 777
+    rows = rng.standard_normal((n, dim)).astype(np.float32)
+    qs = rng.standard_normal((3, dim)).astype(np.float32)
+    with MlaNodeBank(rows) as bank:
+        res = bank.route(qs, 7)
+    ids, sc, _ = oracle.mla_route(rows, qs, 7)
+    assert_same(res.ids, res.scores, ids, sc)
+
+
+def test_duplicate_rows_tie_to_lowest_node_id(hip_lib):
+    rng = np.random.default_rng(5)
+    base = rng.standard_normal((40, 64)).astype(np.float32)
+    rows = np.repeat(base, 25, axis=0)           # 1000 rows, 25-way tie blocks
+    node_ids = rng.permutation(1000).astype(np.uint64) + 1000
+    q = base[7] + np.float32(0.25) * base[3]
+    with MlaNodeBank(rows, node_ids) as bank:
+        res = bank.route(q, 16)
+    ids, sc, _ = oracle.mla_route(rows, q, 16, node_ids=node_ids)
+    assert_same(res.ids, res.scores, ids, sc)
+    top_block = node_ids[7 * 25:8 * 25]
+    assert list(res.ids[0]) == sorted(top_block.tolist())[:16]
+
+
+def test_orthonormal_closed_form(hip_lib):
+    dim = 128
+    rows = np.eye(dim, dtype=np.float32)
+    q = np.zeros(dim, dtype=np.float32)
+    q[[5, 9, 77]] = [3.0, 2.0, 1.0]
+    with MlaNodeBank(rows) as bank:
+        res = bank.route(q, 3)
+    assert res.ids[0].tolist() == [5, 9, 77]
+    qn = np.sqrt(14.0)
+    want = [np.float32(v / (qn * 1.0 + 1e-8)) for v in (3.0, 2.0, 1.0)]
+    np.testing.assert_array_equal(res.scores[0], np.asarray(want, np.float32))
+
+
+def test_nan_rows_dropped_and_nan_query_unfilled(hip_lib):
+    rng = np.random.default_rng(9)
+    rows = rng.standard_normal((300, 48)).astype(np.float32)
+    rows[[0, 17, 299], 3] = np.nan
+    rows[42, 0] = np.inf
+    qs = rng.standard_normal((2, 48)).astype(np.float32)
+    with MlaNodeBank(rows) as bank:
+        res = bank.route(qs, 10)
+        ids, sc, _ = oracle.mla_route(rows, qs, 10)
+        assert_same(res.ids, res.scores, ids, sc)
+        assert not set(res.ids.ravel().tolist()) & {0, 17, 42, 299}
+        bad = qs[:1].copy()
+        bad[0, 5] = np.nan
+        res = bank.route(bad, 4)
+        assert np.all(res.ids == NO_ID)
+    # reference hand case: tests/test_grm_router_baseline.py:26-33
+    routes = np.asarray([[np.nan, 0.0], [1.0, 0.0], [0.0, 1.0]], np.float32)
+    with MlaNodeBank(routes) as bank:
+        res = bank.route(np.asarray([1.0, 0.0], np.float32), 2)
+    assert res.ids[0].tolist() == [1, 2]
+
+
+def test_bf16_bank_parity(hip_lib):
+    rows = wl.mla_rows(5000, 288, seed=21, dtype="bf16")
+    qs = wl.mla_queries(8, 288, seed=21, dtype="bf16")
+    with MlaNodeBank(rows, dtype="bf16") as bank:
+        res = bank.route(qs, 8)
+    ids, sc, _ = oracle.mla_route(bf16_bits_to_f32(rows).reshape(rows.shape),
+                                  bf16_bits_to_f32(qs).reshape(qs.shape), 8)
+    assert_same(res.ids, res.scores, ids, sc)
+
+
+def test_append_evict_matches_oracle_on_live_set(hip_lib):
+    rng = np.random.default_rng(33)
+    dim = 96
+    rows = rng.standard_normal((1000, dim)).astype(np.float32)
+    ids0 = np.arange(1000, dtype=np.uint64) * 3
+    qs = rng.standard_normal((4, dim)).astype(np.float32)
+    with MlaNodeBank(rows, ids0, capacity=1500) as bank:
+        live = {int(i): rows[j] for j, i in enumerate(ids0)}
+        for step in range(4):
+            ev = rng.choice(sorted(live), size=60, replace=False).astype(np.uint64)
+            bank.evict(ev)
+            for i in ev.tolist():
+                del live[i]
+            new_ids = np.arange(60, dtype=np.uint64) + 10_000 + step * 100
+            new_rows = rng.standard_normal((60, dim)).astype(np.float32)
+            bank.append(new_rows, new_ids)
+            for i, r in zip(new_ids.tolist(), new_rows):
+                live[i] = r
+            res = bank.route(qs, 9)
+            keys = np.asarray(sorted(live), dtype=np.uint64)
+            mat = np.stack([live[int(k)] for k in keys])
+            want, wsc, _ = oracle.mla_route(mat, qs, 9, node_ids=keys)
+            assert_same(res.ids, res.scores, want, wsc)
+        info = bank.info()
+        assert info["live"] == len(live)
+        with pytest.raises(RuntimeError):
+            bank.evict([123456789])
+        with pytest.raises(RuntimeError):
+            bank.append(rows[:1], [int(keys[0])])
+
+
+def test_reference_surface_row_ids_and_device_entry(hip_lib):
+    rows = wl.mla_rows(2000, 128, seed=44)
+    qs = wl.mla_queries(6, 128, seed=44)
+    node_ids = np.arange(2000, dtype=np.uint64) + 500
+    sidecar = CudaMLARouteSidecar.build()
+    bank = sidecar.create_bank(rows, node_ids)
+    mapped, receipt = bank.route_topk(qs, topk=5, warmup=2)
+    want, _, _ = oracle.mla_route(rows, qs, 5)
+    np.testing.assert_array_equal(mapped, node_ids[want])
+    assert receipt.measured_queries == 4
+    probe = HipProbe()
+    dq = probe.upload_queries(qs)
+    mapped_d, _ = bank.route_topk_device(dq, topk=5)
+    np.testing.assert_array_equal(mapped_d, mapped)
+    dq.close()
+    one_shot, _, _ = probe.route_topk(rows, qs, warmup=0, topk=5)
+    np.testing.assert_array_equal(one_shot, want)
+    bank.close()
+    with pytest.raises(RuntimeError):
+        bank.route_topk(qs, topk=5)
+
+
+def test_invalid_arguments_rejected(hip_lib):
+    rows = wl.mla_rows(100, 16, seed=1)
+    with MlaNodeBank(rows) as bank:
+        for k in (0, 17, 101):
+            with pytest.raises(RuntimeError):
+                bank.route(rows[:1], k)
+        with pytest.raises(RuntimeError):
+            bank.route(rows[:2], 3, warmup=2)
+    arena = HipProbe().create_arena(rows)
+    with pytest.raises(ValueError):
+        arena.route_topk(rows[:1, :8], warmup=0, topk=1)
+
+
+def test_repeated_calls_are_stable(hip_lib):
+    rows = wl.mla_rows(200_000, 288, seed=55)
+    qs = wl.mla_queries(3, 288, seed=55)
+    ids, sc, _ = oracle.mla_route(rows, qs, 5)
+    with MlaNodeBank(rows) as bank:
+        for _ in range(40):
+            res = bank.route(qs, 5)
+            assert_same(res.ids, res.scores, ids, sc)
+
+
+def test_headline_size_parity(hip_lib):
+    cfg = wl.MLA_HEADLINE
+    rows = wl.mla_rows(cfg["nodes"], cfg["dim"], seed=cfg["seed"])
+    qs = wl.mla_queries(3, cfg["dim"], seed=cfg["seed"])
+    with MlaNodeBank(rows) as bank:
+        res = bank.route(qs, cfg["topk"])
+    ids, sc, _ = oracle.mla_route(rows, qs, cfg["topk"])
+    assert_same(res.ids, res.scores, ids, sc)
