@@ -200,15 +200,14 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_heads_kernel(
   }
 }
 
-// Finalize: exact score per slot, fused top-k into out[0..k).
+// Finalize: exact score per slot; each block writes its k best entries to
+// block_out for topk_merge_kernel (which also clears the query flag).
 __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
     unsigned long long* __restrict__ hmax, int H, uint32_t n_slots,
     const uint32_t* __restrict__ lens, const uint32_t* __restrict__ flags,
-    const uint64_t* __restrict__ ids, unsigned* __restrict__ qbad, int k,
-    Cand* __restrict__ block_out, unsigned* __restrict__ ticket,
-    Cand* __restrict__ out) {
+    const uint64_t* __restrict__ ids, const unsigned* __restrict__ qbad, int k,
+    Cand* __restrict__ block_out) {
   __shared__ Cand s_lists[kFinWaves][kMaxTopK];
-  __shared__ int s_last;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
@@ -248,34 +247,7 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
     if (need) id = ids[slot];
     wl_consume(L, k, s, id, slot, need);
   }
-  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(L);
-  __syncthreads();
-  if (wave == 0) {
-    WaveList B;
-    block_merge<kFinWaves>(s_lists, k, B);
-    if (lane < k) block_out[static_cast<size_t>(blockIdx.x) * k + lane] = wl_entry(B);
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(ticket, 1u) == gridDim.x - 1) ? 1 : 0;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  WaveList G;
-  wl_init(G);
-  wl_consume_global(G, k, block_out, gridDim.x * static_cast<uint32_t>(k),
-                    static_cast<uint32_t>(wave), kFinWaves);
-  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(G);
-  __syncthreads();
-  if (wave == 0) {
-    WaveList B;
-    block_merge<kFinWaves>(s_lists, k, B);
-    if (lane < k) out[lane] = wl_entry(B);
-    if (lane == 0) {
-      atomicExch(ticket, 0u);
-      atomicExch(qbad, 0u);
-    }
-  }
+  block_topk_write<kFinWaves>(L, k, s_lists, block_out);
 }
 
 // Per-slot key statistics for appended/created slots: bit 1 of flags is set
@@ -408,7 +380,7 @@ struct GqaDeviceArena {
   size_t d_out_count = 0;
   Cand* h_out = nullptr;
   size_t h_out_count = 0;
-  unsigned* d_ticket = nullptr;  // [0] ticket, [1] query-non-finite flag
+  unsigned* d_qbad = nullptr;  // set when a query value is non-finite
   void* d_queries = nullptr;
   size_t d_queries_bytes = 0;
   void* h_stage = nullptr;
@@ -472,7 +444,7 @@ void destroy_arena(GqaDeviceArena* a) {
   if (a->side) (void)hipStreamSynchronize(a->side);
   void* dev[] = {a->d_keys, a->d_scales, a->d_tok_off, a->d_len, a->d_ids, a->d_flags,
                  a->d_nonfinite, a->d_items, a->d_hmax, a->d_block, a->d_out,
-                 a->d_ticket, a->d_queries, a->d_stage};
+                 a->d_qbad, a->d_queries, a->d_stage};
   for (void* p : dev) {
     if (p) (void)hipFree(p);
   }
@@ -691,13 +663,13 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_ids), cap_nodes * sizeof(uint64_t)));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_flags), cap_nodes * sizeof(uint32_t)));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_nonfinite), cap_nodes * sizeof(uint32_t)));
-  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_ticket), 2 * sizeof(unsigned)));
+  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_qbad), sizeof(unsigned)));
   BAIL_HIP(hipMemsetAsync(a->d_tok_off, 0, cap_nodes * sizeof(uint64_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_len, 0, cap_nodes * sizeof(uint32_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_ids, 0xff, cap_nodes * sizeof(uint64_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_flags, 0, cap_nodes * sizeof(uint32_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_nonfinite, 0, cap_nodes * sizeof(uint32_t), a->stream));
-  BAIL_HIP(hipMemsetAsync(a->d_ticket, 0, 2 * sizeof(unsigned), a->stream));
+  BAIL_HIP(hipMemsetAsync(a->d_qbad, 0, sizeof(unsigned), a->stream));
   BAIL_HIP(hipStreamSynchronize(a->stream));
 #undef BAIL_HIP
   if (const char* env = getenv("GRM_HIP_GQA_FIN_BLOCKS")) {
@@ -761,7 +733,7 @@ int launch_exact(GqaDeviceArena* a, const void* q, int q_dtype, int H, int Qt, i
   grm::gqa::gqa_exact_heads_kernel<KDT, RQ><<<blocks, threads, lds, a->stream>>>(          \
       a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_tok_off, a->d_len,       \
       a->d_items, static_cast<uint32_t>(a->n_items), static_cast<int>(a->kv),              \
-      static_cast<int>(a->hd), R, Qt, q, q_dtype, denom, a->d_hmax, H, a->d_ticket + 1)
+      static_cast<int>(a->hd), R, Qt, q, q_dtype, denom, a->d_hmax, H, a->d_qbad)
 #define GRM_EXACT_RQ(KDT)                       \
   switch (rq_pad) {                             \
     case 1: GRM_EXACT(KDT, 1); break;           \
@@ -830,8 +802,11 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
     const void* q = qbase + qi * qstride;
     GRM_CHECK_RC(launch_exact(a, q, q_dtype, H, Qt, rq_pad));
     grm::gqa::gqa_finalize_kernel<<<fin_blocks, per_block, 0, a->stream>>>(
-        a->d_hmax, H, n_slots, a->d_len, a->d_flags, a->d_ids, a->d_ticket + 1, topk, a->d_block,
-        a->d_ticket, a->d_out + static_cast<size_t>(qi) * topk);
+        a->d_hmax, H, n_slots, a->d_len, a->d_flags, a->d_ids, a->d_qbad, topk, a->d_block);
+    GRM_HIP_CHECK(hipGetLastError());
+    grm::topk_merge_kernel<<<1, grm::kMergeWaves * grm::kWave, 0, a->stream>>>(
+        a->d_block, fin_blocks * static_cast<uint32_t>(topk), 0, topk,
+        a->d_out + static_cast<size_t>(qi) * topk, a->d_qbad);
     GRM_HIP_CHECK(hipGetLastError());
   }
   GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));

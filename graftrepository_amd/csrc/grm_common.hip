@@ -25,6 +25,28 @@ int fail_hip(hipError_t rc, const char* what) {
   return hip_code(rc);
 }
 
+// Merge `count` candidates per query (query q reads in + q*in_stride) into
+// out + q*k; one block per query.  Clears flags[q] when flags is given.
+__global__ __launch_bounds__(kMergeWaves * kWave) void topk_merge_kernel(
+    const Cand* __restrict__ in, uint32_t count, size_t in_stride, int k,
+    Cand* __restrict__ out, unsigned* __restrict__ flags) {
+  __shared__ Cand s_lists[kMergeWaves][kMaxTopK];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const Cand* src = in + blockIdx.x * in_stride;
+  WaveList G;
+  wl_init(G);
+  wl_consume_global(G, k, src, count, static_cast<uint32_t>(wave), kMergeWaves);
+  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(G);
+  __syncthreads();
+  if (wave == 0) {
+    WaveList B;
+    block_merge<kMergeWaves>(s_lists, k, B);
+    if (lane < k) out[static_cast<size_t>(blockIdx.x) * k + lane] = wl_entry(B);
+    if (lane == 0 && flags) flags[blockIdx.x] = 0u;
+  }
+}
+
 }  // namespace grm
 
 extern "C" const char* grm_hip_last_error(void) {

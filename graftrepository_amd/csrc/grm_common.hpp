@@ -175,17 +175,60 @@ __device__ inline void wl_consume_global(WaveList& L, int k,
                                          const Cand* __restrict__ src,
                                          uint32_t count, uint32_t w,
                                          uint32_t stride_waves) {
+  // Up to kPrefetch candidates per lane are loaded before any is consumed so
+  // the loads overlap instead of paying one memory latency per 64 entries.
+  constexpr int kPrefetch = 8;
   const int lane = __lane_id();
-  for (uint32_t base = w * kWave; base < count; base += stride_waves * kWave) {
-    const uint32_t i = base + lane;
-    const bool v = i < count;
-    Cand c;
-    c.score = -INFINITY;
-    c.slot = kNoSlot;
-    c.id = kNoId;
-    if (v) c = src[i];
-    wl_consume(L, k, c.score, c.id, c.slot, v && isfinite(c.score));
+  const uint32_t step = stride_waves * kWave;
+  for (uint32_t base = w * kWave; base < count; base += step * kPrefetch) {
+    Cand c[kPrefetch];
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) {
+      const uint32_t i = base + p * step + lane;
+      c[p].score = -INFINITY;
+      c[p].slot = kNoSlot;
+      c[p].id = kNoId;
+      if (i < count) c[p] = src[i];
+    }
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) {
+      if (base + p * step < count) {
+        wl_consume(L, k, c[p].score, c[p].id, c[p].slot, isfinite(c[p].score));
+      }
+    }
   }
 }
+
+
+// Block epilogue shared by the route kernels: merge the block's wave lists
+// in LDS and write the block's k best entries to block_out[blockIdx.x*k ..).
+// Must be reached by every thread of the block.  The entries of all blocks
+// are merged by topk_merge_kernel, launched next on the same stream; the
+// kernel boundary orders the writes, so no device-scope fence (an L2
+// write-back on gfx950) is paid per block.
+template <int NW>
+__device__ inline void block_topk_write(WaveList& L, int k,
+                                        Cand (*s_lists)[kMaxTopK],
+                                        Cand* __restrict__ block_out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(L);
+  __syncthreads();
+  if (wave == 0) {
+    WaveList B;
+    block_merge<NW>(s_lists, k, B);
+    if (lane < k) block_out[static_cast<size_t>(blockIdx.x) * k + lane] = wl_entry(B);
+  }
+}
+
+constexpr int kMergeWaves = 4;
+
+// Merge `count` candidates per query (query q reads in + q*in_stride) into
+// out + q*k; one block of kMergeWaves waves per query.  Clears flags[q] when
+// flags is given.  Defined in grm_common.hip.
+__global__ void topk_merge_kernel(const Cand* __restrict__ in, uint32_t count,
+                                  size_t in_stride, int k,
+                                  Cand* __restrict__ out,
+                                  unsigned* __restrict__ flags);
 
 }  // namespace grm

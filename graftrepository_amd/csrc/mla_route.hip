@@ -10,11 +10,13 @@
 // needs no re-check.  fp64 costs nothing here: the kernel streams 4 bytes
 // (fp32 bank) or 2 bytes (bf16 bank) per multiply-add and is bound by HBM.
 //
-// Bank layout in HBM ("lane-interleaved tiles"): slots are grouped in tiles
-// of 64; a tile stores its rows chunk-major, each 16-byte chunk (4 fp32 or
-// 8 bf16 values of one row) at [tile][chunk][lane].  Lane l of a wavefront
-// owns slot tile*64+l, walks its row in d order (the law's order) and every
-// load instruction of the wave reads 1 KiB of contiguous memory.
+// Bank layout in HBM ("chunk planes"): a row is cut into 16-byte chunks (4
+// fp32 or 8 bf16 values); slots are grouped in tiles of 64 and chunk c of
+// slot tile*64+l lives at [c][tile][l].  Lane l of a wavefront owns one slot
+// and walks its row in d order (the law's order); every load instruction of
+// a wave reads 1 KiB of contiguous memory, and waves working on neighbouring
+// tiles read neighbouring KiB of the same plane, which keeps DRAM rows open
+// the way a plain sequential stream does.
 //
 // Top-k is fused: each wave keeps a distributed top-k list (grm_common.hpp),
 // blocks merge their waves' lists in LDS, and the last block to finish
@@ -66,7 +68,7 @@ __device__ inline double chunk_dot(u32x4 v, const double* __restrict__ q,
 // Dot product of this lane's row with the query, d ascending.
 template <int DT>
 __device__ inline double tile_dot(const u32x4* __restrict__ p, uint32_t chunks,
-                                  const double* __restrict__ qd) {
+                                  size_t plane, const double* __restrict__ qd) {
   constexpr int EPC = DT == kF32 ? 4 : 8;
   constexpr uint32_t kBatch = 8;
   double acc = 0.0;
@@ -75,7 +77,7 @@ __device__ inline double tile_dot(const u32x4* __restrict__ p, uint32_t chunks,
     u32x4 v[kBatch];
 #pragma unroll
     for (uint32_t j = 0; j < kBatch; ++j) {
-      v[j] = __builtin_nontemporal_load(p + static_cast<size_t>(c + j) * kWave);
+      v[j] = __builtin_nontemporal_load(p + static_cast<size_t>(c + j) * plane);
     }
 #pragma unroll
     for (uint32_t j = 0; j < kBatch; ++j) {
@@ -83,26 +85,24 @@ __device__ inline double tile_dot(const u32x4* __restrict__ p, uint32_t chunks,
     }
   }
   for (; c < chunks; ++c) {
-    acc = chunk_dot<DT>(__builtin_nontemporal_load(p + static_cast<size_t>(c) * kWave),
+    acc = chunk_dot<DT>(__builtin_nontemporal_load(p + static_cast<size_t>(c) * plane),
                         qd + c * EPC, acc);
   }
   return acc;
 }
 
-// One query against every slot; writes the query's top-k to `out[0..k)`.
-// Requires gridDim.x * k entries of `block_out` and a zeroed `ticket`; the
-// last block re-zeroes the ticket.
+// One query against every slot; each block writes its k best entries to
+// block_out[blockIdx.x*k ..) for topk_merge_kernel.
 template <int DT, int NW>
 __global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
     const u32x4* __restrict__ tiles, const float* __restrict__ norms,
     const uint64_t* __restrict__ ids, uint32_t num_tiles, uint32_t chunks,
-    uint32_t dim, uint32_t dim_pad, const void* __restrict__ query,
-    int query_dtype, int k, Cand* __restrict__ block_out,
-    unsigned* __restrict__ ticket, Cand* __restrict__ out) {
+    size_t plane, uint32_t dim, uint32_t dim_pad,
+    const void* __restrict__ query, int query_dtype, int k,
+    Cand* __restrict__ block_out) {
   extern __shared__ double qd[];
   __shared__ double s_qnorm;
   __shared__ Cand s_lists[NW][kMaxTopK];
-  __shared__ int s_last;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
   wl_init(L);
   for (uint32_t t = blockIdx.x * NW + wave; t < num_tiles; t += gridDim.x * NW) {
     const double dot = tile_dot<DT>(
-        tiles + static_cast<size_t>(t) * chunks * kWave + lane, chunks, qd);
+        tiles + static_cast<size_t>(t) * kWave + lane, chunks, plane, qd);
     const uint32_t slot = t * kWave + lane;
     const float nrm = norms[slot];  // NaN marks an empty or evicted slot
     const double den = qnorm * static_cast<double>(nrm) + 1.0e-8;
@@ -140,32 +140,130 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
     wl_consume(L, k, s, id, slot, need);
   }
 
-  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(L);
-  __syncthreads();
-  if (wave == 0) {
-    WaveList B;
-    block_merge<NW>(s_lists, k, B);
-    if (lane < k) block_out[static_cast<size_t>(blockIdx.x) * k + lane] = wl_entry(B);
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(ticket, 1u) == gridDim.x - 1) ? 1 : 0;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  block_topk_write<NW>(L, k, s_lists, block_out);
+}
 
-  WaveList G;
-  wl_init(G);
-  wl_consume_global(G, k, block_out, gridDim.x * static_cast<uint32_t>(k),
-                    static_cast<uint32_t>(wave), NW);
-  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(G);
-  __syncthreads();
-  if (wave == 0) {
-    WaveList B;
-    block_merge<NW>(s_lists, k, B);
-    if (lane < k) out[lane] = wl_entry(B);
-    if (lane == 0) atomicExch(ticket, 0u);
+// Stage the query as doubles in LDS (zero beyond dim).
+__device__ inline void stage_query(double* qd, const void* __restrict__ query,
+                                   int query_dtype, uint32_t dim,
+                                   uint32_t dim_pad) {
+  for (uint32_t d = threadIdx.x; d < dim_pad; d += blockDim.x) {
+    double v = 0.0;
+    if (d < dim) {
+      v = query_dtype == kBF16
+              ? static_cast<double>(bf16_to_f32(static_cast<const uint16_t*>(query)[d]))
+              : static_cast<double>(static_cast<const float*>(query)[d]);
+    }
+    qd[d] = v;
   }
+}
+
+template <int DT, int B>
+__device__ inline double batch_dot(const u32x4 (&v)[B],
+                                   const double* __restrict__ q, double acc) {
+  constexpr int EPC = DT == kF32 ? 4 : 8;
+#pragma unroll
+  for (int j = 0; j < B; ++j) acc = chunk_dot<DT>(v[j], q + j * EPC, acc);
+  return acc;
+}
+
+// Software-pipelined variant for rows of a whole number of B-chunk batches:
+// while a batch is folded into the fp64 dot product the next batch (of the
+// same tile or the wave's next tile) is already in flight, and the row norm
+// of the next tile is fetched ahead of its data.  Arithmetic and order are
+// those of mla_route_kernel.
+template <int DT, int NW, int B>
+__global__ __launch_bounds__(NW * kWave) void mla_route_pipe_kernel(
+    const u32x4* __restrict__ tiles, const float* __restrict__ norms,
+    const uint64_t* __restrict__ ids, uint32_t num_tiles, uint32_t chunks,
+    size_t plane, uint32_t dim, uint32_t dim_pad,
+    const void* __restrict__ query, int query_dtype, int k,
+    Cand* __restrict__ block_out) {
+  constexpr int EPC = DT == kF32 ? 4 : 8;
+  extern __shared__ double qd[];
+  __shared__ double s_qnorm;
+  __shared__ Cand s_lists[NW][kMaxTopK];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const uint32_t stride = gridDim.x * NW;
+  const uint32_t nb = chunks / B;
+  // Beyond-the-end prefetches read tile 0's first batch (cache resident).
+  auto batch_ptr = [&](uint32_t t, uint32_t b) {
+    return t < num_tiles
+               ? tiles + static_cast<size_t>(b) * B * plane + static_cast<size_t>(t) * kWave + lane
+               : tiles + lane;
+  };
+  auto load = [&](u32x4 (&v)[B], const u32x4* p) {
+#pragma unroll
+    for (int j = 0; j < B; ++j) v[j] = __builtin_nontemporal_load(p + j * plane);
+  };
+
+  uint32_t t = blockIdx.x * NW + wave;
+  uint32_t b = 0;
+  u32x4 bufA[B], bufB[B];
+  float nrm_cur = norms[(t < num_tiles ? t : 0) * kWave + lane];
+  load(bufA, batch_ptr(t, 0));
+
+  stage_query(qd, query, query_dtype, dim, dim_pad);
+  __syncthreads();
+  if (tid == 0) {
+    double acc = 0.0;  // cpp/grm_runtime.cpp:4310-4314, sequential
+    for (uint32_t d = 0; d < dim; ++d) acc = fma(qd[d], qd[d], acc);
+    s_qnorm = sqrt(acc);
+  }
+  __syncthreads();
+  const double qnorm = s_qnorm;
+
+  WaveList L;
+  wl_init(L);
+  auto finish = [&](uint32_t tt, double dot, float nrm) {
+    const uint32_t slot = tt * kWave + lane;
+    const double den = qnorm * static_cast<double>(nrm) + 1.0e-8;
+    const float s = static_cast<float>(dot / den);
+    const bool need = isfinite(s) && s >= L.th_s;
+    uint64_t id = kNoId;
+    if (need) id = ids[slot];
+    wl_consume(L, k, s, id, slot, need);
+  };
+  double acc = 0.0;
+  float nrm_next = 0.0f;
+  while (t < num_tiles) {
+    uint32_t tn = t, bn = b + 1;
+    if (bn == nb) {
+      tn = t + stride;
+      bn = 0;
+      nrm_next = norms[(tn < num_tiles ? tn : 0) * kWave + lane];
+    }
+    load(bufB, batch_ptr(tn, bn));
+    acc = batch_dot<DT, B>(bufA, qd + b * B * EPC, acc);
+    if (bn == 0) {
+      finish(t, acc, nrm_cur);
+      acc = 0.0;
+      nrm_cur = nrm_next;
+    }
+    t = tn;
+    b = bn;
+    if (t >= num_tiles) break;
+
+    tn = t;
+    bn = b + 1;
+    if (bn == nb) {
+      tn = t + stride;
+      bn = 0;
+      nrm_next = norms[(tn < num_tiles ? tn : 0) * kWave + lane];
+    }
+    load(bufA, batch_ptr(tn, bn));
+    acc = batch_dot<DT, B>(bufB, qd + b * B * EPC, acc);
+    if (bn == 0) {
+      finish(t, acc, nrm_cur);
+      acc = 0.0;
+      nrm_cur = nrm_next;
+    }
+    t = tn;
+    b = bn;
+  }
+  block_topk_write<NW>(L, k, s_lists, block_out);
 }
 
 // Place staged row-major rows into their tile slots and compute row norms
@@ -174,7 +272,7 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
 template <int DT>
 __global__ void mla_place_rows_kernel(const void* __restrict__ rows,
                                       uint64_t count, uint32_t dim,
-                                      uint32_t chunks,
+                                      uint32_t chunks, size_t plane,
                                       const uint64_t* __restrict__ slots,
                                       const uint64_t* __restrict__ ids,
                                       uint64_t slot0, u32x4* __restrict__ tiles,
@@ -186,7 +284,7 @@ __global__ void mla_place_rows_kernel(const void* __restrict__ rows,
     const uint64_t slot = slots ? slots[r] : slot0 + r;
     const uint64_t tile = slot / kWave;
     const uint32_t lane = static_cast<uint32_t>(slot % kWave);
-    u32x4* dst = tiles + tile * chunks * kWave + lane;
+    u32x4* dst = tiles + tile * kWave + lane;
     double acc = 0.0;
     for (uint32_t c = 0; c < chunks; ++c) {
       uint32_t w[4] = {0u, 0u, 0u, 0u};
@@ -215,7 +313,7 @@ __global__ void mla_place_rows_kernel(const void* __restrict__ rows,
       v.y = w[1];
       v.z = w[2];
       v.w = w[3];
-      dst[static_cast<size_t>(c) * kWave] = v;
+      dst[static_cast<size_t>(c) * plane] = v;
     }
     norms[slot] = static_cast<float>(sqrt(acc));
     slot_ids[slot] = ids ? ids[r] : slot;
@@ -269,7 +367,6 @@ struct MlaDeviceArena {
   size_t d_out_count = 0;
   Cand* h_out = nullptr;
   size_t h_out_count = 0;
-  unsigned* d_ticket = nullptr;
   void* h_stage = nullptr;
   size_t h_stage_bytes = 0;
   void* d_stage = nullptr;
@@ -280,7 +377,8 @@ struct MlaDeviceArena {
   hipEvent_t ev_stop = nullptr;
   hipEvent_t ev_mut = nullptr;
   bool mut_pending = false;
-  uint32_t max_blocks = 1024;
+  bool pipeline = true;     // software-pipelined kernel when rows allow it
+  uint32_t max_blocks = 0;  // route grid cap; 0 -> 4 blocks per CU
 };
 
 namespace {
@@ -298,7 +396,6 @@ void destroy_arena(MlaDeviceArena* a) {
   if (a->d_queries) (void)hipFree(a->d_queries);
   if (a->d_block) (void)hipFree(a->d_block);
   if (a->d_out) (void)hipFree(a->d_out);
-  if (a->d_ticket) (void)hipFree(a->d_ticket);
   if (a->d_stage) (void)hipFree(a->d_stage);
   if (a->h_out) (void)hipHostFree(a->h_out);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
@@ -355,12 +452,12 @@ int launch_place(MlaDeviceArena* a, const void* d_rows, uint64_t count,
       std::min<uint64_t>((count + threads - 1) / threads, 4096));
   if (a->dtype == kF32) {
     grm::mla::mla_place_rows_kernel<kF32><<<blocks, threads, 0, stream>>>(
-        d_rows, count, a->dim, a->chunks, d_slots, d_ids, slot0, a->d_tiles,
-        a->d_norms, a->d_ids);
+        d_rows, count, a->dim, a->chunks, a->capacity, d_slots, d_ids, slot0,
+        a->d_tiles, a->d_norms, a->d_ids);
   } else {
     grm::mla::mla_place_rows_kernel<kBF16><<<blocks, threads, 0, stream>>>(
-        d_rows, count, a->dim, a->chunks, d_slots, d_ids, slot0, a->d_tiles,
-        a->d_norms, a->d_ids);
+        d_rows, count, a->dim, a->chunks, a->capacity, d_slots, d_ids, slot0,
+        a->d_tiles, a->d_norms, a->d_ids);
   }
   GRM_HIP_CHECK(hipGetLastError());
   return 0;
@@ -394,10 +491,19 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
   a->dim_pad = (a->dim + a->epc - 1) / a->epc * a->epc;
   a->chunks = a->dim_pad / a->epc;
   a->capacity = (capacity + grm::kWave - 1) / grm::kWave * grm::kWave;
+  {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, a->device) != hipSuccess ||
+        cus <= 0) {
+      cus = 256;
+    }
+    a->max_blocks = static_cast<uint32_t>(cus) * 4;
+  }
   if (const char* env = getenv("GRM_HIP_MLA_BLOCKS")) {
     const long v = strtol(env, nullptr, 10);
     if (v >= 1 && v <= 65536) a->max_blocks = static_cast<uint32_t>(v);
   }
+  if (const char* env = getenv("GRM_HIP_MLA_PIPELINE")) a->pipeline = env[0] != '0';
   a->slot_id.assign(a->capacity, kNoId);
   if (node_ids) {
     a->slot_of.reserve(nodes * 2);
@@ -429,11 +535,9 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_tiles), tiles * tile_bytes));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_norms), a->capacity * sizeof(float)));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_ids), a->capacity * sizeof(uint64_t)));
-  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_ticket), sizeof(unsigned)));
   BAIL_HIP(hipMemsetAsync(a->d_tiles, 0, tiles * tile_bytes, a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_norms, 0xff, a->capacity * sizeof(float), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_ids, 0xff, a->capacity * sizeof(uint64_t), a->stream));
-  BAIL_HIP(hipMemsetAsync(a->d_ticket, 0, sizeof(unsigned), a->stream));
   if (nodes > 0) {
     const size_t row_bytes = static_cast<size_t>(a->dim) * elem_size(dtype);
     const uint64_t batch = std::min<uint64_t>(nodes, grm::mla::kStageRows);
@@ -506,17 +610,37 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
     if (qi == warmup) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
     const void* q = qbase + qi * qstride;
     Cand* out = a->d_out + static_cast<size_t>(qi) * topk;
+    constexpr int NW = grm::mla::kRouteWaves;
+    const dim3 grid(blocks), block(NW * grm::kWave);
+#define GRM_MLA_ARGS                                                               \
+  a->d_tiles, a->d_norms, a->d_ids, num_tiles, a->chunks, a->capacity, a->dim, a->dim_pad, q, \
+      q_dtype, topk, a->d_block
+    const bool pipe = a->pipeline && num_tiles >= 1;
     if (a->dtype == kF32) {
-      grm::mla::mla_route_kernel<kF32, grm::mla::kRouteWaves>
-          <<<blocks, grm::mla::kRouteWaves * grm::kWave, lds, a->stream>>>(
-              a->d_tiles, a->d_norms, a->d_ids, num_tiles, a->chunks, a->dim,
-              a->dim_pad, q, q_dtype, topk, a->d_block, a->d_ticket, out);
+      if (pipe && a->chunks % 9 == 0) {
+        grm::mla::mla_route_pipe_kernel<kF32, NW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      } else if (pipe && a->chunks % 8 == 0) {
+        grm::mla::mla_route_pipe_kernel<kF32, NW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      } else if (pipe && a->chunks % 6 == 0) {
+        grm::mla::mla_route_pipe_kernel<kF32, NW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      } else {
+        grm::mla::mla_route_kernel<kF32, NW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      }
     } else {
-      grm::mla::mla_route_kernel<kBF16, grm::mla::kRouteWaves>
-          <<<blocks, grm::mla::kRouteWaves * grm::kWave, lds, a->stream>>>(
-              a->d_tiles, a->d_norms, a->d_ids, num_tiles, a->chunks, a->dim,
-              a->dim_pad, q, q_dtype, topk, a->d_block, a->d_ticket, out);
+      if (pipe && a->chunks % 9 == 0) {
+        grm::mla::mla_route_pipe_kernel<kBF16, NW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      } else if (pipe && a->chunks % 8 == 0) {
+        grm::mla::mla_route_pipe_kernel<kBF16, NW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      } else if (pipe && a->chunks % 6 == 0) {
+        grm::mla::mla_route_pipe_kernel<kBF16, NW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      } else {
+        grm::mla::mla_route_kernel<kBF16, NW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      }
     }
+#undef GRM_MLA_ARGS
+    GRM_HIP_CHECK(hipGetLastError());
+    grm::topk_merge_kernel<<<1, grm::kMergeWaves * grm::kWave, 0, a->stream>>>(
+        a->d_block, blocks * static_cast<uint32_t>(topk), 0, topk, out, nullptr);
     GRM_HIP_CHECK(hipGetLastError());
   }
   GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
