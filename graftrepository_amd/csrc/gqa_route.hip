@@ -327,6 +327,8 @@ __global__ void gqa_evict_kernel(const uint64_t* __restrict__ slots,
   }
 }
 
+__global__ void gqa_clear_flag_kernel(unsigned* __restrict__ flag) { *flag = 0u; }
+
 }  // namespace gqa
 }  // namespace grm
 
@@ -374,12 +376,8 @@ struct GqaDeviceArena {
   unsigned long long* d_hmax = nullptr;
   size_t d_hmax_count = 0;
   int hmax_heads = 0;
-  Cand* d_block = nullptr;
-  size_t d_block_count = 0;
-  Cand* d_out = nullptr;
-  size_t d_out_count = 0;
-  Cand* h_out = nullptr;
-  size_t h_out_count = 0;
+  grm::MappedCands blocks_out;  // per-query, per-block top-k (host mapped)
+  std::vector<Cand> merged;
   unsigned* d_qbad = nullptr;  // set when a query value is non-finite
   void* d_queries = nullptr;
   size_t d_queries_bytes = 0;
@@ -443,12 +441,11 @@ void destroy_arena(GqaDeviceArena* a) {
   if (a->stream) (void)hipStreamSynchronize(a->stream);
   if (a->side) (void)hipStreamSynchronize(a->side);
   void* dev[] = {a->d_keys, a->d_scales, a->d_tok_off, a->d_len, a->d_ids, a->d_flags,
-                 a->d_nonfinite, a->d_items, a->d_hmax, a->d_block, a->d_out,
-                 a->d_qbad, a->d_queries, a->d_stage};
+                 a->d_nonfinite, a->d_items, a->d_hmax, a->d_qbad, a->d_queries, a->d_stage};
   for (void* p : dev) {
     if (p) (void)hipFree(p);
   }
-  if (a->h_out) (void)hipHostFree(a->h_out);
+  grm::release_mapped(&a->blocks_out);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
@@ -785,9 +782,8 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   const uint32_t n_slots = static_cast<uint32_t>(a->high_water);
   const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
   const uint32_t fin_blocks = std::max<uint32_t>(1, std::min<uint32_t>((n_slots + per_block - 1) / per_block, a->fin_blocks));
-  GRM_CHECK_RC(reserve_device(&a->d_block, &a->d_block_count, static_cast<size_t>(fin_blocks) * grm::kMaxTopK));
-  GRM_CHECK_RC(reserve_device(&a->d_out, &a->d_out_count, static_cast<size_t>(q_count) * topk));
-  GRM_CHECK_RC(reserve_pinned(&a->h_out, &a->h_out_count, static_cast<size_t>(q_count) * topk));
+  const size_t per_q = static_cast<size_t>(fin_blocks) * topk;
+  GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * q_count));
   const size_t qvals = static_cast<size_t>(H) * Qt * a->hd;
   const size_t qstride = qvals * (q_dtype == kF32 ? 4 : 2);
   const unsigned char* qbase = static_cast<const unsigned char*>(queries);
@@ -802,23 +798,25 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
     const void* q = qbase + qi * qstride;
     GRM_CHECK_RC(launch_exact(a, q, q_dtype, H, Qt, rq_pad));
     grm::gqa::gqa_finalize_kernel<<<fin_blocks, per_block, 0, a->stream>>>(
-        a->d_hmax, H, n_slots, a->d_len, a->d_flags, a->d_ids, a->d_qbad, topk, a->d_block);
+        a->d_hmax, H, n_slots, a->d_len, a->d_flags, a->d_ids, a->d_qbad, topk,
+        a->blocks_out.dev + static_cast<size_t>(qi) * per_q);
     GRM_HIP_CHECK(hipGetLastError());
-    grm::topk_merge_kernel<<<1, grm::kMergeWaves * grm::kWave, 0, a->stream>>>(
-        a->d_block, fin_blocks * static_cast<uint32_t>(topk), 0, topk,
-        a->d_out + static_cast<size_t>(qi) * topk, a->d_qbad);
+    grm::gqa::gqa_clear_flag_kernel<<<1, 1, 0, a->stream>>>(a->d_qbad);
     GRM_HIP_CHECK(hipGetLastError());
   }
   GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
-  GRM_HIP_CHECK(hipMemcpyAsync(a->h_out, a->d_out, static_cast<size_t>(q_count) * topk * sizeof(Cand),
-                               hipMemcpyDeviceToHost, a->stream));
   GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
   if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
-  for (size_t i = 0; i < static_cast<size_t>(q_count) * topk; ++i) {
-    const Cand& c = a->h_out[i];
-    const bool ok = isfinite(c.score) && c.id != kNoId;
-    out_ids[i] = ok ? c.id : kNoId;
-    if (out_scores) out_scores[i] = ok ? c.score : __builtin_nanf("");
+  a->merged.resize(topk);
+  for (int qi = 0; qi < q_count; ++qi) {
+    grm::host_topk_merge(a->blocks_out.host + static_cast<size_t>(qi) * per_q, per_q, topk,
+                         a->merged.data());
+    for (int j = 0; j < topk; ++j) {
+      const Cand& c = a->merged[j];
+      const bool ok = isfinite(c.score) && c.id != kNoId;
+      out_ids[static_cast<size_t>(qi) * topk + j] = ok ? c.id : kNoId;
+      if (out_scores) out_scores[static_cast<size_t>(qi) * topk + j] = ok ? c.score : __builtin_nanf("");
+    }
   }
   grm::clear_error();
   return 0;

@@ -25,6 +25,52 @@ int fail_hip(hipError_t rc, const char* what) {
   return hip_code(rc);
 }
 
+void host_topk_merge(const Cand* in, size_t count, int k, Cand* out) {
+  int n = 0;
+  for (size_t i = 0; i < count; ++i) {
+    const Cand& c = in[i];
+    if (!isfinite(c.score) || c.id == kNoId) continue;
+    if (n == k && !better(c.score, c.id, out[k - 1].score, out[k - 1].id)) continue;
+    int pos = n < k ? n : k - 1;
+    while (pos > 0 && better(c.score, c.id, out[pos - 1].score, out[pos - 1].id)) {
+      out[pos] = out[pos - 1];
+      --pos;
+    }
+    out[pos] = c;
+    if (n < k) ++n;
+  }
+  for (int j = n; j < k; ++j) {
+    out[j].score = __builtin_nanf("");
+    out[j].slot = kNoSlot;
+    out[j].id = kNoId;
+  }
+}
+
+int reserve_mapped(MappedCands* m, size_t count) {
+  if (count <= m->count && m->host) return 0;
+  release_mapped(m);
+  void* h = nullptr;
+  GRM_HIP_CHECK(hipHostMalloc(&h, count * sizeof(Cand),
+                              hipHostMallocMapped | hipHostMallocCoherent));
+  void* d = nullptr;
+  hipError_t rc = hipHostGetDevicePointer(&d, h, 0);
+  if (rc != hipSuccess) {
+    (void)hipHostFree(h);
+    return fail_hip(rc, "hipHostGetDevicePointer");
+  }
+  m->host = static_cast<Cand*>(h);
+  m->dev = static_cast<Cand*>(d);
+  m->count = count;
+  return 0;
+}
+
+void release_mapped(MappedCands* m) {
+  if (m->host) (void)hipHostFree(m->host);
+  m->host = nullptr;
+  m->dev = nullptr;
+  m->count = 0;
+}
+
 // Merge `count` candidates per query (query q reads in + q*in_stride) into
 // out + q*k; one block per query.  Clears flags[q] when flags is given.
 __global__ __launch_bounds__(kMergeWaves * kWave) void topk_merge_kernel(

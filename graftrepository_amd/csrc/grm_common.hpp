@@ -223,6 +223,21 @@ __device__ inline void block_topk_write(WaveList& L, int k,
 
 constexpr int kMergeWaves = 4;
 
+// Host side: keep the best k of `count` candidates (tie law above) in out,
+// best first; unfilled entries get score NaN, id kNoId, slot kNoSlot.
+void host_topk_merge(const Cand* in, size_t count, int k, Cand* out);
+
+// Pinned host buffer the device writes directly (mapped, coherent): the
+// route kernels leave their per-block results there so the final merge
+// needs neither a merge launch nor a device-to-host copy call.
+struct MappedCands {
+  Cand* host = nullptr;
+  Cand* dev = nullptr;
+  size_t count = 0;
+};
+int reserve_mapped(MappedCands* m, size_t count);
+void release_mapped(MappedCands* m);
+
 // Merge `count` candidates per query (query q reads in + q*in_stride) into
 // out + q*k; one block of kMergeWaves waves per query.  Clears flags[q] when
 // flags is given.  Defined in grm_common.hip.

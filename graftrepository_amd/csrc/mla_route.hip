@@ -38,7 +38,8 @@ namespace mla {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kMaxDim = 4096;
-constexpr int kRouteWaves = 4;           // waves per route block
+constexpr int kRouteWaves = 4;           // waves per block, plain kernel
+constexpr int kPipeWaves = 16;           // waves per block, pipelined kernel
 constexpr uint32_t kStageRows = 1u << 16;  // rows per attach staging batch
 
 // ------------------------------------------------------------------ kernels
@@ -361,12 +362,8 @@ struct MlaDeviceArena {
   std::set<uint64_t> free_slots;  // freed slots below high_water
   void* d_queries = nullptr;
   size_t d_queries_bytes = 0;
-  Cand* d_block = nullptr;
-  size_t d_block_count = 0;
-  Cand* d_out = nullptr;
-  size_t d_out_count = 0;
-  Cand* h_out = nullptr;
-  size_t h_out_count = 0;
+  grm::MappedCands blocks_out;  // per-query, per-block top-k (host mapped)
+  std::vector<Cand> merged;
   void* h_stage = nullptr;
   size_t h_stage_bytes = 0;
   void* d_stage = nullptr;
@@ -378,7 +375,8 @@ struct MlaDeviceArena {
   hipEvent_t ev_mut = nullptr;
   bool mut_pending = false;
   bool pipeline = true;     // software-pipelined kernel when rows allow it
-  uint32_t max_blocks = 0;  // route grid cap; 0 -> 4 blocks per CU
+  uint32_t cus = 256;       // compute units of the device
+  uint32_t max_blocks = 0;  // plain-kernel grid cap (4 blocks per CU)
 };
 
 namespace {
@@ -394,10 +392,8 @@ void destroy_arena(MlaDeviceArena* a) {
   if (a->d_norms) (void)hipFree(a->d_norms);
   if (a->d_ids) (void)hipFree(a->d_ids);
   if (a->d_queries) (void)hipFree(a->d_queries);
-  if (a->d_block) (void)hipFree(a->d_block);
-  if (a->d_out) (void)hipFree(a->d_out);
   if (a->d_stage) (void)hipFree(a->d_stage);
-  if (a->h_out) (void)hipHostFree(a->h_out);
+  grm::release_mapped(&a->blocks_out);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
@@ -497,6 +493,7 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
         cus <= 0) {
       cus = 256;
     }
+    a->cus = static_cast<uint32_t>(cus);
     a->max_blocks = static_cast<uint32_t>(cus) * 4;
   }
   if (const char* env = getenv("GRM_HIP_MLA_BLOCKS")) {
@@ -587,14 +584,23 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
   GRM_HIP_CHECK(hipSetDevice(a->device));
   const size_t qbytes = static_cast<size_t>(q_count) * a->dim * elem_size(q_dtype);
   const uint32_t num_tiles = static_cast<uint32_t>((a->high_water + grm::kWave - 1) / grm::kWave);
-  const uint32_t want_blocks = (num_tiles + grm::mla::kRouteWaves - 1) / grm::mla::kRouteWaves;
-  const uint32_t blocks = std::max<uint32_t>(1, std::min(want_blocks, a->max_blocks));
-  GRM_CHECK_RC(reserve_device(&a->d_block, &a->d_block_count,
-                              static_cast<size_t>(blocks) * grm::kMaxTopK));
-  GRM_CHECK_RC(reserve_device(&a->d_out, &a->d_out_count,
-                              static_cast<size_t>(q_count) * topk));
-  GRM_CHECK_RC(reserve_pinned(&a->h_out, &a->h_out_count,
-                              static_cast<size_t>(q_count) * topk));
+  // The pipelined kernel runs one 16-wave block per CU (4 waves per SIMD);
+  // the plain kernel (rows that do not split into whole batches) 4-wave
+  // blocks, 4 per CU.
+  int batch = 0;
+  if (a->pipeline) {
+    for (int b : {9, 8, 6}) {
+      if (a->chunks % b == 0) {
+        batch = b;
+        break;
+      }
+    }
+  }
+  const uint32_t nw = batch ? grm::mla::kPipeWaves : grm::mla::kRouteWaves;
+  const uint32_t cap = batch ? std::min(a->cus, a->max_blocks) : a->max_blocks;
+  const uint32_t blocks = std::max<uint32_t>(1, std::min((num_tiles + nw - 1) / nw, cap));
+  const size_t per_q = static_cast<size_t>(blocks) * topk;
+  GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * q_count));
   const unsigned char* qbase = static_cast<const unsigned char*>(queries);
   if (!on_device) {
     GRM_CHECK_RC(reserve_device(reinterpret_cast<unsigned char**>(&a->d_queries),
@@ -606,54 +612,47 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
   if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
   const size_t qstride = static_cast<size_t>(a->dim) * elem_size(q_dtype);
   const size_t lds = static_cast<size_t>(a->dim_pad) * sizeof(double);
+  const dim3 grid(blocks), block(nw * grm::kWave);
   for (int qi = 0; qi < q_count; ++qi) {
     if (qi == warmup) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
     const void* q = qbase + qi * qstride;
-    Cand* out = a->d_out + static_cast<size_t>(qi) * topk;
-    constexpr int NW = grm::mla::kRouteWaves;
-    const dim3 grid(blocks), block(NW * grm::kWave);
-#define GRM_MLA_ARGS                                                               \
+    Cand* bout = a->blocks_out.dev + static_cast<size_t>(qi) * per_q;
+#define GRM_MLA_ARGS                                                                  \
   a->d_tiles, a->d_norms, a->d_ids, num_tiles, a->chunks, a->capacity, a->dim, a->dim_pad, q, \
-      q_dtype, topk, a->d_block
-    const bool pipe = a->pipeline && num_tiles >= 1;
+      q_dtype, topk, bout
+    constexpr int PW = grm::mla::kPipeWaves;
+    constexpr int RW = grm::mla::kRouteWaves;
     if (a->dtype == kF32) {
-      if (pipe && a->chunks % 9 == 0) {
-        grm::mla::mla_route_pipe_kernel<kF32, NW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
-      } else if (pipe && a->chunks % 8 == 0) {
-        grm::mla::mla_route_pipe_kernel<kF32, NW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
-      } else if (pipe && a->chunks % 6 == 0) {
-        grm::mla::mla_route_pipe_kernel<kF32, NW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
-      } else {
-        grm::mla::mla_route_kernel<kF32, NW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      switch (batch) {
+        case 9: grm::mla::mla_route_pipe_kernel<kF32, PW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+        case 8: grm::mla::mla_route_pipe_kernel<kF32, PW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+        case 6: grm::mla::mla_route_pipe_kernel<kF32, PW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+        default: grm::mla::mla_route_kernel<kF32, RW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
       }
     } else {
-      if (pipe && a->chunks % 9 == 0) {
-        grm::mla::mla_route_pipe_kernel<kBF16, NW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
-      } else if (pipe && a->chunks % 8 == 0) {
-        grm::mla::mla_route_pipe_kernel<kBF16, NW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
-      } else if (pipe && a->chunks % 6 == 0) {
-        grm::mla::mla_route_pipe_kernel<kBF16, NW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
-      } else {
-        grm::mla::mla_route_kernel<kBF16, NW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS);
+      switch (batch) {
+        case 9: grm::mla::mla_route_pipe_kernel<kBF16, PW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+        case 8: grm::mla::mla_route_pipe_kernel<kBF16, PW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+        case 6: grm::mla::mla_route_pipe_kernel<kBF16, PW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+        default: grm::mla::mla_route_kernel<kBF16, RW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
       }
     }
 #undef GRM_MLA_ARGS
     GRM_HIP_CHECK(hipGetLastError());
-    grm::topk_merge_kernel<<<1, grm::kMergeWaves * grm::kWave, 0, a->stream>>>(
-        a->d_block, blocks * static_cast<uint32_t>(topk), 0, topk, out, nullptr);
-    GRM_HIP_CHECK(hipGetLastError());
   }
   GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
-  GRM_HIP_CHECK(hipMemcpyAsync(a->h_out, a->d_out,
-                               static_cast<size_t>(q_count) * topk * sizeof(Cand),
-                               hipMemcpyDeviceToHost, a->stream));
   GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
   if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
-  for (size_t i = 0; i < static_cast<size_t>(q_count) * topk; ++i) {
-    const Cand& c = a->h_out[i];
-    const bool ok = isfinite(c.score) && c.id != kNoId;
-    out_ids[i] = ok ? c.id : kNoId;
-    if (out_scores) out_scores[i] = ok ? c.score : __builtin_nanf("");
+  a->merged.resize(topk);
+  for (int qi = 0; qi < q_count; ++qi) {
+    grm::host_topk_merge(a->blocks_out.host + static_cast<size_t>(qi) * per_q, per_q, topk,
+                         a->merged.data());
+    for (int j = 0; j < topk; ++j) {
+      const Cand& c = a->merged[j];
+      const bool ok = isfinite(c.score) && c.id != kNoId;
+      out_ids[static_cast<size_t>(qi) * topk + j] = ok ? c.id : kNoId;
+      if (out_scores) out_scores[static_cast<size_t>(qi) * topk + j] = ok ? c.score : __builtin_nanf("");
+    }
   }
   grm::clear_error();
   return 0;
