@@ -1,30 +1,21 @@
-// gqa_route.hip -- exact ragged GQA route on gfx950.
-//
-// Law (cpp/grm_runtime.cpp:2980-3029 gqa_raw_score; core/graft_arena.py:2888-2900):
-//   score(node) = float( (sum_h best_h) / H )                 h ascending, fp64
-//   best_h      = max over (query token qi, key token t) of |dot| / sqrt(hd)
-//   dot         = sum_d (double)q[h][qi][d] * (double)k[h/R][t][d], d ascending
-// A node with zero key tokens scores 0.0; any non-finite query or key value
-// makes the score NaN (never ranked).  Stacked routing layers are folded
-// into the head axes by the caller (kv head g of layer y -> y*KV+g).
+// gqa_route.hip -- ragged GQA route on gfx950: bank lifecycle, route
+// orchestration and the C ABI.  Device code lives in gqa_kernels.hpp.
 //
 // Bank layout in HBM: ragged CSR.  Node slot i owns tokens
 // [tok_off[i], tok_off[i]+len[i]) of the token arena; its block is
 // [kv][len][hd] values of the storage dtype (f32, bf16, f16 or int8 codes
-// with per-(token, group) scales, dequantised as fp16(code*scale),
-// core/graft_quant.py:136-144).  No padding is stored or read.
+// with per-(token, group) scales).  No padding is stored or read.
 //
-// Route = (1) head-max kernel: one wavefront per (slot, 64-token chunk, kv
-// head); lane t owns one key token, computes its R*Qt dot products in the
-// law's d order in fp64, and the wave folds |dot|/sqrt(hd) into the
-// per-(slot, head) maximum with a 64-bit atomicMax on the bit pattern
-// (non-negative doubles order like their bits, so the result does not depend
-// on scheduling); (2) finalize kernel: per slot the fp64 head sum in h order,
-// the fused top-k, and a re-zero of the maxima for the next call.
-#include "grm_common.hpp"
+// Route (bf16 / fp16 / int8 banks, head_dim 64, 128 or 256):
+//   prep -> screen (MFMA, all key tokens) -> select -> shortlist/certify ->
+//   exact rescore of the shortlist -> exact finalize; the host merges the
+//   shortlist's exact scores.  A query whose shortlist is not certified, or
+//   whose values are non-finite or leave the fp16 range, is routed again
+//   on the exact path, so every result follows the law.
+// Route (fp32 banks and other shapes): exact path over every node.
+#include "gqa_kernels.hpp"
 #include "grm_hip_router.h"
 
-#include <hip/hip_fp16.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -34,311 +25,15 @@
 #include <unordered_map>
 #include <vector>
 
-namespace grm {
-namespace gqa {
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kChunk = 64;          // key tokens per head-max wavefront
-constexpr int kUnitWaves = 4;       // wavefronts per head-max block
-constexpr int kFinWaves = 4;        // wavefronts per finalize block
-constexpr int kMaxRQ = 32;          // R * Qt supported by the exact kernel
-constexpr uint32_t kMaxHeadDim = 512;
-
-// Work item: one 64-token chunk of one slot (all kv heads).
-struct Item {
-  uint32_t slot;
-  uint32_t t0;
-};
-
-__device__ inline float dequant_i8(int code, float scale) {
-  return __half2float(__float2half(static_cast<float>(code) * scale));
-}
-
-__device__ inline float load_scale(const unsigned char* __restrict__ scales,
-                                   int scale_dtype, uint64_t idx) {
-  if (scale_dtype == kF16) {
-    return __half2float(reinterpret_cast<const __half*>(scales)[idx]);
-  }
-  return reinterpret_cast<const float*>(scales)[idx];
-}
-
-// Decode the 16-byte chunk at element index `e0` of a key row into floats.
-// Returns the number of elements (EPC) decoded.
-template <int KDT>
-__device__ inline void decode_chunk(u32x4 v, const unsigned char* __restrict__ scales,
-                                    int scale_dtype, uint64_t scale_idx,
-                                    float* out) {
-  if constexpr (KDT == kF32) {
-    out[0] = __uint_as_float(v.x);
-    out[1] = __uint_as_float(v.y);
-    out[2] = __uint_as_float(v.z);
-    out[3] = __uint_as_float(v.w);
-  } else if constexpr (KDT == kBF16) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[2 * i] = __uint_as_float(w[i] << 16);
-      out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
-  } else if constexpr (KDT == kF16) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __half_raw lo, hi;
-      lo.x = static_cast<unsigned short>(w[i] & 0xffffu);
-      hi.x = static_cast<unsigned short>(w[i] >> 16);
-      out[2 * i] = __half2float(__half(lo));
-      out[2 * i + 1] = __half2float(__half(hi));
-    }
-  } else {
-    const float s = load_scale(scales, scale_dtype, scale_idx);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int code = static_cast<int>(static_cast<int8_t>((w[i] >> (8 * b)) & 0xffu));
-        out[4 * i + b] = dequant_i8(code, s);
-      }
-    }
-  }
-}
-
-template <int KDT>
-struct KeyTraits {
-  static constexpr int kEsize = KDT == kF32 ? 4 : (KDT == kI8 ? 1 : 2);
-  static constexpr int kEpc = 16 / kEsize;  // elements per 16-byte chunk
-};
-
-// Exact per-(slot, head) maxima.  Grid: one wavefront per (item, kv head).
-// hmax[slot * H + h] holds the running max of |dot|/sqrt(hd) as double bits.
-template <int KDT, int RQ>
-__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_heads_kernel(
-    const unsigned char* __restrict__ keys,
-    const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
-    const uint64_t* __restrict__ tok_off, const uint32_t* __restrict__ lens,
-    const Item* __restrict__ items, uint32_t n_items, int kv, int hd, int R,
-    int Qt, const void* __restrict__ query, int q_dtype, double denom,
-    unsigned long long* __restrict__ hmax, int H,
-    unsigned* __restrict__ qbad) {
-  using T = KeyTraits<KDT>;
-  extern __shared__ double qs[];  // [kUnitWaves][RQ][hd]
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const uint64_t unit = static_cast<uint64_t>(blockIdx.x) * kUnitWaves + wave;
-  const bool active = unit < static_cast<uint64_t>(n_items) * kv;
-  const uint32_t item_i = active ? static_cast<uint32_t>(unit / kv) : 0;
-  const int g = active ? static_cast<int>(unit % kv) : 0;
-  double* q = qs + static_cast<size_t>(wave) * RQ * hd;
-  const int rq_used = R * Qt;
-
-  // Stage this kv head's R*Qt query rows as doubles (rows >= R*Qt are 0).
-  bool bad = false;
-  for (int i = lane; i < RQ * hd; i += kWave) {
-    const int rq = i / hd;
-    const int d = i - rq * hd;
-    double v = 0.0;
-    if (active && rq < rq_used) {
-      const int r = rq / Qt;
-      const int qi = rq - r * Qt;
-      const uint64_t src = (static_cast<uint64_t>(g * R + r) * Qt + qi) * hd + d;
-      const float f = q_dtype == kBF16
-                          ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
-                          : static_cast<const float*>(query)[src];
-      bad = bad || !isfinite(f);
-      v = static_cast<double>(f);
-    }
-    q[i] = v;
-  }
-  if (__ballot(bad) != 0ull && lane == 0) atomicOr(qbad, 1u);
-  __syncthreads();
-  if (!active) return;
-
-  const Item it = items[item_i];
-  const uint32_t L = lens[it.slot];
-  const uint32_t t = it.t0 + lane;
-  const bool has = t < L;
-  double acc[RQ];
-#pragma unroll
-  for (int j = 0; j < RQ; ++j) acc[j] = 0.0;
-  if (has) {
-    const uint64_t row = (tok_off[it.slot] * kv + static_cast<uint64_t>(g) * L + t);
-    const u32x4* p = reinterpret_cast<const u32x4*>(keys + row * hd * T::kEsize);
-    const int groups = KDT == kI8 ? hd / group_size : 1;
-    for (int c = 0; c < hd / T::kEpc; ++c) {
-      const u32x4 v = p[c];
-      float f[T::kEpc];
-      const int e0 = c * T::kEpc;
-      const uint64_t sidx = KDT == kI8 ? row * groups + e0 / group_size : 0;
-      decode_chunk<KDT>(v, scales, scale_dtype, sidx, f);
-#pragma unroll
-      for (int e = 0; e < T::kEpc; ++e) {
-        const double kd = static_cast<double>(f[e]);
-#pragma unroll
-        for (int j = 0; j < RQ; ++j) acc[j] = fma(kd, q[j * hd + e0 + e], acc[j]);
-      }
-    }
-  }
-  // best_h over this lane's token, then over the wave's tokens.
-  for (int r = 0; r < R; ++r) {
-    double m = 0.0;
-#pragma unroll
-    for (int j = 0; j < RQ; ++j) {
-      if (j / Qt == r && j < rq_used && has) {
-        const double v = fabs(acc[j]) / denom;
-        m = (v > m || isnan(v)) ? v : m;
-      }
-    }
-    unsigned long long bits = __double_as_longlong(m);
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const unsigned long long o = __shfl_xor(bits, off);
-      bits = o > bits ? o : bits;
-    }
-    if (lane == 0) atomicMax(hmax + static_cast<uint64_t>(it.slot) * H + g * R + r, bits);
-  }
-}
-
-// Finalize: exact score per slot; each block writes its k best entries to
-// block_out for topk_merge_kernel (which also clears the query flag).
-__global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
-    unsigned long long* __restrict__ hmax, int H, uint32_t n_slots,
-    const uint32_t* __restrict__ lens, const uint32_t* __restrict__ flags,
-    const uint64_t* __restrict__ ids, const unsigned* __restrict__ qbad, int k,
-    Cand* __restrict__ block_out) {
-  __shared__ Cand s_lists[kFinWaves][kMaxTopK];
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
-  const bool q_bad = *qbad != 0u;
-  WaveList L;
-  wl_init(L);
-  const uint32_t stride = gridDim.x * blockDim.x;
-  for (uint32_t base = blockIdx.x * blockDim.x + wave * kWave; base < n_slots;
-       base += stride) {
-    const uint32_t slot = base + lane;
-    float s = __builtin_nanf("");
-    bool valid = false;
-    if (slot < n_slots) {
-      const uint32_t f = flags[slot];
-      if (f & 1u) {  // live
-        const uint32_t len = lens[slot];
-        if (len == 0) {
-          s = 0.0f;
-        } else {
-          // Read and re-zero the maxima of every scored slot (NaN bits of a
-          // non-finite node included) so the next call starts from zero.
-          double total = 0.0;
-          unsigned long long* hm = hmax + static_cast<uint64_t>(slot) * H;
-          for (int h = 0; h < H; ++h) {
-            total += __longlong_as_double(hm[h]);
-            hm[h] = 0ull;
-          }
-          if ((f & 2u) && !q_bad) {  // all key and query values finite
-            s = static_cast<float>(total / static_cast<double>(H));
-          }
-        }
-        valid = isfinite(s);
-      }
-    }
-    const bool need = valid && s >= L.th_s;
-    uint64_t id = kNoId;
-    if (need) id = ids[slot];
-    wl_consume(L, k, s, id, slot, need);
-  }
-  block_topk_write<kFinWaves>(L, k, s_lists, block_out);
-}
-
-// Per-slot key statistics for appended/created slots: bit 1 of flags is set
-// when every decoded key value is finite.  One wave per (item, kv head).
-template <int KDT>
-__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_key_stats_kernel(
-    const unsigned char* __restrict__ keys,
-    const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
-    const uint64_t* __restrict__ tok_off, const uint32_t* __restrict__ lens,
-    const Item* __restrict__ items, uint32_t n_items, int kv, int hd,
-    uint32_t* __restrict__ nonfinite) {
-  using T = KeyTraits<KDT>;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const uint64_t unit = static_cast<uint64_t>(blockIdx.x) * kUnitWaves + wave;
-  if (unit >= static_cast<uint64_t>(n_items) * kv) return;
-  const Item it = items[unit / kv];
-  const int g = static_cast<int>(unit % kv);
-  const uint32_t L = lens[it.slot];
-  const uint32_t t = it.t0 + lane;
-  bool bad = false;
-  if (t < L) {
-    const uint64_t row = (tok_off[it.slot] * kv + static_cast<uint64_t>(g) * L + t);
-    const u32x4* p = reinterpret_cast<const u32x4*>(keys + row * hd * T::kEsize);
-    const int groups = KDT == kI8 ? hd / group_size : 1;
-    for (int c = 0; c < hd / T::kEpc; ++c) {
-      float f[T::kEpc];
-      const int e0 = c * T::kEpc;
-      decode_chunk<KDT>(p[c], scales, scale_dtype,
-                        KDT == kI8 ? row * groups + e0 / group_size : 0, f);
-#pragma unroll
-      for (int e = 0; e < T::kEpc; ++e) bad = bad || !isfinite(f[e]);
-    }
-  }
-  if (__ballot(bad) != 0ull && lane == 0) atomicOr(nonfinite + it.slot, 1u);
-}
-
-// flags[slot] = live | finite<<1, ids/offsets/lens written for the listed
-// slots (metadata arrays packed back to back in `meta`).
-__global__ void gqa_set_slots_kernel(const uint64_t* __restrict__ meta,
-                                     uint64_t count,
-                                     uint64_t* __restrict__ tok_off,
-                                     uint32_t* __restrict__ lens,
-                                     uint64_t* __restrict__ ids,
-                                     uint32_t* __restrict__ flags,
-                                     uint32_t* __restrict__ nonfinite) {
-  // meta: [count slots][count tok_off][count lens][count ids]
-  for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
-       i < count; i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint64_t s = meta[i];
-    tok_off[s] = meta[count + i];
-    lens[s] = static_cast<uint32_t>(meta[2 * count + i]);
-    ids[s] = meta[3 * count + i];
-    flags[s] = 0u;  // finite bit set by gqa_commit_slots_kernel
-    nonfinite[s] = 0u;
-  }
-}
-
-__global__ void gqa_commit_slots_kernel(const uint64_t* __restrict__ slots,
-                                        uint64_t count,
-                                        uint32_t* __restrict__ flags,
-                                        const uint32_t* __restrict__ nonfinite) {
-  for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
-       i < count; i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint64_t s = slots[i];
-    flags[s] = 1u | (nonfinite[s] ? 0u : 2u);
-  }
-}
-
-__global__ void gqa_evict_kernel(const uint64_t* __restrict__ slots,
-                                 uint64_t count, uint32_t* __restrict__ flags,
-                                 uint64_t* __restrict__ ids) {
-  for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
-       i < count; i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    flags[slots[i]] = 0u;
-    ids[slots[i]] = kNoId;
-  }
-}
-
-__global__ void gqa_clear_flag_kernel(unsigned* __restrict__ flag) { *flag = 0u; }
-
-}  // namespace gqa
-}  // namespace grm
-
 using grm::Cand;
 using grm::kBF16;
 using grm::kF16;
 using grm::kF32;
 using grm::kI8;
 using grm::kNoId;
+using grm::kNoSlot;
 using grm::gqa::Item;
+using grm::gqa::u32x4;
 
 // ------------------------------------------------------------------ host side
 
@@ -360,8 +55,9 @@ struct GqaDeviceArena {
   uint64_t* d_tok_off = nullptr;
   uint32_t* d_len = nullptr;
   uint64_t* d_ids = nullptr;
-  uint32_t* d_flags = nullptr;
+  uint32_t* d_flags = nullptr;  // bit 0 live, bit 1 all key values finite
   uint32_t* d_nonfinite = nullptr;
+  unsigned* d_kmax = nullptr;   // float bits: max key norm per slot
   // host mirrors
   std::vector<uint64_t> tok_off;
   std::vector<uint32_t> len;
@@ -369,16 +65,44 @@ struct GqaDeviceArena {
   std::unordered_map<uint64_t, uint64_t> slot_of;
   std::set<uint64_t> free_slots;
   // route work list, rebuilt when the epoch moves
+  uint32_t chunk = 64;  // key tokens per work item
   Item* d_items = nullptr;
   size_t d_items_count = 0;
   uint64_t n_items = 0;
   uint64_t items_epoch = ~0ull;
+  uint32_t max_len = 0;  // longest live node
+  // exact path
   unsigned long long* d_hmax = nullptr;
   size_t d_hmax_count = 0;
   int hmax_heads = 0;
   grm::MappedCands blocks_out;  // per-query, per-block top-k (host mapped)
+  unsigned* d_qbad = nullptr;   // set when a query value is non-finite
+  // screen path
+  bool screen = true;
+  u32x4* d_bfrag = nullptr;
+  size_t d_bfrag_count = 0;
+  float* d_coef = nullptr;
+  size_t d_coef_count = 0;
+  unsigned* d_qflags = nullptr;
+  size_t d_qflags_count = 0;
+  unsigned* d_hms = nullptr;
+  size_t d_hms_count = 0;
+  int hms_heads = 0;
+  Cand* d_bu = nullptr;
+  size_t d_bu_count = 0;
+  Cand* d_bl = nullptr;
+  size_t d_bl_count = 0;
+  uint32_t* d_shortlist = nullptr;
+  size_t d_shortlist_count = 0;
+  unsigned long long* d_hex = nullptr;
+  size_t d_hex_count = 0;
+  grm::MappedCands short_out;  // exact scores of the shortlists (host mapped)
+  grm::MappedBuf qstate;       // per query: prep flags, then status (host mapped)
+  uint32_t sel_blocks = 256;
+  uint32_t screen_waves = 8192;  // persistent screen wavefronts (all kv heads)
+  uint64_t routes = 0;          // route calls
+  uint64_t fallbacks = 0;       // queries re-routed on the exact path
   std::vector<Cand> merged;
-  unsigned* d_qbad = nullptr;  // set when a query value is non-finite
   void* d_queries = nullptr;
   size_t d_queries_bytes = 0;
   void* h_stage = nullptr;
@@ -421,6 +145,15 @@ int reserve_device(T** ptr, size_t* have, size_t want) {
   return 0;
 }
 
+// As reserve_device, and zero-filled on (re)allocation.
+template <typename T>
+int reserve_device_zero(T** ptr, size_t* have, size_t want, hipStream_t st) {
+  if (want <= *have && *ptr) return 0;
+  GRM_CHECK_RC(reserve_device(ptr, have, want));
+  GRM_HIP_CHECK(hipMemsetAsync(*ptr, 0, std::max<size_t>(1, want) * sizeof(T), st));
+  return 0;
+}
+
 template <typename T>
 int reserve_pinned(T** ptr, size_t* have, size_t want) {
   if (want <= *have && *ptr) return 0;
@@ -440,12 +173,17 @@ void destroy_arena(GqaDeviceArena* a) {
   (void)hipSetDevice(a->device);
   if (a->stream) (void)hipStreamSynchronize(a->stream);
   if (a->side) (void)hipStreamSynchronize(a->side);
-  void* dev[] = {a->d_keys, a->d_scales, a->d_tok_off, a->d_len, a->d_ids, a->d_flags,
-                 a->d_nonfinite, a->d_items, a->d_hmax, a->d_qbad, a->d_queries, a->d_stage};
+  void* dev[] = {a->d_keys,  a->d_scales, a->d_tok_off, a->d_len,   a->d_ids,
+                 a->d_flags, a->d_nonfinite, a->d_kmax, a->d_items, a->d_hmax,
+                 a->d_qbad,  a->d_queries, a->d_stage,  a->d_bfrag, a->d_coef,
+                 a->d_hms,   a->d_bu,     a->d_bl,      a->d_shortlist, a->d_hex,
+                 a->d_qflags};
   for (void* p : dev) {
     if (p) (void)hipFree(p);
   }
   grm::release_mapped(&a->blocks_out);
+  grm::release_mapped(&a->short_out);
+  grm::release_mapped_bytes(&a->qstate);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
@@ -463,27 +201,27 @@ int wait_mutations(GqaDeviceArena* a) {
   return 0;
 }
 
-std::vector<Item> make_items(const GqaDeviceArena* a, const uint64_t* slots, uint64_t count) {
-  std::vector<Item> items;
-  for (uint64_t i = 0; i < count; ++i) {
-    const uint64_t s = slots[i];
-    for (uint32_t t0 = 0; t0 < a->len[s]; t0 += grm::gqa::kChunk) {
-      items.push_back(Item{static_cast<uint32_t>(s), t0});
-    }
+void append_items(std::vector<Item>& items, uint32_t slot, uint64_t base, uint64_t len,
+                  uint32_t chunk) {
+  for (uint64_t t0 = 0; t0 < len; t0 += chunk) {
+    Item it;
+    it.base = base;
+    it.slot = slot;
+    it.t0 = static_cast<uint32_t>(t0);
+    it.count = static_cast<uint32_t>(std::min<uint64_t>(chunk, len - t0));
+    it.len = static_cast<uint32_t>(len);
+    items.push_back(it);
   }
-  return items;
 }
 
 int launch_stats(GqaDeviceArena* a, const Item* d_items, uint64_t n_items, hipStream_t st) {
   if (n_items == 0) return 0;
-  const uint64_t units = n_items * a->kv;
-  const unsigned blocks = static_cast<unsigned>((units + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves);
+  const dim3 grid(static_cast<unsigned>((n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves), a->kv);
   const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
 #define GRM_STATS(KDT)                                                              \
-  grm::gqa::gqa_key_stats_kernel<KDT><<<blocks, threads, 0, st>>>(                  \
-      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_tok_off, a->d_len, \
-      d_items, static_cast<uint32_t>(n_items), static_cast<int>(a->kv),             \
-      static_cast<int>(a->hd), a->d_nonfinite)
+  grm::gqa::gqa_key_stats_kernel<KDT><<<grid, threads, 0, st>>>(                    \
+      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, d_items,               \
+      static_cast<uint32_t>(n_items), static_cast<int>(a->hd), a->d_nonfinite, a->d_kmax)
   switch (a->key_dtype) {
     case kF32: GRM_STATS(kF32); break;
     case kBF16: GRM_STATS(kBF16); break;
@@ -527,9 +265,7 @@ int place_nodes(GqaDeviceArena* a, const std::vector<uint64_t>& slots,
   const size_t sbytes = tokens * token_scale_bytes(a);
   std::vector<Item> items;
   for (uint64_t i = 0; i < count; ++i) {
-    for (uint64_t t0 = 0; t0 < tok_counts[i]; t0 += grm::gqa::kChunk) {
-      items.push_back(Item{static_cast<uint32_t>(slots[i]), static_cast<uint32_t>(t0)});
-    }
+    append_items(items, static_cast<uint32_t>(slots[i]), offs[i] * a->kv, tok_counts[i], 64);
   }
   const size_t meta_bytes = 4 * count * sizeof(uint64_t);
   const size_t item_bytes = items.size() * sizeof(Item);
@@ -564,7 +300,7 @@ int place_nodes(GqaDeviceArena* a, const std::vector<uint64_t>& slots,
   const unsigned blocks = static_cast<unsigned>(std::min<uint64_t>((count + threads - 1) / threads, 1024));
   grm::gqa::gqa_set_slots_kernel<<<blocks, threads, 0, st>>>(
       reinterpret_cast<const uint64_t*>(d), count, a->d_tok_off, a->d_len, a->d_ids, a->d_flags,
-      a->d_nonfinite);
+      a->d_nonfinite, a->d_kmax);
   GRM_HIP_CHECK(hipGetLastError());
   GRM_CHECK_RC(launch_stats(a, reinterpret_cast<const Item*>(d + o_items), items.size(), st));
   grm::gqa::gqa_commit_slots_kernel<<<blocks, threads, 0, st>>>(
@@ -631,6 +367,26 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   a->tok_off.assign(cap_nodes, 0);
   a->len.assign(cap_nodes, 0);
   a->slot_id.assign(cap_nodes, kNoId);
+  // Larger banks use longer work items so the grid stays near a few
+  // hundred thousand wavefronts.
+  a->chunk = cap_tokens * a->kv > (8ull << 20) ? 256 : 64;
+  if (const char* env = getenv("GRM_HIP_GQA_CHUNK")) {
+    const long v = strtol(env, nullptr, 10);
+    if (v >= 16 && v <= 4096 && v % 16 == 0) a->chunk = static_cast<uint32_t>(v);
+  }
+  if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen = env[0] != '0';
+  {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, a->device) != hipSuccess ||
+        cus <= 0) {
+      cus = 256;
+    }
+    a->screen_waves = static_cast<uint32_t>(cus) * 16;  // 4 per SIMD
+  }
+  if (const char* env = getenv("GRM_HIP_GQA_SCREEN_WAVES")) {
+    const long v = strtol(env, nullptr, 10);
+    if (v >= 64 && v <= (1l << 22)) a->screen_waves = static_cast<uint32_t>(v);
+  }
   std::vector<uint64_t> ids(nodes), slots(nodes);
   a->slot_of.reserve(nodes * 2);
   for (uint64_t i = 0; i < nodes; ++i) {
@@ -660,12 +416,14 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_ids), cap_nodes * sizeof(uint64_t)));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_flags), cap_nodes * sizeof(uint32_t)));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_nonfinite), cap_nodes * sizeof(uint32_t)));
+  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_kmax), cap_nodes * sizeof(unsigned)));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_qbad), sizeof(unsigned)));
   BAIL_HIP(hipMemsetAsync(a->d_tok_off, 0, cap_nodes * sizeof(uint64_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_len, 0, cap_nodes * sizeof(uint32_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_ids, 0xff, cap_nodes * sizeof(uint64_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_flags, 0, cap_nodes * sizeof(uint32_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_nonfinite, 0, cap_nodes * sizeof(uint32_t), a->stream));
+  BAIL_HIP(hipMemsetAsync(a->d_kmax, 0, cap_nodes * sizeof(unsigned), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_qbad, 0, sizeof(unsigned), a->stream));
   BAIL_HIP(hipStreamSynchronize(a->stream));
 #undef BAIL_HIP
@@ -701,12 +459,14 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
 
 int ensure_items(GqaDeviceArena* a) {
   if (a->items_epoch == a->epoch && a->d_items) return 0;
-  std::vector<uint64_t> live_slots;
-  live_slots.reserve(a->live);
+  std::vector<Item> items;
+  items.reserve(a->live * 2);
+  uint32_t max_len = 0;
   for (uint64_t s = 0; s < a->high_water; ++s) {
-    if (a->slot_id[s] != kNoId) live_slots.push_back(s);
+    if (a->slot_id[s] == kNoId) continue;
+    append_items(items, static_cast<uint32_t>(s), a->tok_off[s] * a->kv, a->len[s], a->chunk);
+    max_len = std::max(max_len, a->len[s]);
   }
-  std::vector<Item> items = make_items(a, live_slots.data(), live_slots.size());
   GRM_CHECK_RC(reserve_device(&a->d_items, &a->d_items_count, items.size()));
   if (!items.empty()) {
     GRM_HIP_CHECK(hipMemcpyAsync(a->d_items, items.data(), items.size() * sizeof(Item),
@@ -714,23 +474,32 @@ int ensure_items(GqaDeviceArena* a) {
     GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
   }
   a->n_items = items.size();
+  a->max_len = max_len;
   a->items_epoch = a->epoch;
   return 0;
 }
 
-int launch_exact(GqaDeviceArena* a, const void* q, int q_dtype, int H, int Qt, int rq_pad) {
+int rq_pad_of(int rq) {
+  int p = 1;
+  while (p < rq) p *= 2;
+  return p;
+}
+
+// --------------------------------------------------------------- exact path
+
+int launch_exact_heads(GqaDeviceArena* a, const void* q, int q_dtype, int H, int Qt) {
   if (a->n_items == 0) return 0;
   const int R = H / static_cast<int>(a->kv);
-  const uint64_t units = a->n_items * a->kv;
-  const unsigned blocks = static_cast<unsigned>((units + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves);
+  const int rq_pad = rq_pad_of(R * Qt);
+  const dim3 grid(static_cast<unsigned>((a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves), a->kv);
   const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
-  const size_t lds = static_cast<size_t>(grm::gqa::kUnitWaves) * rq_pad * a->hd * sizeof(double);
+  const size_t lds = static_cast<size_t>(rq_pad) * a->hd * sizeof(double);
   const double denom = sqrt(static_cast<double>(a->hd));
 #define GRM_EXACT(KDT, RQ)                                                                  \
-  grm::gqa::gqa_exact_heads_kernel<KDT, RQ><<<blocks, threads, lds, a->stream>>>(          \
-      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_tok_off, a->d_len,       \
-      a->d_items, static_cast<uint32_t>(a->n_items), static_cast<int>(a->kv),              \
-      static_cast<int>(a->hd), R, Qt, q, q_dtype, denom, a->d_hmax, H, a->d_qbad)
+  grm::gqa::gqa_exact_heads_kernel<KDT, RQ><<<grid, threads, lds, a->stream>>>(            \
+      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                   \
+      static_cast<uint32_t>(a->n_items), static_cast<int>(a->hd), R, Qt, q, q_dtype, denom,  \
+      a->d_hmax, a->cap_nodes, a->d_qbad)
 #define GRM_EXACT_RQ(KDT)                       \
   switch (rq_pad) {                             \
     case 1: GRM_EXACT(KDT, 1); break;           \
@@ -752,6 +521,206 @@ int launch_exact(GqaDeviceArena* a, const void* q, int q_dtype, int H, int Qt, i
   return 0;
 }
 
+// Enqueue the exact route of one query; its per-block top-k lands in
+// blocks_out at `bout`.
+int enqueue_exact(GqaDeviceArena* a, const void* q, int q_dtype, int H, int Qt, int topk,
+                  uint32_t fin_blocks, Cand* bout) {
+  if (a->hmax_heads != H || a->d_hmax_count < a->cap_nodes * static_cast<size_t>(H)) {
+    GRM_CHECK_RC(reserve_device(&a->d_hmax, &a->d_hmax_count, a->cap_nodes * static_cast<size_t>(H)));
+    GRM_HIP_CHECK(hipMemsetAsync(a->d_hmax, 0, a->d_hmax_count * sizeof(unsigned long long), a->stream));
+    a->hmax_heads = H;
+  }
+  GRM_CHECK_RC(launch_exact_heads(a, q, q_dtype, H, Qt));
+  const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
+  grm::gqa::gqa_finalize_kernel<<<fin_blocks, per_block, 0, a->stream>>>(
+      a->d_hmax, a->cap_nodes, H, static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags,
+      a->d_ids, a->d_qbad, topk, bout);
+  GRM_HIP_CHECK(hipGetLastError());
+  grm::gqa::gqa_clear_flags_kernel<<<1, 64, 0, a->stream>>>(a->d_qbad, 1);
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
+void write_result(const Cand* merged, int topk, uint64_t* out_ids, float* out_scores) {
+  for (int j = 0; j < topk; ++j) {
+    const Cand& c = merged[j];
+    const bool ok = isfinite(c.score) && c.id != kNoId;
+    out_ids[j] = ok ? c.id : kNoId;
+    if (out_scores) out_scores[j] = ok ? c.score : __builtin_nanf("");
+  }
+}
+
+// -------------------------------------------------------------- screen path
+
+struct ScreenPlan {
+  int R = 0, Qt = 0, H = 0;
+  int KS = 0;        // head_dim / 32
+  int qb_max = 0;    // queries per screen pass (<= 64 columns)
+  int M = 0;         // shortlist length
+  int mfma = kBF16;  // MFMA operand type
+};
+
+bool screen_plan(const GqaDeviceArena* a, int H, int Qt, int topk, ScreenPlan* p) {
+  if (!a->screen || a->key_dtype == kF32) return false;
+  if (a->hd != 64 && a->hd != 128 && a->hd != 256) return false;
+  const int R = H / static_cast<int>(a->kv);
+  if (R * Qt > 64) return false;
+  p->R = R;
+  p->Qt = Qt;
+  p->H = H;
+  p->KS = static_cast<int>(a->hd / 32);
+  p->qb_max = std::max(1, 64 / (R * Qt));
+  p->M = std::min(grm::gqa::kMaxShort - 1, std::max(16, 2 * topk));
+  p->mfma = a->key_dtype == kBF16 ? kBF16 : kF16;
+  return true;
+}
+
+// Enqueue the screen route of queries [q0, q0+qb) of a call of q_total
+// queries (device pointer `qbase`, `qstride` bytes per query).  Shortlist
+// exact scores land in short_out at q0*M; qstate holds the queries' prep
+// flags at [q] and certificate status at [q_total + q].
+int enqueue_screen(GqaDeviceArena* a, const ScreenPlan& p, const unsigned char* qbase,
+                   size_t qstride, int q_dtype, int q0, int qb, int q_total, int topk) {
+  const int kv = static_cast<int>(a->kv);
+  const int cols = qb * p.R * p.Qt;
+  const int NT = (cols + 15) / 16;
+  const int ntp = NT <= 1 ? 1 : (NT <= 2 ? 2 : 4);
+  const int H = p.H;
+  const int M = p.M;
+  const int mU = M + 1;
+  GRM_CHECK_RC(reserve_device(&a->d_bfrag, &a->d_bfrag_count,
+                              static_cast<size_t>(kv) * ntp * p.KS * grm::kWave));
+  GRM_CHECK_RC(reserve_device(&a->d_coef, &a->d_coef_count, static_cast<size_t>(p.qb_max)));
+  if (a->hms_heads != H || a->d_hms_count < static_cast<size_t>(p.qb_max) * a->cap_nodes * H) {
+    a->d_hms_count = 0;
+    GRM_CHECK_RC(reserve_device_zero(&a->d_hms, &a->d_hms_count,
+                                     static_cast<size_t>(p.qb_max) * a->cap_nodes * H, a->stream));
+    a->hms_heads = H;
+  }
+  const uint32_t n_slots = static_cast<uint32_t>(a->high_water);
+  const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
+  const uint32_t nblk = std::max<uint32_t>(1, std::min<uint32_t>((n_slots + per_block - 1) / per_block, a->sel_blocks));
+  GRM_CHECK_RC(reserve_device(&a->d_bu, &a->d_bu_count, static_cast<size_t>(qb) * nblk * mU));
+  GRM_CHECK_RC(reserve_device(&a->d_bl, &a->d_bl_count, static_cast<size_t>(qb) * nblk * topk));
+  GRM_CHECK_RC(reserve_device(&a->d_shortlist, &a->d_shortlist_count, static_cast<size_t>(p.qb_max) * M));
+  if (a->d_hex_count < static_cast<size_t>(p.qb_max) * M * H) {
+    a->d_hex_count = 0;
+    GRM_CHECK_RC(reserve_device_zero(&a->d_hex, &a->d_hex_count, static_cast<size_t>(p.qb_max) * M * H,
+                                     a->stream));
+  }
+  GRM_CHECK_RC(reserve_device(&a->d_qflags, &a->d_qflags_count, static_cast<size_t>(p.qb_max)));
+  // 1. query prep (fragments, error coefficient, flags)
+  grm::gqa::gqa_clear_flags_kernel<<<(qb + 63) / 64, 64, 0, a->stream>>>(a->d_qflags, qb);
+  GRM_HIP_CHECK(hipGetLastError());
+  const unsigned char* qptr = qbase + static_cast<size_t>(q0) * qstride;
+  const double gamma = 2.0 * (a->hd + 2.0 * p.KS) * ldexp(1.0, -24);
+  double delta = 0.0, sigma = 0.0;
+  if (p.mfma == kBF16) {
+    delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
+    sigma = ldexp(1.0, -130);
+  } else {
+    delta = q_dtype == kF32 ? ldexp(1.0, -11) : 0.0;
+    sigma = ldexp(1.0, -25);
+  }
+  if (p.mfma == kBF16) {
+    grm::gqa::gqa_query_prep_kernel<kBF16><<<kv + qb, 256, 0, a->stream>>>(
+        qptr, q_dtype, qb, H, p.Qt, static_cast<int>(a->hd), kv, p.R, ntp, p.KS, a->d_bfrag,
+        a->d_qflags, a->d_coef, gamma, delta, sigma);
+  } else {
+    grm::gqa::gqa_query_prep_kernel<kF16><<<kv + qb, 256, 0, a->stream>>>(
+        qptr, q_dtype, qb, H, p.Qt, static_cast<int>(a->hd), kv, p.R, ntp, p.KS, a->d_bfrag,
+        a->d_qflags, a->d_coef, gamma, delta, sigma);
+  }
+  GRM_HIP_CHECK(hipGetLastError());
+  // 2. screen
+  if (a->n_items > 0) {
+    // Persistent stream: about screen_waves wavefronts in all, spread over
+    // the kv heads (grid y); each walks items w, w+W, ...
+    const uint64_t per_plane = std::max<uint64_t>(1, a->screen_waves / a->kv);
+    const uint64_t bx = std::min<uint64_t>((a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves,
+                                           (per_plane + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves);
+    const dim3 grid(static_cast<unsigned>(std::max<uint64_t>(1, bx)), a->kv);
+    const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
+    const size_t hstride = a->cap_nodes * static_cast<size_t>(H);
+#define GRM_SCREEN(KDT, KS, NTT)                                                              \
+  grm::gqa::gqa_screen_kernel<KDT, KS, NTT><<<grid, threads, 0, a->stream>>>(                 \
+      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                      \
+      static_cast<uint32_t>(a->n_items), p.R, p.Qt, cols, a->d_bfrag, a->d_hms, hstride,      \
+      a->cap_nodes)
+#define GRM_SCREEN_NT(KDT, KS)                 \
+  switch (ntp) {                               \
+    case 1: GRM_SCREEN(KDT, KS, 1); break;     \
+    case 2: GRM_SCREEN(KDT, KS, 2); break;     \
+    default: GRM_SCREEN(KDT, KS, 4); break;    \
+  }
+#define GRM_SCREEN_KS(KDT)                     \
+  switch (p.KS) {                              \
+    case 2: GRM_SCREEN_NT(KDT, 2); break;      \
+    case 4: GRM_SCREEN_NT(KDT, 4); break;      \
+    default: GRM_SCREEN_NT(KDT, 8); break;     \
+  }
+    switch (a->key_dtype) {
+      case kBF16: GRM_SCREEN_KS(kBF16); break;
+      case kF16: GRM_SCREEN_KS(kF16); break;
+      default: GRM_SCREEN_KS(kI8); break;
+    }
+#undef GRM_SCREEN_KS
+#undef GRM_SCREEN_NT
+#undef GRM_SCREEN
+    GRM_HIP_CHECK(hipGetLastError());
+  }
+  // 3. select, 4. shortlist + certificate
+  const float inv_scale = static_cast<float>(1.0 / (H * sqrt(static_cast<double>(a->hd))));
+  const float slack_rel = static_cast<float>((H + 8) * ldexp(1.0, -22));
+  grm::gqa::gqa_select_kernel<<<dim3(nblk, qb), per_block, 0, a->stream>>>(
+      a->d_hms, a->cap_nodes * static_cast<size_t>(H), a->cap_nodes, H, n_slots, a->d_len,
+      a->d_flags, a->d_ids,
+      reinterpret_cast<const float*>(a->d_kmax), a->d_coef, inv_scale, slack_rel, mU, topk,
+      a->d_bu, a->d_bl);
+  GRM_HIP_CHECK(hipGetLastError());
+  unsigned* out_flags = static_cast<unsigned*>(a->qstate.dev) + q0;
+  unsigned* out_status = static_cast<unsigned*>(a->qstate.dev) + q_total + q0;
+  grm::gqa::gqa_shortlist_kernel<<<qb, per_block, 0, a->stream>>>(
+      a->d_bu, a->d_bl, nblk, mU, topk, M, a->d_shortlist, a->d_qflags, out_flags, out_status);
+  GRM_HIP_CHECK(hipGetLastError());
+  // 5. exact rescore of the shortlist, 6. exact scores out
+  const int rq_pad = rq_pad_of(p.R * p.Qt);
+  const uint32_t max_chunks = std::max<uint32_t>(1, (a->max_len + grm::kWave - 1) / grm::kWave);
+  const uint64_t units = static_cast<uint64_t>(qb) * M * max_chunks;
+  const dim3 rgrid(static_cast<unsigned>((units + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves), a->kv);
+  const size_t lds = static_cast<size_t>(grm::gqa::kUnitWaves) * rq_pad * a->hd * sizeof(double);
+  const double denom = sqrt(static_cast<double>(a->hd));
+  const size_t q_elems = static_cast<size_t>(H) * p.Qt * a->hd;
+#define GRM_RESCORE(KDT, RQ)                                                                  \
+  grm::gqa::gqa_rescore_kernel<KDT, RQ><<<rgrid, grm::gqa::kUnitWaves * grm::kWave, lds, a->stream>>>( \
+      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_tok_off, a->d_len,           \
+      a->d_shortlist, M, qb, max_chunks, kv, static_cast<int>(a->hd), p.R, p.Qt, qptr,          \
+      q_dtype, q_elems, denom, a->d_hex)
+#define GRM_RESCORE_RQ(KDT)                     \
+  switch (rq_pad) {                             \
+    case 1: GRM_RESCORE(KDT, 1); break;         \
+    case 2: GRM_RESCORE(KDT, 2); break;         \
+    case 4: GRM_RESCORE(KDT, 4); break;         \
+    case 8: GRM_RESCORE(KDT, 8); break;         \
+    case 16: GRM_RESCORE(KDT, 16); break;       \
+    default: GRM_RESCORE(KDT, 32); break;       \
+  }
+  switch (a->key_dtype) {
+    case kBF16: GRM_RESCORE_RQ(kBF16); break;
+    case kF16: GRM_RESCORE_RQ(kF16); break;
+    default: GRM_RESCORE_RQ(kI8); break;
+  }
+#undef GRM_RESCORE_RQ
+#undef GRM_RESCORE
+  GRM_HIP_CHECK(hipGetLastError());
+  const uint32_t total = static_cast<uint32_t>(qb) * M;
+  grm::gqa::gqa_rescore_finalize_kernel<<<(total + 255) / 256, 256, 0, a->stream>>>(
+      a->d_hex, H, a->d_shortlist, total, a->d_len, a->d_ids,
+      a->short_out.dev + static_cast<size_t>(q0) * M);
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
 int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_device, int q_count,
                int H, int Qt, int warmup, int topk, uint64_t* out_ids, float* out_scores,
                float* elapsed_ms) {
@@ -766,24 +735,13 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   }
   const int R = H / static_cast<int>(a->kv);
   if (R * Qt > grm::gqa::kMaxRQ) return grm::fail(-1, "(heads / kv_heads) * query_tokens above 32");
-  int rq_pad = 1;
-  while (rq_pad < R * Qt) rq_pad *= 2;
-  if (static_cast<size_t>(grm::gqa::kUnitWaves) * rq_pad * a->hd * sizeof(double) > 65536) {
+  if (static_cast<size_t>(rq_pad_of(R * Qt)) * a->hd * sizeof(double) * grm::gqa::kUnitWaves > 65536) {
     return grm::fail(-1, "(heads / kv_heads) * query_tokens * head_dim above 2048");
   }
   GRM_HIP_CHECK(hipSetDevice(a->device));
   if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
   GRM_CHECK_RC(ensure_items(a));
-  if (a->hmax_heads != H || a->d_hmax_count < a->cap_nodes * static_cast<size_t>(H)) {
-    GRM_CHECK_RC(reserve_device(&a->d_hmax, &a->d_hmax_count, a->cap_nodes * static_cast<size_t>(H)));
-    GRM_HIP_CHECK(hipMemsetAsync(a->d_hmax, 0, a->d_hmax_count * sizeof(unsigned long long), a->stream));
-    a->hmax_heads = H;
-  }
-  const uint32_t n_slots = static_cast<uint32_t>(a->high_water);
-  const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
-  const uint32_t fin_blocks = std::max<uint32_t>(1, std::min<uint32_t>((n_slots + per_block - 1) / per_block, a->fin_blocks));
-  const size_t per_q = static_cast<size_t>(fin_blocks) * topk;
-  GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * q_count));
+  a->routes += 1;
   const size_t qvals = static_cast<size_t>(H) * Qt * a->hd;
   const size_t qstride = qvals * (q_dtype == kF32 ? 4 : 2);
   const unsigned char* qbase = static_cast<const unsigned char*>(queries);
@@ -793,31 +751,75 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
     GRM_HIP_CHECK(hipMemcpyAsync(a->d_queries, queries, qstride * q_count, hipMemcpyHostToDevice, a->stream));
     qbase = static_cast<const unsigned char*>(a->d_queries);
   }
-  for (int qi = 0; qi < q_count; ++qi) {
-    if (qi == warmup) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
-    const void* q = qbase + qi * qstride;
-    GRM_CHECK_RC(launch_exact(a, q, q_dtype, H, Qt, rq_pad));
-    grm::gqa::gqa_finalize_kernel<<<fin_blocks, per_block, 0, a->stream>>>(
-        a->d_hmax, H, n_slots, a->d_len, a->d_flags, a->d_ids, a->d_qbad, topk,
-        a->blocks_out.dev + static_cast<size_t>(qi) * per_q);
-    GRM_HIP_CHECK(hipGetLastError());
-    grm::gqa::gqa_clear_flag_kernel<<<1, 1, 0, a->stream>>>(a->d_qbad);
-    GRM_HIP_CHECK(hipGetLastError());
-  }
-  GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
-  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
-  if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
+  const uint32_t n_slots = static_cast<uint32_t>(a->high_water);
+  const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
+  const uint32_t fin_blocks = std::max<uint32_t>(1, std::min<uint32_t>((n_slots + per_block - 1) / per_block, a->fin_blocks));
+  const size_t per_q = static_cast<size_t>(fin_blocks) * topk;
   a->merged.resize(topk);
-  for (int qi = 0; qi < q_count; ++qi) {
-    grm::host_topk_merge(a->blocks_out.host + static_cast<size_t>(qi) * per_q, per_q, topk,
-                         a->merged.data());
-    for (int j = 0; j < topk; ++j) {
-      const Cand& c = a->merged[j];
-      const bool ok = isfinite(c.score) && c.id != kNoId;
-      out_ids[static_cast<size_t>(qi) * topk + j] = ok ? c.id : kNoId;
-      if (out_scores) out_scores[static_cast<size_t>(qi) * topk + j] = ok ? c.score : __builtin_nanf("");
+  ScreenPlan plan;
+  const bool use_screen = screen_plan(a, H, Qt, topk, &plan);
+  std::vector<int> redo;
+  if (use_screen) {
+    GRM_CHECK_RC(grm::reserve_mapped(&a->short_out, static_cast<size_t>(q_count) * plan.M));
+    GRM_CHECK_RC(grm::reserve_mapped_bytes(&a->qstate, static_cast<size_t>(q_count) * 2 * sizeof(unsigned)));
+    // untimed warmup queries first, then the timed ones
+    int q0 = 0;
+    const int segments[2][2] = {{0, warmup}, {warmup, q_count}};
+    for (const auto& seg : segments) {
+      if (seg[0] == warmup) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+      for (q0 = seg[0]; q0 < seg[1]; q0 += plan.qb_max) {
+        const int qb = std::min(plan.qb_max, seg[1] - q0);
+        GRM_CHECK_RC(enqueue_screen(a, plan, qbase, qstride, q_dtype, q0, qb, q_count, topk));
+      }
+    }
+    GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
+    GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+    const unsigned* st = static_cast<const unsigned*>(a->qstate.host);
+    for (int qi = 0; qi < q_count; ++qi) {
+      const unsigned flags = st[qi], certified = st[q_count + qi];
+      if (flags != 0u || certified != 1u) {
+        redo.push_back(qi);
+        continue;
+      }
+      grm::host_topk_merge(a->short_out.host + static_cast<size_t>(qi) * plan.M, plan.M, topk,
+                           a->merged.data());
+      write_result(a->merged.data(), topk, out_ids + static_cast<size_t>(qi) * topk,
+                   out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
+    }
+    a->fallbacks += redo.size();
+  } else {
+    for (int qi = 0; qi < q_count; ++qi) redo.push_back(qi);
+  }
+  if (!redo.empty()) {
+    GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * redo.size()));
+    if (!use_screen) {
+      if (warmup > 0) {
+        for (int qi = 0; qi < warmup; ++qi) {
+          GRM_CHECK_RC(enqueue_exact(a, qbase + qi * qstride, q_dtype, H, Qt, topk, fin_blocks,
+                                     a->blocks_out.dev + static_cast<size_t>(qi) * per_q));
+        }
+      }
+      GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+      for (int qi = warmup; qi < q_count; ++qi) {
+        GRM_CHECK_RC(enqueue_exact(a, qbase + qi * qstride, q_dtype, H, Qt, topk, fin_blocks,
+                                   a->blocks_out.dev + static_cast<size_t>(qi) * per_q));
+      }
+      GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
+    } else {
+      for (size_t j = 0; j < redo.size(); ++j) {
+        GRM_CHECK_RC(enqueue_exact(a, qbase + redo[j] * qstride, q_dtype, H, Qt, topk, fin_blocks,
+                                   a->blocks_out.dev + j * per_q));
+      }
+    }
+    GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+    for (size_t j = 0; j < redo.size(); ++j) {
+      const int qi = redo[j];
+      grm::host_topk_merge(a->blocks_out.host + j * per_q, per_q, topk, a->merged.data());
+      write_result(a->merged.data(), topk, out_ids + static_cast<size_t>(qi) * topk,
+                   out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
     }
   }
+  if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
   grm::clear_error();
   return 0;
 }

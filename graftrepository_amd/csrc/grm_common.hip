@@ -64,6 +64,31 @@ int reserve_mapped(MappedCands* m, size_t count) {
   return 0;
 }
 
+int reserve_mapped_bytes(MappedBuf* m, size_t bytes) {
+  if (bytes <= m->bytes && m->host) return 0;
+  release_mapped_bytes(m);
+  void* h = nullptr;
+  GRM_HIP_CHECK(hipHostMalloc(&h, bytes ? bytes : 1,
+                              hipHostMallocMapped | hipHostMallocCoherent));
+  void* d = nullptr;
+  hipError_t rc = hipHostGetDevicePointer(&d, h, 0);
+  if (rc != hipSuccess) {
+    (void)hipHostFree(h);
+    return fail_hip(rc, "hipHostGetDevicePointer");
+  }
+  m->host = h;
+  m->dev = d;
+  m->bytes = bytes;
+  return 0;
+}
+
+void release_mapped_bytes(MappedBuf* m) {
+  if (m->host) (void)hipHostFree(m->host);
+  m->host = nullptr;
+  m->dev = nullptr;
+  m->bytes = 0;
+}
+
 void release_mapped(MappedCands* m) {
   if (m->host) (void)hipHostFree(m->host);
   m->host = nullptr;

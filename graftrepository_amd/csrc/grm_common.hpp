@@ -87,49 +87,68 @@ __device__ inline void wl_init(WaveList& L) {
   L.th_id = kNoId;
 }
 
+// Wave-uniform copies of lane `src` (src must be wave-uniform).
+__device__ inline float lane_f32(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+__device__ inline uint32_t lane_u32(uint32_t v, int src) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), src));
+}
+__device__ inline uint64_t lane_u64(uint64_t v, int src) {
+  const uint32_t lo = lane_u32(static_cast<uint32_t>(v), src);
+  const uint32_t hi = lane_u32(static_cast<uint32_t>(v >> 32), src);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 __device__ inline void wl_refresh(WaveList& L, int k) {
-  L.th_s = __shfl(L.s, k - 1);
-  L.th_id = __shfl(L.id, k - 1);
+  L.th_s = lane_f32(L.s, k - 1);
+  L.th_id = lane_u64(L.id, k - 1);
 }
 
 // Offer one candidate per lane (`valid` lanes only) and keep the best k of
 // list + candidates.  Each iteration extracts the best remaining candidate
-// with a butterfly arg-max and inserts it, so the loop runs at most k times
-// and not at all once no lane beats the bar.
+// (a max-reduction of the scores, then the lowest id among lanes holding
+// that score) and inserts it, so the loop runs at most k times and not at
+// all once no lane beats the bar.
 __device__ inline void wl_consume(WaveList& L, int k, float s, uint64_t id,
                                   uint32_t slot, bool valid) {
   const int lane = __lane_id();
   bool cand = valid && better(s, id, L.th_s, L.th_id);
-  while (__ballot(cand) != 0ull) {
-    float bs = cand ? s : -INFINITY;
-    uint64_t bid = cand ? id : kNoId;
-    uint32_t bslot = slot;
-    int bl = cand ? lane : kWave;
+  uint64_t mask = __ballot(cand);
+  while (mask != 0ull) {
+    int bl;
+    if (__popcll(mask) == 1) {
+      bl = __ffsll(static_cast<long long>(mask)) - 1;
+    } else {
+      float bs = cand ? s : -INFINITY;
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const float os = __shfl_xor(bs, off);
-      const uint64_t oid = __shfl_xor(bid, off);
-      const uint32_t oslot = __shfl_xor(bslot, off);
-      const int ol = __shfl_xor(bl, off);
-      const bool take =
-          better(os, oid, bs, bid) || (os == bs && oid == bid && ol < bl);
-      if (take) {
-        bs = os;
-        bid = oid;
-        bslot = oslot;
-        bl = ol;
+      for (int off = 1; off < kWave; off <<= 1) bs = fmaxf(bs, __shfl_xor(bs, off));
+      const uint64_t tie = __ballot(cand && s == bs);
+      if (__popcll(tie) == 1) {
+        bl = __ffsll(static_cast<long long>(tie)) - 1;
+      } else {
+        uint64_t bid = (cand && s == bs) ? id : kNoId;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+          const uint64_t o = __shfl_xor(bid, off);
+          bid = o < bid ? o : bid;
+        }
+        bl = __ffsll(static_cast<long long>(__ballot(cand && s == bs && id == bid))) - 1;
       }
     }
+    const float ws = lane_f32(s, bl);
+    const uint64_t wid = lane_u64(id, bl);
+    const uint32_t wslot = lane_u32(slot, bl);
     // Entries ahead of the winner form a prefix of the sorted list.
-    const bool ahead = lane < k && better(L.s, L.id, bs, bid);
+    const bool ahead = lane < k && better(L.s, L.id, ws, wid);
     const int pos = __popcll(__ballot(ahead));
     const float ps = __shfl_up(L.s, 1);
     const uint64_t pid = __shfl_up(L.id, 1);
     const uint32_t pslot = __shfl_up(L.slot, 1);
     if (lane == pos) {
-      L.s = bs;
-      L.id = bid;
-      L.slot = bslot;
+      L.s = ws;
+      L.id = wid;
+      L.slot = wslot;
     } else if (lane > pos && lane < k) {
       L.s = ps;
       L.id = pid;
@@ -138,6 +157,7 @@ __device__ inline void wl_consume(WaveList& L, int k, float s, uint64_t id,
     wl_refresh(L, k);
     if (lane == bl) cand = false;
     cand = cand && better(s, id, L.th_s, L.th_id);
+    mask = __ballot(cand);
   }
 }
 
@@ -152,9 +172,8 @@ __device__ inline Cand wl_entry(const WaveList& L) {
 // Merge the per-wave lists of a block (written to `lists[wave][0..k)`) into
 // wave 0's list.  Caller synchronises the block before and reads the result
 // from wave 0 after.
-template <int NW>
-__device__ inline void block_merge(Cand (*lists)[kMaxTopK], int k,
-                                   WaveList& out) {
+template <int NW, int CAP>
+__device__ inline void block_merge(Cand (*lists)[CAP], int k, WaveList& out) {
   const int lane = __lane_id();
   wl_init(out);
   for (int base = 0; base < NW * k; base += kWave) {
@@ -206,13 +225,13 @@ __device__ inline void wl_consume_global(WaveList& L, int k,
 // are merged by topk_merge_kernel, launched next on the same stream; the
 // kernel boundary orders the writes, so no device-scope fence (an L2
 // write-back on gfx950) is paid per block.
-template <int NW>
+template <int NW, int CAP>
 __device__ inline void block_topk_write(WaveList& L, int k,
-                                        Cand (*s_lists)[kMaxTopK],
+                                        Cand (*s_lists)[CAP],
                                         Cand* __restrict__ block_out) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(L);
+  if (lane < CAP) s_lists[wave][lane] = wl_entry(L);
   __syncthreads();
   if (wave == 0) {
     WaveList B;
@@ -226,6 +245,16 @@ constexpr int kMergeWaves = 4;
 // Host side: keep the best k of `count` candidates (tie law above) in out,
 // best first; unfilled entries get score NaN, id kNoId, slot kNoSlot.
 void host_topk_merge(const Cand* in, size_t count, int k, Cand* out);
+
+// Pinned host buffer of raw bytes that the device reads and writes directly
+// (mapped, coherent).
+struct MappedBuf {
+  void* host = nullptr;
+  void* dev = nullptr;
+  size_t bytes = 0;
+};
+int reserve_mapped_bytes(MappedBuf* m, size_t bytes);
+void release_mapped_bytes(MappedBuf* m);
 
 // Pinned host buffer the device writes directly (mapped, coherent): the
 // route kernels leave their per-block results there so the final merge

@@ -199,3 +199,53 @@ def test_ragged_config_parity(hip_lib):
                                   bf16_bits_to_f32(qs).reshape(qs.shape),
                                   cfg["topk"])
     assert_same(res, ids, sc)
+
+
+@pytest.mark.parametrize("Qt", [1, 4])
+def test_screen_path_matches_exact_path(hip_lib, monkeypatch, Qt):
+    lens = wl.gqa_lengths(400, seed=31, lo=1, hi=300)
+    keys, offs = wl.gqa_bank(lens, 16, 128, seed=31, dtype="bf16")
+    qs = wl.gqa_queries(20, 64, Qt, 128, seed=31, dtype="bf16")  # 2 screen batches
+    results = {}
+    for screen in ("1", "0"):
+        monkeypatch.setenv("GRM_HIP_GQA_SCREEN", screen)
+        with GqaNodeBank(keys, offs, kv_heads=16, head_dim=128,
+                         dtype="bf16") as bank:
+            results[screen] = bank.route(qs, 5, query_dtype="bf16", warmup=3)
+    ids, sc, _ = oracle.gqa_route(keys, oracle.BF16, offs, 16, 128,
+                                  bf16_bits_to_f32(qs).reshape(qs.shape), 5)
+    for r in results.values():
+        assert_same(r, ids, sc)
+
+
+def test_tied_nodes_fall_back_to_exact_path(hip_lib):
+    # 100 identical nodes tie exactly: no shortlist of 16 can be certified,
+    # so the query is re-routed on the exact path; ties go to the lowest id.
+    rng = np.random.default_rng(8)
+    block = rng.standard_normal(8 * 40 * 64).astype(np.float32)
+    others = rng.standard_normal(8 * 40 * 64 * 5).astype(np.float32) * 0.1
+    keys = np.concatenate([np.tile(block, 100), others])
+    offs = np.arange(106, dtype=np.uint64) * 40
+    ids = (np.arange(105, dtype=np.uint64)[::-1] + 7).copy()
+    q = rng.standard_normal((1, 16, 1, 64)).astype(np.float32)
+    with GqaNodeBank(keys, offs, kv_heads=8, head_dim=64, dtype="bf16",
+                     node_ids=ids) as bank:
+        res = bank.route(q, 10)
+    want, wsc, _ = oracle.gqa_route(oracle.bf16_bits(keys), oracle.BF16, offs,
+                                    8, 64, q, 10, node_ids=ids)
+    assert_same(res, want, wsc)
+    assert res.ids[0].tolist() == sorted(ids[:100].tolist())[:10]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_f32_queries_on_half_banks(hip_lib, dtype):
+    # fp32 query values are converted for the matrix cores; the bound covers
+    # the conversion and the exact rescore uses the fp32 values.
+    lens = wl.gqa_lengths(200, seed=41, lo=8, hi=128)
+    keys, offs = wl.gqa_bank(lens, 8, 64, seed=41, dtype=dtype)
+    qs = wl.gqa_queries(3, 32, 2, 64, seed=41, dtype="f32")
+    with GqaNodeBank(keys, offs, kv_heads=8, head_dim=64, dtype=dtype) as bank:
+        res = bank.route(qs, 4)
+    code = oracle.BF16 if dtype == "bf16" else oracle.F16
+    ids, sc, _ = oracle.gqa_route(keys, code, offs, 8, 64, qs, 4)
+    assert_same(res, ids, sc)
