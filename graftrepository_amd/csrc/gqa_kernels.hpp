@@ -8,16 +8,19 @@
 // A node with zero key tokens scores 0.0; any non-finite query or key value
 // makes the score NaN (never ranked).
 //
-// Two kernel families:
-//  * exact  -- the law itself in fp64, one lane per key token, d in order;
-//              per-(node, head) maxima combine with a 64-bit atomicMax on
-//              the bit pattern (non-negative doubles order like their bits,
-//              so the result does not depend on scheduling);
-//  * screen -- |q.k| for every key token on the matrix cores (bf16 or fp16
-//              MFMA 16x16x32, fp32 accumulate), reduced to a screened node
-//              score with a rigorous error bound; a select/shortlist pass
-//              keeps the nodes that can still reach the top-k and certifies
-//              the shortlist; the exact family then rescores only those.
+// Two kernel families produce the per-(node, head) maxima best_h, both
+// exactly as the law defines them; the maxima combine with a 64-bit
+// atomicMax on the bit pattern (non-negative doubles order like their
+// bits, so the result does not depend on scheduling):
+//  * exact           -- the law itself in fp64 for every key token, one
+//                       lane per token, d in order (fp32 banks, other
+//                       head sizes);
+//  * screen + refine -- |q.k| for every key token on the matrix cores (bf16
+//                       or fp16 MFMA 16x16x32, fp32 accumulate) with a
+//                       rigorous error bound; only the tokens the bound
+//                       cannot exclude from a maximum are recomputed in the
+//                       law's fp64 order.
+// A finalize kernel sums the maxima over heads in order.
 #pragma once
 
 #include "grm_common.hpp"
@@ -32,17 +35,28 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kUnitWaves = 4;     // wavefronts per exact/stats/screen block
-constexpr int kFinWaves = 4;      // wavefronts per finalize/select block
+constexpr int kUnitWaves = 4;     // wavefronts per work-item block
+constexpr int kFinWaves = 4;      // wavefronts per finalize block
 constexpr int kMaxRQ = 32;        // R * Qt supported by the exact kernels
-constexpr int kMaxShort = 64;     // shortlist capacity + 1 (one wave list)
 constexpr uint32_t kMaxHeadDim = 512;
 
-constexpr int kRowBatch = 8;      // 16-byte chunks of a key row loaded at once
+// Key chunk planes.  The block of (slot, kv head g) -- the slot's key
+// tokens of head_dim values, in L rows (the token count rounded up to
+// kTokAlign) -- is stored as C = head_dim / epc planes of L 16-byte chunks
+// (epc values each): chunk c of token t is chunk index row0 * C + c * L + t
+// of the key arena, with row0 = tok_off * kv + g * L.  INT8 scales follow
+// the same rule per group: scale of group j of token t is element
+// row0 * G + j * L + t (G = head_dim / group_size).  A wave that gives one
+// token to each lane reads 64 consecutive chunks -- 1 KiB -- per load
+// instruction; every run of kTokAlign tokens starts a 128-byte line, so no
+// two streams share a line; a slot's blocks stay contiguous
+// (tok_off * kv * head_dim values), so whole nodes move as one copy.  Rows
+// past the token count are never read.
+constexpr uint32_t kTokAlign = 8;
 
 // Work item: `count` consecutive key tokens, from t0, of one slot (all kv
-// heads).  Token t of kv head g is key row base + g*len + t (rows of
-// head_dim values).
+// heads).  `base` = tok_off[slot] * kv, so row0 of kv head g is
+// base + g * len, `len` being the slot's padded row count.
 struct Item {
   uint64_t base;  // tok_off[slot] * kv
   uint32_t slot;
@@ -71,11 +85,10 @@ struct KeyTraits {
   static constexpr int kEpc = 16 / kEsize;  // elements per 16-byte chunk
 };
 
-// Decode one 16-byte chunk of a key row into floats (law-level values).
+// Decode one 16-byte chunk into floats (law-level values); `scale` is the
+// chunk's INT8 group scale (ignored for the other types).
 template <int KDT>
-__device__ inline void decode_chunk(u32x4 v, const unsigned char* __restrict__ scales,
-                                    int scale_dtype, uint64_t scale_idx,
-                                    float* out) {
+__device__ inline void decode_chunk(u32x4 v, float scale, float* out) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   if constexpr (KDT == kF32) {
 #pragma unroll
@@ -93,13 +106,12 @@ __device__ inline void decode_chunk(u32x4 v, const unsigned char* __restrict__ s
       out[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(w[i] >> 16)));
     }
   } else {
-    const float s = load_scale(scales, scale_dtype, scale_idx);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int code = static_cast<int>(static_cast<int8_t>((w[i] >> (8 * b)) & 0xffu));
-        out[4 * i + b] = static_cast<float>(dequant_i8(code, s));
+        out[4 * i + b] = static_cast<float>(dequant_i8(code, scale));
       }
     }
   }
@@ -107,195 +119,301 @@ __device__ inline void decode_chunk(u32x4 v, const unsigned char* __restrict__ s
 
 // ----------------------------------------------------------------- exact
 
-// Stage the R*Qt query rows of kv head g (rows >= R*Qt are zero) as doubles.
-// Returns true when this lane saw a non-finite value.
-__device__ inline bool stage_group_query(double* __restrict__ q, int RQ,
-                                         const void* __restrict__ query,
-                                         int q_dtype, int g, int R, int Qt,
-                                         int hd, bool active, int lane,
-                                         int nthreads) {
+// Query rows as doubles for the exact kernels: q64[((qb * kv + g) * hd + d)
+// * RQP + j] = q[qb][g*R + j/Qt][j%Qt][d] for j < R*Qt, 0 for the padding
+// rows j < RQP.  The d-major order lets a wave read the RQP values of one
+// d as one wave-uniform (scalar) load.  qflags[qb * kv + g] = 1 when a
+// value of query qb read by kv head g is non-finite, else 0.  grid (kv, Qb).
+__global__ __launch_bounds__(256) void gqa_q64_kernel(
+    const void* __restrict__ query, int q_dtype, size_t q_elems, int Qt,
+    int hd, int kv, int R, int RQP, double* __restrict__ q64,
+    unsigned* __restrict__ qflags) {
+  const int g = blockIdx.x;
+  const int qb = blockIdx.y;
+  const int rq = R * Qt;
   bool bad = false;
-  const int rq_used = R * Qt;
-  for (int i = lane; i < RQ * hd; i += nthreads) {
-    const int rq = i / hd;
-    const int d = i - rq * hd;
+  for (int idx = threadIdx.x; idx < RQP * hd; idx += blockDim.x) {
+    const int d = idx / RQP;
+    const int j = idx - d * RQP;
     double v = 0.0;
-    if (active && rq < rq_used) {
-      const int r = rq / Qt;
-      const int qi = rq - r * Qt;
-      const uint64_t src = (static_cast<uint64_t>(g * R + r) * Qt + qi) * hd + d;
+    if (j < rq) {
+      const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
+                           (static_cast<uint64_t>(g * R + j / Qt) * Qt + j % Qt) * hd + d;
       const float f = q_dtype == kBF16
                           ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
                           : static_cast<const float*>(query)[src];
       bad = bad || !isfinite(f);
       v = static_cast<double>(f);
     }
-    q[i] = v;
+    q64[(static_cast<size_t>(qb * kv + g) * hd + d) * RQP + idx % RQP] = v;
   }
-  return bad;
+  bad = __syncthreads_or(bad);
+  if (threadIdx.x == 0) qflags[qb * kv + g] = bad ? 1u : 0u;
 }
 
-// Exact maxima of one (slot, kv head g, token range): lane t walks tokens
-// t0+lane, t0+lane+64, ...; for every query row the dot product runs in the
-// law's d order in fp64.  Folds max|dot|/denom per query head r into
-// target[(g*R + r) * tstride] (double bits, atomicMax).  row0 = key row of
-// token 0 of (slot, g).  Row chunks load kRowBatch at a time.
+// Chunks per stage of the pipelined exact kernel (two stages live in
+// registers): at most 8, and at most 64 (RQ <= 8) or 32 decoded values.
 template <int KDT, int RQ>
-__device__ inline void exact_unit(const unsigned char* __restrict__ keys,
-                                  const unsigned char* __restrict__ scales,
-                                  int scale_dtype, int group_size,
-                                  uint64_t row0, uint32_t t0, uint32_t count,
-                                  const double* __restrict__ q, int g, int R,
-                                  int Qt, int hd, double denom,
-                                  unsigned long long* __restrict__ target,
-                                  size_t tstride) {
+constexpr int exact_stage_chunks() {
+  constexpr int epc = KeyTraits<KDT>::kEpc;
+  constexpr int cap = (RQ <= 8 ? 64 : 32) / epc;
+  return cap < 1 ? 1 : (cap > 8 ? 8 : cap);
+}
+
+// Exact maxima for every (kv head, item) pair against one query (q64 of
+// gqa_q64_kernel, query 0), as a software pipeline: wavefront w of W walks
+// pairs p = w, w+W, ... (p = g * n_items + item, so neighbouring waves
+// share a kv head and its query rows stay in the scalar cache) as one
+// stream of stages -- NB chunks of one 64-token tile -- and loads the next
+// stage while it folds the current one, so every wave keeps HBM reads in
+// flight while its fp64 work runs.  Lane l owns token t+l of the tile; a
+// stage's chunks are the law's d order, so the dot products stay
+// sequential in d.  hmax is head-major: hmax[h * cap + slot].
+template <int KDT, int RQ, int NB>
+__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
+    const unsigned char* __restrict__ keys,
+    const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
+    const Item* __restrict__ items, uint32_t n_items, int kv, int hd, int R,
+    int Qt, const double* __restrict__ q64, double denom,
+    unsigned long long* __restrict__ hmax, size_t cap) {
   using T = KeyTraits<KDT>;
   const int lane = threadIdx.x & (kWave - 1);
-  const int rq_used = R * Qt;
-  const int nch = hd / T::kEpc;
-  double best[RQ];
+  const uint32_t W = gridDim.x * kUnitWaves;
+  const uint32_t n_pairs = n_items * static_cast<uint32_t>(kv);
+  uint32_t p_cur = blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  if (p_cur >= n_pairs) return;
+  const int C = hd / T::kEpc;
+  const int nb = (C + NB - 1) / NB;  // stages per tile
+  const int G = KDT == kI8 ? hd / group_size : 1;
+  const int cpg = KDT == kI8 ? group_size / T::kEpc : 1;
+  const int ses = scale_dtype == kF16 ? 2 : 4;
+
+  // Loads are unconditional (no branch around them, so the compiler can
+  // count outstanding loads instead of draining them): lanes past the
+  // item's end read its last token and chunks past C read chunk C-1; those
+  // values are never folded (see `fold` and the tile end).
+  auto load = [&](u32x4 (&v)[NB], float (&sc)[NB], const Item& it, int g, uint32_t t, int b) {
+    const uint64_t row0 = it.base + static_cast<uint64_t>(g) * it.len;
+    const uint32_t tl = min(t + lane, it.t0 + it.count - 1);
+    const u32x4* kp = reinterpret_cast<const u32x4*>(keys) + row0 * C + tl;
 #pragma unroll
-  for (int j = 0; j < RQ; ++j) best[j] = 0.0;
-  const int groups = KDT == kI8 ? hd / group_size : 1;
-  for (uint32_t t = t0 + lane; t < t0 + count; t += kWave) {
-    double acc[RQ];
-#pragma unroll
-    for (int j = 0; j < RQ; ++j) acc[j] = 0.0;
-    const uint64_t row = row0 + t;
-    const u32x4* p = reinterpret_cast<const u32x4*>(keys + row * hd * T::kEsize);
-    for (int c0 = 0; c0 < nch; c0 += kRowBatch) {
-      u32x4 v[kRowBatch];
-#pragma unroll
-      for (int b = 0; b < kRowBatch; ++b) {
-        if (c0 + b < nch) v[b] = p[c0 + b];
+    for (int j = 0; j < NB; ++j) {
+      const int c = min(b * NB + j, C - 1);
+      v[j] = __builtin_nontemporal_load(kp + static_cast<uint64_t>(c) * it.len);
+      sc[j] = 0.0f;
+      if constexpr (KDT == kI8) {
+        sc[j] = load_scale(scales + (row0 * G + tl) * ses, scale_dtype,
+                           static_cast<uint64_t>(c / cpg) * it.len);
       }
+    }
+  };
+  double acc[RQ], best[RQ];
 #pragma unroll
-      for (int b = 0; b < kRowBatch; ++b) {
-        if (c0 + b >= nch) break;
+  for (int j = 0; j < RQ; ++j) {
+    acc[j] = 0.0;
+    best[j] = 0.0;
+  }
+  auto fold = [&](const u32x4 (&v)[NB], const float (&sc)[NB], int g, int b) {
+    const double* __restrict__ qg = q64 + static_cast<size_t>(g) * hd * RQ;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int c = b * NB + j;
+      if (c < C) {
         float f[T::kEpc];
-        const int e0 = (c0 + b) * T::kEpc;
-        decode_chunk<KDT>(v[b], scales, scale_dtype,
-                          KDT == kI8 ? row * groups + e0 / group_size : 0, f);
+        decode_chunk<KDT>(v[j], sc[j], f);
+        const double* qc = qg + static_cast<size_t>(c) * T::kEpc * RQ;
 #pragma unroll
         for (int e = 0; e < T::kEpc; ++e) {
           const double kd = static_cast<double>(f[e]);
 #pragma unroll
-          for (int j = 0; j < RQ; ++j) acc[j] = fma(kd, q[j * hd + e0 + e], acc[j]);
+          for (int r = 0; r < RQ; ++r) acc[r] = fma(kd, qc[e * RQ + r], acc[r]);
         }
       }
     }
+  };
+  auto emit = [&](const Item& it, int g) {
+    const int rq_used = R * Qt;
+    for (int r = 0; r < R; ++r) {
+      double m = 0.0;
 #pragma unroll
-    for (int j = 0; j < RQ; ++j) {
-      const double v = fabs(acc[j]);
-      best[j] = (v > best[j] || isnan(v)) ? v : best[j];
-    }
-  }
-  // Division by the positive constant sqrt(hd) is monotone under rounding to
-  // nearest, so max(|dot|)/denom equals the law's max(|dot|/denom).
-  for (int r = 0; r < R; ++r) {
-    double m = 0.0;
+      for (int j = 0; j < RQ; ++j) {
+        if (j / Qt == r && j < rq_used) m = (best[j] > m || isnan(best[j])) ? best[j] : m;
+      }
+      // max(|dot|)/denom equals the law's max(|dot|/denom): division by a
+      // positive constant is monotone under rounding to nearest
+      unsigned long long bits = __double_as_longlong(m / denom);
 #pragma unroll
-    for (int j = 0; j < RQ; ++j) {
-      if (j / Qt == r && j < rq_used) m = (best[j] > m || isnan(best[j])) ? best[j] : m;
+      for (int off = 1; off < kWave; off <<= 1) {
+        const unsigned long long o = __shfl_xor(bits, off);
+        bits = o > bits ? o : bits;
+      }
+      if (lane == 0) atomicMax(hmax + static_cast<size_t>(g * R + r) * cap + it.slot, bits);
     }
-    unsigned long long bits = __double_as_longlong(m / denom);
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const unsigned long long o = __shfl_xor(bits, off);
-      bits = o > bits ? o : bits;
-    }
-    if (lane == 0) atomicMax(target + static_cast<size_t>(g * R + r) * tstride, bits);
-  }
-}
+    for (int j = 0; j < RQ; ++j) best[j] = 0.0;
+  };
 
-// Exact maxima for every item; grid (ceil(items / 4), kv heads).  All
-// waves of a block share kv head blockIdx.y and its staged query rows.
-// hmax is head-major: hmax[h * cap + slot].
-template <int KDT, int RQ>
-__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_heads_kernel(
-    const unsigned char* __restrict__ keys,
-    const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
-    const Item* __restrict__ items, uint32_t n_items, int hd, int R, int Qt,
-    const void* __restrict__ query, int q_dtype, double denom,
-    unsigned long long* __restrict__ hmax, size_t cap,
-    unsigned* __restrict__ qbad) {
-  extern __shared__ double qs[];  // [RQ][hd]
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int g = blockIdx.y;
-  const uint32_t item_i = blockIdx.x * kUnitWaves + wave;
-  const bool bad = stage_group_query(qs, RQ, query, q_dtype, g, R, Qt, hd,
-                                     true, threadIdx.x, blockDim.x);
-  if (__ballot(bad) != 0ull && lane == 0) atomicOr(qbad, 1u);
-  __syncthreads();
-  if (item_i >= n_items) return;
-  const Item it = items[item_i];
-  exact_unit<KDT, RQ>(keys, scales, scale_dtype, group_size,
-                      it.base + static_cast<uint64_t>(g) * it.len, it.t0, it.count,
-                      qs, g, R, Qt, hd, denom, hmax + it.slot, cap);
+  int g_cur = static_cast<int>(p_cur / n_items);
+  Item cur = items[p_cur - static_cast<uint32_t>(g_cur) * n_items];
+  uint32_t p_nxt = p_cur + W;
+  int g_nxt = static_cast<int>(min(p_nxt, n_pairs - 1) / n_items);
+  Item nxt = items[min(p_nxt, n_pairs - 1) - static_cast<uint32_t>(g_nxt) * n_items];
+  uint32_t t = cur.t0;
+  int b = 0;
+  u32x4 v0[NB], v1[NB];
+  float s0[NB], s1[NB];
+  load(v0, s0, cur, g_cur, t, 0);
+  // One stage: fold `now` while the next stage loads into `later` (the
+  // stream's last stage reloads itself, harmlessly, to keep the load
+  // unconditional).  Returns false when the wave's stream is exhausted.
+  auto step = [&](u32x4 (&now)[NB], float (&snow)[NB], u32x4 (&later)[NB],
+                  float (&slater)[NB]) -> bool {
+    const bool last_b = b + 1 == nb;
+    const bool last_t = t + kWave >= cur.t0 + cur.count;
+    const bool item_end = last_b && last_t;
+    const bool more = !item_end || p_nxt < n_pairs;
+    const bool jump = item_end && more;
+    const Item& nit = jump ? nxt : cur;
+    const int ng = jump ? g_nxt : g_cur;
+    const uint32_t nt = !more ? t : (item_end ? nxt.t0 : (last_b ? t + kWave : t));
+    const int nbb = (!more || !last_b) ? (more ? b + 1 : b) : 0;
+    load(later, slater, nit, ng, nt, nbb);
+    fold(now, snow, g_cur, b);
+    if (!last_b) {
+      ++b;
+      return true;
+    }
+    // tile done: fold |dot| of the lane's token (if inside the item) into
+    // the item maxima
+    const bool in_item = t + lane < cur.t0 + cur.count;
+#pragma unroll
+    for (int j = 0; j < RQ; ++j) {
+      const double a = fabs(acc[j]);
+      if (in_item) best[j] = (a > best[j] || isnan(a)) ? a : best[j];
+      acc[j] = 0.0;
+    }
+    b = 0;
+    if (!last_t) {
+      t += kWave;
+      return true;
+    }
+    emit(cur, g_cur);
+    if (p_nxt >= n_pairs) return false;
+    p_cur = p_nxt;
+    g_cur = g_nxt;
+    cur = nxt;
+    t = cur.t0;
+    p_nxt = p_cur + W;
+    g_nxt = static_cast<int>(min(p_nxt, n_pairs - 1) / n_items);
+    nxt = items[min(p_nxt, n_pairs - 1) - static_cast<uint32_t>(g_nxt) * n_items];
+    return true;
+  };
+  while (step(v0, s0, v1, s1) && step(v1, s1, v0, s0)) {
+  }
 }
 
 // Exact scores of every live slot from the head-major maxima (h in order,
-// fp64); each block writes its k best entries (block_topk_write).
-// Re-zeroes the maxima it read.
+// fp64); grid (blocks, queries), grid-stride over groups of 64 slots.
+// Query qb's maxima are hmax[qb*hstride + h*cap + slot].  All waves of the
+// block stage the group's maxima in LDS -- every load of a group is in
+// flight at once, since the atomics that produced them leave them outside
+// the cache -- and re-zero them; wave 0 sums each slot's heads in order,
+// keeps the block's k best and writes them to
+// block_out[(qb*gridDim.x + blockIdx.x)*k ..).  qbad[qb*kv + g] are the
+// query's non-finite flags.
+constexpr int kFinSlots = 64;    // slots per finalize group (one per lane)
+constexpr int kFinHeads = 128;   // heads staged per pass
+
 __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
-    unsigned long long* __restrict__ hmax, size_t cap, int H, uint32_t n_slots,
+    unsigned long long* __restrict__ hmax, size_t hstride, size_t cap, int H, uint32_t n_slots,
     const uint32_t* __restrict__ lens, const uint32_t* __restrict__ flags,
-    const uint64_t* __restrict__ ids, const unsigned* __restrict__ qbad, int k,
-    Cand* __restrict__ block_out) {
-  constexpr int kHB = 16;  // head maxima loaded at once
-  __shared__ Cand s_lists[kFinWaves][kMaxTopK];
+    const uint64_t* __restrict__ ids, const unsigned* __restrict__ qbad, int kv,
+    int k, Cand* __restrict__ block_out) {
+  __shared__ double s_h[kFinHeads][kFinSlots];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const bool q_bad = *qbad != 0u;
+  const int qb = blockIdx.y;
+  hmax += qb * hstride;
+  bool q_bad = false;
+  for (int g0 = 0; g0 < kv; g0 += kWave) {  // one vector load per 64 heads
+    const bool b = g0 + lane < kv && qbad[qb * kv + g0 + lane] != 0u;
+    q_bad = q_bad || __ballot(b) != 0ull;
+  }
   WaveList L;
   wl_init(L);
-  const uint32_t stride = gridDim.x * blockDim.x;
-  for (uint32_t base = blockIdx.x * blockDim.x + wave * kWave; base < n_slots;
-       base += stride) {
+  for (uint32_t base = blockIdx.x * kFinSlots; base < n_slots; base += gridDim.x * kFinSlots) {
     const uint32_t slot = base + lane;
     const bool in = slot < n_slots;
-    const uint32_t f = in ? flags[slot] : 0u;
-    const uint32_t len = in ? lens[slot] : 0u;
-    const bool scored = (f & 1u) && len > 0;
+    uint32_t f = 0u, len = 0u;
+    if (wave == 0 && in) {
+      f = flags[slot];
+      len = lens[slot];
+    }
     double total = 0.0;
-    for (int h0 = 0; h0 < H; h0 += kHB) {
-      double v[kHB];
+    for (int h0 = 0; h0 < H; h0 += kFinHeads) {
+      const int nh = min(kFinHeads, H - h0);
+      constexpr int kPer = kFinHeads / kFinWaves;
+      double v[kPer];
 #pragma unroll
-      for (int j = 0; j < kHB; ++j) {
-        v[j] = (scored && h0 + j < H) ? __longlong_as_double(hmax[(h0 + j) * cap + slot]) : 0.0;
+      for (int i = 0; i < kPer; ++i) {
+        const int h = wave + kFinWaves * i;
+        v[i] = (in && h < nh) ? __longlong_as_double(hmax[(h0 + h) * cap + slot]) : 0.0;
       }
 #pragma unroll
-      for (int j = 0; j < kHB; ++j) total += v[j];  // h ascending
-#pragma unroll
-      for (int j = 0; j < kHB; ++j) {
-        if (scored && h0 + j < H) hmax[(h0 + j) * cap + slot] = 0ull;
+      for (int i = 0; i < kPer; ++i) {
+        const int h = wave + kFinWaves * i;
+        if (h < nh) {
+          s_h[h][lane] = v[i];
+          if (in) hmax[(h0 + h) * cap + slot] = 0ull;
+        }
       }
+      __syncthreads();
+      if (wave == 0) {
+        for (int h = 0; h < nh; ++h) total += s_h[h][lane];  // h ascending
+      }
+      __syncthreads();
     }
-    float s = __builtin_nanf("");
-    if (f & 1u) {
-      if (len == 0) {
-        s = 0.0f;
-      } else if ((f & 2u) && !q_bad) {  // all key and query values finite
-        s = static_cast<float>(total / static_cast<double>(H));
+    if (wave == 0) {
+      float sc = __builtin_nanf("");
+      if (f & 1u) {
+        if (len == 0) {
+          sc = 0.0f;
+        } else if ((f & 2u) && !q_bad) {  // all key and query values finite
+          sc = static_cast<float>(total / static_cast<double>(H));
+        }
       }
+      const bool need = isfinite(sc) && sc >= L.th_s;
+      uint64_t id = kNoId;
+      if (need) id = ids[slot];
+      wl_consume(L, k, sc, id, slot, need);
     }
-    const bool need = isfinite(s) && s >= L.th_s;
-    uint64_t id = kNoId;
-    if (need) id = ids[slot];
-    wl_consume(L, k, s, id, slot, need);
   }
-  block_topk_write<kFinWaves>(L, k, s_lists, block_out);
+  if (wave == 0 && lane < k) {
+    block_out[(static_cast<size_t>(qb) * gridDim.x + blockIdx.x) * k + lane] = wl_entry(L);
+  }
 }
 
-// ---------------------------------------------------------------- screen
+// ------------------------------------------------------- screen and refine
+//
+// For bf16, fp16 and INT8 banks every key token is screened on the matrix
+// cores: s~ = |q~ . k| with the key as stored (bf16, fp16, or the law's
+// fp16 dequantisation of INT8) and the query column rounded to the MFMA
+// type (bf16 or fp16), fp32 accumulation.  For every query column and key
+// token of a node the screen obeys |s~ - |s|| <= E = coef(column) * kmax +
+// eabs(column) (see gqa_sr_prep_kernel), s the law's fp64 dot and kmax the
+// node's largest key norm.  Within one work item, with
+// M~ the largest screened value of a column, a token with s~ < M~ - 2E
+// cannot hold the item's largest |s| (its |s| < M~ - E <= |s| of the token
+// that gave M~), so the exact item maximum is the largest exact |s| over
+// the candidates s~ >= M~ - 2E, recomputed in the law's fp64 order.  The
+// result per (node, head) is therefore the law's value for every node --
+// no shortlist, no certificate, no second route.
 
 // MFMA operand type of a key storage type: bf16 keys run bf16 MFMA; fp16
 // and int8 (dequantised to fp16 by the law) run fp16 MFMA.
 template <int KDT>
 struct ScreenTraits {
   static constexpr int kMfma = KDT == kBF16 ? kBF16 : kF16;
-  static constexpr int kEsize = KDT == kI8 ? 1 : 2;
 };
 
 template <int MT>
@@ -314,146 +432,230 @@ __device__ inline uint32_t pack_f16x2(_Float16 lo, _Float16 hi) {
          (static_cast<uint32_t>(__builtin_bit_cast(unsigned short, hi)) << 16);
 }
 
-// Query preparation, one launch per batch of Qb queries:
-//  blocks [0, kv): B fragments of the screen MFMAs.  Fragment (g, nt, ks)
-//    lane l holds column c = l%16 of N-tile nt -- batch column
-//    cg = nt*16 + c = (qb*R + r)*Qt + qi -- at dims
-//    d = ks*32 + (l/16)*8 + j, j < 8, converted to the MFMA type with
-//    round to nearest even; flags[qb] bit 0: non-finite value, bit 1:
-//    value outside the fp16 range.
-//  blocks [kv, kv+Qb): coef[qb], the screen error coefficient (see
-//    gqa_select_kernel): ((g + d + g*d)*Qsum + s*(1+g)*sqrt(hd)) / sqrt(hd)
-//    with g = gamma, d = delta, s = sigma and Qsum the mean over heads of
-//    max over query tokens of ||q||_2, rounded up.
+constexpr int kMaxCols = 64;  // query columns (Qb * R * Qt) per screen pass
+
+// Query preparation of one screen pass; grid (kv), one block per kv head g.
+// Column cg = (qb*R + r)*Qt + qi (cg < cols) is query qb's row of head
+// g*R + r at query token qi.
+//  * scale(cg) = 2^-e, the power of two that brings max|q| of the column
+//    under 2^emax (the MFMA type's safe range), 1 for ordinary values;
+//  * B fragments of the MFMAs: fragment (nt, ks) lane l holds column
+//    nt*16 + l%16 at dims ks*32 + (l/16)*8 + j, j < 8, of q * scale,
+//    rounded to nearest even in the MFMA type (columns >= cols are zero);
+//  * ecoef[g*cpad + cg] = {coef, eabs} * scale (the bound in the scaled
+//    units the screen works in; rounded up):
+//      coef = (gamma + delta + gamma*delta) * ||q||
+//             + sigma_q * (1 + gamma) * sqrt(hd) / scale + 2^-40 * ||q||
+//      eabs = sigma_k * sqrt(hd) * ||q|| + sigma_p * hd / scale
+//    gamma bounds the fp32 accumulation, delta the query's rounding,
+//    sigma_q a scaled query value flushed or rounded near zero, sigma_k a
+//    key value flushed near zero, sigma_p a product lost to underflow, and
+//    2^-40 the law's own fp64 rounding; ||q|| is rounded up;
+//  * q32c[(g*cpad + cg)*hd + d]: the column's values as fp32 (exact: the
+//    query is fp32 or bf16) for the exact recomputation;
+//  * qflags[qb*kv + g] = 1 when a value of query qb read here is non-finite.
 template <int MT>
-__global__ __launch_bounds__(256) void gqa_query_prep_kernel(
-    const void* __restrict__ query, int q_dtype, int Qb, int H, int Qt, int hd,
-    int kv, int R, int NT, int KS, u32x4* __restrict__ bfrag,
-    unsigned* __restrict__ qflags, float* __restrict__ coef, double gamma,
-    double delta, double sigma) {
+__global__ __launch_bounds__(256) void gqa_sr_prep_kernel(
+    const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int Qt,
+    int hd, int kv, int R, int NT, int KS, int emax, double gamma,
+    double delta, double sigma_q, double sigma_k, double sigma_p,
+    u32x4* __restrict__ bfrag, float2* __restrict__ ecoef, float* __restrict__ q32c,
+    unsigned* __restrict__ qflags) {
+  __shared__ float s_scale[kMaxCols];
+  __shared__ unsigned s_bad[kMaxCols];
+  const int g = blockIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int RQ = R * Qt;
+  const int cols = Qb * RQ;
+  const int cpad = NT * 16;
+  auto src_index = [&](int cg, int d) -> uint64_t {
+    const int qb = cg / RQ;
+    const int r = (cg % RQ) / Qt;
+    const int qi = cg % Qt;
+    return static_cast<uint64_t>(qb) * q_elems +
+           (static_cast<uint64_t>(g * R + r) * Qt + qi) * hd + d;
+  };
   auto qval = [&](uint64_t idx) -> float {
     return q_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(query)[idx])
                             : static_cast<const float*>(query)[idx];
   };
-  if (blockIdx.x < static_cast<unsigned>(kv)) {
-    const int g = blockIdx.x;
-    const int cols = Qb * R * Qt;
-    for (int idx = threadIdx.x; idx < NT * KS * kWave; idx += blockDim.x) {
-      const int lane = idx % kWave;
-      const int ks = (idx / kWave) % KS;
-      const int nt = idx / (kWave * KS);
-      const int cg = nt * 16 + (lane & 15);
-      uint32_t w[4] = {0u, 0u, 0u, 0u};
-      if (cg < cols) {
-        const int qb = cg / (R * Qt);
-        const int r = (cg % (R * Qt)) / Qt;
-        const int qi = cg % Qt;
-        const uint64_t base =
-            ((static_cast<uint64_t>(qb) * H + g * R + r) * Qt + qi) * hd +
-            ks * 32 + (lane >> 4) * 8;
-        unsigned bad = 0u;
-        for (int j = 0; j < 8; j += 2) {
-          const float f0 = qval(base + j), f1 = qval(base + j + 1);
-          if (!isfinite(f0) || !isfinite(f1)) bad |= 1u;
-          uint32_t packed;
-          if constexpr (MT == kBF16) {
-            // round to nearest even; inputs are finite here or flagged
-            auto rne = [](float f) {
-              uint32_t u = __float_as_uint(f);
-              return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-            };
-            packed = rne(f0) | (rne(f1) << 16);
-          } else {
-            const _Float16 h0 = static_cast<_Float16>(f0);
-            const _Float16 h1 = static_cast<_Float16>(f1);
-            if (isfinite(f0) && !isfinite(static_cast<float>(h0))) bad |= 2u;
-            if (isfinite(f1) && !isfinite(static_cast<float>(h1))) bad |= 2u;
-            packed = pack_f16x2(h0, h1);
-          }
-          w[j / 2] = packed;
-        }
-        if (bad) atomicOr(qflags + qb, bad);
-      }
-      u32x4 v;
-      v.x = w[0];
-      v.y = w[1];
-      v.z = w[2];
-      v.w = w[3];
-      bfrag[(static_cast<size_t>(g * NT + nt) * KS + ks) * kWave + lane] = v;
-    }
-    return;
-  }
-  // norms block for query qb: one wave per (head, query token) row, lanes
-  // over d (order is free: the norm only bounds the screen error)
-  __shared__ double s_row[kMaxRQ * 128];  // per (h, qi) row: ||q||_2
-  __shared__ double s_sum[256];
-  const int qb = blockIdx.x - kv;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
-  const int rows = H * Qt;
-  double part = 0.0;
-  const int chunk_rows = (kMaxRQ * 128 / Qt) * Qt;  // whole heads per chunk
-  for (int r0 = 0; r0 < rows; r0 += chunk_rows) {
-    const int nrow = min(rows - r0, chunk_rows);
-    for (int r = wave; r < nrow; r += nw) {
-      const uint64_t base = (static_cast<uint64_t>(qb) * rows + r0 + r) * hd;
-      double acc = 0.0;
+  // 1. per column: norm, range, scale, error coefficient
+  for (int cg = wave; cg < cpad; cg += nw) {
+    double ss = 0.0;
+    float mx = 0.0f;
+    bool bad = false;
+    if (cg < cols) {
       for (int d = lane; d < hd; d += kWave) {
-        const double v = static_cast<double>(qval(base + d));
-        acc = fma(v, v, acc);
+        const float f = qval(src_index(cg, d));
+        bad = bad || !isfinite(f);
+        mx = fmaxf(mx, fabsf(f));
+        ss = fma(static_cast<double>(f), static_cast<double>(f), ss);
       }
+    }
 #pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) acc += __shfl_xor(acc, off);
-      if (lane == 0) s_row[r] = sqrt(acc);
+    for (int off = 1; off < kWave; off <<= 1) {
+      ss += __shfl_xor(ss, off);
+      mx = fmaxf(mx, __shfl_xor(mx, off));
     }
-    __syncthreads();
-    // max over query tokens of each head, summed over heads
-    for (int hh = threadIdx.x; hh * Qt < nrow; hh += blockDim.x) {
-      double mx = 0.0;
-      for (int qi = 0; qi < Qt; ++qi) mx = fmax(mx, s_row[hh * Qt + qi]);
-      part += mx;
+    bad = __ballot(bad) != 0ull;
+    if (lane == 0) {
+      int e = 0;
+      if (isfinite(mx) && mx > 0.0f) {
+        const int ex = ilogbf(mx);  // mx in [2^ex, 2^(ex+1))
+        if (ex >= emax) e = ex - emax + 1;
+      }
+      const float scale = ldexpf(1.0f, -e);
+      const double norm = sqrt(ss) * (1.0 + 0x1p-40);
+      const double sq = sqrt(static_cast<double>(hd));
+      double c = 0.0, ea = 0.0;
+      if (cg < cols) {
+        c = (gamma + delta + gamma * delta) * norm + sigma_q * (1.0 + gamma) * sq / scale +
+            0x1p-40 * norm;
+        ea = sigma_k * sq * norm + sigma_p * hd / scale;
+      }
+      const double up = 1.0 + 0x1p-20;
+      c *= up * scale * up;
+      ea *= up * scale * up;
+      s_scale[cg] = scale;
+      s_bad[cg] = bad ? 1u : 0u;
+      ecoef[g * cpad + cg] = make_float2(isfinite(c) ? static_cast<float>(c) * 1.000001f : INFINITY,
+                                         isfinite(ea) ? static_cast<float>(ea) * 1.000001f : INFINITY);
     }
-    __syncthreads();
   }
-  s_sum[threadIdx.x] = part;
   __syncthreads();
-  for (int off = blockDim.x / 2; off > 0; off >>= 1) {
-    if (threadIdx.x < static_cast<unsigned>(off)) s_sum[threadIdx.x] += s_sum[threadIdx.x + off];
-    __syncthreads();
+  // 2. B fragments
+  for (int idx = threadIdx.x; idx < NT * KS * kWave; idx += blockDim.x) {
+    const int l = idx % kWave;
+    const int ks = (idx / kWave) % KS;
+    const int nt = idx / (kWave * KS);
+    const int cg = nt * 16 + (l & 15);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (cg < cols) {
+      const float sc = s_scale[cg];
+      const int d0 = ks * 32 + (l >> 4) * 8;
+      for (int j = 0; j < 8; j += 2) {
+        const float f0 = qval(src_index(cg, d0 + j)) * sc;
+        const float f1 = qval(src_index(cg, d0 + j + 1)) * sc;
+        if constexpr (MT == kBF16) {
+          auto rne = [](float f) {  // round to nearest even (finite inputs)
+            const uint32_t u = __float_as_uint(f);
+            return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+          };
+          w[j / 2] = rne(f0) | (rne(f1) << 16);
+        } else {
+          w[j / 2] = pack_f16x2(static_cast<_Float16>(f0), static_cast<_Float16>(f1));
+        }
+      }
+    }
+    u32x4 v;
+    v.x = w[0];
+    v.y = w[1];
+    v.z = w[2];
+    v.w = w[3];
+    bfrag[(static_cast<size_t>(g * NT + nt) * KS + ks) * kWave + l] = v;
   }
-  if (threadIdx.x == 0) {
-    const double qsum = s_sum[0] / H;
-    const double sq = sqrt(static_cast<double>(hd));
-    const double c = ((gamma + delta + gamma * delta) * qsum + sigma * (1.0 + gamma) * sq) / sq;
-    coef[qb] = static_cast<float>(c * (1.0 + 1e-6));
+  // 3. fp32 columns for the exact recomputation
+  for (int idx = threadIdx.x; idx < cols * hd; idx += blockDim.x) {
+    const int cg = idx / hd;
+    q32c[static_cast<size_t>(g * cpad) * hd + idx] = qval(src_index(cg, idx - cg * hd));
+  }
+  // 4. non-finite flags per query
+  for (int qb = threadIdx.x; qb < Qb; qb += blockDim.x) {
+    unsigned bad = 0u;
+    for (int j = 0; j < RQ; ++j) bad |= s_bad[qb * RQ + j];
+    qflags[qb * kv + g] = bad;
   }
 }
 
-// Screen: |q.k| on the matrix cores for every key token, for all batch
-// columns at once; grid (blocks, kv).  Each wavefront walks the items
-// w, w+W, ... of kv head blockIdx.y as one stream of 16-token steps with
-// the next step's loads in flight while the current one is folded.  The
-// per-(query, node, head) maxima land in head-major hms
-// [qb][h][slot] (fp32 bits, atomicMax; non-negative floats order like their
-// bits).  K-step ks of lane l covers dims ks*32 + (l/16)*8 .. +8 of key
-// token l%16 (matching the B fragments), so one load instruction reads 64
-// contiguous bytes of each of 16 key rows.  Tokens past an item read as
-// zero, and |0| never raises a maximum.
+// Exact |dot| of one lane's (key token, query column) pair in the law's
+// order: the token's chunks come from the planes at kp (chunk c at
+// kp + c*L), 64 values' worth in flight at once, the column's
+// values from qrow (LDS, fp32, exact).  Only lanes with `active` set read
+// memory (the others return 0): the candidates are a few lanes of the
+// wave, and their rows are all that is read again.
+template <int KDT, int HD>
+__device__ __forceinline__ double exact_pair(bool active, const u32x4* __restrict__ kp,
+                                             uint64_t L, const unsigned char* __restrict__ sp,
+                                             int scale_dtype, int cpg, const float* qrow) {
+  using T = KeyTraits<KDT>;
+  constexpr int C = HD / T::kEpc;
+  constexpr int kB = C < 64 / T::kEpc ? C : 64 / T::kEpc;  // 64 values per batch
+  double acc = 0.0;
+  if (!active) return 0.0;
+  for (int c0 = 0; c0 < C; c0 += kB) {
+    u32x4 v[kB];
+    float sc[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      v[b] = kp[static_cast<uint64_t>(c0 + b) * L];
+      sc[b] = 0.0f;
+      if constexpr (KDT == kI8) {
+        sc[b] = load_scale(sp, scale_dtype, static_cast<uint64_t>((c0 + b) / cpg) * L);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      float f[T::kEpc];
+      decode_chunk<KDT>(v[b], sc[b], f);
+      const float* q = qrow + (c0 + b) * T::kEpc;
+#pragma unroll
+      for (int e = 0; e < T::kEpc; ++e) {
+        acc = fma(static_cast<double>(f[e]), static_cast<double>(q[e]), acc);
+      }
+    }
+  }
+  return fabs(acc);
+}
+
+// Screen and refine; grid (ceil(items / 4), kv heads), one wavefront per
+// (item, kv head g).  The item's tokens stream in 16-token tiles, two
+// tiles ahead of the one being screened.  Lane l sees column
+// nt*16 + l%16 of tokens (l/16)*4 + i of every tile; it keeps the two
+// largest screened values with their tokens and the third largest value.
+// At the item's end: M~ per column (over the four lanes of the column),
+// threshold M~ - 2E; if no lane's third value reaches the threshold the
+// candidates are among the kept two and are recomputed exactly, otherwise
+// the item is screened again tile by tile and every token at or above the
+// threshold is recomputed.  The per-column exact maxima, divided by
+// sqrt(hd) (monotone), fold into hmax[qb*hstride + (g*R + r)*cap + slot]
+// (double bits, atomicMax).
 template <int KDT, int KS, int NT>
-__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_screen_kernel(
+__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     const unsigned char* __restrict__ keys,
     const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
-    const Item* __restrict__ items, uint32_t n_items, int R, int Qt, int cols,
-    const u32x4* __restrict__ bfrag, unsigned* __restrict__ hms,
-    size_t hms_qstride, size_t cap) {
-  using ST = ScreenTraits<KDT>;
+    const Item* __restrict__ items, uint32_t n_items, int kv, int R, int Qt,
+    int cols, const u32x4* __restrict__ bfrag,
+    const float2* __restrict__ ecoef, const float* __restrict__ q32c,
+    const unsigned* __restrict__ qflags, const float* __restrict__ kmax, double denom,
+    unsigned long long* __restrict__ hmax, size_t hstride, size_t cap) {
+  using KT = KeyTraits<KDT>;
+  constexpr int MT = ScreenTraits<KDT>::kMfma;
   constexpr int HD = 32 * KS;
+  constexpr int C = HD / KT::kEpc;  // chunks per key row
+  extern __shared__ float s_q[];  // [cols][HD]: the block's query columns
   const int lane = threadIdx.x & (kWave - 1);
-  const uint32_t W = gridDim.x * kUnitWaves;
-  uint32_t i_cur = blockIdx.x * kUnitWaves + threadIdx.x / kWave;
-  if (i_cur >= n_items) return;
   const int g = blockIdx.y;
+  for (int i = threadIdx.x; i < cols * HD; i += blockDim.x) {
+    s_q[i] = q32c[static_cast<size_t>(g * NT * 16) * HD + i];
+  }
+  __syncthreads();
+  const uint32_t item_i = blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  if (item_i >= n_items) return;
+  const Item it = items[item_i];
+  const uint64_t L = it.len;
+  const uint64_t row0 = it.base + static_cast<uint64_t>(g) * L;
+  const int G = KDT == kI8 ? HD / group_size : 1;
+  const int cpg = KDT == kI8 ? group_size / KT::kEpc : 1;
+  const int ses = scale_dtype == kF16 ? 2 : 4;
+  const u32x4* kplane = reinterpret_cast<const u32x4*>(keys) + row0 * C;
+  const unsigned char* splane = KDT == kI8 ? scales + row0 * G * ses : nullptr;
+  const int quarter = lane >> 4;
+  const int r16 = lane & 15;
+  const uint32_t last = it.t0 + it.count - 1;  // last token of the item
+  const int ntiles = static_cast<int>((it.count + 15) / 16);
+
   u32x4 bq[NT][KS];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -462,305 +664,220 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_screen_kernel(
       bq[nt][ks] = bfrag[(static_cast<size_t>(g * NT + nt) * KS + ks) * kWave + lane];
     }
   }
-  const int quarter = lane >> 4;
-  const int r16 = lane & 15;
-  const int groups = KDT == kI8 ? HD / group_size : 1;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
 
-  auto load_step = [&](u32x4 (&a)[KS], const Item& it, uint32_t s) {
-    const uint32_t tl = s * 16 + r16;
-    const bool ok = tl < it.count;
-    const uint64_t row = it.base + static_cast<uint64_t>(g) * it.len + it.t0 + tl;
+  // Raw data of tile `tile` for this lane: token min(t0 + 16*tile + l%16,
+  // last), dims ks*32 + (l/16)*8 .. +8 (loads are unconditional; rows past
+  // the item are masked when folded).  INT8 tiles keep codes and scales
+  // and are dequantised when folded, so no load is waited for early.
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  struct Tile {
+    u32x4 v[KDT == kI8 ? 1 : KS];
+    u32x2 c[KDT == kI8 ? KS : 1];
+    float s[KDT == kI8 ? KS : 1];
+  };
+  auto load_tile = [&](Tile& b, int tile) {
+    const uint32_t t = min(it.t0 + static_cast<uint32_t>(tile) * 16 + r16, last);
     if constexpr (KDT != kI8) {
-      const u32x4* p = reinterpret_cast<const u32x4*>(keys + (row * HD + quarter * 8) * ST::kEsize);
+      const u32x4* p = kplane + quarter * L + t;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) a[ks] = ok ? p[ks * 4] : zero;  // +64 bytes per K-step
+      for (int ks = 0; ks < KS; ++ks) b.v[ks] = __builtin_nontemporal_load(p + ks * 4 * L);
     } else {
-      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-      const u32x2* p = reinterpret_cast<const u32x2*>(keys + row * HD + quarter * 8);
+      // half (quarter & 1) of chunk (ks*2 + quarter/2)
+      const u32x2* p = reinterpret_cast<const u32x2*>(kplane + (quarter >> 1) * L + t) + (quarter & 1);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const u32x2 v = ok ? p[ks * 4] : u32x2{0u, 0u};  // +32 bytes per K-step
-        const float sc = ok ? load_scale(scales, scale_dtype,
-                                         row * groups + (ks * 32 + quarter * 8) / group_size)
-                            : 0.0f;
-        const uint32_t w[2] = {v.x, v.y};
-        uint32_t o[4];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          o[2 * i] = pack_f16x2(dequant_i8(static_cast<int8_t>(w[i] & 0xffu), sc),
-                                dequant_i8(static_cast<int8_t>((w[i] >> 8) & 0xffu), sc));
-          o[2 * i + 1] = pack_f16x2(dequant_i8(static_cast<int8_t>((w[i] >> 16) & 0xffu), sc),
-                                    dequant_i8(static_cast<int8_t>(w[i] >> 24), sc));
-        }
-        a[ks].x = o[0];
-        a[ks].y = o[1];
-        a[ks].z = o[2];
-        a[ks].w = o[3];
+        b.c[ks] = __builtin_nontemporal_load(p + ks * 4 * L);
+        b.s[ks] = load_scale(splane, scale_dtype,
+                             static_cast<uint64_t>((ks * 32 + quarter * 8) / group_size) * L + t);
       }
     }
   };
-  float m[NT];
+  auto frag = [&](const Tile& b, int ks) -> u32x4 {
+    if constexpr (KDT != kI8) {
+      return b.v[ks];
+    } else {
+      const uint32_t w[2] = {b.c[ks].x, b.c[ks].y};
+      const float sc = b.s[ks];
+      uint32_t o[4];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) m[nt] = 0.0f;
-  auto fold = [&](const u32x4 (&a)[KS]) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) c = mfma16x16x32<ST::kMfma>(a[ks], bq[nt][ks], c);
-      m[nt] = fmaxf(m[nt], fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))));
+      for (int i = 0; i < 2; ++i) {
+        o[2 * i] = pack_f16x2(dequant_i8(static_cast<int8_t>(w[i] & 0xffu), sc),
+                              dequant_i8(static_cast<int8_t>((w[i] >> 8) & 0xffu), sc));
+        o[2 * i + 1] = pack_f16x2(dequant_i8(static_cast<int8_t>((w[i] >> 16) & 0xffu), sc),
+                                  dequant_i8(static_cast<int8_t>(w[i] >> 24), sc));
+      }
+      u32x4 a;
+      a.x = o[0];
+      a.y = o[1];
+      a.z = o[2];
+      a.w = o[3];
+      return a;
     }
   };
-  auto emit = [&](const Item& it) {
+  // Screened |s~| of the lane's 4 rows of `tile` for column block nt;
+  // rows past the item read -inf.
+  auto screen = [&](const Tile& b, int tile, int nt, float (&v)[4]) {
+    f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float v = fmaxf(m[nt], __shfl_xor(m[nt], 16));
-      v = fmaxf(v, __shfl_xor(v, 32));
-      const int cg = nt * 16 + lane;
-      if (lane < 16 && cg < cols) {
-        const int qb = cg / (R * Qt);
-        const int r = (cg % (R * Qt)) / Qt;
-        atomicMax(hms + qb * hms_qstride + static_cast<size_t>(g * R + r) * cap + it.slot,
-                  __float_as_uint(v));
-      }
-      m[nt] = 0.0f;
-    }
+    for (int ks = 0; ks < KS; ++ks) c = mfma16x16x32<MT>(frag(b, ks), bq[nt][ks], c);
+    const uint32_t tb = static_cast<uint32_t>(tile) * 16 + quarter * 4;  // item-relative
+    const float cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = tb + i < it.count ? fabsf(cv[i]) : -INFINITY;
   };
 
-  Item cur = items[i_cur];
-  uint32_t i_nxt = i_cur + W;
-  Item nxt = items[i_nxt < n_items ? i_nxt : i_cur];
-  uint32_t s = 0;
-  uint32_t nsteps = (cur.count + 15) / 16;
-  u32x4 a0[KS], a1[KS];
-  load_step(a0, cur, 0);
-  // One step: fold `now` while the following step loads into `later`.
-  // Returns false when the wave's stream is exhausted.
-  auto step = [&](u32x4 (&now)[KS], u32x4 (&later)[KS]) -> bool {
-    const bool last_of_item = s + 1 == nsteps;
-    if (!last_of_item) {
-      load_step(later, cur, s + 1);
-    } else if (i_nxt < n_items) {
-      load_step(later, nxt, 0);
-    }
-    fold(now);
-    if (!last_of_item) {
-      ++s;
-      return true;
-    }
-    emit(cur);
-    if (i_nxt >= n_items) return false;
-    i_cur = i_nxt;
-    cur = nxt;
-    i_nxt = i_cur + W;
-    nxt = items[i_nxt < n_items ? i_nxt : i_cur];
-    s = 0;
-    nsteps = (cur.count + 15) / 16;
-    return true;
-  };
-  while (step(a0, a1) && step(a1, a0)) {
+  float b1[NT], b2[NT], b3[NT];
+  uint32_t t1[NT], t2[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    b1[nt] = b2[nt] = b3[nt] = -INFINITY;
+    t1[nt] = t2[nt] = 0u;
   }
-}
-
-// Select: per (query, live slot) the screened score S~ = sum_h m_h /
-// (H sqrt(hd)) and its bound B = coef*kmax + slack*|S~| (|S~ - S| <= B for
-// the law's score S); keeps the best mU slots by U = S~ + B and the best k
-// by Lo = S~ - B (ties to the lower node id).  grid (blocks, Qb).  Reads the
-// head-major maxima coalesced and re-zeroes them.
-__global__ __launch_bounds__(kFinWaves * kWave) void gqa_select_kernel(
-    unsigned* __restrict__ hms, size_t hms_qstride, size_t cap, int H,
-    uint32_t n_slots, const uint32_t* __restrict__ lens,
-    const uint32_t* __restrict__ flags, const uint64_t* __restrict__ ids,
-    const float* __restrict__ kmax, const float* __restrict__ coef,
-    float inv_scale, float slack_rel, int mU, int k, Cand* __restrict__ bu,
-    Cand* __restrict__ bl) {
-  constexpr int kHB = 32;  // head maxima loaded at once
-  __shared__ Cand s_u[kFinWaves][kMaxShort];
-  __shared__ Cand s_l[kFinWaves][kMaxTopK];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int qb = blockIdx.y;
-  const float cq = coef[qb];
-  unsigned* hq = hms + qb * hms_qstride;
-  WaveList WU, WL;
-  wl_init(WU);
-  wl_init(WL);
-  const uint32_t stride = gridDim.x * blockDim.x;
-  for (uint32_t base = blockIdx.x * blockDim.x + wave * kWave; base < n_slots;
-       base += stride) {
-    const uint32_t slot = base + lane;
-    const bool in = slot < n_slots;
-    const uint32_t f = in ? flags[slot] : 0u;
-    const uint32_t len = in ? lens[slot] : 0u;
-    const bool scored = (f & 1u) && len > 0;
-    float sum = 0.0f;
-    for (int h0 = 0; h0 < H; h0 += kHB) {
-      float v[kHB];
+  auto fold = [&](const Tile& b, int tile) {
 #pragma unroll
-      for (int j = 0; j < kHB; ++j) {
-        v[j] = (scored && h0 + j < H) ? __uint_as_float(hq[(h0 + j) * cap + slot]) : 0.0f;
-      }
+    for (int nt = 0; nt < NT; ++nt) {
+      float v[4];
+      screen(b, tile, nt, v);
+      const uint32_t tb = static_cast<uint32_t>(tile) * 16 + quarter * 4;
 #pragma unroll
-      for (int j = 0; j < kHB; ++j) sum += v[j];
-#pragma unroll
-      for (int j = 0; j < kHB; ++j) {
-        if (scored && h0 + j < H) hq[(h0 + j) * cap + slot] = 0u;
-      }
-    }
-    bool valid = false;
-    float u = 0.0f, lo = 0.0f;
-    if (f & 1u) {
-      if (len == 0) {
-        valid = true;  // exact score 0.0
-      } else if (f & 2u) {
-        valid = true;
-        const float sc = sum * inv_scale;
-        const float b = cq * kmax[slot] + slack_rel * fabsf(sc);
-        u = sc + b;
-        lo = sc - b;
-        if (!isfinite(u) || !isfinite(lo)) {
-          u = 3.0e38f;  // unbounded screen value: always shortlisted
-          lo = -3.0e38f;
+      for (int i = 0; i < 4; ++i) {
+        // NaN compares false everywhere and is never kept
+        const bool gt1 = v[i] > b1[nt];
+        const bool gt2 = v[i] > b2[nt];
+        const bool gt3 = v[i] > b3[nt];
+        b3[nt] = gt2 ? b2[nt] : (gt3 ? v[i] : b3[nt]);
+        const float nb2 = gt1 ? b1[nt] : (gt2 ? v[i] : b2[nt]);
+        const uint32_t nt2 = gt1 ? t1[nt] : (gt2 ? tb + i : t2[nt]);
+        b2[nt] = nb2;
+        t2[nt] = nt2;
+        if (gt1) {
+          b1[nt] = v[i];
+          t1[nt] = tb + i;
         }
       }
     }
-    const uint64_t id = valid ? ids[slot] : kNoId;
-    wl_consume(WU, mU, u, id, slot, valid);
-    wl_consume(WL, k, lo, id, slot, valid);
-  }
-  Cand* bu_q = bu + (static_cast<size_t>(qb) * gridDim.x) * mU;
-  Cand* bl_q = bl + (static_cast<size_t>(qb) * gridDim.x) * k;
-  block_topk_write<kFinWaves>(WU, mU, s_u, bu_q);
-  __syncthreads();
-  block_topk_write<kFinWaves>(WL, k, s_l, bl_q);
-}
+  };
 
-// Shortlist: merge the select blocks of query blockIdx.x; shortlist the best
-// M slots by U and certify: every node outside it has U <= U_(M+1), every
-// node's law score lies in [Lo, U], so if U_(M+1) < Lo_(k) (k-th best Lo)
-// the law's top-k lies inside the shortlist.  Writes status[q] = 1 when
-// certified and copies the query's prep flags to out_flags[q] (both host
-// mapped).
-__global__ __launch_bounds__(kFinWaves * kWave) void gqa_shortlist_kernel(
-    const Cand* __restrict__ bu, const Cand* __restrict__ bl, uint32_t nblk,
-    int mU, int k, int M, uint32_t* __restrict__ shortlist,
-    const unsigned* __restrict__ qflags, unsigned* __restrict__ out_flags,
-    unsigned* __restrict__ status) {
-  __shared__ Cand s_u[kFinWaves][kMaxShort];
-  __shared__ Cand s_l[kFinWaves][kMaxTopK];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int qb = blockIdx.x;
-  WaveList WU, WL;
-  wl_init(WU);
-  wl_init(WL);
-  wl_consume_global(WU, mU, bu + static_cast<size_t>(qb) * nblk * mU, nblk * mU,
-                    static_cast<uint32_t>(wave), kFinWaves);
-  wl_consume_global(WL, k, bl + static_cast<size_t>(qb) * nblk * k, nblk * k,
-                    static_cast<uint32_t>(wave), kFinWaves);
-  if (lane < kMaxShort) s_u[wave][lane] = wl_entry(WU);
-  if (lane < kMaxTopK) s_l[wave][lane] = wl_entry(WL);
-  __syncthreads();
-  if (wave == 0) {
-    WaveList BU, BL;
-    block_merge<kFinWaves>(s_u, mU, BU);
-    block_merge<kFinWaves>(s_l, k, BL);
-    const bool filled = lane < mU && BU.id != kNoId;
-    const int count = __popcll(__ballot(filled));
-    const float u_next = __shfl(BU.s, M);
-    const float tau = __shfl(BL.s, k - 1);  // -inf when fewer than k nodes
-    if (lane < M) shortlist[static_cast<size_t>(qb) * M + lane] = lane < count ? BU.slot : kNoSlot;
-    if (lane == 0) {
-      status[qb] = (count <= M || u_next < tau) ? 1u : 0u;
-      out_flags[qb] = qflags[qb];
+  // stream: five tile buffers, four tiles in flight ahead of the fold
+  Tile x0, x1, x2, x3, x4;
+  load_tile(x0, 0);
+  load_tile(x1, 1);
+  load_tile(x2, 2);
+  load_tile(x3, 3);
+  int tile = 0;
+  auto step = [&](Tile& now, Tile& free) -> bool {
+    load_tile(free, tile + 4);  // past the end: reloads the last token
+    fold(now, tile);
+    return ++tile < ntiles;
+  };
+  while (step(x0, x4) && step(x1, x0) && step(x2, x1) && step(x3, x2) && step(x4, x3)) {
+  }
+
+  // thresholds and candidates; a column whose query holds a non-finite
+  // value takes no part (every score of that query is NaN)
+  const int RQc = R * Qt;
+  const float km = kmax[it.slot];
+  double thr[NT];
+  bool live[NT];
+  bool amb = false;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float m = b1[nt];
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    const int cg = nt * 16 + r16;
+    live[nt] = cg < cols && qflags[(min(cg, cols - 1) / RQc) * kv + g] == 0u;
+    const float2 ec = ecoef[g * NT * 16 + cg];
+    const double e = static_cast<double>(ec.x) * static_cast<double>(km) + static_cast<double>(ec.y);
+    thr[nt] = static_cast<double>(m) - 2.0 * e;
+    if (live[nt]) {
+      amb = amb || !(thr[nt] > -INFINITY) || !isfinite(e) ||
+            static_cast<double>(b3[nt]) >= thr[nt];
     }
   }
-}
+  const bool enumerate = __ballot(amb) != 0ull;
 
-// Exact rescore of the shortlisted slots; grid (ceil(units / 4), kv) with
-// units = Qb * M * max_chunks (64-token chunks).  hex[h * QM + (qb*M + m)]
-// (QM = Qb*M) receives the exact maxima (double bits, atomicMax).
-template <int KDT, int RQ>
-__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_rescore_kernel(
-    const unsigned char* __restrict__ keys,
-    const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
-    const uint64_t* __restrict__ tok_off, const uint32_t* __restrict__ lens,
-    const uint32_t* __restrict__ shortlist, int M, int Qb, uint32_t max_chunks,
-    int kv, int hd, int R, int Qt, const void* __restrict__ query, int q_dtype,
-    size_t q_stride, double denom, unsigned long long* __restrict__ hex) {
-  extern __shared__ double qs[];  // [kUnitWaves][RQ][hd]
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int g = blockIdx.y;
-  const uint64_t unit = static_cast<uint64_t>(blockIdx.x) * kUnitWaves + wave;
-  const uint64_t units = static_cast<uint64_t>(Qb) * M * max_chunks;
-  const bool in_range = unit < units;
-  const uint32_t qm = in_range ? static_cast<uint32_t>(unit / max_chunks) : 0;
-  const uint32_t chunk = in_range ? static_cast<uint32_t>(unit % max_chunks) : 0;
-  const int qb = static_cast<int>(qm / M);
-  const uint32_t slot = in_range ? shortlist[qm] : kNoSlot;
-  const uint32_t L = slot != kNoSlot ? lens[slot] : 0u;
-  const uint32_t t0 = chunk * kWave;
-  const bool active = slot != kNoSlot && t0 < L;
-  double* q = qs + static_cast<size_t>(wave) * RQ * hd;
-  const unsigned char* qptr = static_cast<const unsigned char*>(query) +
-                              static_cast<size_t>(qb) * q_stride * (q_dtype == kBF16 ? 2 : 4);
-  stage_group_query(q, RQ, qptr, q_dtype, g, R, Qt, hd, active, lane, kWave);
-  __syncthreads();
-  if (!active) return;
-  exact_unit<KDT, RQ>(keys, scales, scale_dtype, group_size,
-                      tok_off[slot] * kv + static_cast<uint64_t>(g) * L, t0,
-                      min(static_cast<uint32_t>(kWave), L - t0), q, g, R, Qt, hd,
-                      denom, hex + qm, static_cast<size_t>(Qb) * M);
-}
-
-// Exact scores of the shortlist entries into out[qb*M + m] (host mapped),
-// h in order in fp64, re-zeroing the maxima.  One thread per entry.
-__global__ void gqa_rescore_finalize_kernel(
-    unsigned long long* __restrict__ hex, int H,
-    const uint32_t* __restrict__ shortlist, uint32_t total,
-    const uint32_t* __restrict__ lens, const uint64_t* __restrict__ ids,
-    Cand* __restrict__ out) {
-  constexpr int kHB = 16;
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const uint32_t slot = shortlist[i];
-  double sum = 0.0;
-  for (int h0 = 0; h0 < H; h0 += kHB) {
-    double v[kHB];
+  auto pair = [&](bool active, uint32_t t, int cg) -> double {
+    const uint32_t tt = min(it.t0 + t, last);
+    return exact_pair<KDT, HD>(active, kplane + tt, L,
+                           KDT == kI8 ? splane + static_cast<size_t>(tt) * ses : nullptr,
+                           scale_dtype, cpg, s_q + min(cg, cols - 1) * HD);
+  };
+  double best[NT];
 #pragma unroll
-    for (int j = 0; j < kHB; ++j) {
-      v[j] = h0 + j < H ? __longlong_as_double(hex[static_cast<size_t>(h0 + j) * total + i]) : 0.0;
+  for (int nt = 0; nt < NT; ++nt) best[nt] = -1.0;
+  if (!enumerate) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int cg = nt * 16 + r16;
+      const bool c1 = live[nt] && static_cast<double>(b1[nt]) >= thr[nt];
+      const bool c2 = live[nt] && static_cast<double>(b2[nt]) >= thr[nt];
+      if (__ballot(c1) != 0ull) {
+        const double x = pair(c1, t1[nt], cg);
+        if (c1) best[nt] = x;
+      }
+      if (__ballot(c2) != 0ull) {
+        const double x = pair(c2, t2[nt], cg);
+        if (c2) best[nt] = (x > best[nt] || isnan(x)) ? x : best[nt];
+      }
     }
+  } else {
+    for (int tl = 0; tl < ntiles; ++tl) {
+      Tile a;
+      load_tile(a, tl);
 #pragma unroll
-    for (int j = 0; j < kHB; ++j) sum += v[j];  // h ascending
-#pragma unroll
-    for (int j = 0; j < kHB; ++j) {
-      if (h0 + j < H) hex[static_cast<size_t>(h0 + j) * total + i] = 0ull;
+      for (int nt = 0; nt < NT; ++nt) {
+        float v[4];
+        screen(a, tl, nt, v);
+        const int cg = nt * 16 + r16;
+        const uint32_t tb = static_cast<uint32_t>(tl) * 16 + quarter * 4;
+        for (int i = 0; i < 4; ++i) {
+          // a NaN screen value (non-finite keys) is recomputed too
+          const bool c = live[nt] && (static_cast<double>(v[i]) >= thr[nt] || isnan(v[i]) ||
+                                      !(thr[nt] > -INFINITY));
+          if (__ballot(c) != 0ull) {
+            const double x = pair(c, tb + i, cg);
+            if (c) best[nt] = (x > best[nt] || isnan(x)) ? x : best[nt];
+          }
+        }
+      }
     }
   }
-  Cand c;
-  c.score = __builtin_nanf("");
-  c.slot = kNoSlot;
-  c.id = kNoId;
-  if (slot != kNoSlot) {
-    c.score = lens[slot] == 0 ? 0.0f : static_cast<float>(sum / static_cast<double>(H));
-    c.slot = slot;
-    c.id = ids[slot];
+  // per column over its four lanes, then one atomic per valid column
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    unsigned long long bits = best[nt] >= 0.0 || isnan(best[nt])
+                                  ? __double_as_longlong(best[nt] / denom)
+                                  : 0ull;
+#pragma unroll
+    for (int off = 16; off < kWave; off <<= 1) {
+      const unsigned long long o = __shfl_xor(bits, off);
+      bits = o > bits ? o : bits;
+    }
+    const int cg = nt * 16 + lane;
+    if (lane < 16 && cg < cols && bits != 0ull) {
+      const int qb = cg / RQc;
+      const int r = (cg % RQc) / Qt;
+      atomicMax(hmax + qb * hstride + static_cast<size_t>(g * R + r) * cap + it.slot, bits);
+    }
   }
-  out[i] = c;
 }
 
 // ----------------------------------------------------------- bank upkeep
 
-// Key statistics of new slots: nonfinite[slot] set when a decoded value is
-// not finite; kmax[slot] = max over kv heads and tokens of ||k||_2, rounded
-// up (float bits, atomicMax).  grid (ceil(items / 4), kv).
+// Placement of new slots: copy their key rows (and INT8 scales) from the
+// staging layout -- per slot [kv][len][head_dim] values, rows of
+// [kv][len][G] scales, slot blocks back to back from staged token 0 -- into
+// the chunk planes, and gather key statistics on the way: nonfinite[slot]
+// set when a decoded value is not finite; kmax[slot] = max over kv heads
+// and tokens of ||k||_2, rounded up (float bits, atomicMax).  Items carry
+// the destination base; the staged row of (item, g, t) is
+// base - src_base + g*len + t.  grid (ceil(items / 4), kv).
 template <int KDT>
-__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_key_stats_kernel(
-    const unsigned char* __restrict__ keys,
-    const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
+__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_place_kernel(
+    const u32x4* __restrict__ src_keys, const unsigned char* __restrict__ src_scales,
+    uint64_t src_base, unsigned char* __restrict__ keys,
+    unsigned char* __restrict__ scales, int scale_dtype, int group_size,
     const Item* __restrict__ items, uint32_t n_items, int hd,
     uint32_t* __restrict__ nonfinite, unsigned* __restrict__ kmax) {
   using T = KeyTraits<KDT>;
@@ -769,18 +886,37 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_key_stats_kernel(
   if (item_i >= n_items) return;
   const int g = blockIdx.y;
   const Item it = items[item_i];
-  const int groups = KDT == kI8 ? hd / group_size : 1;
+  const int C = hd / T::kEpc;
+  const int G = KDT == kI8 ? hd / group_size : 1;
+  const int cpg = KDT == kI8 ? group_size / T::kEpc : 1;
+  const size_t ses = scale_dtype == kF16 ? 2 : 4;
+  const uint64_t row0 = it.base + static_cast<uint64_t>(g) * it.len;
+  const uint64_t srow0 = row0 - src_base;
+  u32x4* dst = reinterpret_cast<u32x4*>(keys) + row0 * C;
   bool bad = false;
   double mx = 0.0;
   for (uint32_t t = it.t0 + lane; t < it.t0 + it.count; t += kWave) {
-    const uint64_t row = it.base + static_cast<uint64_t>(g) * it.len + t;
-    const u32x4* p = reinterpret_cast<const u32x4*>(keys + row * hd * T::kEsize);
+    const u32x4* src = src_keys + (srow0 + t) * C;
     double acc = 0.0;
-    for (int c = 0; c < hd / T::kEpc; ++c) {
+    for (int c = 0; c < C; ++c) {
+      const u32x4 v = src[c];
+      dst[static_cast<uint64_t>(c) * it.len + t] = v;
+      float sc = 0.0f;
+      if constexpr (KDT == kI8) {
+        const int j = c / cpg;
+        const unsigned char* s_in = src_scales + ((srow0 + t) * G + j) * ses;
+        unsigned char* s_out = scales + ((row0 * G) + static_cast<uint64_t>(j) * it.len + t) * ses;
+        if (c % cpg == 0) {
+          if (ses == 2) {
+            *reinterpret_cast<uint16_t*>(s_out) = *reinterpret_cast<const uint16_t*>(s_in);
+          } else {
+            *reinterpret_cast<uint32_t*>(s_out) = *reinterpret_cast<const uint32_t*>(s_in);
+          }
+        }
+        sc = load_scale(src_scales, scale_dtype, (srow0 + t) * G + j);
+      }
       float f[T::kEpc];
-      const int e0 = c * T::kEpc;
-      decode_chunk<KDT>(p[c], scales, scale_dtype,
-                        KDT == kI8 ? row * groups + e0 / group_size : 0, f);
+      decode_chunk<KDT>(v, sc, f);
 #pragma unroll
       for (int e = 0; e < T::kEpc; ++e) {
         bad = bad || !isfinite(f[e]);

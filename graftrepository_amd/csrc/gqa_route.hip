@@ -1,12 +1,18 @@
 // gqa_route.hip -- ragged GQA route on gfx950: bank lifecycle, route
 // orchestration and the C ABI.  Device code lives in gqa_kernels.hpp.
 //
-// Bank layout in HBM: ragged CSR.  Node slot i owns tokens
-// [tok_off[i], tok_off[i]+len[i]) of the token arena; its block is
-// [kv][len][hd] values of the storage dtype (f32, bf16, f16 or int8 codes
-// with per-(token, group) scales).  No padding is stored or read.
+// Bank layout in HBM: ragged CSR.  Node slot i owns token rows
+// [tok_off[i], tok_off[i] + L') of the token arena, L' = len[i] rounded up
+// to 8; its block holds kv * L' * hd values of the storage dtype (f32,
+// bf16, f16 or int8 codes with per-(token, group) scales) as chunk planes
+// per kv head: chunk c (16 bytes) of token t of head g at c*L' + t within
+// the head's block (gqa_kernels.hpp).  The rounding puts every 8-token run
+// of a plane on its own 128-byte line, so streams never share a line; the
+// rows past len[i] are never read.
 //
 // Route (bf16 / fp16 / int8 banks, head_dim 64, 128 or 256):
+//   when (heads / kv) * query_tokens <= 4 the exact path below streams the
+//   bank at the HBM rate by itself; otherwise
 //   prep -> screen (MFMA, all key tokens) -> select -> shortlist/certify ->
 //   exact rescore of the shortlist -> exact finalize; the host merges the
 //   shortlist's exact scores.  A query whose shortlist is not certified, or
@@ -65,43 +71,30 @@ struct GqaDeviceArena {
   std::unordered_map<uint64_t, uint64_t> slot_of;
   std::set<uint64_t> free_slots;
   // route work list, rebuilt when the epoch moves
-  uint32_t chunk = 64;  // key tokens per work item
+  uint32_t chunk = 256;  // key tokens per work item
   Item* d_items = nullptr;
   size_t d_items_count = 0;
   uint64_t n_items = 0;
   uint64_t items_epoch = ~0ull;
   uint32_t max_len = 0;  // longest live node
-  // exact path
+  // per-(query, head, slot) maxima, head-major per query (double bits)
   unsigned long long* d_hmax = nullptr;
   size_t d_hmax_count = 0;
-  int hmax_heads = 0;
   grm::MappedCands blocks_out;  // per-query, per-block top-k (host mapped)
-  unsigned* d_qbad = nullptr;   // set when a query value is non-finite
-  // screen path
-  bool screen = true;
+  unsigned* d_qbad = nullptr;   // per (query, kv head): non-finite query value
+  size_t d_qbad_count = 0;
+  // exact path
+  double* d_q64 = nullptr;      // query rows as doubles (gqa_q64_kernel)
+  size_t d_q64_count = 0;
+  // screen-and-refine path
+  int screen_mode = -1;  // -1 whenever the shape allows, 0 never
   u32x4* d_bfrag = nullptr;
   size_t d_bfrag_count = 0;
-  float* d_coef = nullptr;
-  size_t d_coef_count = 0;
-  unsigned* d_qflags = nullptr;
-  size_t d_qflags_count = 0;
-  unsigned* d_hms = nullptr;
-  size_t d_hms_count = 0;
-  int hms_heads = 0;
-  Cand* d_bu = nullptr;
-  size_t d_bu_count = 0;
-  Cand* d_bl = nullptr;
-  size_t d_bl_count = 0;
-  uint32_t* d_shortlist = nullptr;
-  size_t d_shortlist_count = 0;
-  unsigned long long* d_hex = nullptr;
-  size_t d_hex_count = 0;
-  grm::MappedCands short_out;  // exact scores of the shortlists (host mapped)
-  grm::MappedBuf qstate;       // per query: prep flags, then status (host mapped)
-  uint32_t sel_blocks = 256;
-  uint32_t screen_waves = 8192;  // persistent screen wavefronts (all kv heads)
+  float2* d_ecoef = nullptr;
+  size_t d_ecoef_count = 0;
+  float* d_q32c = nullptr;      // query columns as fp32, d contiguous
+  size_t d_q32c_count = 0;
   uint64_t routes = 0;          // route calls
-  uint64_t fallbacks = 0;       // queries re-routed on the exact path
   std::vector<Cand> merged;
   void* d_queries = nullptr;
   size_t d_queries_bytes = 0;
@@ -115,7 +108,10 @@ struct GqaDeviceArena {
   hipEvent_t ev_stop = nullptr;
   hipEvent_t ev_mut = nullptr;
   bool mut_pending = false;
-  uint32_t fin_blocks = 256;
+  uint32_t fin_blocks = 1024;
+  // Exact-path wavefronts; the default gives every (kv head, item) pair a
+  // wavefront of its own, a smaller count makes them walk several pairs.
+  uint32_t exact_waves = 1u << 30;
 };
 
 namespace {
@@ -175,15 +171,12 @@ void destroy_arena(GqaDeviceArena* a) {
   if (a->side) (void)hipStreamSynchronize(a->side);
   void* dev[] = {a->d_keys,  a->d_scales, a->d_tok_off, a->d_len,   a->d_ids,
                  a->d_flags, a->d_nonfinite, a->d_kmax, a->d_items, a->d_hmax,
-                 a->d_qbad,  a->d_queries, a->d_stage,  a->d_bfrag, a->d_coef,
-                 a->d_hms,   a->d_bu,     a->d_bl,      a->d_shortlist, a->d_hex,
-                 a->d_qflags};
+                 a->d_qbad,  a->d_queries, a->d_stage,  a->d_bfrag, a->d_ecoef,
+                 a->d_q32c,  a->d_q64};
   for (void* p : dev) {
     if (p) (void)hipFree(p);
   }
   grm::release_mapped(&a->blocks_out);
-  grm::release_mapped(&a->short_out);
-  grm::release_mapped_bytes(&a->qstate);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
@@ -201,6 +194,9 @@ int wait_mutations(GqaDeviceArena* a) {
   return 0;
 }
 
+// Token rows a node of `len` tokens occupies in the planes.
+uint64_t padded_len(uint64_t len) { return (len + grm::gqa::kTokAlign - 1) & ~uint64_t(grm::gqa::kTokAlign - 1); }
+
 void append_items(std::vector<Item>& items, uint32_t slot, uint64_t base, uint64_t len,
                   uint32_t chunk) {
   for (uint64_t t0 = 0; t0 < len; t0 += chunk) {
@@ -209,28 +205,9 @@ void append_items(std::vector<Item>& items, uint32_t slot, uint64_t base, uint64
     it.slot = slot;
     it.t0 = static_cast<uint32_t>(t0);
     it.count = static_cast<uint32_t>(std::min<uint64_t>(chunk, len - t0));
-    it.len = static_cast<uint32_t>(len);
+    it.len = static_cast<uint32_t>(padded_len(len));
     items.push_back(it);
   }
-}
-
-int launch_stats(GqaDeviceArena* a, const Item* d_items, uint64_t n_items, hipStream_t st) {
-  if (n_items == 0) return 0;
-  const dim3 grid(static_cast<unsigned>((n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves), a->kv);
-  const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
-#define GRM_STATS(KDT)                                                              \
-  grm::gqa::gqa_key_stats_kernel<KDT><<<grid, threads, 0, st>>>(                    \
-      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, d_items,               \
-      static_cast<uint32_t>(n_items), static_cast<int>(a->hd), a->d_nonfinite, a->d_kmax)
-  switch (a->key_dtype) {
-    case kF32: GRM_STATS(kF32); break;
-    case kBF16: GRM_STATS(kBF16); break;
-    case kF16: GRM_STATS(kF16); break;
-    default: GRM_STATS(kI8); break;
-  }
-#undef GRM_STATS
-  GRM_HIP_CHECK(hipGetLastError());
-  return 0;
 }
 
 int stage_buffers(GqaDeviceArena* a, size_t bytes, unsigned char** h, unsigned char** d) {
@@ -243,22 +220,24 @@ int stage_buffers(GqaDeviceArena* a, size_t bytes, unsigned char** h, unsigned c
 }
 
 // Place `count` nodes whose keys (and scales) are packed back to back in
-// host memory at the bump pointer; `slots` are already assigned on the host.
+// host memory ([kv][len][hd] per node) at the bump pointer; `slots` are
+// already assigned on the host.  The staging copy takes the padded row
+// layout of the bank, so a staged row and its bank row share an index.
 // Everything runs on `st`; the staging buffer stays busy until `st` passes
 // the recorded mutation event.
 int place_nodes(GqaDeviceArena* a, const std::vector<uint64_t>& slots,
                 const std::vector<uint64_t>& ids, const uint64_t* tok_counts,
                 const void* keys_host, const void* scales_host, hipStream_t st) {
   const uint64_t count = slots.size();
-  uint64_t tokens = 0;
-  for (uint64_t i = 0; i < count; ++i) tokens += tok_counts[i];
+  uint64_t tokens = 0;  // padded token rows
+  for (uint64_t i = 0; i < count; ++i) tokens += padded_len(tok_counts[i]);
   const uint64_t first_tok = a->used_tokens;
   std::vector<uint64_t> offs(count);
   {
     uint64_t t = first_tok;
     for (uint64_t i = 0; i < count; ++i) {
       offs[i] = t;
-      t += tok_counts[i];
+      t += padded_len(tok_counts[i]);
     }
   }
   const size_t kbytes = tokens * token_key_bytes(a);
@@ -285,24 +264,51 @@ int place_nodes(GqaDeviceArena* a, const std::vector<uint64_t>& slots,
     meta[3 * count + i] = ids[i];
   }
   memcpy(h + o_items, items.data(), item_bytes);
-  if (kbytes) memcpy(h + o_keys, keys_host, kbytes);
-  if (sbytes) memcpy(h + o_scales, scales_host, sbytes);
+  {
+    const size_t rk = static_cast<size_t>(a->hd) * key_esize(a->key_dtype);  // bytes per key row
+    const size_t rs = token_scale_bytes(a) / a->kv;                         // bytes per scale row
+    const unsigned char* ksrc = static_cast<const unsigned char*>(keys_host);
+    const unsigned char* ssrc = static_cast<const unsigned char*>(scales_host);
+    for (uint64_t i = 0; i < count; ++i) {
+      const uint64_t L = tok_counts[i], Lp = padded_len(L);
+      const uint64_t row = (offs[i] - first_tok) * a->kv;
+      for (uint32_t g = 0; g < a->kv; ++g) {
+        if (L == 0) break;
+        memcpy(h + o_keys + (row + g * Lp) * rk, ksrc, L * rk);
+        ksrc += L * rk;
+        if (rs) {
+          memcpy(h + o_scales + (row + g * Lp) * rs, ssrc, L * rs);
+          ssrc += L * rs;
+        }
+      }
+    }
+  }
   GRM_HIP_CHECK(hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, st));
-  if (kbytes) {
-    GRM_HIP_CHECK(hipMemcpyAsync(a->d_keys + first_tok * token_key_bytes(a), d + o_keys, kbytes,
-                                 hipMemcpyDeviceToDevice, st));
-  }
-  if (sbytes) {
-    GRM_HIP_CHECK(hipMemcpyAsync(a->d_scales + first_tok * token_scale_bytes(a), d + o_scales,
-                                 sbytes, hipMemcpyDeviceToDevice, st));
-  }
   const unsigned threads = 256;
   const unsigned blocks = static_cast<unsigned>(std::min<uint64_t>((count + threads - 1) / threads, 1024));
   grm::gqa::gqa_set_slots_kernel<<<blocks, threads, 0, st>>>(
       reinterpret_cast<const uint64_t*>(d), count, a->d_tok_off, a->d_len, a->d_ids, a->d_flags,
       a->d_nonfinite, a->d_kmax);
   GRM_HIP_CHECK(hipGetLastError());
-  GRM_CHECK_RC(launch_stats(a, reinterpret_cast<const Item*>(d + o_items), items.size(), st));
+  if (!items.empty()) {
+    // staged rows -> chunk planes, with the key statistics
+    const dim3 grid(static_cast<unsigned>((items.size() + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves),
+                    a->kv);
+    const unsigned pthreads = grm::gqa::kUnitWaves * grm::kWave;
+#define GRM_PLACE(KDT)                                                                          \
+  grm::gqa::gqa_place_kernel<KDT><<<grid, pthreads, 0, st>>>(                                    \
+      reinterpret_cast<const u32x4*>(d + o_keys), d + o_scales, first_tok * a->kv, a->d_keys,    \
+      a->d_scales, a->scale_dtype, a->group_size, reinterpret_cast<const Item*>(d + o_items),    \
+      static_cast<uint32_t>(items.size()), static_cast<int>(a->hd), a->d_nonfinite, a->d_kmax)
+    switch (a->key_dtype) {
+      case kF32: GRM_PLACE(kF32); break;
+      case kBF16: GRM_PLACE(kBF16); break;
+      case kF16: GRM_PLACE(kF16); break;
+      default: GRM_PLACE(kI8); break;
+    }
+#undef GRM_PLACE
+    GRM_HIP_CHECK(hipGetLastError());
+  }
   grm::gqa::gqa_commit_slots_kernel<<<blocks, threads, 0, st>>>(
       reinterpret_cast<const uint64_t*>(d), count, a->d_flags, a->d_nonfinite);
   GRM_HIP_CHECK(hipGetLastError());
@@ -344,11 +350,13 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   for (uint64_t i = 0; i < nodes; ++i) {
     if (tok_offsets[i + 1] < tok_offsets[i]) return grm::fail(-1, "tok_offsets must be non-decreasing");
     counts[i] = tok_offsets[i + 1] - tok_offsets[i];
-    if (counts[i] > 0xffffffffull) return grm::fail(-1, "node too long");
+    if (counts[i] > 0xffffffffull - 8) return grm::fail(-1, "node too long");
   }
   if (nodes > 0) tokens = tok_offsets[nodes];
   cap_nodes = std::max(cap_nodes, nodes);
   cap_tokens = std::max(cap_tokens, tokens);
+  // room for the row padding of every node slot
+  cap_tokens += (grm::gqa::kTokAlign - 1) * cap_nodes;
   if (cap_nodes == 0) return grm::fail(-1, "bank needs nodes or capacity");
   if (cap_nodes >= 0xffffffffull) return grm::fail(-1, "node capacity too large");
   auto* a = new GqaDeviceArena();
@@ -367,25 +375,14 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   a->tok_off.assign(cap_nodes, 0);
   a->len.assign(cap_nodes, 0);
   a->slot_id.assign(cap_nodes, kNoId);
-  // Larger banks use longer work items so the grid stays near a few
-  // hundred thousand wavefronts.
-  a->chunk = cap_tokens * a->kv > (8ull << 20) ? 256 : 64;
   if (const char* env = getenv("GRM_HIP_GQA_CHUNK")) {
     const long v = strtol(env, nullptr, 10);
     if (v >= 16 && v <= 4096 && v % 16 == 0) a->chunk = static_cast<uint32_t>(v);
   }
-  if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen = env[0] != '0';
-  {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, a->device) != hipSuccess ||
-        cus <= 0) {
-      cus = 256;
-    }
-    a->screen_waves = static_cast<uint32_t>(cus) * 16;  // 4 per SIMD
-  }
-  if (const char* env = getenv("GRM_HIP_GQA_SCREEN_WAVES")) {
+  if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
+  if (const char* env = getenv("GRM_HIP_GQA_EXACT_WAVES")) {
     const long v = strtol(env, nullptr, 10);
-    if (v >= 64 && v <= (1l << 22)) a->screen_waves = static_cast<uint32_t>(v);
+    if (v >= 64 && v <= (1l << 30)) a->exact_waves = static_cast<uint32_t>(v);
   }
   std::vector<uint64_t> ids(nodes), slots(nodes);
   a->slot_of.reserve(nodes * 2);
@@ -417,14 +414,12 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_flags), cap_nodes * sizeof(uint32_t)));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_nonfinite), cap_nodes * sizeof(uint32_t)));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_kmax), cap_nodes * sizeof(unsigned)));
-  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_qbad), sizeof(unsigned)));
   BAIL_HIP(hipMemsetAsync(a->d_tok_off, 0, cap_nodes * sizeof(uint64_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_len, 0, cap_nodes * sizeof(uint32_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_ids, 0xff, cap_nodes * sizeof(uint64_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_flags, 0, cap_nodes * sizeof(uint32_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_nonfinite, 0, cap_nodes * sizeof(uint32_t), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_kmax, 0, cap_nodes * sizeof(unsigned), a->stream));
-  BAIL_HIP(hipMemsetAsync(a->d_qbad, 0, sizeof(unsigned), a->stream));
   BAIL_HIP(hipStreamSynchronize(a->stream));
 #undef BAIL_HIP
   if (const char* env = getenv("GRM_HIP_GQA_FIN_BLOCKS")) {
@@ -437,8 +432,8 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   uint64_t i0 = 0;
   while (i0 < nodes) {
     uint64_t i1 = i0, tok = 0;
-    while (i1 < nodes && (i1 == i0 || tok + counts[i1] <= batch_tokens_cap)) {
-      tok += counts[i1];
+    while (i1 < nodes && (i1 == i0 || tok + padded_len(counts[i1]) <= batch_tokens_cap)) {
+      tok += padded_len(counts[i1]);
       ++i1;
     }
     std::vector<uint64_t> bslots(slots.begin() + i0, slots.begin() + i1);
@@ -485,21 +480,58 @@ int rq_pad_of(int rq) {
   return p;
 }
 
+// Maxima for up to qb queries; all zero between routes (the finalize
+// kernel re-zeroes what it reads).
+int ensure_hmax(GqaDeviceArena* a, int H, int qb) {
+  const size_t want = static_cast<size_t>(qb) * a->cap_nodes * static_cast<size_t>(H);
+  return reserve_device_zero(&a->d_hmax, &a->d_hmax_count, want, a->stream);
+}
+
+int launch_finalize(GqaDeviceArena* a, int H, int qb, int topk, uint32_t fin_blocks, Cand* bout) {
+  const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
+  grm::gqa::gqa_finalize_kernel<<<dim3(fin_blocks, qb), per_block, 0, a->stream>>>(
+      a->d_hmax, a->cap_nodes * static_cast<size_t>(H), a->cap_nodes, H,
+      static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags, a->d_ids, a->d_qbad,
+      static_cast<int>(a->kv), topk, bout);
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
 // --------------------------------------------------------------- exact path
 
-int launch_exact_heads(GqaDeviceArena* a, const void* q, int q_dtype, int H, int Qt) {
+// Query rows of queries [0, qb) at q as doubles in d_q64; d_qbad records
+// non-finite values.
+int launch_q64(GqaDeviceArena* a, const void* q, int q_dtype, int qb, int H, int Qt) {
+  const int R = H / static_cast<int>(a->kv);
+  const int rq_pad = rq_pad_of(R * Qt);
+  GRM_CHECK_RC(reserve_device(&a->d_q64, &a->d_q64_count,
+                              static_cast<size_t>(qb) * a->kv * a->hd * rq_pad));
+  GRM_CHECK_RC(reserve_device(&a->d_qbad, &a->d_qbad_count, static_cast<size_t>(qb) * a->kv));
+  grm::gqa::gqa_q64_kernel<<<dim3(a->kv, qb), 256, 0, a->stream>>>(
+      q, q_dtype, static_cast<size_t>(H) * Qt * a->hd, Qt, static_cast<int>(a->hd),
+      static_cast<int>(a->kv), R, rq_pad, a->d_q64, a->d_qbad);
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
+int launch_exact(GqaDeviceArena* a, int H, int Qt) {
   if (a->n_items == 0) return 0;
   const int R = H / static_cast<int>(a->kv);
   const int rq_pad = rq_pad_of(R * Qt);
-  const dim3 grid(static_cast<unsigned>((a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves), a->kv);
+  // Persistent stream: about exact_waves wavefronts, each walking the
+  // (kv head, item) pairs w, w+W, ...
+  const uint64_t pairs = a->n_items * a->kv;
+  if (pairs >= 0xffffffffull) return grm::fail(-1, "too many work items");
+  const uint64_t bx = std::min<uint64_t>((pairs + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves,
+                                         (a->exact_waves + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves);
+  const dim3 grid(static_cast<unsigned>(std::max<uint64_t>(1, bx)));
   const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
-  const size_t lds = static_cast<size_t>(rq_pad) * a->hd * sizeof(double);
   const double denom = sqrt(static_cast<double>(a->hd));
 #define GRM_EXACT(KDT, RQ)                                                                  \
-  grm::gqa::gqa_exact_heads_kernel<KDT, RQ><<<grid, threads, lds, a->stream>>>(            \
+  grm::gqa::gqa_exact_kernel<KDT, RQ, grm::gqa::exact_stage_chunks<KDT, RQ>()><<<grid, threads, 0, a->stream>>>( \
       a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                   \
-      static_cast<uint32_t>(a->n_items), static_cast<int>(a->hd), R, Qt, q, q_dtype, denom,  \
-      a->d_hmax, a->cap_nodes, a->d_qbad)
+      static_cast<uint32_t>(a->n_items), static_cast<int>(a->kv), static_cast<int>(a->hd), R, \
+      Qt, a->d_q64, denom, a->d_hmax, a->cap_nodes)
 #define GRM_EXACT_RQ(KDT)                       \
   switch (rq_pad) {                             \
     case 1: GRM_EXACT(KDT, 1); break;           \
@@ -521,24 +553,13 @@ int launch_exact_heads(GqaDeviceArena* a, const void* q, int q_dtype, int H, int
   return 0;
 }
 
-// Enqueue the exact route of one query; its per-block top-k lands in
-// blocks_out at `bout`.
+// Enqueue the exact route of one query; its per-block top-k lands at bout.
 int enqueue_exact(GqaDeviceArena* a, const void* q, int q_dtype, int H, int Qt, int topk,
                   uint32_t fin_blocks, Cand* bout) {
-  if (a->hmax_heads != H || a->d_hmax_count < a->cap_nodes * static_cast<size_t>(H)) {
-    GRM_CHECK_RC(reserve_device(&a->d_hmax, &a->d_hmax_count, a->cap_nodes * static_cast<size_t>(H)));
-    GRM_HIP_CHECK(hipMemsetAsync(a->d_hmax, 0, a->d_hmax_count * sizeof(unsigned long long), a->stream));
-    a->hmax_heads = H;
-  }
-  GRM_CHECK_RC(launch_exact_heads(a, q, q_dtype, H, Qt));
-  const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
-  grm::gqa::gqa_finalize_kernel<<<fin_blocks, per_block, 0, a->stream>>>(
-      a->d_hmax, a->cap_nodes, H, static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags,
-      a->d_ids, a->d_qbad, topk, bout);
-  GRM_HIP_CHECK(hipGetLastError());
-  grm::gqa::gqa_clear_flags_kernel<<<1, 64, 0, a->stream>>>(a->d_qbad, 1);
-  GRM_HIP_CHECK(hipGetLastError());
-  return 0;
+  GRM_CHECK_RC(ensure_hmax(a, H, 1));
+  GRM_CHECK_RC(launch_q64(a, q, q_dtype, 1, H, Qt));
+  GRM_CHECK_RC(launch_exact(a, H, Qt));
+  return launch_finalize(a, H, 1, topk, fin_blocks, bout);
 }
 
 void write_result(const Cand* merged, int topk, uint64_t* out_ids, float* out_scores) {
@@ -550,175 +571,120 @@ void write_result(const Cand* merged, int topk, uint64_t* out_ids, float* out_sc
   }
 }
 
-// -------------------------------------------------------------- screen path
+// ---------------------------------------------------- screen-and-refine path
 
-struct ScreenPlan {
+struct SrPlan {
   int R = 0, Qt = 0, H = 0;
   int KS = 0;        // head_dim / 32
-  int qb_max = 0;    // queries per screen pass (<= 64 columns)
-  int M = 0;         // shortlist length
+  int qb_max = 0;    // queries per pass (<= 64 columns)
   int mfma = kBF16;  // MFMA operand type
 };
 
-bool screen_plan(const GqaDeviceArena* a, int H, int Qt, int topk, ScreenPlan* p) {
-  if (!a->screen || a->key_dtype == kF32) return false;
+// Maxima memory per pass is bounded by this many bytes (when one query
+// alone needs more, passes take one query).
+constexpr size_t kMaxHmaxBytes = 2ull << 30;
+
+bool sr_plan(const GqaDeviceArena* a, int H, int Qt, SrPlan* p) {
+  if (a->screen_mode == 0 || a->key_dtype == kF32) return false;
   if (a->hd != 64 && a->hd != 128 && a->hd != 256) return false;
   const int R = H / static_cast<int>(a->kv);
-  if (R * Qt > 64) return false;
+  if (R * Qt > grm::gqa::kMaxCols) return false;
   p->R = R;
   p->Qt = Qt;
   p->H = H;
   p->KS = static_cast<int>(a->hd / 32);
-  p->qb_max = std::max(1, 64 / (R * Qt));
-  p->M = std::min(grm::gqa::kMaxShort - 1, std::max(16, 2 * topk));
+  const size_t per_q = a->cap_nodes * static_cast<size_t>(H) * sizeof(unsigned long long);
+  p->qb_max = std::max(1, std::min(grm::gqa::kMaxCols / (R * Qt),
+                                   static_cast<int>(std::max<size_t>(1, kMaxHmaxBytes / per_q))));
   p->mfma = a->key_dtype == kBF16 ? kBF16 : kF16;
   return true;
 }
 
-// Enqueue the screen route of queries [q0, q0+qb) of a call of q_total
-// queries (device pointer `qbase`, `qstride` bytes per query).  Shortlist
-// exact scores land in short_out at q0*M; qstate holds the queries' prep
-// flags at [q] and certificate status at [q_total + q].
-int enqueue_screen(GqaDeviceArena* a, const ScreenPlan& p, const unsigned char* qbase,
-                   size_t qstride, int q_dtype, int q0, int qb, int q_total, int topk) {
+// Enqueue one screen-and-refine pass over queries [0, qb) at qptr (device,
+// `qstride` bytes apart); their per-block top-k lands at bout.
+int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
+               int topk, uint32_t fin_blocks, Cand* bout) {
   const int kv = static_cast<int>(a->kv);
-  const int cols = qb * p.R * p.Qt;
-  const int NT = (cols + 15) / 16;
-  const int ntp = NT <= 1 ? 1 : (NT <= 2 ? 2 : 4);
+  const int RQ = p.R * p.Qt;
+  const int cols = qb * RQ;
+  const int nt_need = (cols + 15) / 16;
+  const int NT = nt_need <= 1 ? 1 : (nt_need <= 2 ? 2 : 4);
   const int H = p.H;
-  const int M = p.M;
-  const int mU = M + 1;
   GRM_CHECK_RC(reserve_device(&a->d_bfrag, &a->d_bfrag_count,
-                              static_cast<size_t>(kv) * ntp * p.KS * grm::kWave));
-  GRM_CHECK_RC(reserve_device(&a->d_coef, &a->d_coef_count, static_cast<size_t>(p.qb_max)));
-  if (a->hms_heads != H || a->d_hms_count < static_cast<size_t>(p.qb_max) * a->cap_nodes * H) {
-    a->d_hms_count = 0;
-    GRM_CHECK_RC(reserve_device_zero(&a->d_hms, &a->d_hms_count,
-                                     static_cast<size_t>(p.qb_max) * a->cap_nodes * H, a->stream));
-    a->hms_heads = H;
-  }
-  const uint32_t n_slots = static_cast<uint32_t>(a->high_water);
-  const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
-  const uint32_t nblk = std::max<uint32_t>(1, std::min<uint32_t>((n_slots + per_block - 1) / per_block, a->sel_blocks));
-  GRM_CHECK_RC(reserve_device(&a->d_bu, &a->d_bu_count, static_cast<size_t>(qb) * nblk * mU));
-  GRM_CHECK_RC(reserve_device(&a->d_bl, &a->d_bl_count, static_cast<size_t>(qb) * nblk * topk));
-  GRM_CHECK_RC(reserve_device(&a->d_shortlist, &a->d_shortlist_count, static_cast<size_t>(p.qb_max) * M));
-  if (a->d_hex_count < static_cast<size_t>(p.qb_max) * M * H) {
-    a->d_hex_count = 0;
-    GRM_CHECK_RC(reserve_device_zero(&a->d_hex, &a->d_hex_count, static_cast<size_t>(p.qb_max) * M * H,
-                                     a->stream));
-  }
-  GRM_CHECK_RC(reserve_device(&a->d_qflags, &a->d_qflags_count, static_cast<size_t>(p.qb_max)));
-  // 1. query prep (fragments, error coefficient, flags)
-  grm::gqa::gqa_clear_flags_kernel<<<(qb + 63) / 64, 64, 0, a->stream>>>(a->d_qflags, qb);
-  GRM_HIP_CHECK(hipGetLastError());
-  const unsigned char* qptr = qbase + static_cast<size_t>(q0) * qstride;
+                              static_cast<size_t>(kv) * NT * p.KS * grm::kWave));
+  GRM_CHECK_RC(reserve_device(&a->d_ecoef, &a->d_ecoef_count, static_cast<size_t>(kv) * NT * 16));
+  GRM_CHECK_RC(reserve_device(&a->d_q32c, &a->d_q32c_count,
+                              static_cast<size_t>(kv) * NT * 16 * a->hd));
+  GRM_CHECK_RC(reserve_device(&a->d_qbad, &a->d_qbad_count, static_cast<size_t>(qb) * kv));
+  GRM_CHECK_RC(ensure_hmax(a, H, p.qb_max));
+  // 1. query preparation.  Error-bound constants (per query column):
+  //   gamma  fp32 accumulation of hd products, MFMA internal order unknown
+  //   delta  rounding of an fp32 query value to the MFMA type
+  //   sigma_q, sigma_k  a query / key value near zero flushed or rounded
+  //   sigma_p  a product lost to fp32 underflow
   const double gamma = 2.0 * (a->hd + 2.0 * p.KS) * ldexp(1.0, -24);
-  double delta = 0.0, sigma = 0.0;
+  double delta, sigma_q, sigma_k, sigma_p;
+  int emax;
   if (p.mfma == kBF16) {
     delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
-    sigma = ldexp(1.0, -130);
+    sigma_q = sigma_k = sigma_p = ldexp(1.0, -125);
+    emax = 126;
   } else {
     delta = q_dtype == kF32 ? ldexp(1.0, -11) : 0.0;
-    sigma = ldexp(1.0, -25);
+    sigma_q = sigma_k = ldexp(1.0, -14);
+    sigma_p = 0.0;
+    emax = 15;
   }
+  const size_t q_elems = static_cast<size_t>(H) * p.Qt * a->hd;
+#define GRM_SR_PREP(MT)                                                                        \
+  grm::gqa::gqa_sr_prep_kernel<MT><<<kv, 256, 0, a->stream>>>(                                 \
+      qptr, q_dtype, q_elems, qb, p.Qt, static_cast<int>(a->hd), kv, p.R, NT, p.KS, emax,        \
+      gamma, delta, sigma_q, sigma_k, sigma_p, a->d_bfrag, a->d_ecoef, a->d_q32c, a->d_qbad)
   if (p.mfma == kBF16) {
-    grm::gqa::gqa_query_prep_kernel<kBF16><<<kv + qb, 256, 0, a->stream>>>(
-        qptr, q_dtype, qb, H, p.Qt, static_cast<int>(a->hd), kv, p.R, ntp, p.KS, a->d_bfrag,
-        a->d_qflags, a->d_coef, gamma, delta, sigma);
+    GRM_SR_PREP(kBF16);
   } else {
-    grm::gqa::gqa_query_prep_kernel<kF16><<<kv + qb, 256, 0, a->stream>>>(
-        qptr, q_dtype, qb, H, p.Qt, static_cast<int>(a->hd), kv, p.R, ntp, p.KS, a->d_bfrag,
-        a->d_qflags, a->d_coef, gamma, delta, sigma);
+    GRM_SR_PREP(kF16);
   }
+#undef GRM_SR_PREP
   GRM_HIP_CHECK(hipGetLastError());
-  // 2. screen
+  // 2. screen and refine every (item, kv head)
   if (a->n_items > 0) {
-    // Persistent stream: about screen_waves wavefronts in all, spread over
-    // the kv heads (grid y); each walks items w, w+W, ...
-    const uint64_t per_plane = std::max<uint64_t>(1, a->screen_waves / a->kv);
-    const uint64_t bx = std::min<uint64_t>((a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves,
-                                           (per_plane + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves);
-    const dim3 grid(static_cast<unsigned>(std::max<uint64_t>(1, bx)), a->kv);
+    const dim3 grid(static_cast<unsigned>((a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves),
+                    a->kv);
     const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
     const size_t hstride = a->cap_nodes * static_cast<size_t>(H);
-#define GRM_SCREEN(KDT, KS, NTT)                                                              \
-  grm::gqa::gqa_screen_kernel<KDT, KS, NTT><<<grid, threads, 0, a->stream>>>(                 \
-      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                      \
-      static_cast<uint32_t>(a->n_items), p.R, p.Qt, cols, a->d_bfrag, a->d_hms, hstride,      \
+    const double denom = sqrt(static_cast<double>(a->hd));
+    const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);  // <= 64 KiB
+#define GRM_SR(KDT, KS, NTT)                                                                    \
+  grm::gqa::gqa_sr_kernel<KDT, KS, NTT><<<grid, threads, lds, a->stream>>>(                     \
+      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                        \
+      static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, cols, a->d_bfrag, a->d_ecoef,             \
+      a->d_q32c, a->d_qbad, reinterpret_cast<const float*>(a->d_kmax), denom, a->d_hmax, hstride, \
       a->cap_nodes)
-#define GRM_SCREEN_NT(KDT, KS)                 \
-  switch (ntp) {                               \
-    case 1: GRM_SCREEN(KDT, KS, 1); break;     \
-    case 2: GRM_SCREEN(KDT, KS, 2); break;     \
-    default: GRM_SCREEN(KDT, KS, 4); break;    \
+#define GRM_SR_NT(KDT, KS)                 \
+  switch (NT) {                            \
+    case 1: GRM_SR(KDT, KS, 1); break;     \
+    case 2: GRM_SR(KDT, KS, 2); break;     \
+    default: GRM_SR(KDT, KS, 4); break;    \
   }
-#define GRM_SCREEN_KS(KDT)                     \
-  switch (p.KS) {                              \
-    case 2: GRM_SCREEN_NT(KDT, 2); break;      \
-    case 4: GRM_SCREEN_NT(KDT, 4); break;      \
-    default: GRM_SCREEN_NT(KDT, 8); break;     \
+#define GRM_SR_KS(KDT)                     \
+  switch (p.KS) {                          \
+    case 2: GRM_SR_NT(KDT, 2); break;      \
+    case 4: GRM_SR_NT(KDT, 4); break;      \
+    default: GRM_SR_NT(KDT, 8); break;     \
   }
     switch (a->key_dtype) {
-      case kBF16: GRM_SCREEN_KS(kBF16); break;
-      case kF16: GRM_SCREEN_KS(kF16); break;
-      default: GRM_SCREEN_KS(kI8); break;
+      case kBF16: GRM_SR_KS(kBF16); break;
+      case kF16: GRM_SR_KS(kF16); break;
+      default: GRM_SR_KS(kI8); break;
     }
-#undef GRM_SCREEN_KS
-#undef GRM_SCREEN_NT
-#undef GRM_SCREEN
+#undef GRM_SR_KS
+#undef GRM_SR_NT
+#undef GRM_SR
     GRM_HIP_CHECK(hipGetLastError());
   }
-  // 3. select, 4. shortlist + certificate
-  const float inv_scale = static_cast<float>(1.0 / (H * sqrt(static_cast<double>(a->hd))));
-  const float slack_rel = static_cast<float>((H + 8) * ldexp(1.0, -22));
-  grm::gqa::gqa_select_kernel<<<dim3(nblk, qb), per_block, 0, a->stream>>>(
-      a->d_hms, a->cap_nodes * static_cast<size_t>(H), a->cap_nodes, H, n_slots, a->d_len,
-      a->d_flags, a->d_ids,
-      reinterpret_cast<const float*>(a->d_kmax), a->d_coef, inv_scale, slack_rel, mU, topk,
-      a->d_bu, a->d_bl);
-  GRM_HIP_CHECK(hipGetLastError());
-  unsigned* out_flags = static_cast<unsigned*>(a->qstate.dev) + q0;
-  unsigned* out_status = static_cast<unsigned*>(a->qstate.dev) + q_total + q0;
-  grm::gqa::gqa_shortlist_kernel<<<qb, per_block, 0, a->stream>>>(
-      a->d_bu, a->d_bl, nblk, mU, topk, M, a->d_shortlist, a->d_qflags, out_flags, out_status);
-  GRM_HIP_CHECK(hipGetLastError());
-  // 5. exact rescore of the shortlist, 6. exact scores out
-  const int rq_pad = rq_pad_of(p.R * p.Qt);
-  const uint32_t max_chunks = std::max<uint32_t>(1, (a->max_len + grm::kWave - 1) / grm::kWave);
-  const uint64_t units = static_cast<uint64_t>(qb) * M * max_chunks;
-  const dim3 rgrid(static_cast<unsigned>((units + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves), a->kv);
-  const size_t lds = static_cast<size_t>(grm::gqa::kUnitWaves) * rq_pad * a->hd * sizeof(double);
-  const double denom = sqrt(static_cast<double>(a->hd));
-  const size_t q_elems = static_cast<size_t>(H) * p.Qt * a->hd;
-#define GRM_RESCORE(KDT, RQ)                                                                  \
-  grm::gqa::gqa_rescore_kernel<KDT, RQ><<<rgrid, grm::gqa::kUnitWaves * grm::kWave, lds, a->stream>>>( \
-      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_tok_off, a->d_len,           \
-      a->d_shortlist, M, qb, max_chunks, kv, static_cast<int>(a->hd), p.R, p.Qt, qptr,          \
-      q_dtype, q_elems, denom, a->d_hex)
-#define GRM_RESCORE_RQ(KDT)                     \
-  switch (rq_pad) {                             \
-    case 1: GRM_RESCORE(KDT, 1); break;         \
-    case 2: GRM_RESCORE(KDT, 2); break;         \
-    case 4: GRM_RESCORE(KDT, 4); break;         \
-    case 8: GRM_RESCORE(KDT, 8); break;         \
-    case 16: GRM_RESCORE(KDT, 16); break;       \
-    default: GRM_RESCORE(KDT, 32); break;       \
-  }
-  switch (a->key_dtype) {
-    case kBF16: GRM_RESCORE_RQ(kBF16); break;
-    case kF16: GRM_RESCORE_RQ(kF16); break;
-    default: GRM_RESCORE_RQ(kI8); break;
-  }
-#undef GRM_RESCORE_RQ
-#undef GRM_RESCORE
-  GRM_HIP_CHECK(hipGetLastError());
-  const uint32_t total = static_cast<uint32_t>(qb) * M;
-  grm::gqa::gqa_rescore_finalize_kernel<<<(total + 255) / 256, 256, 0, a->stream>>>(
-      a->d_hex, H, a->d_shortlist, total, a->d_len, a->d_ids,
-      a->short_out.dev + static_cast<size_t>(q0) * M);
-  GRM_HIP_CHECK(hipGetLastError());
-  return 0;
+  // 3. exact scores and per-block top-k
+  return launch_finalize(a, H, qb, topk, fin_blocks, bout);
 }
 
 int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_device, int q_count,
@@ -735,9 +701,6 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   }
   const int R = H / static_cast<int>(a->kv);
   if (R * Qt > grm::gqa::kMaxRQ) return grm::fail(-1, "(heads / kv_heads) * query_tokens above 32");
-  if (static_cast<size_t>(rq_pad_of(R * Qt)) * a->hd * sizeof(double) * grm::gqa::kUnitWaves > 65536) {
-    return grm::fail(-1, "(heads / kv_heads) * query_tokens * head_dim above 2048");
-  }
   GRM_HIP_CHECK(hipSetDevice(a->device));
   if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
   GRM_CHECK_RC(ensure_items(a));
@@ -752,72 +715,37 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
     qbase = static_cast<const unsigned char*>(a->d_queries);
   }
   const uint32_t n_slots = static_cast<uint32_t>(a->high_water);
-  const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
-  const uint32_t fin_blocks = std::max<uint32_t>(1, std::min<uint32_t>((n_slots + per_block - 1) / per_block, a->fin_blocks));
+  const uint32_t fin_blocks = std::max<uint32_t>(
+      1, std::min<uint32_t>((n_slots + grm::gqa::kFinSlots - 1) / grm::gqa::kFinSlots, a->fin_blocks));
   const size_t per_q = static_cast<size_t>(fin_blocks) * topk;
+  GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * q_count));
   a->merged.resize(topk);
-  ScreenPlan plan;
-  const bool use_screen = screen_plan(a, H, Qt, topk, &plan);
-  std::vector<int> redo;
-  if (use_screen) {
-    GRM_CHECK_RC(grm::reserve_mapped(&a->short_out, static_cast<size_t>(q_count) * plan.M));
-    GRM_CHECK_RC(grm::reserve_mapped_bytes(&a->qstate, static_cast<size_t>(q_count) * 2 * sizeof(unsigned)));
-    // untimed warmup queries first, then the timed ones
-    int q0 = 0;
-    const int segments[2][2] = {{0, warmup}, {warmup, q_count}};
-    for (const auto& seg : segments) {
-      if (seg[0] == warmup) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
-      for (q0 = seg[0]; q0 < seg[1]; q0 += plan.qb_max) {
+  SrPlan plan;
+  const bool use_sr = sr_plan(a, H, Qt, &plan);
+  // untimed warmup queries first, then the timed ones
+  const int segments[2][2] = {{0, warmup}, {warmup, q_count}};
+  for (const auto& seg : segments) {
+    if (seg[0] == warmup) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+    if (use_sr) {
+      for (int q0 = seg[0]; q0 < seg[1]; q0 += plan.qb_max) {
         const int qb = std::min(plan.qb_max, seg[1] - q0);
-        GRM_CHECK_RC(enqueue_screen(a, plan, qbase, qstride, q_dtype, q0, qb, q_count, topk));
+        GRM_CHECK_RC(enqueue_sr(a, plan, qbase + static_cast<size_t>(q0) * qstride, q_dtype, qb, topk,
+                                fin_blocks, a->blocks_out.dev + static_cast<size_t>(q0) * per_q));
       }
-    }
-    GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
-    GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
-    const unsigned* st = static_cast<const unsigned*>(a->qstate.host);
-    for (int qi = 0; qi < q_count; ++qi) {
-      const unsigned flags = st[qi], certified = st[q_count + qi];
-      if (flags != 0u || certified != 1u) {
-        redo.push_back(qi);
-        continue;
-      }
-      grm::host_topk_merge(a->short_out.host + static_cast<size_t>(qi) * plan.M, plan.M, topk,
-                           a->merged.data());
-      write_result(a->merged.data(), topk, out_ids + static_cast<size_t>(qi) * topk,
-                   out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
-    }
-    a->fallbacks += redo.size();
-  } else {
-    for (int qi = 0; qi < q_count; ++qi) redo.push_back(qi);
-  }
-  if (!redo.empty()) {
-    GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * redo.size()));
-    if (!use_screen) {
-      if (warmup > 0) {
-        for (int qi = 0; qi < warmup; ++qi) {
-          GRM_CHECK_RC(enqueue_exact(a, qbase + qi * qstride, q_dtype, H, Qt, topk, fin_blocks,
-                                     a->blocks_out.dev + static_cast<size_t>(qi) * per_q));
-        }
-      }
-      GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
-      for (int qi = warmup; qi < q_count; ++qi) {
-        GRM_CHECK_RC(enqueue_exact(a, qbase + qi * qstride, q_dtype, H, Qt, topk, fin_blocks,
-                                   a->blocks_out.dev + static_cast<size_t>(qi) * per_q));
-      }
-      GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
     } else {
-      for (size_t j = 0; j < redo.size(); ++j) {
-        GRM_CHECK_RC(enqueue_exact(a, qbase + redo[j] * qstride, q_dtype, H, Qt, topk, fin_blocks,
-                                   a->blocks_out.dev + j * per_q));
+      for (int qi = seg[0]; qi < seg[1]; ++qi) {
+        GRM_CHECK_RC(enqueue_exact(a, qbase + static_cast<size_t>(qi) * qstride, q_dtype, H, Qt, topk,
+                                   fin_blocks, a->blocks_out.dev + static_cast<size_t>(qi) * per_q));
       }
     }
-    GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
-    for (size_t j = 0; j < redo.size(); ++j) {
-      const int qi = redo[j];
-      grm::host_topk_merge(a->blocks_out.host + j * per_q, per_q, topk, a->merged.data());
-      write_result(a->merged.data(), topk, out_ids + static_cast<size_t>(qi) * topk,
-                   out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
-    }
+  }
+  GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
+  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  for (int qi = 0; qi < q_count; ++qi) {
+    grm::host_topk_merge(a->blocks_out.host + static_cast<size_t>(qi) * per_q, per_q, topk,
+                         a->merged.data());
+    write_result(a->merged.data(), topk, out_ids + static_cast<size_t>(qi) * topk,
+                 out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
   }
   if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
   grm::clear_error();
@@ -928,8 +856,8 @@ extern "C" int grm_gqa_hip_append(GqaDeviceArena* a, const void* keys_host,
           !seen.emplace(node_ids[i], 1).second) {
         return grm::fail(-1, "append id already live, repeated or reserved");
       }
-      if (tok_counts[i] > 0xffffffffull) return grm::fail(-1, "node too long");
-      tokens += tok_counts[i];
+      if (tok_counts[i] > 0xffffffffull - 8) return grm::fail(-1, "node too long");
+      tokens += padded_len(tok_counts[i]);
     }
   }
   if (tokens > 0 && !keys_host) return grm::fail(-1, "null keys");
@@ -1029,7 +957,7 @@ extern "C" int grm_gqa_hip_compact(GqaDeviceArena* a) {
   for (size_t i = 0; i < order.size(); ++i) {
     const uint64_t s = order[i];
     const uint64_t src = a->tok_off[s];
-    const uint64_t n = a->len[s];
+    const uint64_t n = padded_len(a->len[s]);
     if (src != dst && n > 0) {
       if (src - dst >= n) {
         GRM_HIP_CHECK(hipMemcpyAsync(a->d_keys + dst * kb, a->d_keys + src * kb, n * kb,

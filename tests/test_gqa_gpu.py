@@ -218,9 +218,9 @@ def test_screen_path_matches_exact_path(hip_lib, monkeypatch, Qt):
         assert_same(r, ids, sc)
 
 
-def test_tied_nodes_fall_back_to_exact_path(hip_lib):
-    # 100 identical nodes tie exactly: no shortlist of 16 can be certified,
-    # so the query is re-routed on the exact path; ties go to the lowest id.
+def test_tied_nodes_order_by_lowest_id(hip_lib):
+    # 100 identical nodes tie exactly on the screen-and-refine path; the
+    # exact maxima are equal, so the order falls to the node ids.
     rng = np.random.default_rng(8)
     block = rng.standard_normal(8 * 40 * 64).astype(np.float32)
     others = rng.standard_normal(8 * 40 * 64 * 5).astype(np.float32) * 0.1
@@ -248,4 +248,63 @@ def test_f32_queries_on_half_banks(hip_lib, dtype):
         res = bank.route(qs, 4)
     code = oracle.BF16 if dtype == "bf16" else oracle.F16
     ids, sc, _ = oracle.gqa_route(keys, code, offs, 8, 64, qs, 4)
+    assert_same(res, ids, sc)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_repeated_tokens_within_nodes(hip_lib, dtype):
+    # Nodes whose key tokens repeat: screened values tie three or more ways,
+    # so the item is screened again and every candidate is recomputed.
+    rng = np.random.default_rng(17)
+    kv, hd, H = 4, 64, 16
+    lens = rng.integers(1, 300, size=60).astype(np.uint64)
+    lens[:4] = [1, 16, 17, 299]
+    offs = np.zeros(lens.size + 1, np.uint64)
+    offs[1:] = np.cumsum(lens)
+    blocks = []
+    for i, L in enumerate(lens.tolist()):
+        if i % 3 == 0:  # one token repeated L times per kv head
+            tok = rng.standard_normal((kv, 1, hd)).astype(np.float32)
+            blocks.append(np.repeat(tok, L, axis=1))
+        elif i % 3 == 1:  # a few distinct tokens, each repeated
+            toks = rng.standard_normal((kv, 3, hd)).astype(np.float32)
+            blocks.append(toks[:, rng.integers(0, 3, size=L), :])
+        else:
+            blocks.append(rng.standard_normal((kv, L, hd)).astype(np.float32))
+    keys = np.concatenate([b.reshape(-1) for b in blocks])
+    bits = oracle.bf16_bits(keys) if dtype == "bf16" else oracle.f16_bits(keys)
+    code = oracle.BF16 if dtype == "bf16" else oracle.F16
+    qs = rng.standard_normal((3, H, 2, hd)).astype(np.float32)
+    with GqaNodeBank(bits, offs, kv_heads=kv, head_dim=hd, dtype=dtype) as bank:
+        res = bank.route(qs, 8)
+    ids, sc, _ = oracle.gqa_route(bits, code, offs, kv, hd, qs, 8)
+    assert_same(res, ids, sc)
+
+
+@pytest.mark.parametrize("scale", [3.0e6, 1.0e-7])
+def test_f16_bank_queries_outside_half_range(hip_lib, scale):
+    # Query values beyond (or far below) the fp16 range are screened with a
+    # power-of-two column scale; the result still follows the fp64 law.
+    lens = wl.gqa_lengths(120, seed=51, lo=1, hi=100)
+    keys, offs = wl.gqa_bank(lens, 4, 128, seed=51, dtype="f16")
+    qs = wl.gqa_queries(2, 16, 1, 128, seed=51, dtype="f32") * np.float32(scale)
+    qs[0, 3, 0, 7] = np.float32(70000.0 * max(scale, 1.0))
+    with GqaNodeBank(keys, offs, kv_heads=4, head_dim=128, dtype="f16") as bank:
+        res = bank.route(qs, 6)
+    ids, sc, _ = oracle.gqa_route(keys, oracle.F16, offs, 4, 128, qs, 6)
+    assert_same(res, ids, sc)
+
+
+def test_int8_bank_batched_queries(hip_lib):
+    # 16 queries x 4 heads per kv head = 64 query columns in one pass.
+    rng = np.random.default_rng(61)
+    keys, offs = ragged(rng, 300, 8, 128, 1, 400)
+    codes, scales = oracle.quantize_int8(keys.reshape(-1, 128), 32, "f16")
+    qs = rng.standard_normal((16, 32, 1, 128)).astype(np.float32)
+    with GqaNodeBank(codes, offs, kv_heads=8, head_dim=128, dtype="i8",
+                     scales=scales, scale_dtype="f16", group_size=32) as bank:
+        res = bank.route(qs, 5)
+    ids, sc, _ = oracle.gqa_route(codes, oracle.I8, offs, 8, 128, qs, 5,
+                                  scales=scales, scale_dtype="f16",
+                                  group_size=32)
     assert_same(res, ids, sc)
