@@ -17,6 +17,12 @@ ABI (kernel + top-k + device->host copy of the k results).  Reported:
              this host's cores for a bounded number of queries
 
 Prints one JSON line on stdout; progress goes to stderr.
+
+`roofline.traffic` is the HBM bytes per launch that rocprofv3 counted for
+the kernel (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter reads
+for a device-to-device copy of known size); the figures and the commands
+that produced them are in profiles/, read from profiles/traffic.json.
+`--copy-calibration` runs that copy (1 GiB, 5 times) and nothing else.
 """
 
 from __future__ import annotations
@@ -42,6 +48,29 @@ def log(msg: str) -> None:
 
 def pct(xs, p):
     return float(np.percentile(np.asarray(xs, dtype=np.float64), p))
+
+
+def copy_calibration(gib: float = 1.0, reps: int = 5) -> dict:
+    """A device-to-device copy of known size, for scaling rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    n = int(gib * (1 << 30)) // 4
+    src = torch.full((n,), 1.0, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "reps": reps}
+
+
+def load_traffic() -> dict:
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        return json.loads(path.read_text())
+    except (OSError, ValueError):
+        return {}
 
 
 def bench_mla(steps: int, warmup: int):
@@ -149,6 +178,8 @@ def main() -> int:
     ap.add_argument("--only", choices=["all", "mla", "gqa"], default="all")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run the 1 GiB device copy used to scale counters")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -158,6 +189,11 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    if args.copy_calibration:
+        print(json.dumps(copy_calibration()), flush=True)
+        return 0
+
+    traffic = load_traffic()
     out = {}
     m = g = None
     if args.only in ("all", "mla"):
@@ -191,8 +227,8 @@ def main() -> int:
             "roofline": {"bound": "hbm", "achieved": round(m["achieved"], 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(m["achieved"] / HBM_PEAK_GBS, 4),
-                         "traffic": None,
-                         "kernel": "mla_route_kernel<f32>",
+                         "traffic": traffic.get("mla_route", {}).get("bytes_per_launch"),
+                         "kernel": "mla_route_pipe_kernel<f32, 16, 9>",
                          "bytes_per_launch": m["bytes"]},
         }
     if g is not None:
@@ -208,6 +244,8 @@ def main() -> int:
             "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),
+                         "traffic": traffic.get("gqa_sr", {}).get("bytes_per_launch"),
+                         "kernel": "gqa_sr_kernel<bf16, 4, 1>",
                          "bytes_per_call": g["bytes"]},
         }
         if out:

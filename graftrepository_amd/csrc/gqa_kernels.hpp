@@ -40,19 +40,29 @@ constexpr int kFinWaves = 4;      // wavefronts per finalize block
 constexpr int kMaxRQ = 32;        // R * Qt supported by the exact kernels
 constexpr uint32_t kMaxHeadDim = 512;
 
-// Key chunk planes.  The block of (slot, kv head g) -- the slot's key
-// tokens of head_dim values, in L rows (the token count rounded up to
-// kTokAlign) -- is stored as C = head_dim / epc planes of L 16-byte chunks
-// (epc values each): chunk c of token t is chunk index row0 * C + c * L + t
-// of the key arena, with row0 = tok_off * kv + g * L.  INT8 scales follow
-// the same rule per group: scale of group j of token t is element
-// row0 * G + j * L + t (G = head_dim / group_size).  A wave that gives one
-// token to each lane reads 64 consecutive chunks -- 1 KiB -- per load
-// instruction; every run of kTokAlign tokens starts a 128-byte line, so no
-// two streams share a line; a slot's blocks stay contiguous
+// Key chunk planes.  A key row of head_dim values is C 16-byte pieces
+// (epc values each); S consecutive pieces (S = 4 when the row is a
+// multiple of 64 bytes, else 2 or 1) form a chunk.  The block of (slot,
+// kv head g) -- the slot's key tokens, in L rows (the token count rounded
+// up to kTokAlign) -- is stored as C/S planes of L chunks: piece p of
+// token t is piece index
+//     row0 * C + (p / S) * L * S + t * S + p % S
+// of the key arena, with row0 = tok_off * kv + g * L.  INT8 scales are
+// planes per group: scale of group j of token t is element
+// row0 * G + j * L + t (G = head_dim / group_size).  Sixteen consecutive
+// tokens' chunk is one contiguous run (1 KiB with S = 4), a token's row is
+// C/S whole chunks, every run of kTokAlign tokens starts a 128-byte line
+// (no two streams share a line), and a slot's blocks stay contiguous
 // (tok_off * kv * head_dim values), so whole nodes move as one copy.  Rows
 // past the token count are never read.
 constexpr uint32_t kTokAlign = 8;
+
+// Piece p of token t of a block whose piece 0 is at `kb` (S = 1 << sS).
+__device__ inline const u32x4* piece_ptr(const u32x4* kb, uint64_t L, int sS, uint32_t t,
+                                         int p) {
+  return kb + (static_cast<uint64_t>(p >> sS) * L << sS) + (static_cast<uint64_t>(t) << sS) +
+         (p & ((1 << sS) - 1));
+}
 
 // Work item: `count` consecutive key tokens, from t0, of one slot (all kv
 // heads).  `base` = tok_off[slot] * kv, so row0 of kv head g is
@@ -173,7 +183,7 @@ template <int KDT, int RQ, int NB>
 __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
     const unsigned char* __restrict__ keys,
     const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
-    const Item* __restrict__ items, uint32_t n_items, int kv, int hd, int R,
+    const Item* __restrict__ items, uint32_t n_items, int kv, int hd, int sS, int R,
     int Qt, const double* __restrict__ q64, double denom,
     unsigned long long* __restrict__ hmax, size_t cap) {
   using T = KeyTraits<KDT>;
@@ -195,11 +205,11 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
   auto load = [&](u32x4 (&v)[NB], float (&sc)[NB], const Item& it, int g, uint32_t t, int b) {
     const uint64_t row0 = it.base + static_cast<uint64_t>(g) * it.len;
     const uint32_t tl = min(t + lane, it.t0 + it.count - 1);
-    const u32x4* kp = reinterpret_cast<const u32x4*>(keys) + row0 * C + tl;
+    const u32x4* kb = reinterpret_cast<const u32x4*>(keys) + row0 * C;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int c = min(b * NB + j, C - 1);
-      v[j] = __builtin_nontemporal_load(kp + static_cast<uint64_t>(c) * it.len);
+      v[j] = __builtin_nontemporal_load(piece_ptr(kb, it.len, sS, tl, c));
       sc[j] = 0.0f;
       if constexpr (KDT == kI8) {
         sc[j] = load_scale(scales + (row0 * G + tl) * ses, scale_dtype,
@@ -334,20 +344,25 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
   const int wave = threadIdx.x / kWave;
   const int qb = blockIdx.y;
   hmax += qb * hstride;
-  bool q_bad = false;
-  for (int g0 = 0; g0 < kv; g0 += kWave) {  // one vector load per 64 heads
-    const bool b = g0 + lane < kv && qbad[qb * kv + g0 + lane] != 0u;
-    q_bad = q_bad || __ballot(b) != 0ull;
+  // Every load a group needs is issued before any result is used: slot
+  // metadata, ids and the query flags ride along with the maxima.
+  unsigned qbad_lane = 0u;
+  for (int g0 = 0; g0 < kv; g0 += kWave) {
+    if (g0 + lane < kv) qbad_lane |= qbad[qb * kv + g0 + lane];
   }
   WaveList L;
   wl_init(L);
+  bool q_bad = false;
+  bool q_bad_known = false;
   for (uint32_t base = blockIdx.x * kFinSlots; base < n_slots; base += gridDim.x * kFinSlots) {
     const uint32_t slot = base + lane;
     const bool in = slot < n_slots;
     uint32_t f = 0u, len = 0u;
+    uint64_t id = kNoId;
     if (wave == 0 && in) {
       f = flags[slot];
       len = lens[slot];
+      id = ids[slot];
     }
     double total = 0.0;
     for (int h0 = 0; h0 < H; h0 += kFinHeads) {
@@ -362,16 +377,35 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
         const int h = wave + kFinWaves * i;
-        if (h < nh) {
-          s_h[h][lane] = v[i];
-          if (in) hmax[(h0 + h) * cap + slot] = 0ull;
-        }
+        if (h < nh) s_h[h][lane] = v[i];
+      }
+      // The re-zeroing stores go after every LDS write: a store in between
+      // would make each later write wait for it (stores and loads share
+      // one counter).
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int h = wave + kFinWaves * i;
+        if (h < nh && in) hmax[(h0 + h) * cap + slot] = 0ull;
       }
       __syncthreads();
       if (wave == 0) {
-        for (int h = 0; h < nh; ++h) total += s_h[h][lane];  // h ascending
+        // h ascending; LDS reads go out 16 at a time ahead of the adds
+        int h = 0;
+        for (; h + 16 <= nh; h += 16) {
+          double x[16];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) x[j] = s_h[h + j][lane];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) total += x[j];
+        }
+        for (; h < nh; ++h) total += s_h[h][lane];
       }
       __syncthreads();
+    }
+    if (!q_bad_known) {
+      q_bad = __ballot(qbad_lane != 0u) != 0ull;
+      q_bad_known = true;
     }
     if (wave == 0) {
       float sc = __builtin_nanf("");
@@ -383,8 +417,6 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
         }
       }
       const bool need = isfinite(sc) && sc >= L.th_s;
-      uint64_t id = kNoId;
-      if (need) id = ids[slot];
       wl_consume(L, k, sc, id, slot, need);
     }
   }
@@ -434,144 +466,10 @@ __device__ inline uint32_t pack_f16x2(_Float16 lo, _Float16 hi) {
 
 constexpr int kMaxCols = 64;  // query columns (Qb * R * Qt) per screen pass
 
-// Query preparation of one screen pass; grid (kv), one block per kv head g.
-// Column cg = (qb*R + r)*Qt + qi (cg < cols) is query qb's row of head
-// g*R + r at query token qi.
-//  * scale(cg) = 2^-e, the power of two that brings max|q| of the column
-//    under 2^emax (the MFMA type's safe range), 1 for ordinary values;
-//  * B fragments of the MFMAs: fragment (nt, ks) lane l holds column
-//    nt*16 + l%16 at dims ks*32 + (l/16)*8 + j, j < 8, of q * scale,
-//    rounded to nearest even in the MFMA type (columns >= cols are zero);
-//  * ecoef[g*cpad + cg] = {coef, eabs} * scale (the bound in the scaled
-//    units the screen works in; rounded up):
-//      coef = (gamma + delta + gamma*delta) * ||q||
-//             + sigma_q * (1 + gamma) * sqrt(hd) / scale + 2^-40 * ||q||
-//      eabs = sigma_k * sqrt(hd) * ||q|| + sigma_p * hd / scale
-//    gamma bounds the fp32 accumulation, delta the query's rounding,
-//    sigma_q a scaled query value flushed or rounded near zero, sigma_k a
-//    key value flushed near zero, sigma_p a product lost to underflow, and
-//    2^-40 the law's own fp64 rounding; ||q|| is rounded up;
-//  * q32c[(g*cpad + cg)*hd + d]: the column's values as fp32 (exact: the
-//    query is fp32 or bf16) for the exact recomputation;
-//  * qflags[qb*kv + g] = 1 when a value of query qb read here is non-finite.
-template <int MT>
-__global__ __launch_bounds__(256) void gqa_sr_prep_kernel(
-    const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int Qt,
-    int hd, int kv, int R, int NT, int KS, int emax, double gamma,
-    double delta, double sigma_q, double sigma_k, double sigma_p,
-    u32x4* __restrict__ bfrag, float2* __restrict__ ecoef, float* __restrict__ q32c,
-    unsigned* __restrict__ qflags) {
-  __shared__ float s_scale[kMaxCols];
-  __shared__ unsigned s_bad[kMaxCols];
-  const int g = blockIdx.x;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
-  const int RQ = R * Qt;
-  const int cols = Qb * RQ;
-  const int cpad = NT * 16;
-  auto src_index = [&](int cg, int d) -> uint64_t {
-    const int qb = cg / RQ;
-    const int r = (cg % RQ) / Qt;
-    const int qi = cg % Qt;
-    return static_cast<uint64_t>(qb) * q_elems +
-           (static_cast<uint64_t>(g * R + r) * Qt + qi) * hd + d;
-  };
-  auto qval = [&](uint64_t idx) -> float {
-    return q_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(query)[idx])
-                            : static_cast<const float*>(query)[idx];
-  };
-  // 1. per column: norm, range, scale, error coefficient
-  for (int cg = wave; cg < cpad; cg += nw) {
-    double ss = 0.0;
-    float mx = 0.0f;
-    bool bad = false;
-    if (cg < cols) {
-      for (int d = lane; d < hd; d += kWave) {
-        const float f = qval(src_index(cg, d));
-        bad = bad || !isfinite(f);
-        mx = fmaxf(mx, fabsf(f));
-        ss = fma(static_cast<double>(f), static_cast<double>(f), ss);
-      }
-    }
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      ss += __shfl_xor(ss, off);
-      mx = fmaxf(mx, __shfl_xor(mx, off));
-    }
-    bad = __ballot(bad) != 0ull;
-    if (lane == 0) {
-      int e = 0;
-      if (isfinite(mx) && mx > 0.0f) {
-        const int ex = ilogbf(mx);  // mx in [2^ex, 2^(ex+1))
-        if (ex >= emax) e = ex - emax + 1;
-      }
-      const float scale = ldexpf(1.0f, -e);
-      const double norm = sqrt(ss) * (1.0 + 0x1p-40);
-      const double sq = sqrt(static_cast<double>(hd));
-      double c = 0.0, ea = 0.0;
-      if (cg < cols) {
-        c = (gamma + delta + gamma * delta) * norm + sigma_q * (1.0 + gamma) * sq / scale +
-            0x1p-40 * norm;
-        ea = sigma_k * sq * norm + sigma_p * hd / scale;
-      }
-      const double up = 1.0 + 0x1p-20;
-      c *= up * scale * up;
-      ea *= up * scale * up;
-      s_scale[cg] = scale;
-      s_bad[cg] = bad ? 1u : 0u;
-      ecoef[g * cpad + cg] = make_float2(isfinite(c) ? static_cast<float>(c) * 1.000001f : INFINITY,
-                                         isfinite(ea) ? static_cast<float>(ea) * 1.000001f : INFINITY);
-    }
-  }
-  __syncthreads();
-  // 2. B fragments
-  for (int idx = threadIdx.x; idx < NT * KS * kWave; idx += blockDim.x) {
-    const int l = idx % kWave;
-    const int ks = (idx / kWave) % KS;
-    const int nt = idx / (kWave * KS);
-    const int cg = nt * 16 + (l & 15);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-    if (cg < cols) {
-      const float sc = s_scale[cg];
-      const int d0 = ks * 32 + (l >> 4) * 8;
-      for (int j = 0; j < 8; j += 2) {
-        const float f0 = qval(src_index(cg, d0 + j)) * sc;
-        const float f1 = qval(src_index(cg, d0 + j + 1)) * sc;
-        if constexpr (MT == kBF16) {
-          auto rne = [](float f) {  // round to nearest even (finite inputs)
-            const uint32_t u = __float_as_uint(f);
-            return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-          };
-          w[j / 2] = rne(f0) | (rne(f1) << 16);
-        } else {
-          w[j / 2] = pack_f16x2(static_cast<_Float16>(f0), static_cast<_Float16>(f1));
-        }
-      }
-    }
-    u32x4 v;
-    v.x = w[0];
-    v.y = w[1];
-    v.z = w[2];
-    v.w = w[3];
-    bfrag[(static_cast<size_t>(g * NT + nt) * KS + ks) * kWave + l] = v;
-  }
-  // 3. fp32 columns for the exact recomputation
-  for (int idx = threadIdx.x; idx < cols * hd; idx += blockDim.x) {
-    const int cg = idx / hd;
-    q32c[static_cast<size_t>(g * cpad) * hd + idx] = qval(src_index(cg, idx - cg * hd));
-  }
-  // 4. non-finite flags per query
-  for (int qb = threadIdx.x; qb < Qb; qb += blockDim.x) {
-    unsigned bad = 0u;
-    for (int j = 0; j < RQ; ++j) bad |= s_bad[qb * RQ + j];
-    qflags[qb * kv + g] = bad;
-  }
-}
-
 // Exact |dot| of one lane's (key token, query column) pair in the law's
-// order: the token's chunks come from the planes at kp (chunk c at
-// kp + c*L), 64 values' worth in flight at once, the column's
+// order: the token's pieces come from the planes (piece c at
+// kp + (c/4)*L*4 + c%4, kp the token's piece 0; chunks of S = 4 pieces),
+// 64 values' worth in flight at once, the column's
 // values from qrow (LDS, fp32, exact).  Only lanes with `active` set read
 // memory (the others return 0): the candidates are a few lanes of the
 // wave, and their rows are all that is read again.
@@ -589,7 +487,7 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
     float sc[kB];
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
-      v[b] = kp[static_cast<uint64_t>(c0 + b) * L];
+      v[b] = kp[(static_cast<uint64_t>((c0 + b) >> 2) * L << 2) + ((c0 + b) & 3)];
       sc[b] = 0.0f;
       if constexpr (KDT == kI8) {
         sc[b] = load_scale(sp, scale_dtype, static_cast<uint64_t>((c0 + b) / cpg) * L);
@@ -610,7 +508,28 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
 }
 
 // Screen and refine; grid (ceil(items / 4), kv heads), one wavefront per
-// (item, kv head g).  The item's tokens stream in 16-token tiles, two
+// (item, kv head g).
+//
+// Each block first prepares kv head g's query columns from the raw
+// queries (Qb of them, q_elems values apart): column cg = (qb*R + r)*Qt +
+// qi (cg < cols) is query qb's row of head g*R + r at query token qi.
+//  * s_q[cg][d]: the values as fp32 (exact: queries are fp32 or bf16), for
+//    the screen fragments and the exact recomputation;
+//  * scale(cg) = 2^-e, the power of two that brings max|q| of the column
+//    under 2^emax (the MFMA type's safe range), 1 for ordinary values;
+//  * the column's bound per unit of the node's key norm, and its absolute
+//    part, in the scaled units the screen works in (rounded up):
+//      coef = ((gamma + delta + gamma*delta) * ||q||
+//              + sigma_q * (1 + gamma) * sqrt(hd) / scale + 2^-40 * ||q||) * scale
+//      eabs = (sigma_k * sqrt(hd) * ||q|| + sigma_p * hd / scale) * scale
+//    gamma bounds the fp32 accumulation, delta the query's rounding to
+//    the MFMA type, sigma_q a scaled query value flushed or rounded near
+//    zero, sigma_k a key value flushed near zero, sigma_p a product lost
+//    to underflow, and 2^-40 the law's own fp64 rounding;
+//  * blocks with blockIdx.x == 0 write qflags[qb*kv + g] = 1 when a value
+//    of query qb read by kv head g is non-finite (0 otherwise).
+// Columns with a non-finite value take no part in the screen (every score
+// of that query is NaN).  The item's tokens stream in 16-token tiles, two
 // tiles ahead of the one being screened.  Lane l sees column
 // nt*16 + l%16 of tokens (l/16)*4 + i of every tile; it keeps the two
 // largest screened values with their tokens and the third largest value.
@@ -626,24 +545,28 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     const unsigned char* __restrict__ keys,
     const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
     const Item* __restrict__ items, uint32_t n_items, int kv, int R, int Qt,
-    int cols, const u32x4* __restrict__ bfrag,
-    const float2* __restrict__ ecoef, const float* __restrict__ q32c,
-    const unsigned* __restrict__ qflags, const float* __restrict__ kmax, double denom,
+    const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
+    double gamma, double delta, double sigma_q, double sigma_k, double sigma_p,
+    unsigned* __restrict__ qflags, const float* __restrict__ kmax, double denom,
     unsigned long long* __restrict__ hmax, size_t hstride, size_t cap) {
   using KT = KeyTraits<KDT>;
   constexpr int MT = ScreenTraits<KDT>::kMfma;
   constexpr int HD = 32 * KS;
   constexpr int C = HD / KT::kEpc;  // chunks per key row
   extern __shared__ float s_q[];  // [cols][HD]: the block's query columns
+  __shared__ float4 s_ec[kMaxCols];  // {coef, eabs, scale, 0} per column
+  __shared__ unsigned s_bad[kMaxCols];
   const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
   const int g = blockIdx.y;
-  for (int i = threadIdx.x; i < cols * HD; i += blockDim.x) {
-    s_q[i] = q32c[static_cast<size_t>(g * NT * 16) * HD + i];
-  }
-  __syncthreads();
-  const uint32_t item_i = blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  if (item_i >= n_items) return;
-  const Item it = items[item_i];
+  const int RQc = R * Qt;
+  const int cols = Qb * RQc;
+  // The wave's first tiles are requested before the block prepares its
+  // query columns, so the two overlap; a wave without an item issues no
+  // loads but joins the block's barriers.
+  const uint32_t item_raw = blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const bool has_item = item_raw < n_items;
+  const Item it = items[has_item ? item_raw : n_items - 1];
   const uint64_t L = it.len;
   const uint64_t row0 = it.base + static_cast<uint64_t>(g) * L;
   const int G = KDT == kI8 ? HD / group_size : 1;
@@ -655,15 +578,6 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
   const int r16 = lane & 15;
   const uint32_t last = it.t0 + it.count - 1;  // last token of the item
   const int ntiles = static_cast<int>((it.count + 15) / 16);
-
-  u32x4 bq[NT][KS];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      bq[nt][ks] = bfrag[(static_cast<size_t>(g * NT + nt) * KS + ks) * kWave + lane];
-    }
-  }
 
   // Raw data of tile `tile` for this lane: token min(t0 + 16*tile + l%16,
   // last), dims ks*32 + (l/16)*8 .. +8 (loads are unconditional; rows past
@@ -677,21 +591,120 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
   };
   auto load_tile = [&](Tile& b, int tile) {
     const uint32_t t = min(it.t0 + static_cast<uint32_t>(tile) * 16 + r16, last);
+    // chunks of 4 pieces: piece p of token t at kplane + (p/4)*L*4 + t*4 + p%4
     if constexpr (KDT != kI8) {
-      const u32x4* p = kplane + quarter * L + t;
+      // piece ks*4 + quarter: one 1 KiB run per load over the 16 tokens
+      const u32x4* p = kplane + static_cast<uint64_t>(t) * 4 + quarter;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) b.v[ks] = __builtin_nontemporal_load(p + ks * 4 * L);
     } else {
-      // half (quarter & 1) of chunk (ks*2 + quarter/2)
-      const u32x2* p = reinterpret_cast<const u32x2*>(kplane + (quarter >> 1) * L + t) + (quarter & 1);
+      // half (quarter & 1) of piece ks*2 + quarter/2
+      const u32x2* p = reinterpret_cast<const u32x2*>(kplane + static_cast<uint64_t>(t) * 4 + (quarter >> 1)) +
+                       (quarter & 1);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        b.c[ks] = __builtin_nontemporal_load(p + ks * 4 * L);
+        b.c[ks] = __builtin_nontemporal_load(p + 2 * ((ks >> 1) * 4 * L + 2 * (ks & 1)));
         b.s[ks] = load_scale(splane, scale_dtype,
                              static_cast<uint64_t>((ks * 32 + quarter * 8) / group_size) * L + t);
       }
     }
   };
+  Tile x0, x1, x2, x3, x4;
+  if (has_item) {
+    load_tile(x0, 0);
+    load_tile(x1, 1);
+    load_tile(x2, 2);
+    load_tile(x3, 3);
+  }
+  for (int i = threadIdx.x; i < cols * HD; i += blockDim.x) {
+    const int cg = i / HD;
+    const int qb = cg / RQc;
+    const int r = (cg % RQc) / Qt;
+    const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
+                         (static_cast<uint64_t>(g * R + r) * Qt + cg % Qt) * HD + (i - cg * HD);
+    s_q[i] = q_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
+                              : static_cast<const float*>(query)[src];
+  }
+  __syncthreads();
+  for (int cg = wave; cg < cols; cg += kUnitWaves) {
+    double ss = 0.0;
+    float mx = 0.0f;
+    bool bad = false;
+    for (int d = lane; d < HD; d += kWave) {
+      const float f = s_q[cg * HD + d];
+      bad = bad || !isfinite(f);
+      mx = fmaxf(mx, fabsf(f));
+      ss = fma(static_cast<double>(f), static_cast<double>(f), ss);
+    }
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      ss += __shfl_xor(ss, off);
+      mx = fmaxf(mx, __shfl_xor(mx, off));
+    }
+    bad = __ballot(bad) != 0ull;
+    if (lane == 0) {
+      int e = 0;
+      if (isfinite(mx) && mx > 0.0f) {
+        const int ex = ilogbf(mx);  // mx in [2^ex, 2^(ex+1))
+        if (ex >= emax) e = ex - emax + 1;
+      }
+      const float scale = ldexpf(1.0f, -e);
+      const double norm = sqrt(ss) * (1.0 + 0x1p-40);
+      const double sq = sqrt(static_cast<double>(HD));
+      double c = (gamma + delta + gamma * delta) * norm + sigma_q * (1.0 + gamma) * sq / scale +
+                 0x1p-40 * norm;
+      double ea = sigma_k * sq * norm + sigma_p * HD / scale;
+      const double up = 1.0 + 0x1p-20;
+      c *= up * scale * up;
+      ea *= up * scale * up;
+      s_ec[cg] = make_float4(isfinite(c) ? static_cast<float>(c) * 1.000001f : INFINITY,
+                             isfinite(ea) ? static_cast<float>(ea) * 1.000001f : INFINITY, scale,
+                             0.0f);
+      s_bad[cg] = bad ? 1u : 0u;
+    }
+  }
+  __syncthreads();
+  if (blockIdx.x == 0 && threadIdx.x < static_cast<unsigned>(Qb)) {
+    unsigned bad = 0u;
+    for (int j = 0; j < RQc; ++j) bad |= s_bad[threadIdx.x * RQc + j];
+    qflags[threadIdx.x * kv + g] = bad;
+  }
+  if (!has_item) return;
+
+  // B fragments from the staged columns: fragment (nt, ks) lane l holds
+  // column nt*16 + l%16 at dims ks*32 + (l/16)*8 + j, j < 8, of q * scale
+  // rounded to nearest even in the MFMA type (columns >= cols are zero).
+  u32x4 bq[NT][KS];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int cg = nt * 16 + r16;
+    const float sc = cg < cols ? s_ec[cg].z : 0.0f;
+    const float* qc = s_q + min(cg, cols - 1) * HD;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const int d = ks * 32 + quarter * 8 + j;
+        const float f0 = cg < cols ? qc[d] * sc : 0.0f;
+        const float f1 = cg < cols ? qc[d + 1] * sc : 0.0f;
+        if constexpr (MT == kBF16) {
+          auto rne = [](float f) {  // round to nearest even (finite inputs)
+            const uint32_t u = __float_as_uint(f);
+            return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+          };
+          w[j / 2] = rne(f0) | (rne(f1) << 16);
+        } else {
+          w[j / 2] = pack_f16x2(static_cast<_Float16>(f0), static_cast<_Float16>(f1));
+        }
+      }
+      bq[nt][ks].x = w[0];
+      bq[nt][ks].y = w[1];
+      bq[nt][ks].z = w[2];
+      bq[nt][ks].w = w[3];
+    }
+  }
+
   auto frag = [&](const Tile& b, int ks) -> u32x4 {
     if constexpr (KDT != kI8) {
       return b.v[ks];
@@ -759,11 +772,6 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
   };
 
   // stream: five tile buffers, four tiles in flight ahead of the fold
-  Tile x0, x1, x2, x3, x4;
-  load_tile(x0, 0);
-  load_tile(x1, 1);
-  load_tile(x2, 2);
-  load_tile(x3, 3);
   int tile = 0;
   auto step = [&](Tile& now, Tile& free) -> bool {
     load_tile(free, tile + 4);  // past the end: reloads the last token
@@ -773,9 +781,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
   while (step(x0, x4) && step(x1, x0) && step(x2, x1) && step(x3, x2) && step(x4, x3)) {
   }
 
-  // thresholds and candidates; a column whose query holds a non-finite
-  // value takes no part (every score of that query is NaN)
-  const int RQc = R * Qt;
+  // thresholds and candidates
   const float km = kmax[it.slot];
   double thr[NT];
   bool live[NT];
@@ -786,8 +792,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     m = fmaxf(m, __shfl_xor(m, 16));
     m = fmaxf(m, __shfl_xor(m, 32));
     const int cg = nt * 16 + r16;
-    live[nt] = cg < cols && qflags[(min(cg, cols - 1) / RQc) * kv + g] == 0u;
-    const float2 ec = ecoef[g * NT * 16 + cg];
+    live[nt] = cg < cols && s_bad[min(cg, cols - 1)] == 0u;
+    const float4 ec = s_ec[min(cg, cols - 1)];
     const double e = static_cast<double>(ec.x) * static_cast<double>(km) + static_cast<double>(ec.y);
     thr[nt] = static_cast<double>(m) - 2.0 * e;
     if (live[nt]) {
@@ -799,7 +805,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
 
   auto pair = [&](bool active, uint32_t t, int cg) -> double {
     const uint32_t tt = min(it.t0 + t, last);
-    return exact_pair<KDT, HD>(active, kplane + tt, L,
+    return exact_pair<KDT, HD>(active, kplane + static_cast<uint64_t>(tt) * 4, L,
                            KDT == kI8 ? splane + static_cast<size_t>(tt) * ses : nullptr,
                            scale_dtype, cpg, s_q + min(cg, cols - 1) * HD);
   };
@@ -878,7 +884,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_place_kernel(
     const u32x4* __restrict__ src_keys, const unsigned char* __restrict__ src_scales,
     uint64_t src_base, unsigned char* __restrict__ keys,
     unsigned char* __restrict__ scales, int scale_dtype, int group_size,
-    const Item* __restrict__ items, uint32_t n_items, int hd,
+    const Item* __restrict__ items, uint32_t n_items, int hd, int sS,
     uint32_t* __restrict__ nonfinite, unsigned* __restrict__ kmax) {
   using T = KeyTraits<KDT>;
   const int lane = threadIdx.x & (kWave - 1);
@@ -893,6 +899,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_place_kernel(
   const uint64_t row0 = it.base + static_cast<uint64_t>(g) * it.len;
   const uint64_t srow0 = row0 - src_base;
   u32x4* dst = reinterpret_cast<u32x4*>(keys) + row0 * C;
+  const int S = 1 << sS;
   bool bad = false;
   double mx = 0.0;
   for (uint32_t t = it.t0 + lane; t < it.t0 + it.count; t += kWave) {
@@ -900,7 +907,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_place_kernel(
     double acc = 0.0;
     for (int c = 0; c < C; ++c) {
       const u32x4 v = src[c];
-      dst[static_cast<uint64_t>(c) * it.len + t] = v;
+      dst[(static_cast<uint64_t>(c >> sS) * it.len << sS) + (static_cast<uint64_t>(t) << sS) + (c & (S - 1))] = v;
       float sc = 0.0f;
       if constexpr (KDT == kI8) {
         const int j = c / cpg;

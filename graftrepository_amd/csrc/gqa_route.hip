@@ -5,10 +5,10 @@
 // [tok_off[i], tok_off[i] + L') of the token arena, L' = len[i] rounded up
 // to 8; its block holds kv * L' * hd values of the storage dtype (f32,
 // bf16, f16 or int8 codes with per-(token, group) scales) as chunk planes
-// per kv head: chunk c (16 bytes) of token t of head g at c*L' + t within
-// the head's block (gqa_kernels.hpp).  The rounding puts every 8-token run
-// of a plane on its own 128-byte line, so streams never share a line; the
-// rows past len[i] are never read.
+// per kv head: chunk c (64 bytes when the row allows) of token t of head g
+// at c*L' + t within the head's block (gqa_kernels.hpp).  The rounding
+// puts every 8-token run of a plane on its own 128-byte lines, so streams
+// never share a line; the rows past len[i] are never read.
 //
 // Route (bf16 / fp16 / int8 banks, head_dim 64, 128 or 256):
 //   when (heads / kv) * query_tokens <= 4 the exact path below streams the
@@ -50,6 +50,7 @@ struct GqaDeviceArena {
   int group_size = 0;
   uint32_t kv = 0;
   uint32_t hd = 0;
+  int piece_shift = 0;  // log2 of the 16-byte pieces per plane chunk
   uint64_t cap_nodes = 0;
   uint64_t cap_tokens = 0;
   uint64_t used_tokens = 0;  // bump pointer of the token arena
@@ -88,12 +89,6 @@ struct GqaDeviceArena {
   size_t d_q64_count = 0;
   // screen-and-refine path
   int screen_mode = -1;  // -1 whenever the shape allows, 0 never
-  u32x4* d_bfrag = nullptr;
-  size_t d_bfrag_count = 0;
-  float2* d_ecoef = nullptr;
-  size_t d_ecoef_count = 0;
-  float* d_q32c = nullptr;      // query columns as fp32, d contiguous
-  size_t d_q32c_count = 0;
   uint64_t routes = 0;          // route calls
   std::vector<Cand> merged;
   void* d_queries = nullptr;
@@ -171,8 +166,7 @@ void destroy_arena(GqaDeviceArena* a) {
   if (a->side) (void)hipStreamSynchronize(a->side);
   void* dev[] = {a->d_keys,  a->d_scales, a->d_tok_off, a->d_len,   a->d_ids,
                  a->d_flags, a->d_nonfinite, a->d_kmax, a->d_items, a->d_hmax,
-                 a->d_qbad,  a->d_queries, a->d_stage,  a->d_bfrag, a->d_ecoef,
-                 a->d_q32c,  a->d_q64};
+                 a->d_qbad,  a->d_queries, a->d_stage,  a->d_q64};
   for (void* p : dev) {
     if (p) (void)hipFree(p);
   }
@@ -299,7 +293,8 @@ int place_nodes(GqaDeviceArena* a, const std::vector<uint64_t>& slots,
   grm::gqa::gqa_place_kernel<KDT><<<grid, pthreads, 0, st>>>(                                    \
       reinterpret_cast<const u32x4*>(d + o_keys), d + o_scales, first_tok * a->kv, a->d_keys,    \
       a->d_scales, a->scale_dtype, a->group_size, reinterpret_cast<const Item*>(d + o_items),    \
-      static_cast<uint32_t>(items.size()), static_cast<int>(a->hd), a->d_nonfinite, a->d_kmax)
+      static_cast<uint32_t>(items.size()), static_cast<int>(a->hd), a->piece_shift,           \
+      a->d_nonfinite, a->d_kmax)
     switch (a->key_dtype) {
       case kF32: GRM_PLACE(kF32); break;
       case kBF16: GRM_PLACE(kBF16); break;
@@ -370,6 +365,12 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   a->group_size = key_dtype == kI8 ? group_size : 0;
   a->kv = static_cast<uint32_t>(kv_heads);
   a->hd = static_cast<uint32_t>(head_dim);
+  {
+    const size_t row_bytes = static_cast<size_t>(head_dim) * key_esize(key_dtype);
+    // fp32 banks take the lane-per-token exact path, which streams best
+    // from 16-byte pieces; the others read whole 64-byte chunks
+    a->piece_shift = key_dtype == kF32 ? 0 : (row_bytes % 64 == 0 ? 2 : (row_bytes % 32 == 0 ? 1 : 0));
+  }
   a->cap_nodes = cap_nodes;
   a->cap_tokens = cap_tokens;
   a->tok_off.assign(cap_nodes, 0);
@@ -530,8 +531,8 @@ int launch_exact(GqaDeviceArena* a, int H, int Qt) {
 #define GRM_EXACT(KDT, RQ)                                                                  \
   grm::gqa::gqa_exact_kernel<KDT, RQ, grm::gqa::exact_stage_chunks<KDT, RQ>()><<<grid, threads, 0, a->stream>>>( \
       a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                   \
-      static_cast<uint32_t>(a->n_items), static_cast<int>(a->kv), static_cast<int>(a->hd), R, \
-      Qt, a->d_q64, denom, a->d_hmax, a->cap_nodes)
+      static_cast<uint32_t>(a->n_items), static_cast<int>(a->kv), static_cast<int>(a->hd),    \
+      a->piece_shift, R, Qt, a->d_q64, denom, a->d_hmax, a->cap_nodes)
 #define GRM_EXACT_RQ(KDT)                       \
   switch (rq_pad) {                             \
     case 1: GRM_EXACT(KDT, 1); break;           \
@@ -587,6 +588,7 @@ constexpr size_t kMaxHmaxBytes = 2ull << 30;
 bool sr_plan(const GqaDeviceArena* a, int H, int Qt, SrPlan* p) {
   if (a->screen_mode == 0 || a->key_dtype == kF32) return false;
   if (a->hd != 64 && a->hd != 128 && a->hd != 256) return false;
+  if (a->piece_shift != 2) return false;  // the screen reads 64-byte chunks
   const int R = H / static_cast<int>(a->kv);
   if (R * Qt > grm::gqa::kMaxCols) return false;
   p->R = R;
@@ -600,8 +602,15 @@ bool sr_plan(const GqaDeviceArena* a, int H, int Qt, SrPlan* p) {
   return true;
 }
 
+// Device buffers of screen-and-refine passes of up to p.qb_max queries.
+int prepare_sr(GqaDeviceArena* a, const SrPlan& p) {
+  GRM_CHECK_RC(reserve_device(&a->d_qbad, &a->d_qbad_count, static_cast<size_t>(p.qb_max) * a->kv));
+  return ensure_hmax(a, p.H, p.qb_max);
+}
+
 // Enqueue one screen-and-refine pass over queries [0, qb) at qptr (device,
-// `qstride` bytes apart); their per-block top-k lands at bout.
+// `qstride` bytes apart); their per-block top-k lands at bout.  Launches
+// only (prepare_sr allocates), so the pass can be captured in a graph.
 int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
                int topk, uint32_t fin_blocks, Cand* bout) {
   const int kv = static_cast<int>(a->kv);
@@ -610,14 +619,7 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   const int nt_need = (cols + 15) / 16;
   const int NT = nt_need <= 1 ? 1 : (nt_need <= 2 ? 2 : 4);
   const int H = p.H;
-  GRM_CHECK_RC(reserve_device(&a->d_bfrag, &a->d_bfrag_count,
-                              static_cast<size_t>(kv) * NT * p.KS * grm::kWave));
-  GRM_CHECK_RC(reserve_device(&a->d_ecoef, &a->d_ecoef_count, static_cast<size_t>(kv) * NT * 16));
-  GRM_CHECK_RC(reserve_device(&a->d_q32c, &a->d_q32c_count,
-                              static_cast<size_t>(kv) * NT * 16 * a->hd));
-  GRM_CHECK_RC(reserve_device(&a->d_qbad, &a->d_qbad_count, static_cast<size_t>(qb) * kv));
-  GRM_CHECK_RC(ensure_hmax(a, H, p.qb_max));
-  // 1. query preparation.  Error-bound constants (per query column):
+  // Error-bound constants (per query column, see gqa_sr_kernel):
   //   gamma  fp32 accumulation of hd products, MFMA internal order unknown
   //   delta  rounding of an fp32 query value to the MFMA type
   //   sigma_q, sigma_k  a query / key value near zero flushed or rounded
@@ -636,18 +638,8 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
     emax = 15;
   }
   const size_t q_elems = static_cast<size_t>(H) * p.Qt * a->hd;
-#define GRM_SR_PREP(MT)                                                                        \
-  grm::gqa::gqa_sr_prep_kernel<MT><<<kv, 256, 0, a->stream>>>(                                 \
-      qptr, q_dtype, q_elems, qb, p.Qt, static_cast<int>(a->hd), kv, p.R, NT, p.KS, emax,        \
-      gamma, delta, sigma_q, sigma_k, sigma_p, a->d_bfrag, a->d_ecoef, a->d_q32c, a->d_qbad)
-  if (p.mfma == kBF16) {
-    GRM_SR_PREP(kBF16);
-  } else {
-    GRM_SR_PREP(kF16);
-  }
-#undef GRM_SR_PREP
-  GRM_HIP_CHECK(hipGetLastError());
-  // 2. screen and refine every (item, kv head)
+  // 1. screen and refine every (item, kv head), preparing the query
+  // columns in each block
   if (a->n_items > 0) {
     const dim3 grid(static_cast<unsigned>((a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves),
                     a->kv);
@@ -658,9 +650,9 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
 #define GRM_SR(KDT, KS, NTT)                                                                    \
   grm::gqa::gqa_sr_kernel<KDT, KS, NTT><<<grid, threads, lds, a->stream>>>(                     \
       a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                        \
-      static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, cols, a->d_bfrag, a->d_ecoef,             \
-      a->d_q32c, a->d_qbad, reinterpret_cast<const float*>(a->d_kmax), denom, a->d_hmax, hstride, \
-      a->cap_nodes)
+      static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, qptr, q_dtype, q_elems, qb, emax, gamma,  \
+      delta, sigma_q, sigma_k, sigma_p, a->d_qbad, reinterpret_cast<const float*>(a->d_kmax),     \
+      denom, a->d_hmax, hstride, a->cap_nodes)
 #define GRM_SR_NT(KDT, KS)                 \
   switch (NT) {                            \
     case 1: GRM_SR(KDT, KS, 1); break;     \
@@ -682,8 +674,11 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
 #undef GRM_SR_NT
 #undef GRM_SR
     GRM_HIP_CHECK(hipGetLastError());
+  } else {
+    // no key tokens at all: only the query flags are needed
+    GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt));
   }
-  // 3. exact scores and per-block top-k
+  // 2. exact scores and per-block top-k
   return launch_finalize(a, H, qb, topk, fin_blocks, bout);
 }
 
@@ -722,10 +717,12 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   a->merged.resize(topk);
   SrPlan plan;
   const bool use_sr = sr_plan(a, H, Qt, &plan);
+  if (use_sr) GRM_CHECK_RC(prepare_sr(a, plan));
   // untimed warmup queries first, then the timed ones
   const int segments[2][2] = {{0, warmup}, {warmup, q_count}};
-  for (const auto& seg : segments) {
-    if (seg[0] == warmup) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+  for (int si = 0; si < 2; ++si) {
+    const auto& seg = segments[si];
+    if (si == 1) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
     if (use_sr) {
       for (int q0 = seg[0]; q0 < seg[1]; q0 += plan.qb_max) {
         const int qb = std::min(plan.qb_max, seg[1] - q0);
@@ -740,7 +737,7 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
     }
   }
   GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
-  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  GRM_CHECK_RC(grm::wait_event(a->ev_stop));
   for (int qi = 0; qi < q_count; ++qi) {
     grm::host_topk_merge(a->blocks_out.host + static_cast<size_t>(qi) * per_q, per_q, topk,
                          a->merged.data());

@@ -3,6 +3,7 @@
 #include "grm_common.hpp"
 
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 namespace grm {
@@ -62,6 +63,22 @@ int reserve_mapped(MappedCands* m, size_t count) {
   m->dev = static_cast<Cand*>(d);
   m->count = count;
   return 0;
+}
+
+int wait_event(hipEvent_t ev) {
+  static const bool blocking = [] {
+    const char* env = getenv("GRM_HIP_BLOCKING_SYNC");
+    return env && env[0] == '1';
+  }();
+  if (blocking) {
+    GRM_HIP_CHECK(hipEventSynchronize(ev));
+    return 0;
+  }
+  for (;;) {
+    const hipError_t e = hipEventQuery(ev);
+    if (e == hipSuccess) return 0;
+    if (e != hipErrorNotReady) return fail_hip(e, "hipEventQuery");
+  }
 }
 
 int reserve_mapped_bytes(MappedBuf* m, size_t bytes) {

@@ -246,6 +246,11 @@ constexpr int kMergeWaves = 4;
 // best first; unfilled entries get score NaN, id kNoId, slot kNoSlot.
 void host_topk_merge(const Cand* in, size_t count, int k, Cand* out);
 
+// Wait until `ev` has completed by polling it: a route's result is read
+// the moment its last kernel ends instead of after a blocking wake-up.
+// With GRM_HIP_BLOCKING_SYNC=1 in the environment the wait blocks instead.
+int wait_event(hipEvent_t ev);
+
 // Pinned host buffer of raw bytes that the device reads and writes directly
 // (mapped, coherent).
 struct MappedBuf {

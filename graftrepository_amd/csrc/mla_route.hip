@@ -641,7 +641,7 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
     GRM_HIP_CHECK(hipGetLastError());
   }
   GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
-  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  GRM_CHECK_RC(grm::wait_event(a->ev_stop));
   if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
   a->merged.resize(topk);
   for (int qi = 0; qi < q_count; ++qi) {

@@ -308,3 +308,40 @@ def test_int8_bank_batched_queries(hip_lib):
                                   scales=scales, scale_dtype="f16",
                                   group_size=32)
     assert_same(res, ids, sc)
+
+
+def test_repeated_routes_follow_query_and_bank_changes(hip_lib):
+    # Repeated single-query routes on one device buffer read the query and
+    # the bank as they are at each call; batched routes run in between.
+    torch = pytest.importorskip("torch")
+    lens = wl.gqa_lengths(200, seed=71, lo=1, hi=300)
+    keys, offs = wl.gqa_bank(lens, 8, 128, seed=71, dtype="bf16")
+    node_ids = np.arange(200, dtype=np.uint64) + 5
+    qs = [wl.gqa_queries(1, 32, 1, 128, seed=71 + i, dtype="f32") for i in range(2)]
+    dq = torch.from_numpy(qs[0]).cuda()
+    torch.cuda.synchronize()
+
+    def want(q, live):
+        blocks = [keys[int(offs[j]) * 8 * 128:int(offs[j + 1]) * 8 * 128] for j in live]
+        o = np.zeros(len(live) + 1, np.uint64)
+        o[1:] = np.cumsum([lens[j] for j in live])
+        return oracle.gqa_route(np.concatenate(blocks), oracle.BF16, o, 8, 128, q, 4,
+                                node_ids=node_ids[live])
+
+    live = list(range(200))
+    with GqaNodeBank(keys, offs, kv_heads=8, head_dim=128, dtype="bf16",
+                     node_ids=node_ids) as bank:
+        ids, sc, _ = want(qs[0], live)
+        for _ in range(3):
+            assert_same(bank.route(dq, 4, on_device=True), ids, sc)
+            eager = bank.route(np.concatenate([qs[0], qs[0]]), 4, warmup=1)
+            assert_same(eager, np.concatenate([ids, ids]), np.concatenate([sc, sc]))
+        dq.copy_(torch.from_numpy(qs[1]))
+        torch.cuda.synchronize()
+        ids, sc, _ = want(qs[1], live)
+        assert_same(bank.route(dq, 4, on_device=True), ids, sc)
+        bank.evict(node_ids[:7])
+        live = live[7:]
+        ids, sc, _ = want(qs[1], live)
+        for _ in range(2):
+            assert_same(bank.route(dq, 4, on_device=True), ids, sc)
