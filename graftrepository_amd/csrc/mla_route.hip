@@ -19,8 +19,15 @@
 // the way a plain sequential stream does.
 //
 // Top-k is fused: each wave keeps a distributed top-k list (grm_common.hpp),
-// blocks merge their waves' lists in LDS, and the last block to finish
-// merges the per-block lists -- the score vector never leaves registers.
+// blocks merge their waves' lists in LDS and write their k best entries to
+// mapped host memory, where the host merges the per-block lists after the
+// kernel's completion event -- the score vector never leaves registers.
+//
+// Batched queries on a bf16 bank take the matrix-core path (mla_batch.hpp):
+// an MFMA screen of 32 slots x up to 256 queries per wave keeps a per-lane
+// shortlist, a merge kernel certifies each query's top-k against a proven
+// bound on the screen's rounding error and rescores the shortlist with the
+// exact law; queries without a certificate are routed again here.
 #include "grm_common.hpp"
 #include "grm_hip_router.h"
 
@@ -269,7 +276,8 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_pipe_kernel(
 
 // Place staged row-major rows into their tile slots and compute row norms
 // (cpp/grm_runtime.cpp:3232-3241).  rows: [count][dim] of DT; slots/ids may be
-// null (contiguous slots from slot0 / ids = slot).
+// null (contiguous slots from slot0 / ids = slot).  min_norm tracks the
+// smallest positive norm ever placed (float bits, atomicMin).
 template <int DT>
 __global__ void mla_place_rows_kernel(const void* __restrict__ rows,
                                       uint64_t count, uint32_t dim,
@@ -278,7 +286,8 @@ __global__ void mla_place_rows_kernel(const void* __restrict__ rows,
                                       const uint64_t* __restrict__ ids,
                                       uint64_t slot0, u32x4* __restrict__ tiles,
                                       float* __restrict__ norms,
-                                      uint64_t* __restrict__ slot_ids) {
+                                      uint64_t* __restrict__ slot_ids,
+                                      unsigned* __restrict__ min_norm) {
   constexpr int EPC = DT == kF32 ? 4 : 8;
   for (uint64_t r = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
        r < count; r += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
@@ -316,8 +325,11 @@ __global__ void mla_place_rows_kernel(const void* __restrict__ rows,
       v.w = w[3];
       dst[static_cast<size_t>(c) * plane] = v;
     }
-    norms[slot] = static_cast<float>(sqrt(acc));
+    const float nf = static_cast<float>(sqrt(acc));
+    norms[slot] = nf;
     slot_ids[slot] = ids ? ids[r] : slot;
+    // smallest positive row norm (positive floats order like their bits)
+    if (nf > 0.0f && isfinite(nf)) atomicMin(min_norm, __float_as_uint(nf));
   }
 }
 
@@ -334,6 +346,8 @@ __global__ void mla_evict_kernel(const uint64_t* __restrict__ slots,
 
 }  // namespace mla
 }  // namespace grm
+
+#include "mla_batch.hpp"
 
 using grm::Cand;
 using grm::kBF16;
@@ -374,6 +388,22 @@ struct MlaDeviceArena {
   hipEvent_t ev_stop = nullptr;
   hipEvent_t ev_mut = nullptr;
   bool mut_pending = false;
+  unsigned* d_min_norm = nullptr;  // smallest positive row norm placed (float bits)
+  // batched route (bf16 banks): pass buffers and per-query results
+  uint16_t* d_qpad = nullptr;
+  size_t d_qpad_count = 0;
+  float* d_inv_qn = nullptr;
+  size_t d_inv_qn_count = 0;
+  grm::mla::BatchEntry* d_entries = nullptr;
+  size_t d_entries_count = 0;
+  grm::MappedCands batch_out;
+  grm::MappedBuf batch_status;
+  int batch_min = 4;         // timed queries per call from which the batched path runs
+  size_t lds_max = 65536;    // dynamic LDS one block may use
+  uint64_t batch_queries = 0;    // queries screened on the matrix cores
+  uint64_t batch_fallbacks = 0;  // of those, routed again on the single-query path
+  uint64_t batch_passes = 0;     // screen passes
+  uint64_t single_queries = 0;   // queries through the single-query kernel
   bool pipeline = true;     // software-pipelined kernel when rows allow it
   uint32_t cus = 256;       // compute units of the device
   uint32_t max_blocks = 0;  // plain-kernel grid cap (4 blocks per CU)
@@ -393,6 +423,12 @@ void destroy_arena(MlaDeviceArena* a) {
   if (a->d_ids) (void)hipFree(a->d_ids);
   if (a->d_queries) (void)hipFree(a->d_queries);
   if (a->d_stage) (void)hipFree(a->d_stage);
+  if (a->d_min_norm) (void)hipFree(a->d_min_norm);
+  if (a->d_qpad) (void)hipFree(a->d_qpad);
+  if (a->d_inv_qn) (void)hipFree(a->d_inv_qn);
+  if (a->d_entries) (void)hipFree(a->d_entries);
+  grm::release_mapped(&a->batch_out);
+  grm::release_mapped_bytes(&a->batch_status);
   grm::release_mapped(&a->blocks_out);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
@@ -449,11 +485,11 @@ int launch_place(MlaDeviceArena* a, const void* d_rows, uint64_t count,
   if (a->dtype == kF32) {
     grm::mla::mla_place_rows_kernel<kF32><<<blocks, threads, 0, stream>>>(
         d_rows, count, a->dim, a->chunks, a->capacity, d_slots, d_ids, slot0,
-        a->d_tiles, a->d_norms, a->d_ids);
+        a->d_tiles, a->d_norms, a->d_ids, a->d_min_norm);
   } else {
     grm::mla::mla_place_rows_kernel<kBF16><<<blocks, threads, 0, stream>>>(
         d_rows, count, a->dim, a->chunks, a->capacity, d_slots, d_ids, slot0,
-        a->d_tiles, a->d_norms, a->d_ids);
+        a->d_tiles, a->d_norms, a->d_ids, a->d_min_norm);
   }
   GRM_HIP_CHECK(hipGetLastError());
   return 0;
@@ -501,6 +537,21 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
     if (v >= 1 && v <= 65536) a->max_blocks = static_cast<uint32_t>(v);
   }
   if (const char* env = getenv("GRM_HIP_MLA_PIPELINE")) a->pipeline = env[0] != '0';
+  if (const char* env = getenv("GRM_HIP_MLA_BATCH_MIN")) {
+    const long v = strtol(env, nullptr, 10);
+    if (v >= 1) a->batch_min = static_cast<int>(std::min<long>(v, 1l << 30));
+  }
+  {
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeSharedMemPerBlockOptin, a->device) == hipSuccess &&
+        lds > 0) {
+      a->lds_max = static_cast<size_t>(lds);
+    } else if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, a->device) ==
+                   hipSuccess &&
+               lds > 0) {
+      a->lds_max = static_cast<size_t>(lds);
+    }
+  }
   a->slot_id.assign(a->capacity, kNoId);
   if (node_ids) {
     a->slot_of.reserve(nodes * 2);
@@ -535,6 +586,13 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
   BAIL_HIP(hipMemsetAsync(a->d_tiles, 0, tiles * tile_bytes, a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_norms, 0xff, a->capacity * sizeof(float), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_ids, 0xff, a->capacity * sizeof(uint64_t), a->stream));
+  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_min_norm), sizeof(unsigned)));
+  {
+    const unsigned inf_bits = 0x7f800000u;
+    BAIL_HIP(hipMemcpyAsync(a->d_min_norm, &inf_bits, sizeof(unsigned), hipMemcpyHostToDevice,
+                            a->stream));
+    BAIL_HIP(hipStreamSynchronize(a->stream));
+  }
   if (nodes > 0) {
     const size_t row_bytes = static_cast<size_t>(a->dim) * elem_size(dtype);
     const uint64_t batch = std::min<uint64_t>(nodes, grm::mla::kStageRows);
@@ -569,6 +627,141 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
   return 0;
 }
 
+// Launch geometry of the single-query route kernel.
+struct SingleGeom {
+  uint32_t num_tiles = 0, blocks = 0, nw = 0;
+  int batch = 0;  // chunks per pipelined load batch (0: plain kernel)
+};
+
+SingleGeom single_geom(const MlaDeviceArena* a) {
+  SingleGeom g;
+  g.num_tiles = static_cast<uint32_t>((a->high_water + grm::kWave - 1) / grm::kWave);
+  // The pipelined kernel runs one 16-wave block per CU (4 waves per SIMD);
+  // the plain kernel (rows that do not split into whole batches) 4-wave
+  // blocks, 4 per CU.
+  if (a->pipeline) {
+    for (int b : {9, 8, 6}) {
+      if (a->chunks % b == 0) {
+        g.batch = b;
+        break;
+      }
+    }
+  }
+  g.nw = g.batch ? grm::mla::kPipeWaves : grm::mla::kRouteWaves;
+  const uint32_t cap = g.batch ? std::min(a->cus, a->max_blocks) : a->max_blocks;
+  g.blocks = std::max<uint32_t>(1, std::min((g.num_tiles + g.nw - 1) / g.nw, cap));
+  return g;
+}
+
+// One query (device pointer q) through the single-query kernel; its
+// per-block top-k lands at bout (g.blocks * topk entries).
+int launch_single(MlaDeviceArena* a, const SingleGeom& g, const void* q, int q_dtype, int topk,
+                  Cand* bout) {
+  const size_t lds = static_cast<size_t>(a->dim_pad) * sizeof(double);
+  const dim3 grid(g.blocks), block(g.nw * grm::kWave);
+#define GRM_MLA_ARGS                                                                  \
+  a->d_tiles, a->d_norms, a->d_ids, g.num_tiles, a->chunks, a->capacity, a->dim, a->dim_pad, q, \
+      q_dtype, topk, bout
+  constexpr int PW = grm::mla::kPipeWaves;
+  constexpr int RW = grm::mla::kRouteWaves;
+  if (a->dtype == kF32) {
+    switch (g.batch) {
+      case 9: grm::mla::mla_route_pipe_kernel<kF32, PW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+      case 8: grm::mla::mla_route_pipe_kernel<kF32, PW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+      case 6: grm::mla::mla_route_pipe_kernel<kF32, PW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+      default: grm::mla::mla_route_kernel<kF32, RW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+    }
+  } else {
+    switch (g.batch) {
+      case 9: grm::mla::mla_route_pipe_kernel<kBF16, PW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+      case 8: grm::mla::mla_route_pipe_kernel<kBF16, PW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+      case 6: grm::mla::mla_route_pipe_kernel<kBF16, PW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+      default: grm::mla::mla_route_kernel<kBF16, RW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+    }
+  }
+#undef GRM_MLA_ARGS
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
+void write_cands(const Cand* c, int topk, uint64_t* out_ids, float* out_scores) {
+  for (int j = 0; j < topk; ++j) {
+    const bool ok = isfinite(c[j].score) && c[j].id != kNoId;
+    out_ids[j] = ok ? c[j].id : kNoId;
+    if (out_scores) out_scores[j] = ok ? c[j].score : __builtin_nanf("");
+  }
+}
+
+// Batched-route plan: K-steps of 16 dims (template), LDS row stride.
+struct BatchPlan {
+  int ks = 0;        // 8, 16 or 18
+  int stride = 0;    // bf16 elements per staged query row
+  int qp_max = 0;    // queries per pass (multiple of 32, <= 256)
+};
+
+bool batch_plan(const MlaDeviceArena* a, int q_timed, BatchPlan* p) {
+  if (a->dtype != kBF16 || q_timed < a->batch_min) return false;
+  const uint32_t ks_need = (a->chunks + 1) / 2;
+  p->ks = ks_need <= 8 ? 8 : (ks_need <= 16 ? 16 : (ks_need <= 18 ? 18 : 0));
+  if (p->ks == 0) return false;
+  p->stride = static_cast<int>(std::max<uint32_t>(a->dim_pad, 16u * p->ks)) + 8;
+  const size_t row = static_cast<size_t>(p->stride) * 2;
+  int qp = grm::mla::kBatchMaxCols;
+  while (qp >= 32 && static_cast<size_t>(qp) * row > a->lds_max) qp /= 2;
+  if (qp < 32) return false;
+  p->qp_max = qp;
+  return true;
+}
+
+template <int KS, int CT>
+int launch_screen(MlaDeviceArena* a, uint32_t n_tiles32, int stride, size_t lds) {
+  auto kern = grm::mla::mla_batch_screen_kernel<KS, CT>;
+  if (lds > 65536) {
+    GRM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds)));
+  }
+  kern<<<a->cus, grm::mla::kBatchWaves * grm::kWave, lds, a->stream>>>(
+      a->d_tiles, a->d_norms, a->capacity, a->chunks, n_tiles32, a->d_qpad, stride, a->d_inv_qn,
+      a->d_entries);
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
+// One pass: queries [0, qc) at q (device, dim values each) through the
+// screen and the merge; results at out[0, qc*topk), certificates at
+// status[0, qc).
+int enqueue_batch_pass(MlaDeviceArena* a, const BatchPlan& p, const unsigned char* q, int q_dtype,
+                       int qc, int topk, Cand* out, unsigned* status) {
+  const int ct = qc <= 32 ? 1 : (qc <= 64 ? 2 : (qc <= 128 ? 4 : 8));
+  const int qp = 32 * ct;
+  grm::mla::mla_batch_qprep_kernel<<<qp, grm::kWave, 0, a->stream>>>(
+      q, q_dtype, qc, a->dim, p.stride, a->d_qpad, a->d_inv_qn);
+  GRM_HIP_CHECK(hipGetLastError());
+  const uint32_t n_tiles32 = static_cast<uint32_t>((a->high_water + 31) / 32);
+  const size_t lds = static_cast<size_t>(qp) * p.stride * 2;
+#define GRM_SCREEN_CT(KS)                                                   \
+  switch (ct) {                                                             \
+    case 1: GRM_CHECK_RC((launch_screen<KS, 1>(a, n_tiles32, p.stride, lds))); break; \
+    case 2: GRM_CHECK_RC((launch_screen<KS, 2>(a, n_tiles32, p.stride, lds))); break; \
+    case 4: GRM_CHECK_RC((launch_screen<KS, 4>(a, n_tiles32, p.stride, lds))); break; \
+    default: GRM_CHECK_RC((launch_screen<KS, 8>(a, n_tiles32, p.stride, lds))); break; \
+  }
+  switch (p.ks) {
+    case 8: GRM_SCREEN_CT(8); break;
+    case 16: GRM_SCREEN_CT(16); break;
+    default: GRM_SCREEN_CT(18); break;
+  }
+#undef GRM_SCREEN_CT
+  const double gamma = 2.0 * (16.0 * p.ks + 2.0 * p.ks) * ldexp(1.0, -24);
+  const double delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
+  grm::mla::mla_batch_merge_kernel<<<qc, grm::mla::kMergeWavesB * grm::kWave, 0, a->stream>>>(
+      a->d_entries, a->cus * grm::mla::kBatchWaves, qp, a->d_tiles, a->d_norms, a->d_ids,
+      a->capacity, a->dim, q, q_dtype, a->dim, gamma, delta, a->d_min_norm, topk, out, status);
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
 int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
                bool on_device, int q_count, int dim, int warmup, int topk,
                uint64_t* out_ids, float* out_scores, float* elapsed_ms) {
@@ -583,24 +776,8 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
   }
   GRM_HIP_CHECK(hipSetDevice(a->device));
   const size_t qbytes = static_cast<size_t>(q_count) * a->dim * elem_size(q_dtype);
-  const uint32_t num_tiles = static_cast<uint32_t>((a->high_water + grm::kWave - 1) / grm::kWave);
-  // The pipelined kernel runs one 16-wave block per CU (4 waves per SIMD);
-  // the plain kernel (rows that do not split into whole batches) 4-wave
-  // blocks, 4 per CU.
-  int batch = 0;
-  if (a->pipeline) {
-    for (int b : {9, 8, 6}) {
-      if (a->chunks % b == 0) {
-        batch = b;
-        break;
-      }
-    }
-  }
-  const uint32_t nw = batch ? grm::mla::kPipeWaves : grm::mla::kRouteWaves;
-  const uint32_t cap = batch ? std::min(a->cus, a->max_blocks) : a->max_blocks;
-  const uint32_t blocks = std::max<uint32_t>(1, std::min((num_tiles + nw - 1) / nw, cap));
-  const size_t per_q = static_cast<size_t>(blocks) * topk;
-  GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * q_count));
+  const SingleGeom g = single_geom(a);
+  const size_t per_q = static_cast<size_t>(g.blocks) * topk;
   const unsigned char* qbase = static_cast<const unsigned char*>(queries);
   if (!on_device) {
     GRM_CHECK_RC(reserve_device(reinterpret_cast<unsigned char**>(&a->d_queries),
@@ -611,47 +788,72 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
   }
   if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
   const size_t qstride = static_cast<size_t>(a->dim) * elem_size(q_dtype);
-  const size_t lds = static_cast<size_t>(a->dim_pad) * sizeof(double);
-  const dim3 grid(blocks), block(nw * grm::kWave);
-  for (int qi = 0; qi < q_count; ++qi) {
-    if (qi == warmup) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
-    const void* q = qbase + qi * qstride;
-    Cand* bout = a->blocks_out.dev + static_cast<size_t>(qi) * per_q;
-#define GRM_MLA_ARGS                                                                  \
-  a->d_tiles, a->d_norms, a->d_ids, num_tiles, a->chunks, a->capacity, a->dim, a->dim_pad, q, \
-      q_dtype, topk, bout
-    constexpr int PW = grm::mla::kPipeWaves;
-    constexpr int RW = grm::mla::kRouteWaves;
-    if (a->dtype == kF32) {
-      switch (batch) {
-        case 9: grm::mla::mla_route_pipe_kernel<kF32, PW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
-        case 8: grm::mla::mla_route_pipe_kernel<kF32, PW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
-        case 6: grm::mla::mla_route_pipe_kernel<kF32, PW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
-        default: grm::mla::mla_route_kernel<kF32, RW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
-      }
-    } else {
-      switch (batch) {
-        case 9: grm::mla::mla_route_pipe_kernel<kBF16, PW, 9><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
-        case 8: grm::mla::mla_route_pipe_kernel<kBF16, PW, 8><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
-        case 6: grm::mla::mla_route_pipe_kernel<kBF16, PW, 6><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
-        default: grm::mla::mla_route_kernel<kBF16, RW><<<grid, block, lds, a->stream>>>(GRM_MLA_ARGS); break;
+  BatchPlan bp;
+  const bool batched = batch_plan(a, q_count - warmup, &bp);
+  std::vector<int> redo;  // queries for the single-query kernel
+  if (batched) {
+    GRM_CHECK_RC(reserve_device(&a->d_qpad, &a->d_qpad_count, static_cast<size_t>(bp.qp_max) * bp.stride));
+    GRM_CHECK_RC(reserve_device(&a->d_inv_qn, &a->d_inv_qn_count, static_cast<size_t>(bp.qp_max)));
+    GRM_CHECK_RC(reserve_device(&a->d_entries, &a->d_entries_count,
+                                static_cast<size_t>(a->cus) * grm::mla::kBatchWaves * bp.qp_max * 2));
+    GRM_CHECK_RC(grm::reserve_mapped(&a->batch_out, static_cast<size_t>(q_count) * topk));
+    GRM_CHECK_RC(grm::reserve_mapped_bytes(&a->batch_status, static_cast<size_t>(q_count) * sizeof(unsigned)));
+    unsigned* st = static_cast<unsigned*>(a->batch_status.dev);
+    const int segments[2][2] = {{0, warmup}, {warmup, q_count}};
+    for (int si = 0; si < 2; ++si) {
+      if (si == 1) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+      for (int q0 = segments[si][0]; q0 < segments[si][1]; q0 += bp.qp_max) {
+        const int qc = std::min(bp.qp_max, segments[si][1] - q0);
+        GRM_CHECK_RC(enqueue_batch_pass(a, bp, qbase + q0 * qstride, q_dtype, qc, topk,
+                                        a->batch_out.dev + static_cast<size_t>(q0) * topk, st + q0));
+        a->batch_passes += 1;
       }
     }
-#undef GRM_MLA_ARGS
-    GRM_HIP_CHECK(hipGetLastError());
+    GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
+    GRM_CHECK_RC(grm::wait_event(a->ev_stop));
+    if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
+    const unsigned* hs = static_cast<const unsigned*>(a->batch_status.host);
+    for (int qi = 0; qi < q_count; ++qi) {
+      if (hs[qi] == 1u) {
+        write_cands(a->batch_out.host + static_cast<size_t>(qi) * topk, topk,
+                    out_ids + static_cast<size_t>(qi) * topk,
+                    out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
+      } else {
+        redo.push_back(qi);
+      }
+    }
+    a->batch_queries += static_cast<uint64_t>(q_count);
+    a->batch_fallbacks += redo.size();
+  } else {
+    for (int qi = 0; qi < q_count; ++qi) redo.push_back(qi);
   }
-  GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
-  GRM_CHECK_RC(grm::wait_event(a->ev_stop));
-  if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
-  a->merged.resize(topk);
-  for (int qi = 0; qi < q_count; ++qi) {
-    grm::host_topk_merge(a->blocks_out.host + static_cast<size_t>(qi) * per_q, per_q, topk,
-                         a->merged.data());
-    for (int j = 0; j < topk; ++j) {
-      const Cand& c = a->merged[j];
-      const bool ok = isfinite(c.score) && c.id != kNoId;
-      out_ids[static_cast<size_t>(qi) * topk + j] = ok ? c.id : kNoId;
-      if (out_scores) out_scores[static_cast<size_t>(qi) * topk + j] = ok ? c.score : __builtin_nanf("");
+  if (!redo.empty()) {
+    a->single_queries += redo.size();
+    GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * redo.size()));
+    // Uncertified batched queries add their time to the timed segment.
+    bool started = false;
+    for (size_t j = 0; j < redo.size(); ++j) {
+      const int qi = redo[j];
+      if (!started && (batched || qi == warmup)) {
+        GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+        started = true;
+      }
+      GRM_CHECK_RC(launch_single(a, g, qbase + qi * qstride, q_dtype, topk,
+                                 a->blocks_out.dev + j * per_q));
+    }
+    GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
+    GRM_CHECK_RC(grm::wait_event(a->ev_stop));
+    if (elapsed_ms) {
+      float ms = 0.0f;
+      GRM_HIP_CHECK(hipEventElapsedTime(&ms, a->ev_start, a->ev_stop));
+      *elapsed_ms = batched ? *elapsed_ms + ms : ms;
+    }
+    a->merged.resize(topk);
+    for (size_t j = 0; j < redo.size(); ++j) {
+      const int qi = redo[j];
+      grm::host_topk_merge(a->blocks_out.host + j * per_q, per_q, topk, a->merged.data());
+      write_cands(a->merged.data(), topk, out_ids + static_cast<size_t>(qi) * topk,
+                  out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
     }
   }
   grm::clear_error();
@@ -899,5 +1101,14 @@ extern "C" int grm_mla_hip_bank_info(MlaDeviceArena* a, uint64_t* out6) {
   out6[3] = a->epoch;
   out6[4] = a->dim;
   out6[5] = static_cast<uint64_t>(a->dtype);
+  return 0;
+}
+
+extern "C" int grm_mla_hip_route_stats(MlaDeviceArena* a, uint64_t* out4) {
+  if (!a || !out4) return grm::fail(-1, "null argument");
+  out4[0] = a->batch_queries;
+  out4[1] = a->batch_fallbacks;
+  out4[2] = a->single_queries;
+  out4[3] = a->batch_passes;
   return 0;
 }

@@ -212,6 +212,16 @@ class MlaNodeBank(_Bank):
         keys = ("live", "capacity", "slots_in_use", "epoch", "dim", "dtype")
         return {k: int(v) for k, v in zip(keys, out)}
 
+    def route_stats(self) -> dict:
+        """Counters since create: batched (matrix-core) queries, their
+        fallbacks to the single-query kernel, single-kernel queries, passes."""
+        self._need_open()
+        out = np.zeros(4, dtype=np.uint64)
+        _lib.check(self._lib.grm_mla_hip_route_stats(self._h, _ptr(out)),
+                   "MLA route stats")
+        keys = ("batched", "fallbacks", "single", "passes")
+        return {k: int(v) for k, v in zip(keys, out)}
+
 
 class GqaNodeBank(_Bank):
     """Ragged GQA bank: node i has a key block [kv_heads, L_i, head_dim]."""

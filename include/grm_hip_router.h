@@ -170,6 +170,12 @@ int grm_mla_hip_sync(MlaDeviceArena* arena);
  * No counterpart. */
 int grm_mla_hip_bank_info(MlaDeviceArena* arena, uint64_t* out6);
 
+/* Route counters since create: [queries screened by the batched
+ * matrix-core path, of those routed again on the single-query path (no
+ * certificate), queries through the single-query kernel, screen passes].
+ * No counterpart. */
+int grm_mla_hip_route_stats(MlaDeviceArena* arena, uint64_t* out4);
+
 /* Ragged GQA node bank over CSR token offsets (no counterpart: the reference
  * zero-pads every node to the longest, core/graft_arena.py:2979-3042).
  * keys_host: node i's block [kv_heads][L_i][head_dim] starts at value

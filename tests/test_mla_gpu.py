@@ -194,3 +194,100 @@ def test_headline_size_parity(hip_lib):
         res = bank.route(qs, cfg["topk"])
     ids, sc, _ = oracle.mla_route(rows, qs, cfg["topk"])
     assert_same(res.ids, res.scores, ids, sc)
+
+
+# ------------------------------------------------ batched route (bf16 banks)
+
+def _f32(bits):
+    return bf16_bits_to_f32(bits).reshape(bits.shape)
+
+
+@pytest.mark.parametrize("nq,k", [(4, 1), (33, 8), (64, 16), (256, 8), (300, 5)])
+def test_batched_bf16_route_matches_oracle(hip_lib, nq, k):
+    rows = wl.mla_rows(40_000, 288, seed=61, dtype="bf16")
+    qs = wl.mla_queries(nq, 288, seed=61, dtype="bf16")
+    with MlaNodeBank(rows, dtype="bf16") as bank:
+        res = bank.route(qs, k)
+        stats = bank.route_stats()
+    ids, sc, _ = oracle.mla_route(_f32(rows), _f32(qs), k)
+    assert_same(res.ids, res.scores, ids, sc)
+    assert stats["batched"] == nq and stats["fallbacks"] <= max(1, nq // 50)
+
+
+@pytest.mark.parametrize("dim", [16, 100, 128, 200, 256, 288])
+def test_batched_dims(hip_lib, dim):
+    rows = wl.mla_rows(3000, dim, seed=dim, dtype="bf16")
+    qs = wl.mla_queries(40, dim, seed=dim, dtype="bf16")
+    with MlaNodeBank(rows, dtype="bf16") as bank:
+        res = bank.route(qs, 6, warmup=3)
+        stats = bank.route_stats()
+    ids, sc, _ = oracle.mla_route(_f32(rows), _f32(qs), 6)
+    assert_same(res.ids, res.scores, ids, sc)
+    assert stats["batched"] == 40
+
+
+def test_batched_ties_zero_and_nan_rows(hip_lib):
+    # Duplicate rows tie exactly (lowest node id first, possibly through
+    # the single-query path when no certificate exists), an all-zero row
+    # scores 0, NaN rows and a NaN query are never ranked.
+    rng = np.random.default_rng(62)
+    base = rng.standard_normal((60, 128)).astype(np.float32)
+    rows = np.repeat(base, 20, axis=0)
+    rows[5] = 0.0
+    rows[17, 3] = np.nan
+    node_ids = rng.permutation(rows.shape[0]).astype(np.uint64) + 7
+    qs = np.concatenate([base[:12] + 0.1 * base[12:24],
+                         np.zeros((1, 128), np.float32)])
+    qs[3, 0] = np.nan
+    bits, qbits = oracle.bf16_bits(rows), oracle.bf16_bits(qs)
+    with MlaNodeBank(bits, node_ids, dtype="bf16") as bank:
+        res = bank.route(qbits, 10)
+    ids, sc, _ = oracle.mla_route(_f32(bits), _f32(qbits), 10, node_ids=node_ids)
+    assert_same(res.ids, res.scores, ids, sc)
+
+
+def test_batched_f32_queries_on_bf16_bank(hip_lib):
+    # fp32 queries are rounded to bf16 for the matrix cores; the bound
+    # covers the rounding and the law uses the fp32 values.
+    rows = wl.mla_rows(20_000, 288, seed=63, dtype="bf16")
+    qs = wl.mla_queries(16, 288, seed=63)
+    with MlaNodeBank(rows, dtype="bf16") as bank:
+        res = bank.route(qs, 5, query_dtype="f32")
+    ids, sc, _ = oracle.mla_route(_f32(rows), qs, 5)
+    assert_same(res.ids, res.scores, ids, sc)
+
+
+def test_batched_after_append_and_evict(hip_lib):
+    rng = np.random.default_rng(64)
+    rows = wl.mla_rows(5000, 256, seed=64, dtype="bf16")
+    ids0 = np.arange(5000, dtype=np.uint64) * 2 + 1
+    qs = wl.mla_queries(24, 256, seed=64, dtype="bf16")
+    live = {int(i): rows[j] for j, i in enumerate(ids0)}
+    with MlaNodeBank(rows, ids0, dtype="bf16", capacity=6000) as bank:
+        for step in range(3):
+            ev = rng.choice(sorted(live), size=300, replace=False).astype(np.uint64)
+            bank.evict(ev)
+            for i in ev.tolist():
+                del live[i]
+            new = wl.mla_rows(250, 256, seed=640 + step, dtype="bf16")
+            nid = np.arange(250, dtype=np.uint64) + 100_000 + 1000 * step
+            bank.append(new, nid)
+            live.update({int(i): r for i, r in zip(nid.tolist(), new)})
+            res = bank.route(qs, 8)
+            keys = np.asarray(sorted(live), dtype=np.uint64)
+            mat = np.stack([live[int(k)] for k in keys])
+            want, wsc, _ = oracle.mla_route(_f32(mat), _f32(qs), 8, node_ids=keys)
+            assert_same(res.ids, res.scores, want, wsc)
+
+
+def test_batched_config_parity(hip_lib):
+    # 256 queries x 1,000,000 x 288 bf16, top-8: one screen pass
+    cfg = wl.MLA_BATCHED
+    rows = wl.mla_rows(cfg["nodes"], cfg["dim"], seed=cfg["seed"], dtype="bf16")
+    qs = wl.mla_queries(cfg["queries"], cfg["dim"], seed=cfg["seed"], dtype="bf16")
+    with MlaNodeBank(rows, dtype="bf16") as bank:
+        res = bank.route(qs, cfg["topk"])
+        stats = bank.route_stats()
+    ids, sc, _ = oracle.mla_route(_f32(rows), _f32(qs), cfg["topk"])
+    assert_same(res.ids, res.scores, ids, sc)
+    assert stats["passes"] == 1 and stats["fallbacks"] <= 2
