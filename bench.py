@@ -107,6 +107,78 @@ def bench_mla(steps: int, warmup: int):
                 mean_dev=mean_dev, cfg=cfg)
 
 
+def bench_mla_batched(steps: int, warmup: int, cpu_queries: int):
+    """256 bf16 queries per call on a 1,000,000 x 288 bf16 bank, top-8:
+    the matrix-core screen, the certified merge and exact rescore, plus
+    any single-query fallbacks, all inside the timed call."""
+    import oracle
+    from graftrepository_amd import MlaNodeBank, workloads as wl
+    from graftrepository_amd.mla_probe import HipProbe
+
+    cfg = wl.MLA_BATCHED
+    n, d, nq, k = cfg["nodes"], cfg["dim"], cfg["queries"], cfg["topk"]
+    rows = wl.mla_rows(n, d, seed=cfg["seed"], dtype="bf16")
+    q = wl.mla_queries(nq, d, seed=cfg["seed"], dtype="bf16")
+    bank = MlaNodeBank(rows, dtype="bf16")
+    probe = HipProbe()
+    dq = probe.upload_queries(q.view(np.float32))  # bf16 bits, uploaded raw
+    for _ in range(warmup):
+        bank.route(dq, k, on_device=True, query_dtype="bf16", query_count=nq)
+    s0 = bank.route_stats()
+    walls, devs, screens = [], [], []
+    for _ in range(steps):
+        r = bank.route(dq, k, on_device=True, query_dtype="bf16", query_count=nq)
+        walls.append(r.wall_ms)
+        devs.append(r.device_ms)
+        screens.append(bank.screen_ms())
+    s1 = bank.route_stats()
+    dq.close()
+    bank.close()
+    fallbacks = (s1["fallbacks"] - s0["fallbacks"]) / max(1, steps)
+    # parity on a bounded sample of the queries (oracle fp64 law on the host)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    sample = min(cpu_queries, nq)
+    cpu = None
+    if sample > 0:
+        rf = oracle.bf16_to_f32(rows).reshape(rows.shape)
+        qf = oracle.bf16_to_f32(q[:sample]).reshape(sample, d)
+        t0 = time.perf_counter()
+        ids, sc, _ = oracle.mla_route(rf, qf, k, threads=threads)
+        cpu_ms = (time.perf_counter() - t0) * 1e3
+        match = bool(np.array_equal(ids, r.ids[:sample])) and bool(
+            np.array_equal(sc.view(np.uint32), r.scores[:sample].view(np.uint32)))
+        cpu = {"value": round(cpu_ms / sample * nq, 1), "unit": "ms per call",
+               "cores": threads, "kind": "port",
+               "sample": f"{sample} of the {nq} queries through the oracle's "
+                         f"fp64 law on the same bank, scaled to {nq}",
+               "parity_with_gpu": match}
+    flops = 2.0 * nq * n * d
+    bytes_screen = n * d * 2 + n * 4
+    scr = float(np.mean(screens))
+    tflops = flops / (scr * 1e-3) / 1e12
+    gbs = bytes_screen / (scr * 1e-3) / 1e9
+    log(f"[mla-batched] {nq} queries/call  p50 {pct(walls, 50):.4f} ms  "
+        f"device {np.mean(devs):.4f} ms  screen {scr:.4f} ms  {tflops:.0f} TFLOP/s  "
+        f"{gbs:.0f} GB/s  fallbacks/call {fallbacks:.2f}  "
+        f"oracle match {cpu['parity_with_gpu'] if cpu else 'not checked'}")
+    return {
+        "workload": "mla_batched_route", "nodes": n, "dim": d, "queries_per_call": nq,
+        "bank_dtype": "bf16", "query_dtype": "bf16", "topk": k, "steps": steps,
+        "p50_ms": round(pct(walls, 50), 5), "p99_ms": round(pct(walls, 99), 5),
+        "device_ms_mean": round(float(np.mean(devs)), 5),
+        "queries_per_s": round(nq / (pct(walls, 50) * 1e-3), 1),
+        "fallbacks_per_call": fallbacks,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
+                     "kernel": "mla_batch_screen_kernel<18, 8>",
+                     "flops_per_launch": flops, "kernel_ms_mean": round(scr, 5)},
+        "roofline_hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "bytes_per_launch": bytes_screen},
+        "cpu_baseline": cpu,
+    }
+
+
 def bench_gqa(steps: int, warmup: int):
     from graftrepository_amd import GqaNodeBank, workloads as wl
     from graftrepository_amd.gqa_probe import HipProbe
@@ -175,7 +247,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--gqa-steps", type=int, default=300)
-    ap.add_argument("--only", choices=["all", "mla", "gqa"], default="all")
+    ap.add_argument("--batched-steps", type=int, default=100)
+    ap.add_argument("--only", choices=["all", "mla", "gqa", "batched"], default="all")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -200,6 +273,10 @@ def main() -> int:
         m = bench_mla(args.steps, args.warmup)
     if args.only in ("all", "gqa"):
         g = bench_gqa(args.gqa_steps, min(args.warmup, 20))
+    b = None
+    if args.only in ("all", "batched"):
+        b = bench_mla_batched(args.batched_steps, min(args.warmup, 5),
+                              0 if args.skip_cpu else 4)
     cpu = None
     if m is not None and not args.skip_cpu:
         cpu = cpu_baseline_mla(m, args.cpu_seconds)
@@ -258,6 +335,16 @@ def main() -> int:
                    "higher_is_better": False, "scaling": "weak",
                    "vs_baseline": None, "dtype": "f64",
                    "data": "synthetic", "config": gq}
+    if b is not None:
+        if out:
+            out["mla_batched"] = b
+        else:
+            out = {"metric": "p50 batched MLA route latency (ms per 256-query call)",
+                   "value": b["p50_ms"], "unit": "ms", "n_gpus": 1,
+                   "steps": args.batched_steps, "warmup": args.warmup,
+                   "ms_per_step": b["p50_ms"], "higher_is_better": False,
+                   "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                   "data": "synthetic", "config": b}
     if cpu is not None:
         out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)

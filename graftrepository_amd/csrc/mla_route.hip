@@ -394,7 +394,7 @@ struct MlaDeviceArena {
   size_t d_qpad_count = 0;
   float* d_inv_qn = nullptr;
   size_t d_inv_qn_count = 0;
-  grm::mla::BatchEntry* d_entries = nullptr;
+  uint32_t* d_entries = nullptr;   // screen result planes
   size_t d_entries_count = 0;
   grm::MappedCands batch_out;
   grm::MappedBuf batch_status;
@@ -404,6 +404,8 @@ struct MlaDeviceArena {
   uint64_t batch_fallbacks = 0;  // of those, routed again on the single-query path
   uint64_t batch_passes = 0;     // screen passes
   uint64_t single_queries = 0;   // queries through the single-query kernel
+  std::vector<hipEvent_t> screen_ev;  // begin/end pairs around timed screens
+  float screen_ms = 0.0f;        // screen-kernel time of the last batched route
   bool pipeline = true;     // software-pipelined kernel when rows allow it
   uint32_t cus = 256;       // compute units of the device
   uint32_t max_blocks = 0;  // plain-kernel grid cap (4 blocks per CU)
@@ -434,6 +436,7 @@ void destroy_arena(MlaDeviceArena* a) {
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
   if (a->ev_mut) (void)hipEventDestroy(a->ev_mut);
+  for (hipEvent_t e : a->screen_ev) (void)hipEventDestroy(e);
   if (a->stream) (void)hipStreamDestroy(a->stream);
   if (a->side) (void)hipStreamDestroy(a->side);
   delete a;
@@ -705,10 +708,17 @@ bool batch_plan(const MlaDeviceArena* a, int q_timed, BatchPlan* p) {
   p->ks = ks_need <= 8 ? 8 : (ks_need <= 16 ? 16 : (ks_need <= 18 ? 18 : 0));
   if (p->ks == 0) return false;
   p->stride = static_cast<int>(std::max<uint32_t>(a->dim_pad, 16u * p->ks)) + 8;
-  const size_t row = static_cast<size_t>(p->stride) * 2;
+  const size_t row = std::max(static_cast<size_t>(p->stride) * 2,
+                              static_cast<size_t>(grm::mla::kEntryPlanes) * grm::mla::kBatchWaves * 4);
   int qp = grm::mla::kBatchMaxCols;
   while (qp >= 32 && static_cast<size_t>(qp) * row > a->lds_max) qp /= 2;
   if (qp < 32) return false;
+  // the merge holds kMergePer sub-streams (screen wavefronts) per thread
+  if (static_cast<size_t>(a->cus) * grm::mla::kBatchWaves >
+      static_cast<size_t>(grm::mla::kMergeLoaders) * grm::mla::kMergePer) {
+    return false;
+  }
+  if (a->dim > grm::mla::kBatchMaxDim) return false;
   p->qp_max = qp;
   return true;
 }
@@ -730,16 +740,20 @@ int launch_screen(MlaDeviceArena* a, uint32_t n_tiles32, int stride, size_t lds)
 
 // One pass: queries [0, qc) at q (device, dim values each) through the
 // screen and the merge; results at out[0, qc*topk), certificates at
-// status[0, qc).
+// status[0, qc).  ev (optional) is a pair of events recorded around the
+// screen kernel.
 int enqueue_batch_pass(MlaDeviceArena* a, const BatchPlan& p, const unsigned char* q, int q_dtype,
-                       int qc, int topk, Cand* out, unsigned* status) {
+                       int qc, int topk, Cand* out, unsigned* status, hipEvent_t* ev) {
   const int ct = qc <= 32 ? 1 : (qc <= 64 ? 2 : (qc <= 128 ? 4 : 8));
   const int qp = 32 * ct;
   grm::mla::mla_batch_qprep_kernel<<<qp, grm::kWave, 0, a->stream>>>(
       q, q_dtype, qc, a->dim, p.stride, a->d_qpad, a->d_inv_qn);
   GRM_HIP_CHECK(hipGetLastError());
   const uint32_t n_tiles32 = static_cast<uint32_t>((a->high_water + 31) / 32);
-  const size_t lds = static_cast<size_t>(qp) * p.stride * 2;
+  // LDS: the staged queries, later the block's result rows
+  const size_t lds = std::max(static_cast<size_t>(qp) * p.stride * 2,
+                              static_cast<size_t>(grm::mla::kEntryPlanes) * qp * grm::mla::kBatchWaves * 4);
+  if (ev) GRM_HIP_CHECK(hipEventRecord(ev[0], a->stream));
 #define GRM_SCREEN_CT(KS)                                                   \
   switch (ct) {                                                             \
     case 1: GRM_CHECK_RC((launch_screen<KS, 1>(a, n_tiles32, p.stride, lds))); break; \
@@ -753,9 +767,10 @@ int enqueue_batch_pass(MlaDeviceArena* a, const BatchPlan& p, const unsigned cha
     default: GRM_SCREEN_CT(18); break;
   }
 #undef GRM_SCREEN_CT
+  if (ev) GRM_HIP_CHECK(hipEventRecord(ev[1], a->stream));
   const double gamma = 2.0 * (16.0 * p.ks + 2.0 * p.ks) * ldexp(1.0, -24);
   const double delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
-  grm::mla::mla_batch_merge_kernel<<<qc, grm::mla::kMergeWavesB * grm::kWave, 0, a->stream>>>(
+  grm::mla::mla_batch_merge_kernel<<<qc, grm::mla::kMergeThreads, 0, a->stream>>>(
       a->d_entries, a->cus * grm::mla::kBatchWaves, qp, a->d_tiles, a->d_norms, a->d_ids,
       a->capacity, a->dim, q, q_dtype, a->dim, gamma, delta, a->d_min_norm, topk, out, status);
   GRM_HIP_CHECK(hipGetLastError());
@@ -790,28 +805,45 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
   const size_t qstride = static_cast<size_t>(a->dim) * elem_size(q_dtype);
   BatchPlan bp;
   const bool batched = batch_plan(a, q_count - warmup, &bp);
+  a->screen_ms = 0.0f;
   std::vector<int> redo;  // queries for the single-query kernel
   if (batched) {
     GRM_CHECK_RC(reserve_device(&a->d_qpad, &a->d_qpad_count, static_cast<size_t>(bp.qp_max) * bp.stride));
     GRM_CHECK_RC(reserve_device(&a->d_inv_qn, &a->d_inv_qn_count, static_cast<size_t>(bp.qp_max)));
     GRM_CHECK_RC(reserve_device(&a->d_entries, &a->d_entries_count,
-                                static_cast<size_t>(a->cus) * grm::mla::kBatchWaves * bp.qp_max * 2));
+                                static_cast<size_t>(grm::mla::kEntryPlanes) * bp.qp_max * a->cus *
+                                    grm::mla::kBatchWaves));
     GRM_CHECK_RC(grm::reserve_mapped(&a->batch_out, static_cast<size_t>(q_count) * topk));
     GRM_CHECK_RC(grm::reserve_mapped_bytes(&a->batch_status, static_cast<size_t>(q_count) * sizeof(unsigned)));
     unsigned* st = static_cast<unsigned*>(a->batch_status.dev);
+    const int timed_passes = (q_count - warmup + bp.qp_max - 1) / bp.qp_max;
+    while (a->screen_ev.size() < 2 * static_cast<size_t>(timed_passes)) {
+      hipEvent_t e = nullptr;
+      GRM_HIP_CHECK(hipEventCreate(&e));
+      a->screen_ev.push_back(e);
+    }
     const int segments[2][2] = {{0, warmup}, {warmup, q_count}};
+    int tp = 0;
     for (int si = 0; si < 2; ++si) {
       if (si == 1) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
       for (int q0 = segments[si][0]; q0 < segments[si][1]; q0 += bp.qp_max) {
         const int qc = std::min(bp.qp_max, segments[si][1] - q0);
+        hipEvent_t* ev = si == 1 ? &a->screen_ev[2 * tp++] : nullptr;
         GRM_CHECK_RC(enqueue_batch_pass(a, bp, qbase + q0 * qstride, q_dtype, qc, topk,
-                                        a->batch_out.dev + static_cast<size_t>(q0) * topk, st + q0));
+                                        a->batch_out.dev + static_cast<size_t>(q0) * topk, st + q0,
+                                        ev));
         a->batch_passes += 1;
       }
     }
     GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
     GRM_CHECK_RC(grm::wait_event(a->ev_stop));
     if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
+    a->screen_ms = 0.0f;
+    for (int i = 0; i < tp; ++i) {
+      float ms = 0.0f;
+      GRM_HIP_CHECK(hipEventElapsedTime(&ms, a->screen_ev[2 * i], a->screen_ev[2 * i + 1]));
+      a->screen_ms += ms;
+    }
     const unsigned* hs = static_cast<const unsigned*>(a->batch_status.host);
     for (int qi = 0; qi < q_count; ++qi) {
       if (hs[qi] == 1u) {
@@ -1110,5 +1142,11 @@ extern "C" int grm_mla_hip_route_stats(MlaDeviceArena* a, uint64_t* out4) {
   out4[1] = a->batch_fallbacks;
   out4[2] = a->single_queries;
   out4[3] = a->batch_passes;
+  return 0;
+}
+
+extern "C" int grm_mla_hip_screen_ms(MlaDeviceArena* a, float* ms) {
+  if (!a || !ms) return grm::fail(-1, "null argument");
+  *ms = a->screen_ms;
   return 0;
 }

@@ -222,6 +222,15 @@ class MlaNodeBank(_Bank):
         keys = ("batched", "fallbacks", "single", "passes")
         return {k: int(v) for k, v in zip(keys, out)}
 
+    def screen_ms(self) -> float:
+        """Device time of the matrix-core screen kernels in the timed part
+        of the last route (0.0 when it did not take the batched path)."""
+        self._need_open()
+        out = np.zeros(1, dtype=np.float32)
+        _lib.check(self._lib.grm_mla_hip_screen_ms(self._h, _ptr(out)),
+                   "MLA screen time")
+        return float(out[0])
+
 
 class GqaNodeBank(_Bank):
     """Ragged GQA bank: node i has a key block [kv_heads, L_i, head_dim]."""

@@ -176,6 +176,11 @@ int grm_mla_hip_bank_info(MlaDeviceArena* arena, uint64_t* out6);
  * No counterpart. */
 int grm_mla_hip_route_stats(MlaDeviceArena* arena, uint64_t* out4);
 
+/* Device time (ms, from events on the route stream) of the matrix-core
+ * screen kernels in the timed segment of the last batched route; 0 when
+ * the last route was not batched.  No counterpart. */
+int grm_mla_hip_screen_ms(MlaDeviceArena* arena, float* ms);
+
 /* Ragged GQA node bank over CSR token offsets (no counterpart: the reference
  * zero-pads every node to the longest, core/graft_arena.py:2979-3042).
  * keys_host: node i's block [kv_heads][L_i][head_dim] starts at value
