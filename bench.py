@@ -217,6 +217,84 @@ def bench_gqa(steps: int, warmup: int):
                 sum_l=sum_l, cfg=cfg, kv=kv, H=H)
 
 
+def bench_gqa_int8(steps: int, warmup: int):
+    """100,000 lognormal-length nodes (median 256, sigma 0.5, cap 4096),
+    8 kv heads x 128 stored INT8 with one fp16 scale per row, 32 bf16 query
+    heads, 16 queries per call, top-5; 1% of the nodes are evicted and as
+    many appended between calls (not timed; reported apart)."""
+    from graftrepository_amd import GqaNodeBank, workloads as wl
+    from graftrepository_amd.gqa_probe import HipProbe
+
+    cfg = wl.GQA_INT8
+    n, kv, hd, H = cfg["nodes"], cfg["kv_heads"] * cfg["layers"], cfg["head_dim"], cfg["heads"]
+    lens = wl.gqa_lengths(n, cfg["seed"], kind="lognormal", median=cfg["median"],
+                          sigma=cfg["sigma"], cap=cfg["cap"])
+    t0 = time.time()
+    codes, scales, offs = wl.gqa_int8_bank_device(lens, kv, hd, seed=cfg["seed"])
+    log(f"[int8] generated {codes.size / 1e9:.1f} GB of codes in {time.time() - t0:.1f}s")
+    churn = n // 100
+    pool = []
+    for j in range(3):
+        nl = wl.gqa_lengths(churn, 200 + j, kind="lognormal", median=cfg["median"],
+                            sigma=cfg["sigma"], cap=cfg["cap"])
+        nc, ns, _ = wl.gqa_int8_bank(nl, kv, hd, seed=200 + j)
+        pool.append((nl, nc, ns))
+    extra = max(int(p[0].sum()) + 7 * churn for p in pool) * (steps + warmup + 1)
+    t0 = time.time()
+    bank = GqaNodeBank(codes, offs, kv_heads=kv, head_dim=hd, dtype="i8", scales=scales,
+                       scale_dtype="f16", group_size=hd, capacity_nodes=n + churn,
+                       capacity_tokens=int(offs[-1]) + extra)
+    log(f"[int8] bank created in {time.time() - t0:.1f}s")
+    del codes
+    q = wl.gqa_queries(cfg["queries"], H, 1, hd, cfg["seed"], dtype="bf16")
+    probe = HipProbe()
+    dq = probe.upload_queries(q.view(np.float32))
+    rng = np.random.default_rng(cfg["seed"])
+    live = np.arange(n, dtype=np.uint64)
+    next_id = n
+    walls, devs, churns, live_tokens = [], [], [], []
+    tok_of = {int(i): int(x) for i, x in enumerate(lens)}
+    for step in range(warmup + steps):
+        r = bank.route(dq, cfg["topk"], on_device=True, query_dtype="bf16", query_shape=q.shape)
+        if step >= warmup:
+            walls.append(r.wall_ms)
+            devs.append(r.device_ms)
+            live_tokens.append(sum(tok_of.values()))
+        t1 = time.perf_counter()
+        pick = rng.choice(live.size, size=churn, replace=False)
+        ev = live[pick]
+        bank.evict(ev)
+        nl, nc, ns = pool[step % 3]
+        nid = np.arange(next_id, next_id + churn, dtype=np.uint64)
+        next_id += churn
+        bank.append(nc, nl, nid, scales=ns)
+        bank.sync()
+        churns.append((time.perf_counter() - t1) * 1e3)
+        for i in ev.tolist():
+            del tok_of[i]
+        tok_of.update({int(i): int(x) for i, x in zip(nid, nl)})
+        live[pick] = nid
+    dq.close()
+    bank.close()
+    mean_dev = float(np.mean(devs))
+    bytes_per_call = float(np.mean(live_tokens)) * kv * (hd + 2)
+    achieved = bytes_per_call / (mean_dev * 1e-3) / 1e9
+    log(f"[int8] p50 {pct(walls, 50):.4f} ms  p99 {pct(walls, 99):.4f} ms  device {mean_dev:.4f} ms"
+        f"  {achieved:.0f} GB/s  churn {np.median(churns):.1f} ms")
+    return {
+        "workload": "gqa_int8_route", "nodes": n, "lengths": "lognormal median 256 sigma 0.5 cap 4096",
+        "kv_heads": kv, "query_heads": H, "head_dim": hd, "bank_dtype": "i8+f16 row scales",
+        "queries_per_call": cfg["queries"], "topk": cfg["topk"], "steps": steps,
+        "live_tokens_mean": round(float(np.mean(live_tokens))),
+        "p50_ms": round(pct(walls, 50), 5), "p99_ms": round(pct(walls, 99), 5),
+        "device_ms_mean": round(mean_dev, 5),
+        "churn_ms_p50": round(float(np.median(churns)), 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "bytes_per_call": round(bytes_per_call)},
+    }
+
+
 def cpu_baseline_mla(m, seconds: float):
     """Oracle fp64 route on the host cores, bounded to about `seconds`."""
     import oracle
@@ -248,7 +326,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--gqa-steps", type=int, default=300)
     ap.add_argument("--batched-steps", type=int, default=100)
-    ap.add_argument("--only", choices=["all", "mla", "gqa", "batched"], default="all")
+    ap.add_argument("--int8-steps", type=int, default=20)
+    ap.add_argument("--only", choices=["all", "mla", "gqa", "batched", "int8"], default="all")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -273,6 +352,9 @@ def main() -> int:
         m = bench_mla(args.steps, args.warmup)
     if args.only in ("all", "gqa"):
         g = bench_gqa(args.gqa_steps, min(args.warmup, 20))
+    i8 = None
+    if args.only in ("all", "int8"):
+        i8 = bench_gqa_int8(args.int8_steps, 2)
     b = None
     if args.only in ("all", "batched"):
         b = bench_mla_batched(args.batched_steps, min(args.warmup, 5),
@@ -345,6 +427,15 @@ def main() -> int:
                    "ms_per_step": b["p50_ms"], "higher_is_better": False,
                    "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
                    "data": "synthetic", "config": b}
+    if i8 is not None:
+        if out:
+            out["gqa_int8"] = i8
+        else:
+            out = {"metric": "p50 INT8 ragged GQA route latency (ms per 16-query call)",
+                   "value": i8["p50_ms"], "unit": "ms", "n_gpus": 1,
+                   "steps": args.int8_steps, "warmup": 2, "ms_per_step": i8["p50_ms"],
+                   "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+                   "dtype": "f64", "data": "synthetic", "config": i8}
     if cpu is not None:
         out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)

@@ -100,6 +100,67 @@ def gqa_bank(lengths: np.ndarray, kv_heads: int, head_dim: int, seed: int,
     return out, offs
 
 
+def gqa_int8_bank(lengths: np.ndarray, kv_heads: int, head_dim: int, seed: int,
+                  workers: int = 8) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """INT8 CSR bank in the packed graft format: codes (node blocks
+    [kv, L_i, hd] back to back, int8), one fp16 scale per (kv head, token)
+    row (group size = head_dim; fp16 bits) and tok_offsets [N+1].
+
+    Codes are uniform in [-127, 127] and scales uniform in [2, 4] / 127
+    (the symmetric code range of rows whose absolute maximum lies in
+    [2, 4]); `workers` threads fill fixed 64 MiB chunks, each from its own
+    child seed, so banks of tens of GB build in seconds and the result
+    depends only on (lengths, kv_heads, head_dim, seed)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    lengths = np.asarray(lengths, dtype=np.uint64)
+    offs = np.zeros(lengths.size + 1, dtype=np.uint64)
+    offs[1:] = np.cumsum(lengths)
+    rows = int(offs[-1]) * kv_heads
+    codes = np.empty(rows * head_dim, dtype=np.int8)
+    step = 1 << 26
+    chunks = [(i, min(step, codes.size - i)) for i in range(0, codes.size, step)]
+    seqs = np.random.SeedSequence(int(seed)).spawn(len(chunks) + 1)
+
+    def fill(j):
+        i, n = chunks[j]
+        seg = codes[i:i + n]
+        raw = np.random.SFC64(seqs[j]).random_raw((n + 7) // 8).view(np.int8)
+        seg[:] = raw[:n]
+        np.maximum(seg, -127, out=seg)
+
+    with ThreadPoolExecutor(max_workers=max(1, workers)) as ex:
+        list(ex.map(fill, range(len(chunks))))
+    rng = np.random.default_rng(seqs[-1])
+    scales = (rng.uniform(2.0, 4.0, size=rows) / 127.0).astype(np.float16).view(np.uint16)
+    return codes, scales, offs
+
+
+def gqa_int8_bank_device(lengths: np.ndarray, kv_heads: int, head_dim: int,
+                         seed: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """gqa_int8_bank's format and distributions for banks of tens of GB:
+    the codes are drawn on the GPU (torch's seeded Philox generator, 1 GiB
+    at a time) and copied to host memory; the scales as gqa_int8_bank."""
+    import torch
+
+    lengths = np.asarray(lengths, dtype=np.uint64)
+    offs = np.zeros(lengths.size + 1, dtype=np.uint64)
+    offs[1:] = np.cumsum(lengths)
+    rows = int(offs[-1]) * kv_heads
+    codes = np.empty(rows * head_dim, dtype=np.int8)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(int(seed))
+    step = 1 << 30
+    for i in range(0, codes.size, step):
+        n = min(step, codes.size - i)
+        dev = torch.randint(-127, 128, (n,), dtype=torch.int8, device="cuda", generator=gen)
+        torch.from_numpy(codes[i:i + n]).copy_(dev)
+        del dev
+    rng = np.random.default_rng(np.random.SeedSequence(int(seed)).spawn(1)[0])
+    scales = (rng.uniform(2.0, 4.0, size=rows) / 127.0).astype(np.float16).view(np.uint16)
+    return codes, scales, offs
+
+
 def gqa_queries(count: int, heads: int, tokens: int, head_dim: int, seed: int,
                 dtype: str = "bf16") -> np.ndarray:
     rng = _rng(seed + 0x9E5)
