@@ -230,7 +230,7 @@ def bench_gqa_int8(steps: int, warmup: int):
     lens = wl.gqa_lengths(n, cfg["seed"], kind="lognormal", median=cfg["median"],
                           sigma=cfg["sigma"], cap=cfg["cap"])
     t0 = time.time()
-    codes, scales, offs = wl.gqa_int8_bank_device(lens, kv, hd, seed=cfg["seed"])
+    codes, scales, offs = wl.gqa_int8_bank(lens, kv, hd, seed=cfg["seed"])
     log(f"[int8] generated {codes.size / 1e9:.1f} GB of codes in {time.time() - t0:.1f}s")
     churn = n // 100
     pool = []

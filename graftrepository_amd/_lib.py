@@ -88,7 +88,15 @@ def library_path() -> Path:
 
 def load(path: str | Path | None = None) -> ctypes.CDLL:
     """Load the route library once per path; raise HipRouterUnavailable if
-    it is absent or does not export the declared symbols."""
+    it is absent or does not export the declared symbols.
+
+    The library binds to the HIP runtime the process has mapped under the
+    soname libamdhip64.so.7 (ROCm's, unless another copy is mapped first).
+    PyTorch wheels bundle their own copy of that runtime, opened under a
+    different file name, so a process that imports torch after this load
+    maps a second HIP and HSA runtime beside the first, and torch may then
+    find no device.  A process that uses both imports torch first: the
+    library then binds to torch's copy and the two share one runtime."""
     path = Path(path) if path is not None else library_path()
     key = str(path.resolve()) if path.exists() else str(path)
     if key in _libs:

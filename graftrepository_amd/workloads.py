@@ -100,16 +100,45 @@ def gqa_bank(lengths: np.ndarray, kv_heads: int, head_dim: int, seed: int,
     return out, offs
 
 
+_SM1 = np.uint64(0x9E3779B97F4A7C15)
+_SM2 = np.uint64(0xBF58476D1CE4E5B9)
+_SM3 = np.uint64(0x94D049BB133111EB)
+
+
+def _splitmix_fill(out: np.ndarray, start: int, seed: int) -> None:
+    """out[i] = splitmix64 finaliser of ((start + i) * golden + seed): a
+    counter-based stream, so any slice can be filled independently."""
+    blk = 1 << 18
+    tmp = np.empty(min(blk, out.size), dtype=np.uint64)
+    key = np.uint64(seed & 0xFFFFFFFFFFFFFFFF)
+    for i in range(0, out.size, blk):
+        n = min(blk, out.size - i)
+        z = out[i:i + n]
+        t = tmp[:n]
+        z[:] = np.arange(start + i, start + i + n, dtype=np.uint64)
+        z *= _SM1
+        z += key
+        np.right_shift(z, np.uint64(30), out=t)
+        z ^= t
+        z *= _SM2
+        np.right_shift(z, np.uint64(27), out=t)
+        z ^= t
+        z *= _SM3
+        np.right_shift(z, np.uint64(31), out=t)
+        z ^= t
+
+
 def gqa_int8_bank(lengths: np.ndarray, kv_heads: int, head_dim: int, seed: int,
-                  workers: int = 8) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+                  workers: int = 16) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """INT8 CSR bank in the packed graft format: codes (node blocks
     [kv, L_i, hd] back to back, int8), one fp16 scale per (kv head, token)
     row (group size = head_dim; fp16 bits) and tok_offsets [N+1].
 
-    Codes are uniform in [-127, 127] and scales uniform in [2, 4] / 127
-    (the symmetric code range of rows whose absolute maximum lies in
-    [2, 4]); `workers` threads fill fixed 64 MiB chunks, each from its own
-    child seed, so banks of tens of GB build in seconds and the result
+    Codes are uniform in [-127, 127] (the bytes of a splitmix64 counter
+    stream, -128 folded to -127) and scales uniform in [2, 4] / 127 (the
+    symmetric code range of rows whose absolute maximum lies in [2, 4]).
+    `workers` threads fill fixed 32 MiB chunks of the counter stream, so
+    banks of tens of GB build in seconds on the host and the result
     depends only on (lengths, kv_heads, head_dim, seed)."""
     from concurrent.futures import ThreadPoolExecutor
 
@@ -117,46 +146,21 @@ def gqa_int8_bank(lengths: np.ndarray, kv_heads: int, head_dim: int, seed: int,
     offs = np.zeros(lengths.size + 1, dtype=np.uint64)
     offs[1:] = np.cumsum(lengths)
     rows = int(offs[-1]) * kv_heads
-    codes = np.empty(rows * head_dim, dtype=np.int8)
-    step = 1 << 26
-    chunks = [(i, min(step, codes.size - i)) for i in range(0, codes.size, step)]
-    seqs = np.random.SeedSequence(int(seed)).spawn(len(chunks) + 1)
+    n_codes = rows * head_dim
+    words = np.empty((n_codes + 7) // 8, dtype=np.uint64)
+    step = 1 << 22
+    key = (int(seed) * 0xD1B54A32D192ED03 + 0x2545F4914F6CDD1D) & 0xFFFFFFFFFFFFFFFF
 
-    def fill(j):
-        i, n = chunks[j]
-        seg = codes[i:i + n]
-        raw = np.random.SFC64(seqs[j]).random_raw((n + 7) // 8).view(np.int8)
-        seg[:] = raw[:n]
-        np.maximum(seg, -127, out=seg)
+    def fill(i):
+        seg = words[i:i + step]
+        _splitmix_fill(seg, i, key)
+        b = seg.view(np.int8)
+        np.maximum(b, -127, out=b)
 
     with ThreadPoolExecutor(max_workers=max(1, workers)) as ex:
-        list(ex.map(fill, range(len(chunks))))
-    rng = np.random.default_rng(seqs[-1])
-    scales = (rng.uniform(2.0, 4.0, size=rows) / 127.0).astype(np.float16).view(np.uint16)
-    return codes, scales, offs
-
-
-def gqa_int8_bank_device(lengths: np.ndarray, kv_heads: int, head_dim: int,
-                         seed: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
-    """gqa_int8_bank's format and distributions for banks of tens of GB:
-    the codes are drawn on the GPU (torch's seeded Philox generator, 1 GiB
-    at a time) and copied to host memory; the scales as gqa_int8_bank."""
-    import torch
-
-    lengths = np.asarray(lengths, dtype=np.uint64)
-    offs = np.zeros(lengths.size + 1, dtype=np.uint64)
-    offs[1:] = np.cumsum(lengths)
-    rows = int(offs[-1]) * kv_heads
-    codes = np.empty(rows * head_dim, dtype=np.int8)
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(int(seed))
-    step = 1 << 30
-    for i in range(0, codes.size, step):
-        n = min(step, codes.size - i)
-        dev = torch.randint(-127, 128, (n,), dtype=torch.int8, device="cuda", generator=gen)
-        torch.from_numpy(codes[i:i + n]).copy_(dev)
-        del dev
-    rng = np.random.default_rng(np.random.SeedSequence(int(seed)).spawn(1)[0])
+        list(ex.map(fill, range(0, words.size, step)))
+    codes = words.view(np.int8)[:n_codes]
+    rng = _rng(seed + 0x5CA1E)
     scales = (rng.uniform(2.0, 4.0, size=rows) / 127.0).astype(np.float16).view(np.uint16)
     return codes, scales, offs
 

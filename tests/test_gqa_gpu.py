@@ -313,13 +313,17 @@ def test_int8_bank_batched_queries(hip_lib):
 def test_repeated_routes_follow_query_and_bank_changes(hip_lib):
     # Repeated single-query routes on one device buffer read the query and
     # the bank as they are at each call; batched routes run in between.
-    torch = pytest.importorskip("torch")
+    # The buffer comes from the library's own upload entry point and is
+    # rewritten with hipMemcpy of the runtime the library runs on.
+    import ctypes
+    from graftrepository_amd.gqa_probe import HipProbe
     lens = wl.gqa_lengths(200, seed=71, lo=1, hi=300)
     keys, offs = wl.gqa_bank(lens, 8, 128, seed=71, dtype="bf16")
     node_ids = np.arange(200, dtype=np.uint64) + 5
     qs = [wl.gqa_queries(1, 32, 1, 128, seed=71 + i, dtype="f32") for i in range(2)]
-    dq = torch.from_numpy(qs[0]).cuda()
-    torch.cuda.synchronize()
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    dq = HipProbe().upload_queries(qs[0])
 
     def want(q, live):
         blocks = [keys[int(offs[j]) * 8 * 128:int(offs[j + 1]) * 8 * 128] for j in live]
@@ -336,8 +340,7 @@ def test_repeated_routes_follow_query_and_bank_changes(hip_lib):
             assert_same(bank.route(dq, 4, on_device=True), ids, sc)
             eager = bank.route(np.concatenate([qs[0], qs[0]]), 4, warmup=1)
             assert_same(eager, np.concatenate([ids, ids]), np.concatenate([sc, sc]))
-        dq.copy_(torch.from_numpy(qs[1]))
-        torch.cuda.synchronize()
+        assert hip.hipMemcpy(dq.handle, qs[1].ctypes.data, qs[1].nbytes, 1) == 0
         ids, sc, _ = want(qs[1], live)
         assert_same(bank.route(dq, 4, on_device=True), ids, sc)
         bank.evict(node_ids[:7])
