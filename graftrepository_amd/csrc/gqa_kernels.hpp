@@ -66,15 +66,18 @@ __device__ inline const u32x4* piece_ptr(const u32x4* kb, uint64_t L, int sS, ui
 
 // Work item: `count` consecutive key tokens, from t0, of one slot (all kv
 // heads).  `base` = tok_off[slot] * kv, so row0 of kv head g is
-// base + g * len, `len` being the slot's padded row count.
+// base + g * len, `len` being the slot's padded row count.  `q` is the
+// query an item of a candidate list belongs to (0 elsewhere).
 struct Item {
   uint64_t base;  // tok_off[slot] * kv
   uint32_t slot;
   uint32_t t0;
   uint32_t count;
   uint32_t len;
+  uint32_t q;
+  uint32_t pad;
 };
-static_assert(sizeof(Item) == 24, "Item layout");
+static_assert(sizeof(Item) == 32, "Item layout");
 
 __device__ inline float load_scale(const unsigned char* __restrict__ scales,
                                    int scale_dtype, uint64_t idx) {
@@ -84,9 +87,16 @@ __device__ inline float load_scale(const unsigned char* __restrict__ scales,
   return reinterpret_cast<const float*>(scales)[idx];
 }
 
-// INT8 dequant law: fp16(float(code) * scale) (core/graft_quant.py:136-144).
+// INT8 dequant law: fp16(float(code) * scale) (core/graft_quant.py:136-144):
+// the product rounds to fp32, then to fp16.  The empty asm keeps the fp32
+// product a value of its own; without it the compiler fuses multiply and
+// conversion into v_fma_mixlo_f16, which rounds the exact product to fp16
+// once and differs from the law when the fp32 rounding crosses an fp16
+// rounding boundary.
 __device__ inline _Float16 dequant_i8(int code, float scale) {
-  return static_cast<_Float16>(static_cast<float>(code) * scale);
+  float p = static_cast<float>(code) * scale;
+  asm volatile("" : "+v"(p));
+  return static_cast<_Float16>(p);
 }
 
 template <int KDT>
@@ -170,8 +180,10 @@ constexpr int exact_stage_chunks() {
   return cap < 1 ? 1 : (cap > 8 ? 8 : cap);
 }
 
-// Exact maxima for every (kv head, item) pair against one query (q64 of
-// gqa_q64_kernel, query 0), as a software pipeline: wavefront w of W walks
+// Exact maxima for every (kv head, item) pair against query it.q of the
+// item (q64 of gqa_q64_kernel; maxima at hmax + q*hstride), as a software
+// pipeline (the item count is *n_items_dev when that is given, for lists
+// built on the device): wavefront w of W walks
 // pairs p = w, w+W, ... (p = g * n_items + item, so neighbouring waves
 // share a kv head and its query rows stay in the scalar cache) as one
 // stream of stages -- NB chunks of one 64-token tile -- and loads the next
@@ -183,12 +195,13 @@ template <int KDT, int RQ, int NB>
 __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
     const unsigned char* __restrict__ keys,
     const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
-    const Item* __restrict__ items, uint32_t n_items, int kv, int hd, int sS, int R,
-    int Qt, const double* __restrict__ q64, double denom,
-    unsigned long long* __restrict__ hmax, size_t cap) {
+    const Item* __restrict__ items, uint32_t n_items, const uint32_t* __restrict__ n_items_dev,
+    int kv, int hd, int sS, int R, int Qt, const double* __restrict__ q64, double denom,
+    unsigned long long* __restrict__ hmax, size_t hstride, size_t cap) {
   using T = KeyTraits<KDT>;
   const int lane = threadIdx.x & (kWave - 1);
   const uint32_t W = gridDim.x * kUnitWaves;
+  if (n_items_dev) n_items = *n_items_dev;
   const uint32_t n_pairs = n_items * static_cast<uint32_t>(kv);
   uint32_t p_cur = blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   if (p_cur >= n_pairs) return;
@@ -223,8 +236,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
     acc[j] = 0.0;
     best[j] = 0.0;
   }
-  auto fold = [&](const u32x4 (&v)[NB], const float (&sc)[NB], int g, int b) {
-    const double* __restrict__ qg = q64 + static_cast<size_t>(g) * hd * RQ;
+  auto fold = [&](const u32x4 (&v)[NB], const float (&sc)[NB], uint32_t q, int g, int b) {
+    const double* __restrict__ qg = q64 + (static_cast<size_t>(q) * kv + g) * hd * RQ;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int c = b * NB + j;
@@ -257,7 +270,9 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
         const unsigned long long o = __shfl_xor(bits, off);
         bits = o > bits ? o : bits;
       }
-      if (lane == 0) atomicMax(hmax + static_cast<size_t>(g * R + r) * cap + it.slot, bits);
+      if (lane == 0) {
+        atomicMax(hmax + it.q * hstride + static_cast<size_t>(g * R + r) * cap + it.slot, bits);
+      }
     }
 #pragma unroll
     for (int j = 0; j < RQ; ++j) best[j] = 0.0;
@@ -288,7 +303,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
     const uint32_t nt = !more ? t : (item_end ? nxt.t0 : (last_b ? t + kWave : t));
     const int nbb = (!more || !last_b) ? (more ? b + 1 : b) : 0;
     load(later, slater, nit, ng, nt, nbb);
-    fold(now, snow, g_cur, b);
+    fold(now, snow, cur.q, g_cur, b);
     if (!last_b) {
       ++b;
       return true;
@@ -322,8 +337,10 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
   }
 }
 
-// Exact scores of every live slot from the head-major maxima (h in order,
-// fp64); grid (blocks, queries), grid-stride over groups of 64 slots.
+// Exact scores of every live slot -- or, with slot_list, of the slots
+// slot_list[qb*list_stride ..) (list_count[qb] of them) -- from the
+// head-major maxima (h in order, fp64); grid (blocks, queries), grid-stride
+// over groups of 64 slots.
 // Query qb's maxima are hmax[qb*hstride + h*cap + slot].  All waves of the
 // block stage the group's maxima in LDS -- every load of a group is in
 // flight at once, since the atomics that produced them leave them outside
@@ -338,12 +355,17 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
     unsigned long long* __restrict__ hmax, size_t hstride, size_t cap, int H, uint32_t n_slots,
     const uint32_t* __restrict__ lens, const uint32_t* __restrict__ flags,
     const uint64_t* __restrict__ ids, const unsigned* __restrict__ qbad, int kv,
-    int k, Cand* __restrict__ block_out) {
+    int k, Cand* __restrict__ block_out, const uint32_t* __restrict__ slot_list,
+    const uint32_t* __restrict__ list_count, size_t list_stride) {
   __shared__ double s_h[kFinHeads][kFinSlots];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int qb = blockIdx.y;
   hmax += qb * hstride;
+  if (slot_list) {
+    slot_list += qb * list_stride;
+    n_slots = list_count[qb];
+  }
   // Every load a group needs is issued before any result is used: slot
   // metadata, ids and the query flags ride along with the maxima.
   unsigned qbad_lane = 0u;
@@ -355,8 +377,8 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
   bool q_bad = false;
   bool q_bad_known = false;
   for (uint32_t base = blockIdx.x * kFinSlots; base < n_slots; base += gridDim.x * kFinSlots) {
-    const uint32_t slot = base + lane;
-    const bool in = slot < n_slots;
+    const bool in = base + lane < n_slots;
+    const uint32_t slot = slot_list ? (in ? slot_list[base + lane] : 0u) : base + lane;
     uint32_t f = 0u, len = 0u;
     uint64_t id = kNoId;
     if (wave == 0 && in) {
@@ -466,6 +488,141 @@ __device__ inline uint32_t pack_f16x2(_Float16 lo, _Float16 hi) {
 
 constexpr int kMaxCols = 64;  // query columns (Qb * R * Qt) per screen pass
 
+
+// ------------------------------------------------------- query columns
+//
+// A screen pass reads kv head g's query columns: column cg = (qb*R + r)*Qt
+// + qi (cg < cols) is query qb's row of head g*R + r at query token qi,
+// q_elems values after query qb-1's.
+
+// Block-wide: stage the columns in s_q[cg][HD] as fp32 (exact: queries are
+// fp32 or bf16) and derive each column's screen parameters
+//  * scale(cg) = 2^-e, the power of two that brings max|q| of the column
+//    under 2^emax (the MFMA type's safe range), 1 for ordinary values;
+//  * the column's bound per unit of key norm, and its absolute part, in the
+//    scaled units the screen works in (rounded up):
+//      coef = ((gamma + delta + gamma*delta + rho) * ||q||
+//              + sigma_q * (1 + gamma) * sqrt(hd) / scale + 2^-40 * ||q||) * scale
+//      eabs = (sigma_k * sqrt(hd) * ||q|| + sigma_p * hd / scale) * scale
+//    gamma bounds the fp32 accumulation, delta the query's rounding to
+//    the MFMA type, rho the factoring of INT8 row scales out of the dot
+//    product (0 elsewhere), sigma_q a scaled query value flushed or rounded
+//    near zero, sigma_k a key value flushed near zero, sigma_p a product
+//    lost to underflow, and 2^-40 the law's own fp64 rounding;
+// into s_ec[cg] = {coef, eabs, scale, 0} and s_bad[cg] = 1 when the column
+// holds a non-finite value.  Ends with a barrier.
+template <int HD>
+__device__ inline void stage_columns(float* __restrict__ s_q, float4* __restrict__ s_ec,
+                                     unsigned* __restrict__ s_bad, const void* __restrict__ query,
+                                     int q_dtype, size_t q_elems, int cols, int R, int Qt, int g,
+                                     int emax, double gamma, double delta, double rho,
+                                     double sigma_q, double sigma_k, double sigma_p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = blockDim.x / kWave;
+  const int RQc = R * Qt;
+  for (int i = threadIdx.x; i < cols * HD; i += blockDim.x) {
+    const int cg = i / HD;
+    const int qb = cg / RQc;
+    const int r = (cg % RQc) / Qt;
+    const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
+                         (static_cast<uint64_t>(g * R + r) * Qt + cg % Qt) * HD + (i - cg * HD);
+    s_q[i] = q_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
+                              : static_cast<const float*>(query)[src];
+  }
+  __syncthreads();
+  for (int cg = wave; cg < cols; cg += nwaves) {
+    double ss = 0.0;
+    float mx = 0.0f;
+    bool bad = false;
+    for (int d = lane; d < HD; d += kWave) {
+      const float f = s_q[cg * HD + d];
+      bad = bad || !isfinite(f);
+      mx = fmaxf(mx, fabsf(f));
+      ss = fma(static_cast<double>(f), static_cast<double>(f), ss);
+    }
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      ss += __shfl_xor(ss, off);
+      mx = fmaxf(mx, __shfl_xor(mx, off));
+    }
+    bad = __ballot(bad) != 0ull;
+    if (lane == 0) {
+      int e = 0;
+      if (isfinite(mx) && mx > 0.0f) {
+        const int ex = ilogbf(mx);  // mx in [2^ex, 2^(ex+1))
+        if (ex >= emax) e = ex - emax + 1;
+      }
+      const float scale = ldexpf(1.0f, -e);
+      const double norm = sqrt(ss) * (1.0 + 0x1p-40);
+      const double sq = sqrt(static_cast<double>(HD));
+      double c = (gamma + delta + gamma * delta + rho) * norm + sigma_q * (1.0 + gamma) * sq / scale +
+                 0x1p-40 * norm;
+      double ea = sigma_k * sq * norm + sigma_p * HD / scale;
+      const double up = 1.0 + 0x1p-20;
+      c *= up * scale * up;
+      ea *= up * scale * up;
+      s_ec[cg] = make_float4(isfinite(c) ? static_cast<float>(c) * 1.000001f : INFINITY,
+                             isfinite(ea) ? static_cast<float>(ea) * 1.000001f : INFINITY, scale,
+                             0.0f);
+      s_bad[cg] = bad ? 1u : 0u;
+    }
+  }
+  __syncthreads();
+}
+
+// Dimension of position j (< 8) of lane quarter `quarter`'s part of MFMA
+// k-block ks.  Natural order: ks*32 + quarter*8 + j, so a bf16/f16
+// fragment is one 16-byte piece of a key row.  PERM (INT8 streams): a
+// lane's k-blocks 2i and 2i+1 are the 16 consecutive dims i*64 +
+// quarter*16 .. +16, one 16-byte piece of codes, so a wave's key load of
+// 16 tokens is one contiguous 1 KiB run.  A dot product does not depend on
+// the order of its terms, and the screen's bound holds for any order.
+template <bool PERM>
+__device__ inline int frag_dim(int ks, int quarter, int j) {
+  if constexpr (PERM) return (ks >> 1) * 64 + quarter * 16 + (ks & 1) * 8 + j;
+  return ks * 32 + quarter * 8 + j;
+}
+
+// Query fragments of the staged columns: fragment (nt, ks) of lane l holds
+// column nt*16 + l%16 at dims frag_dim(ks, l/16, j), j < 8, of q * scale
+// rounded to nearest even in the MFMA type (columns >= cols are zero).
+template <int MT, bool PERM, int KS, int NT>
+__device__ inline void query_frags(u32x4 (&bq)[NT][KS], const float* __restrict__ s_q,
+                                   const float4* __restrict__ s_ec, int cols, int r16,
+                                   int quarter) {
+  constexpr int HD = 32 * KS;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int cg = nt * 16 + r16;
+    const float sc = cg < cols ? s_ec[cg].z : 0.0f;
+    const float* qc = s_q + min(cg, cols - 1) * HD;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const int d = frag_dim<PERM>(ks, quarter, j);
+        const float f0 = cg < cols ? qc[d] * sc : 0.0f;
+        const float f1 = cg < cols ? qc[d + 1] * sc : 0.0f;
+        if constexpr (MT == kBF16) {
+          auto rne = [](float f) {  // round to nearest even (finite inputs)
+            const uint32_t u = __float_as_uint(f);
+            return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+          };
+          w[j / 2] = rne(f0) | (rne(f1) << 16);
+        } else {
+          w[j / 2] = pack_f16x2(static_cast<_Float16>(f0), static_cast<_Float16>(f1));
+        }
+      }
+      bq[nt][ks].x = w[0];
+      bq[nt][ks].y = w[1];
+      bq[nt][ks].z = w[2];
+      bq[nt][ks].w = w[3];
+    }
+  }
+}
+
 // Exact |dot| of one lane's (key token, query column) pair in the law's
 // order: the token's pieces come from the planes (piece c at
 // kp + (c/4)*L*4 + c%4, kp the token's piece 0; chunks of S = 4 pieces),
@@ -510,24 +667,11 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
 // Screen and refine; grid (ceil(items / 4), kv heads), one wavefront per
 // (item, kv head g).
 //
-// Each block first prepares kv head g's query columns from the raw
-// queries (Qb of them, q_elems values apart): column cg = (qb*R + r)*Qt +
-// qi (cg < cols) is query qb's row of head g*R + r at query token qi.
-//  * s_q[cg][d]: the values as fp32 (exact: queries are fp32 or bf16), for
-//    the screen fragments and the exact recomputation;
-//  * scale(cg) = 2^-e, the power of two that brings max|q| of the column
-//    under 2^emax (the MFMA type's safe range), 1 for ordinary values;
-//  * the column's bound per unit of the node's key norm, and its absolute
-//    part, in the scaled units the screen works in (rounded up):
-//      coef = ((gamma + delta + gamma*delta) * ||q||
-//              + sigma_q * (1 + gamma) * sqrt(hd) / scale + 2^-40 * ||q||) * scale
-//      eabs = (sigma_k * sqrt(hd) * ||q|| + sigma_p * hd / scale) * scale
-//    gamma bounds the fp32 accumulation, delta the query's rounding to
-//    the MFMA type, sigma_q a scaled query value flushed or rounded near
-//    zero, sigma_k a key value flushed near zero, sigma_p a product lost
-//    to underflow, and 2^-40 the law's own fp64 rounding;
-//  * blocks with blockIdx.x == 0 write qflags[qb*kv + g] = 1 when a value
-//    of query qb read by kv head g is non-finite (0 otherwise).
+// Each block first stages kv head g's query columns of the Qb queries
+// (stage_columns: fp32 values for the screen fragments and the exact
+// recomputation, scale and error-bound parameters per column); blocks with
+// blockIdx.x == 0 write qflags[qb*kv + g] = 1 when a value of query qb read
+// by kv head g is non-finite (0 otherwise).
 // Columns with a non-finite value take no part in the screen (every score
 // of that query is NaN).  The item's tokens stream in 16-token tiles, two
 // tiles ahead of the one being screened.  Lane l sees column
@@ -616,53 +760,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     load_tile(x2, 2);
     load_tile(x3, 3);
   }
-  for (int i = threadIdx.x; i < cols * HD; i += blockDim.x) {
-    const int cg = i / HD;
-    const int qb = cg / RQc;
-    const int r = (cg % RQc) / Qt;
-    const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
-                         (static_cast<uint64_t>(g * R + r) * Qt + cg % Qt) * HD + (i - cg * HD);
-    s_q[i] = q_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
-                              : static_cast<const float*>(query)[src];
-  }
-  __syncthreads();
-  for (int cg = wave; cg < cols; cg += kUnitWaves) {
-    double ss = 0.0;
-    float mx = 0.0f;
-    bool bad = false;
-    for (int d = lane; d < HD; d += kWave) {
-      const float f = s_q[cg * HD + d];
-      bad = bad || !isfinite(f);
-      mx = fmaxf(mx, fabsf(f));
-      ss = fma(static_cast<double>(f), static_cast<double>(f), ss);
-    }
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      ss += __shfl_xor(ss, off);
-      mx = fmaxf(mx, __shfl_xor(mx, off));
-    }
-    bad = __ballot(bad) != 0ull;
-    if (lane == 0) {
-      int e = 0;
-      if (isfinite(mx) && mx > 0.0f) {
-        const int ex = ilogbf(mx);  // mx in [2^ex, 2^(ex+1))
-        if (ex >= emax) e = ex - emax + 1;
-      }
-      const float scale = ldexpf(1.0f, -e);
-      const double norm = sqrt(ss) * (1.0 + 0x1p-40);
-      const double sq = sqrt(static_cast<double>(HD));
-      double c = (gamma + delta + gamma * delta) * norm + sigma_q * (1.0 + gamma) * sq / scale +
-                 0x1p-40 * norm;
-      double ea = sigma_k * sq * norm + sigma_p * HD / scale;
-      const double up = 1.0 + 0x1p-20;
-      c *= up * scale * up;
-      ea *= up * scale * up;
-      s_ec[cg] = make_float4(isfinite(c) ? static_cast<float>(c) * 1.000001f : INFINITY,
-                             isfinite(ea) ? static_cast<float>(ea) * 1.000001f : INFINITY, scale,
-                             0.0f);
-      s_bad[cg] = bad ? 1u : 0u;
-    }
-  }
+  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, g, emax, gamma, delta,
+                    0.0, sigma_q, sigma_k, sigma_p);
   __syncthreads();
   if (blockIdx.x == 0 && threadIdx.x < static_cast<unsigned>(Qb)) {
     unsigned bad = 0u;
@@ -672,38 +771,9 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
   if (!has_item) return;
 
   // B fragments from the staged columns: fragment (nt, ks) lane l holds
-  // column nt*16 + l%16 at dims ks*32 + (l/16)*8 + j, j < 8, of q * scale
-  // rounded to nearest even in the MFMA type (columns >= cols are zero).
+  // column nt*16 + l%16 at dims ks*32 + (l/16)*8 + j, j < 8.
   u32x4 bq[NT][KS];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int cg = nt * 16 + r16;
-    const float sc = cg < cols ? s_ec[cg].z : 0.0f;
-    const float* qc = s_q + min(cg, cols - 1) * HD;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      uint32_t w[4];
-#pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        const int d = ks * 32 + quarter * 8 + j;
-        const float f0 = cg < cols ? qc[d] * sc : 0.0f;
-        const float f1 = cg < cols ? qc[d + 1] * sc : 0.0f;
-        if constexpr (MT == kBF16) {
-          auto rne = [](float f) {  // round to nearest even (finite inputs)
-            const uint32_t u = __float_as_uint(f);
-            return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-          };
-          w[j / 2] = rne(f0) | (rne(f1) << 16);
-        } else {
-          w[j / 2] = pack_f16x2(static_cast<_Float16>(f0), static_cast<_Float16>(f1));
-        }
-      }
-      bq[nt][ks].x = w[0];
-      bq[nt][ks].y = w[1];
-      bq[nt][ks].z = w[2];
-      bq[nt][ks].w = w[3];
-    }
-  }
+  query_frags<MT, false, KS, NT>(bq, s_q, s_ec, cols, r16, quarter);
 
   auto frag = [&](const Tile& b, int ks) -> u32x4 {
     if constexpr (KDT != kI8) {
@@ -867,6 +937,458 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
       atomicMax(hmax + qb * hstride + static_cast<size_t>(g * R + r) * cap + it.slot, bits);
     }
   }
+}
+
+// ------------------------------------------------------ bound and verify
+//
+// Routes with many query columns per kv head (batched queries) take the
+// bound-and-verify path: a screen-only pass keeps, per (query column,
+// node), the largest screened |q~.k| over the node's tokens; the screen's
+// error bound turns those maxima into an interval [lb, ub] holding each
+// node's score; every node whose ub reaches the k-th largest lb of its
+// query is a candidate; the law runs exactly (fp64, gqa_exact_kernel) on the
+// candidates only, and the top-k is taken over their exact scores.  At
+// least k nodes score >= tau (the k-th largest lb) and every other node
+// scores < tau, in float as well (lb rounded down, ub rounded up), so the
+// top-k of the candidates is the law's top-k, ties included.
+
+// Four int8 codes (one dword) as four exact f16 values (two dwords, codes
+// 0,1 then 2,3): byte b ^ 0x80 = code + 128 goes under the exponent of
+// 1024 (f16 bits 0x6400 | u = 1024 + u), then 1152 comes off.  Exact:
+// every value involved is an integer below 2048.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ inline void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  const f16x2 bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+  lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
+  hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
+}
+
+// Screen-only pass; grid (P, kv heads), persistent: wave w of block b walks
+// the items b*4 + w, b*4 + w + 4P, ... as one stream of 16-token tiles,
+// four tiles in flight ahead of the one being screened, across item
+// boundaries.  The block stages kv head g's query columns once
+// (stage_columns); blocks with blockIdx.x == 0 write colinfo[g*cols + cg]
+// = {coef, eabs, scale, bad} for the bounds kernel.
+//
+// The MFMA runs with the query columns as the row operand, so lane l holds
+// columns nt*16 + (l/16)*4 + v (v < 4) of token l%16, the token whose key
+// piece it loaded.  Each lane keeps a running max of |s~| per column;
+// loads of tokens past an item's end are clamped to its last token, whose
+// value a max already holds.  FACT (INT8 rows with one scale each): the
+// codes enter the MFMA as exact f16 integers and the lane's row scale
+// multiplies its results, s~ = scale_t * |q~ . c|; the difference to the
+// law's fp16(code * scale) keys is in the bound (rho, and a norm bound
+// that covers c * scale).  At an item's end the maxima of the 16 lanes of
+// each column combine and fold into
+// hmaxf[qb*qstride + ((g*R + r)*Qt + qi)*cap + slot] (float bits,
+// atomicMax: the values are non-negative), in scaled units.
+template <int KDT, int KS, int NT, bool FACT>
+__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
+    const unsigned char* __restrict__ keys, const unsigned char* __restrict__ scales,
+    int scale_dtype, int group_size, const Item* __restrict__ items, uint32_t n_items, int kv,
+    int R, int Qt, const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
+    double gamma, double delta, double rho, double sigma_q, double sigma_k, double sigma_p,
+    float4* __restrict__ colinfo, unsigned* __restrict__ hmaxf, size_t qstride, size_t cap) {
+  using KT = KeyTraits<KDT>;
+  constexpr int MT = ScreenTraits<KDT>::kMfma;
+  constexpr bool PERM = KDT == kI8;
+  constexpr int HD = 32 * KS;
+  constexpr int C = HD / KT::kEpc;            // 16-byte pieces per key row
+  constexpr int NL = PERM ? KS / 2 : KS;       // 16-byte key loads per lane per tile
+  static_assert(!FACT || KDT == kI8, "row-scale factoring is for INT8 banks");
+  constexpr uint32_t kEnd = 0x80000000u;
+  extern __shared__ float s_q[];
+  __shared__ float4 s_ec[kMaxCols];
+  __shared__ unsigned s_bad[kMaxCols];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int g = blockIdx.y;
+  const int RQc = R * Qt;
+  const int cols = Qb * RQc;
+  const int quarter = lane >> 4;
+  const int r16 = lane & 15;
+  const uint32_t stride = gridDim.x * kUnitWaves;
+  uint32_t li = blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const bool has_item = li < n_items;
+  const int G = KDT == kI8 ? HD / group_size : 1;
+  const int ses = scale_dtype == kF16 ? 2 : 4;
+
+  // Loader: the item being loaded, its next tile, the next item's
+  // descriptor (fetched one item ahead).
+  struct Src {
+    const u32x4* kp;           // piece 0 of the (slot, g) block
+    const unsigned char* sp;   // its scales (INT8)
+    uint64_t L;                // padded rows of the block
+    uint32_t t0, last, ntiles, slot;
+  };
+  auto source = [&](const Item& it) {
+    Src d;
+    const uint64_t row0 = it.base + static_cast<uint64_t>(g) * it.len;
+    d.kp = reinterpret_cast<const u32x4*>(keys) + row0 * C;
+    d.sp = KDT == kI8 ? scales + row0 * G * ses : nullptr;
+    d.L = it.len;
+    d.t0 = it.t0;
+    d.last = it.t0 + it.count - 1;
+    d.ntiles = (it.count + 15) / 16;
+    d.slot = it.slot;
+    return d;
+  };
+  struct Tile {
+    u32x4 v[NL];
+    float s[KDT == kI8 ? (FACT ? 1 : NL) : 1];
+    uint32_t fin;  // slot | kEnd on an item's last tile, else kNoSlot
+  };
+  Src ld = source(items[has_item ? li : 0]);
+  uint32_t lt = 0;
+  uint32_t lnext = li + stride;
+  Item nx = items[min(lnext, n_items - 1)];
+  bool ldone = false;
+  auto load_tile = [&](Tile& b, uint32_t tile) {
+    const uint32_t t = min(ld.t0 + tile * 16 + r16, ld.last);
+    // piece p of token t at kp + (p/4)*L*4 + t*4 + p%4 (chunks of 4 pieces);
+    // load i reads piece i*4 + quarter: 16 tokens x 4 pieces, 1 KiB
+    const u32x4* p = ld.kp + static_cast<uint64_t>(t) * 4 + quarter;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) b.v[i] = __builtin_nontemporal_load(p + i * 4 * ld.L);
+    if constexpr (KDT == kI8) {
+      if constexpr (FACT) {
+        b.s[0] = load_scale(ld.sp, scale_dtype, t);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+          b.s[i] = load_scale(ld.sp, scale_dtype,
+                              static_cast<uint64_t>((i * 64 + quarter * 16) / group_size) * ld.L + t);
+        }
+      }
+    }
+  };
+  // Load the stream's next tile into b (past the stream's end: the last
+  // tile again, marked kNoSlot).
+  auto load_next = [&](Tile& b) {
+    load_tile(b, ldone ? ld.ntiles - 1 : lt);
+    b.fin = kNoSlot;
+    if (ldone) return;
+    if (lt + 1 < ld.ntiles) {
+      ++lt;
+      return;
+    }
+    const bool end = lnext >= n_items;
+    b.fin = ld.slot | (end ? kEnd : 0u);
+    if (end) {
+      ldone = true;
+      return;
+    }
+    ld = source(nx);
+    lt = 0;
+    lnext += stride;
+    nx = items[min(lnext, n_items - 1)];
+  };
+  Tile x0, x1, x2, x3, x4;
+  if (has_item) {
+    load_next(x0);
+    load_next(x1);
+    load_next(x2);
+    load_next(x3);
+  }
+  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, g, emax, gamma, delta,
+                    rho, sigma_q, sigma_k, sigma_p);
+  if (blockIdx.x == 0) {
+    for (int cg = threadIdx.x; cg < cols; cg += blockDim.x) {
+      float4 e = s_ec[cg];
+      e.w = s_bad[cg] ? 1.0f : 0.0f;
+      colinfo[g * cols + cg] = e;
+    }
+  }
+  if (!has_item) return;
+
+  u32x4 bq[NT][KS];
+  query_frags<MT, PERM, KS, NT>(bq, s_q, s_ec, cols, r16, quarter);
+
+  // key fragment ks of a tile: 8 values of the lane's token in the MFMA type
+  auto key_frags = [&](const Tile& b, u32x4 (&bk)[KS]) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (KDT != kI8) {
+        bk[ks] = b.v[ks];
+      } else {
+        const u32x4 v = b.v[ks >> 1];
+        const uint32_t w0 = (ks & 1) ? v.z : v.x;
+        const uint32_t w1 = (ks & 1) ? v.w : v.y;
+        if constexpr (FACT) {
+          uint32_t o[4];
+          codes_to_f16(w0, o[0], o[1]);
+          codes_to_f16(w1, o[2], o[3]);
+          bk[ks].x = o[0];
+          bk[ks].y = o[1];
+          bk[ks].z = o[2];
+          bk[ks].w = o[3];
+        } else {
+          const float sc = b.s[ks >> 1];
+          const uint32_t w[2] = {w0, w1};
+          uint32_t o[4];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            o[2 * i] = pack_f16x2(dequant_i8(static_cast<int8_t>(w[i] & 0xffu), sc),
+                                  dequant_i8(static_cast<int8_t>((w[i] >> 8) & 0xffu), sc));
+            o[2 * i + 1] = pack_f16x2(dequant_i8(static_cast<int8_t>((w[i] >> 16) & 0xffu), sc),
+                                      dequant_i8(static_cast<int8_t>(w[i] >> 24), sc));
+          }
+          bk[ks].x = o[0];
+          bk[ks].y = o[1];
+          bk[ks].z = o[2];
+          bk[ks].w = o[3];
+        }
+      }
+    }
+  };
+  float m[NT][4];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) m[nt][v] = 0.0f;
+  }
+  auto fold = [&](const Tile& b) {
+    u32x4 bk[KS];
+    key_frags(b, bk);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) c = mfma16x16x32<MT>(bq[nt][ks], bk[ks], c);
+      const float cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        // fmaxf keeps the number when one side is NaN (non-finite keys make
+        // the node's score NaN through its flags, not through the screen)
+        if constexpr (FACT) {
+          m[nt][v] = fmaxf(m[nt][v], fabsf(cv[v]) * b.s[0]);
+        } else {
+          m[nt][v] = fmaxf(m[nt][v], fabsf(cv[v]));
+        }
+      }
+    }
+  };
+  // item end: the column maxima over the 16 lanes of each quarter; lane
+  // (quarter, r16) then folds column nt*16 + quarter*4 + v, nt = r16/4,
+  // v = r16%4, into the node's cell
+  auto emit = [&](uint32_t slot) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float x = m[nt][v];
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) x = fmaxf(x, __shfl_xor(x, off));
+        m[nt][v] = x;
+      }
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (r16 == nt * 4 + v) mine = m[nt][v];
+        m[nt][v] = 0.0f;
+      }
+    }
+    const int cg = (r16 >> 2) * 16 + quarter * 4 + (r16 & 3);
+    if ((r16 >> 2) < NT && cg < cols) {
+      const int qb = cg / RQc;
+      const int r = (cg % RQc) / Qt;
+      const int qi = cg % Qt;
+      atomicMax(hmaxf + qb * qstride + (static_cast<size_t>((g * R + r) * Qt + qi)) * cap + slot,
+                __float_as_uint(mine));
+    }
+  };
+  auto step = [&](Tile& now, Tile& free) -> bool {
+    load_next(free);
+    fold(now);
+    if (now.fin == kNoSlot) return true;
+    emit(now.fin & ~kEnd);
+    return (now.fin & kEnd) == 0u;
+  };
+  while (step(x0, x4) && step(x1, x0) && step(x2, x1) && step(x3, x2) && step(x4, x3)) {
+  }
+}
+
+// Node-score bounds; grid (blocks, queries), 4 wavefronts, lane = slot,
+// grid-stride over groups of 64 slots.  For query qb and slot s, each
+// column's screened maximum m (hmaxf, scaled units) bounds the law's
+// max_t |dot| / sqrt(hd) of its head and query token from below by
+// max(0, m - E) / scale / denom and from above by (m + E) / scale / denom,
+// E = coef * K + eabs (colinfo), K = kmax[s], or with FACT the bound on
+// ||code * scale|| the screen used: (kmax + 2^-25 sqrt(hd)) / (1 - 2^-10).
+// best_h is the max over the head's query tokens, so its bounds are the
+// max of theirs; the score (sum_h best_h) / H lies in [lb, ub] with
+// lb = sum_h lo_h / H, ub = sum_h hi_h / H, widened by 2^-40 for the fp64
+// arithmetic on both sides and rounded outward to float.  Writes
+// lbub[qb*cap + s] = (lb, ub): (0, 0) for a live node without key tokens,
+// NaN for slots that are not ranked (free, non-finite keys, non-finite
+// query); re-zeroes the maxima it reads; the block's k best lower bounds
+// (tie law) go to block_out[(qb*gridDim.x + blockIdx.x)*k ..).  Also
+// zeroes *zero_counter (the candidates kernel's item count).
+__global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
+    unsigned* __restrict__ hmaxf, size_t qstride, size_t cap, int H, int Qt, int R, int cols,
+    int kv, uint32_t n_slots, const uint32_t* __restrict__ lens,
+    const uint32_t* __restrict__ flags, const uint64_t* __restrict__ ids,
+    const unsigned* __restrict__ kmax, const float4* __restrict__ colinfo,
+    const unsigned* __restrict__ qbad, int fact, int hd, int k, float2* __restrict__ lbub,
+    Cand* __restrict__ block_out, uint32_t* __restrict__ zero_counter) {
+  __shared__ Cand s_lists[kFinWaves][kMaxTopK];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int qb = blockIdx.y;
+  if (blockIdx.x == 0 && qb == 0 && threadIdx.x == 0) *zero_counter = 0u;
+  hmaxf += qb * qstride;
+  const int RQc = R * Qt;
+  const double denom = sqrt(static_cast<double>(hd));
+  const double kadd = 0x1p-25 * denom;
+  bool q_bad = false;
+  for (int g0 = 0; g0 < kv; g0 += kWave) {
+    q_bad = q_bad || (g0 + lane < kv && qbad[qb * kv + g0 + lane] != 0u);
+  }
+  q_bad = __ballot(q_bad) != 0ull;
+  WaveList Lw;
+  wl_init(Lw);
+  const uint32_t gstride = gridDim.x * kFinWaves * kWave;
+  for (uint32_t base = (blockIdx.x * kFinWaves + wave) * kWave; base < n_slots; base += gstride) {
+    const uint32_t slot = base + lane;
+    const bool in = slot < n_slots;
+    const uint32_t f = in ? flags[slot] : 0u;
+    const uint32_t len = in ? lens[slot] : 0u;
+    const uint64_t id = in ? ids[slot] : kNoId;
+    const float kmf = in ? __uint_as_float(kmax[slot]) : 0.0f;
+    const double K = fact ? (static_cast<double>(kmf) + kadd) / (1.0 - 0x1p-10)
+                          : static_cast<double>(kmf);
+    double lo_sum = 0.0, hi_sum = 0.0;
+    for (int h = 0; h < H; ++h) {
+      const int g = h / R;
+      const int r = h - g * R;
+      double lo_h = 0.0, hi_h = 0.0;
+      for (int qi = 0; qi < Qt; ++qi) {
+        const size_t cell = static_cast<size_t>(h * Qt + qi) * cap + slot;
+        const float mv = in ? __uint_as_float(hmaxf[cell]) : 0.0f;
+        if (in && mv != 0.0f) hmaxf[cell] = 0u;
+        const float4 ci = colinfo[g * cols + (qb * R + r) * Qt + qi];
+        const double e = (static_cast<double>(ci.x) * K + static_cast<double>(ci.y)) * (1.0 + 0x1p-50);
+        const double m = static_cast<double>(mv);
+        const double inv = 1.0 / static_cast<double>(ci.z);  // a power of two: exact
+        const double lo = fmax(0.0, m - e) * inv;
+        const double hi = (m + e) * inv;
+        lo_h = fmax(lo_h, lo);
+        hi_h = (hi > hi_h || isnan(hi)) ? hi : hi_h;
+      }
+      lo_sum += lo_h;
+      hi_sum += hi_h;
+    }
+    const double lb = lo_sum / denom / static_cast<double>(H) * (1.0 - 0x1p-40);
+    const double ub = hi_sum / denom / static_cast<double>(H) * (1.0 + 0x1p-40);
+    float lbf = __builtin_nanf(""), ubf = __builtin_nanf("");
+    if (in && (f & 1u)) {
+      if (len == 0) {
+        lbf = ubf = 0.0f;
+      } else if ((f & 2u) && !q_bad) {
+        lbf = static_cast<float>(lb);
+        if (static_cast<double>(lbf) > lb) lbf = nextafterf(lbf, -INFINITY);
+        ubf = static_cast<float>(ub);
+        if (static_cast<double>(ubf) < ub || isnan(ub)) ubf = isnan(ub) ? INFINITY : nextafterf(ubf, INFINITY);
+      }
+    }
+    if (in) lbub[static_cast<size_t>(qb) * cap + slot] = make_float2(lbf, ubf);
+    wl_consume(Lw, k, lbf, id, slot, isfinite(lbf) && lbf >= Lw.th_s);
+  }
+  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(Lw);
+  __syncthreads();
+  if (wave == 0) {
+    WaveList B;
+    block_merge<kFinWaves>(s_lists, k, B);
+    if (lane < k) block_out[(static_cast<size_t>(qb) * gridDim.x + blockIdx.x) * k + lane] = wl_entry(B);
+  }
+}
+
+// Candidates; grid (queries), kCandWaves wavefronts per block.  tau = the
+// k-th best lower bound of query qb (merged from the bounds kernel's block
+// lists; -inf when fewer than k nodes are ranked); every slot with
+// ub >= tau is a candidate: its slot goes to cand_slots[qb*cap ..) (count
+// in cand_count[qb]) and its key tokens, in items of `chunk` tokens, to the
+// shared list citems (count in *n_citems, zeroed before the launch) with
+// q = qb, for the exact kernel.
+constexpr int kCandWaves = 16;
+__global__ __launch_bounds__(kCandWaves * kWave) void gqa_cands_kernel(
+    const Cand* __restrict__ lists, uint32_t n_lists, int k, const float2* __restrict__ lbub,
+    size_t cap, uint32_t n_slots, const uint64_t* __restrict__ tok_off,
+    const uint32_t* __restrict__ lens, int kv, uint32_t chunk, uint32_t* __restrict__ cand_slots,
+    uint32_t* __restrict__ cand_count, Item* __restrict__ citems, uint32_t* __restrict__ n_citems) {
+  __shared__ Cand s_lists[kCandWaves][kMaxTopK];
+  __shared__ float s_tau;
+  __shared__ uint32_t s_count;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int qb = blockIdx.x;
+  WaveList G;
+  wl_init(G);
+  wl_consume_global(G, k, lists + static_cast<size_t>(qb) * n_lists * k, n_lists * k,
+                    static_cast<uint32_t>(wave), kCandWaves);
+  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(G);
+  if (threadIdx.x == 0) s_count = 0u;
+  __syncthreads();
+  if (wave == 0) {
+    WaveList B;
+    block_merge<kCandWaves>(s_lists, k, B);
+    const float t = lane_f32(B.s, k - 1);
+    if (lane == 0) s_tau = isfinite(t) ? t : -INFINITY;
+  }
+  __syncthreads();
+  const float tau = s_tau;
+  const float2* lq = lbub + static_cast<size_t>(qb) * cap;
+  for (uint32_t base = wave * kWave; base < n_slots; base += kCandWaves * kWave) {
+    const uint32_t slot = base + lane;
+    bool c = false;
+    uint32_t len = 0u;
+    if (slot < n_slots) {
+      const float ub = lq[slot].y;
+      c = ub >= tau;  // NaN (not ranked) compares false
+      if (c) len = lens[slot];
+    }
+    const uint64_t cm = __ballot(c);
+    if (cm == 0ull) continue;
+    const uint32_t n_items = c ? (len + chunk - 1) / chunk : 0u;
+    // wave prefix sums of candidates and of their items
+    uint32_t pre_items = n_items;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t o = __shfl_up(pre_items, off);
+      if (lane >= off) pre_items += o;
+    }
+    const uint32_t tot_items = __shfl(pre_items, kWave - 1);
+    pre_items -= n_items;
+    uint32_t cbase = 0u, ibase = 0u;
+    if (lane == 0) {
+      cbase = atomicAdd(&s_count, static_cast<uint32_t>(__popcll(cm)));
+      if (tot_items) ibase = atomicAdd(n_citems, tot_items);
+    }
+    cbase = __shfl(cbase, 0);
+    ibase = __shfl(ibase, 0);
+    if (c) {
+      const uint32_t rank = static_cast<uint32_t>(__popcll(cm & ((1ull << lane) - 1ull)));
+      cand_slots[static_cast<size_t>(qb) * cap + cbase + rank] = slot;
+      const uint64_t b0 = tok_off[slot] * static_cast<uint64_t>(kv);
+      const uint32_t Lp = (len + kTokAlign - 1) & ~(kTokAlign - 1);
+      for (uint32_t j = 0; j < n_items; ++j) {
+        Item it;
+        it.base = b0;
+        it.slot = slot;
+        it.t0 = j * chunk;
+        it.count = min(chunk, len - j * chunk);
+        it.len = Lp;
+        it.q = static_cast<uint32_t>(qb);
+        it.pad = 0u;
+        citems[ibase + pre_items + j] = it;
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) cand_count[qb] = s_count;
 }
 
 // ----------------------------------------------------------- bank upkeep

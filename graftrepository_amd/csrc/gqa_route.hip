@@ -89,6 +89,24 @@ struct GqaDeviceArena {
   size_t d_q64_count = 0;
   // screen-and-refine path
   int screen_mode = -1;  // -1 whenever the shape allows, 0 never
+  // bound-and-verify path (batched queries): -1 when a pass has more than
+  // 16 query columns per kv head, 0 never, 1 whenever the screen runs
+  int bound_mode = -1;
+  unsigned* d_hmaxf = nullptr;   // screened maxima per (query, head, q token, slot), float bits
+  size_t d_hmaxf_count = 0;
+  float4* d_colinfo = nullptr;   // per (kv head, column): coef, eabs, scale, bad
+  size_t d_colinfo_count = 0;
+  float2* d_lbub = nullptr;      // per (query, slot): score bounds
+  size_t d_lbub_count = 0;
+  Cand* d_blists = nullptr;      // per (query, bounds block): k best lower bounds
+  size_t d_blists_count = 0;
+  uint32_t* d_cslots = nullptr;  // per (query): candidate slots
+  size_t d_cslots_count = 0;
+  uint32_t* d_ccount = nullptr;  // per query: candidate count; [qb_max]: exact items
+  size_t d_ccount_count = 0;
+  Item* d_citems = nullptr;      // exact work items of the candidates
+  size_t d_citems_count = 0;
+  uint64_t bv_routes = 0;        // passes routed by bound and verify
   uint64_t routes = 0;          // route calls
   std::vector<Cand> merged;
   void* d_queries = nullptr;
@@ -164,9 +182,11 @@ void destroy_arena(GqaDeviceArena* a) {
   (void)hipSetDevice(a->device);
   if (a->stream) (void)hipStreamSynchronize(a->stream);
   if (a->side) (void)hipStreamSynchronize(a->side);
-  void* dev[] = {a->d_keys,  a->d_scales, a->d_tok_off, a->d_len,   a->d_ids,
-                 a->d_flags, a->d_nonfinite, a->d_kmax, a->d_items, a->d_hmax,
-                 a->d_qbad,  a->d_queries, a->d_stage,  a->d_q64};
+  void* dev[] = {a->d_keys,   a->d_scales,  a->d_tok_off, a->d_len,    a->d_ids,
+                 a->d_flags,  a->d_nonfinite, a->d_kmax,  a->d_items,  a->d_hmax,
+                 a->d_qbad,   a->d_queries, a->d_stage,   a->d_q64,    a->d_hmaxf,
+                 a->d_colinfo, a->d_lbub,   a->d_blists,  a->d_cslots, a->d_ccount,
+                 a->d_citems};
   for (void* p : dev) {
     if (p) (void)hipFree(p);
   }
@@ -200,6 +220,8 @@ void append_items(std::vector<Item>& items, uint32_t slot, uint64_t base, uint64
     it.t0 = static_cast<uint32_t>(t0);
     it.count = static_cast<uint32_t>(std::min<uint64_t>(chunk, len - t0));
     it.len = static_cast<uint32_t>(padded_len(len));
+    it.q = 0;
+    it.pad = 0;
     items.push_back(it);
   }
 }
@@ -381,6 +403,9 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
     if (v >= 16 && v <= 4096 && v % 16 == 0) a->chunk = static_cast<uint32_t>(v);
   }
   if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
+  if (const char* env = getenv("GRM_HIP_GQA_BOUND")) {
+    a->bound_mode = env[0] == '0' ? 0 : (env[0] == '1' ? 1 : -1);
+  }
   if (const char* env = getenv("GRM_HIP_GQA_EXACT_WAVES")) {
     const long v = strtol(env, nullptr, 10);
     if (v >= 64 && v <= (1l << 30)) a->exact_waves = static_cast<uint32_t>(v);
@@ -488,12 +513,15 @@ int ensure_hmax(GqaDeviceArena* a, int H, int qb) {
   return reserve_device_zero(&a->d_hmax, &a->d_hmax_count, want, a->stream);
 }
 
-int launch_finalize(GqaDeviceArena* a, int H, int qb, int topk, uint32_t fin_blocks, Cand* bout) {
+// Exact scores and per-block top-k of every slot, or (slot_list given) of
+// the listed candidate slots of each query.
+int launch_finalize(GqaDeviceArena* a, int H, int qb, int topk, uint32_t fin_blocks, Cand* bout,
+                    const uint32_t* slot_list = nullptr, const uint32_t* list_count = nullptr) {
   const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
   grm::gqa::gqa_finalize_kernel<<<dim3(fin_blocks, qb), per_block, 0, a->stream>>>(
       a->d_hmax, a->cap_nodes * static_cast<size_t>(H), a->cap_nodes, H,
       static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags, a->d_ids, a->d_qbad,
-      static_cast<int>(a->kv), topk, bout);
+      static_cast<int>(a->kv), topk, bout, slot_list, list_count, a->cap_nodes);
   GRM_HIP_CHECK(hipGetLastError());
   return 0;
 }
@@ -515,14 +543,23 @@ int launch_q64(GqaDeviceArena* a, const void* q, int q_dtype, int qb, int H, int
   return 0;
 }
 
-int launch_exact(GqaDeviceArena* a, int H, int Qt) {
-  if (a->n_items == 0) return 0;
+// Exact maxima of the bank's items against query 0, or (n_items_dev given)
+// of the device-built list `items` (at most max_items), each item against
+// its own query.
+int launch_exact(GqaDeviceArena* a, int H, int Qt, const Item* items = nullptr,
+                 uint64_t max_items = 0, const uint32_t* n_items_dev = nullptr) {
+  if (!n_items_dev) {
+    items = a->d_items;
+    max_items = a->n_items;
+  }
+  if (max_items == 0) return 0;
   const int R = H / static_cast<int>(a->kv);
   const int rq_pad = rq_pad_of(R * Qt);
   // Persistent stream: about exact_waves wavefronts, each walking the
-  // (kv head, item) pairs w, w+W, ...
-  const uint64_t pairs = a->n_items * a->kv;
-  if (pairs >= 0xffffffffull) return grm::fail(-1, "too many work items");
+  // (kv head, item) pairs w, w+W, ...; device-built lists get a fixed
+  // number of waves, since their length is known only on the device
+  const uint64_t pairs = n_items_dev ? std::min<uint64_t>(max_items * a->kv, 8192) : max_items * a->kv;
+  if (max_items * a->kv >= 0xffffffffull) return grm::fail(-1, "too many work items");
   const uint64_t bx = std::min<uint64_t>((pairs + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves,
                                          (a->exact_waves + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves);
   const dim3 grid(static_cast<unsigned>(std::max<uint64_t>(1, bx)));
@@ -530,9 +567,10 @@ int launch_exact(GqaDeviceArena* a, int H, int Qt) {
   const double denom = sqrt(static_cast<double>(a->hd));
 #define GRM_EXACT(KDT, RQ)                                                                  \
   grm::gqa::gqa_exact_kernel<KDT, RQ, grm::gqa::exact_stage_chunks<KDT, RQ>()><<<grid, threads, 0, a->stream>>>( \
-      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                   \
-      static_cast<uint32_t>(a->n_items), static_cast<int>(a->kv), static_cast<int>(a->hd),    \
-      a->piece_shift, R, Qt, a->d_q64, denom, a->d_hmax, a->cap_nodes)
+      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, items,                         \
+      static_cast<uint32_t>(max_items), n_items_dev, static_cast<int>(a->kv),                 \
+      static_cast<int>(a->hd), a->piece_shift, R, Qt, a->d_q64, denom, a->d_hmax,             \
+      a->cap_nodes * static_cast<size_t>(H), a->cap_nodes)
 #define GRM_EXACT_RQ(KDT)                       \
   switch (rq_pad) {                             \
     case 1: GRM_EXACT(KDT, 1); break;           \
@@ -682,6 +720,135 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   return launch_finalize(a, H, qb, topk, fin_blocks, bout);
 }
 
+// ------------------------------------------------------ bound-and-verify path
+
+constexpr uint32_t kCandFinBlocks = 16;  // finalize blocks per query over candidates
+
+bool use_bound(const GqaDeviceArena* a, const SrPlan& p, int qb) {
+  if (a->bound_mode == 0) return false;
+  if (a->bound_mode == 1) return true;
+  return qb * p.R * p.Qt > 16;
+}
+
+// Device buffers of bound-and-verify passes of up to p.qb_max queries.
+int prepare_bv(GqaDeviceArena* a, const SrPlan& p, int topk, uint32_t fin_blocks) {
+  const size_t qbm = static_cast<size_t>(p.qb_max);
+  const size_t cap = a->cap_nodes;
+  GRM_CHECK_RC(reserve_device_zero(&a->d_hmaxf, &a->d_hmaxf_count,
+                                   qbm * static_cast<size_t>(p.H) * p.Qt * cap, a->stream));
+  GRM_CHECK_RC(reserve_device(&a->d_colinfo, &a->d_colinfo_count,
+                              static_cast<size_t>(a->kv) * grm::gqa::kMaxCols));
+  GRM_CHECK_RC(reserve_device(&a->d_lbub, &a->d_lbub_count, qbm * cap));
+  GRM_CHECK_RC(reserve_device(&a->d_blists, &a->d_blists_count,
+                              qbm * fin_blocks * static_cast<size_t>(topk)));
+  GRM_CHECK_RC(reserve_device(&a->d_cslots, &a->d_cslots_count, qbm * cap));
+  GRM_CHECK_RC(reserve_device(&a->d_ccount, &a->d_ccount_count, qbm + 1));
+  GRM_CHECK_RC(reserve_device(&a->d_citems, &a->d_citems_count,
+                              std::max<size_t>(1, qbm * a->n_items)));
+  GRM_CHECK_RC(reserve_device(&a->d_q64, &a->d_q64_count,
+                              qbm * a->kv * a->hd * rq_pad_of(p.R * p.Qt)));
+  return 0;
+}
+
+// Enqueue one bound-and-verify pass over queries [0, qb) at qptr; query
+// j's top-k candidates (kCandFinBlocks lists of k) land at bout + j*per_q.
+int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
+               int topk, uint32_t fin_blocks, Cand* bout, size_t per_q) {
+  const int kv = static_cast<int>(a->kv);
+  const int RQ = p.R * p.Qt;
+  const int cols = qb * RQ;
+  const int NT = (cols + 15) / 16 <= 1 ? 1 : ((cols + 15) / 16 <= 2 ? 2 : 4);
+  const int H = p.H;
+  const bool fact = a->key_dtype == kI8 && static_cast<uint32_t>(a->group_size) == a->hd;
+  // error-bound constants as in enqueue_sr; rho: the INT8 row scale
+  // factored out of the dot product (fp32 product then fp16 rounding of
+  // code*scale, and the fp32 product of the screened value by the scale)
+  const double gamma = 2.0 * (a->hd + 2.0 * p.KS) * ldexp(1.0, -24);
+  double delta, sigma_q, sigma_k, sigma_p;
+  int emax;
+  if (p.mfma == kBF16) {
+    delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
+    sigma_q = sigma_k = sigma_p = ldexp(1.0, -125);
+    emax = 126;
+  } else {
+    delta = q_dtype == kF32 ? ldexp(1.0, -11) : 0.0;
+    sigma_q = sigma_k = ldexp(1.0, -14);
+    sigma_p = 0.0;
+    emax = 15;
+  }
+  const double rho = fact ? ldexp(1.0, -11) + ldexp(1.0, -21) : 0.0;
+  const size_t q_elems = static_cast<size_t>(H) * p.Qt * a->hd;
+  const size_t qstride = static_cast<size_t>(H) * p.Qt * a->cap_nodes;
+  const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
+  // 1. query rows as doubles and the query flags (for the exact pass)
+  GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt));
+  // 2. screened maxima of every (column, node)
+  if (a->n_items > 0) {
+    int cus = 256;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, a->device);
+    const uint64_t want_blocks = static_cast<uint64_t>(std::max(1, cus)) * 4;
+    const uint64_t px = std::max<uint64_t>(
+        1, std::min<uint64_t>((a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves,
+                              (want_blocks + a->kv - 1) / a->kv));
+    const dim3 grid(static_cast<unsigned>(px), a->kv);
+    const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);
+#define GRM_SMAX(KDT, KS, NTT, FACT)                                                              \
+  grm::gqa::gqa_smax_kernel<KDT, KS, NTT, FACT><<<grid, threads, lds, a->stream>>>(              \
+      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                          \
+      static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, qptr, q_dtype, q_elems, qb, emax, gamma,   \
+      delta, rho, sigma_q, sigma_k, sigma_p, a->d_colinfo, a->d_hmaxf, qstride, a->cap_nodes)
+#define GRM_SMAX_NT(KDT, KS, FACT)               \
+  switch (NT) {                                  \
+    case 1: GRM_SMAX(KDT, KS, 1, FACT); break;   \
+    case 2: GRM_SMAX(KDT, KS, 2, FACT); break;   \
+    default: GRM_SMAX(KDT, KS, 4, FACT); break;  \
+  }
+#define GRM_SMAX_KS(KDT, FACT)                   \
+  switch (p.KS) {                                \
+    case 2: GRM_SMAX_NT(KDT, 2, FACT); break;    \
+    case 4: GRM_SMAX_NT(KDT, 4, FACT); break;    \
+    default: GRM_SMAX_NT(KDT, 8, FACT); break;   \
+  }
+    switch (a->key_dtype) {
+      case kBF16: GRM_SMAX_KS(kBF16, false); break;
+      case kF16: GRM_SMAX_KS(kF16, false); break;
+      default:
+        if (fact) {
+          GRM_SMAX_KS(kI8, true);
+        } else {
+          GRM_SMAX_KS(kI8, false);
+        }
+        break;
+    }
+#undef GRM_SMAX_KS
+#undef GRM_SMAX_NT
+#undef GRM_SMAX
+    GRM_HIP_CHECK(hipGetLastError());
+  }
+  // 3. score bounds, the k best lower bounds per block (with no key tokens
+  // at all the column parameters are never used: every live node has no
+  // tokens and scores 0)
+  grm::gqa::gqa_bounds_kernel<<<dim3(fin_blocks, qb), grm::gqa::kFinWaves * grm::kWave, 0,
+                                a->stream>>>(
+      a->d_hmaxf, qstride, a->cap_nodes, H, p.Qt, p.R, cols, kv,
+      static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags, a->d_ids, a->d_kmax,
+      a->d_colinfo, a->d_qbad, fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub,
+      a->d_blists, a->d_ccount + p.qb_max);
+  GRM_HIP_CHECK(hipGetLastError());
+  // 4. candidates and their exact work items
+  grm::gqa::gqa_cands_kernel<<<qb, grm::gqa::kCandWaves * grm::kWave, 0, a->stream>>>(
+      a->d_blists, fin_blocks, topk, a->d_lbub, a->cap_nodes, static_cast<uint32_t>(a->high_water),
+      a->d_tok_off, a->d_len, kv, a->chunk, a->d_cslots, a->d_ccount, a->d_citems,
+      a->d_ccount + p.qb_max);
+  GRM_HIP_CHECK(hipGetLastError());
+  // 5. the law on the candidates, then their exact scores and top-k
+  GRM_CHECK_RC(launch_exact(a, H, p.Qt, a->d_citems, static_cast<uint64_t>(qb) * a->n_items,
+                            a->d_ccount + p.qb_max));
+  (void)per_q;
+  return launch_finalize(a, H, qb, topk, std::min(kCandFinBlocks, fin_blocks), bout, a->d_cslots,
+                         a->d_ccount);
+}
+
 int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_device, int q_count,
                int H, int Qt, int warmup, int topk, uint64_t* out_ids, float* out_scores,
                float* elapsed_ms) {
@@ -718,6 +885,11 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   SrPlan plan;
   const bool use_sr = sr_plan(a, H, Qt, &plan);
   if (use_sr) GRM_CHECK_RC(prepare_sr(a, plan));
+  // where each query's per-block lists are, and how many entries they hold
+  std::vector<uint32_t> q_entries(q_count, static_cast<uint32_t>(per_q));
+  std::vector<size_t> q_off(q_count);
+  for (int qi = 0; qi < q_count; ++qi) q_off[qi] = static_cast<size_t>(qi) * per_q;
+  bool bv_ready = false;
   // untimed warmup queries first, then the timed ones
   const int segments[2][2] = {{0, warmup}, {warmup, q_count}};
   for (int si = 0; si < 2; ++si) {
@@ -726,8 +898,25 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
     if (use_sr) {
       for (int q0 = seg[0]; q0 < seg[1]; q0 += plan.qb_max) {
         const int qb = std::min(plan.qb_max, seg[1] - q0);
-        GRM_CHECK_RC(enqueue_sr(a, plan, qbase + static_cast<size_t>(q0) * qstride, q_dtype, qb, topk,
-                                fin_blocks, a->blocks_out.dev + static_cast<size_t>(q0) * per_q));
+        if (use_bound(a, plan, qb)) {
+          if (!bv_ready) {
+            GRM_CHECK_RC(prepare_bv(a, plan, topk, fin_blocks));
+            bv_ready = true;
+          }
+          GRM_CHECK_RC(enqueue_bv(a, plan, qbase + static_cast<size_t>(q0) * qstride, q_dtype, qb,
+                                  topk, fin_blocks, a->blocks_out.dev + static_cast<size_t>(q0) * per_q,
+                                  per_q));
+          // the candidates' lists of the pass's queries are packed back to back
+          const uint32_t ent = std::min(kCandFinBlocks, fin_blocks) * topk;
+          for (int j = 0; j < qb; ++j) {
+            q_entries[q0 + j] = ent;
+            q_off[q0 + j] = static_cast<size_t>(q0) * per_q + static_cast<size_t>(j) * ent;
+          }
+          a->bv_routes += 1;
+        } else {
+          GRM_CHECK_RC(enqueue_sr(a, plan, qbase + static_cast<size_t>(q0) * qstride, q_dtype, qb, topk,
+                                  fin_blocks, a->blocks_out.dev + static_cast<size_t>(q0) * per_q));
+        }
       }
     } else {
       for (int qi = seg[0]; qi < seg[1]; ++qi) {
@@ -739,8 +928,7 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
   GRM_CHECK_RC(grm::wait_event(a->ev_stop));
   for (int qi = 0; qi < q_count; ++qi) {
-    grm::host_topk_merge(a->blocks_out.host + static_cast<size_t>(qi) * per_q, per_q, topk,
-                         a->merged.data());
+    grm::host_topk_merge(a->blocks_out.host + q_off[qi], q_entries[qi], topk, a->merged.data());
     write_result(a->merged.data(), topk, out_ids + static_cast<size_t>(qi) * topk,
                  out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
   }
