@@ -841,15 +841,25 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     }
   };
 
-  // stream: five tile buffers, four tiles in flight ahead of the fold
+  // stream: five tile buffers, four tiles in flight ahead of the fold, in
+  // groups of five steps with the exit at the bottom.  Steps past the
+  // item's last tile fold reloads whose rows all lie past the item (masked
+  // to -inf); an exit between steps would let the compiler sink each load
+  // into the path that continues, behind the fold, and drain the stream.
   int tile = 0;
-  auto step = [&](Tile& now, Tile& free) -> bool {
+  auto step = [&](Tile& now, Tile& free) {
     load_tile(free, tile + 4);  // past the end: reloads the last token
+    __builtin_amdgcn_sched_barrier(0);
     fold(now, tile);
-    return ++tile < ntiles;
+    ++tile;
   };
-  while (step(x0, x4) && step(x1, x0) && step(x2, x1) && step(x3, x2) && step(x4, x3)) {
-  }
+  do {
+    step(x0, x4);
+    step(x1, x0);
+    step(x2, x1);
+    step(x3, x2);
+    step(x4, x3);
+  } while (tile < ntiles);
 
   // thresholds and candidates
   const float km = kmax[it.slot];
@@ -965,7 +975,9 @@ __device__ inline void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 }
 
 // Screen-only pass; grid (P, kv heads), persistent: wave w of block b walks
-// the items b*4 + w, b*4 + w + 4P, ... as one stream of 16-token tiles,
+// the work items b*4 + w, b*4 + w + 4P, ... -- one item per live node with
+// key tokens, all of its tokens, so each (node, kv head) has one writer --
+// as one stream of 16-token tiles,
 // four tiles in flight ahead of the one being screened, across item
 // boundaries.  The block stages kv head g's query columns once
 // (stage_columns); blocks with blockIdx.x == 0 write colinfo[g*cols + cg]
@@ -979,17 +991,18 @@ __device__ inline void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 // codes enter the MFMA as exact f16 integers and the lane's row scale
 // multiplies its results, s~ = scale_t * |q~ . c|; the difference to the
 // law's fp16(code * scale) keys is in the bound (rho, and a norm bound
-// that covers c * scale).  At an item's end the maxima of the 16 lanes of
-// each column combine and fold into
-// hmaxf[qb*qstride + ((g*R + r)*Qt + qi)*cap + slot] (float bits,
-// atomicMax: the values are non-negative), in scaled units.
-template <int KDT, int KS, int NT, bool FACT>
+// that covers c * scale).  At a node's end the maxima of the 16 lanes of
+// each column combine and are stored at
+// hmaxf[(slot*kv + g)*colstride + cg] (float bits, scaled units;
+// colstride >= cols): one (node, kv head)'s columns are one contiguous
+// run, written by one coalesced store.
+template <int KDT, int KS, int NT, bool FACT, bool SF16>
 __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     const unsigned char* __restrict__ keys, const unsigned char* __restrict__ scales,
     int scale_dtype, int group_size, const Item* __restrict__ items, uint32_t n_items, int kv,
     int R, int Qt, const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
     double gamma, double delta, double rho, double sigma_q, double sigma_k, double sigma_p,
-    float4* __restrict__ colinfo, unsigned* __restrict__ hmaxf, size_t qstride, size_t cap) {
+    float4* __restrict__ colinfo, unsigned* __restrict__ hmaxf, int colstride) {
   using KT = KeyTraits<KDT>;
   constexpr int MT = ScreenTraits<KDT>::kMfma;
   constexpr bool PERM = KDT == kI8;
@@ -1033,10 +1046,26 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     d.slot = it.slot;
     return d;
   };
+  // INT8 scales stay raw bits until the tile is folded: a conversion next
+  // to the load would make the wave wait for every load in flight
   struct Tile {
     u32x4 v[NL];
-    float s[KDT == kI8 ? (FACT ? 1 : NL) : 1];
+    uint32_t s[KDT == kI8 ? (FACT ? 1 : NL) : 1];
     uint32_t fin;  // slot | kEnd on an item's last tile, else kNoSlot
+  };
+  auto scale_raw = [](const unsigned char* sp, uint64_t idx) -> uint32_t {
+    if constexpr (SF16) {
+      return reinterpret_cast<const unsigned short*>(sp)[idx];
+    } else {
+      return reinterpret_cast<const uint32_t*>(sp)[idx];
+    }
+  };
+  auto scale_of = [](uint32_t raw) -> float {
+    if constexpr (SF16) {
+      return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(raw)));
+    } else {
+      return __uint_as_float(raw);
+    }
   };
   Src ld = source(items[has_item ? li : 0]);
   uint32_t lt = 0;
@@ -1052,12 +1081,11 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     for (int i = 0; i < NL; ++i) b.v[i] = __builtin_nontemporal_load(p + i * 4 * ld.L);
     if constexpr (KDT == kI8) {
       if constexpr (FACT) {
-        b.s[0] = load_scale(ld.sp, scale_dtype, t);
+        b.s[0] = scale_raw(ld.sp, t);
       } else {
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-          b.s[i] = load_scale(ld.sp, scale_dtype,
-                              static_cast<uint64_t>((i * 64 + quarter * 16) / group_size) * ld.L + t);
+          b.s[i] = scale_raw(ld.sp, static_cast<uint64_t>((i * 64 + quarter * 16) / group_size) * ld.L + t);
         }
       }
     }
@@ -1123,7 +1151,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
           bk[ks].z = o[2];
           bk[ks].w = o[3];
         } else {
-          const float sc = b.s[ks >> 1];
+          const float sc = scale_of(b.s[ks >> 1]);
           const uint32_t w[2] = {w0, w1};
           uint32_t o[4];
 #pragma unroll
@@ -1141,15 +1169,21 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
       }
     }
   };
-  float m[NT][4];
+  // running maxima as float bits: the values are non-negative, so their
+  // bit patterns order like the values (a NaN, possible only from
+  // non-finite keys or query values, wins; such a node or query is never
+  // ranked, by its flags)
+  uint32_t m[NT][4];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) m[nt][v] = 0.0f;
+    for (int v = 0; v < 4; ++v) m[nt][v] = 0u;
   }
   auto fold = [&](const Tile& b) {
     u32x4 bk[KS];
     key_frags(b, bk);
+    float sc = 1.0f;
+    if constexpr (FACT) sc = scale_of(b.s[0]);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1158,62 +1192,67 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
       const float cv[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        // fmaxf keeps the number when one side is NaN (non-finite keys make
-        // the node's score NaN through its flags, not through the screen)
-        if constexpr (FACT) {
-          m[nt][v] = fmaxf(m[nt][v], fabsf(cv[v]) * b.s[0]);
-        } else {
-          m[nt][v] = fmaxf(m[nt][v], fabsf(cv[v]));
-        }
+        const float x = FACT ? fabsf(cv[v]) * sc : fabsf(cv[v]);
+        m[nt][v] = max(m[nt][v], __float_as_uint(x));
       }
     }
   };
-  // item end: the column maxima over the 16 lanes of each quarter; lane
-  // (quarter, r16) then folds column nt*16 + quarter*4 + v, nt = r16/4,
-  // v = r16%4, into the node's cell
+  // node end: the column maxima over the 16 lanes of each quarter; lane
+  // (quarter, r16) then stores column nt*16 + quarter*4 + v, nt = r16/4,
+  // v = r16%4: one (node, kv head)'s columns are one contiguous run,
+  // written by one coalesced store
+  const int my_cg = (r16 >> 2) * 16 + quarter * 4 + (r16 & 3);
+  const bool my_col = (r16 >> 2) < NT && my_cg < cols;
   auto emit = [&](uint32_t slot) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        float x = m[nt][v];
+        uint32_t x = m[nt][v];
 #pragma unroll
-        for (int off = 1; off < 16; off <<= 1) x = fmaxf(x, __shfl_xor(x, off));
+        for (int off = 1; off < 16; off <<= 1) x = max(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), off)));
         m[nt][v] = x;
       }
     }
-    float mine = 0.0f;
+    uint32_t mine = 0u;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         if (r16 == nt * 4 + v) mine = m[nt][v];
-        m[nt][v] = 0.0f;
+        m[nt][v] = 0u;
       }
     }
-    const int cg = (r16 >> 2) * 16 + quarter * 4 + (r16 & 3);
-    if ((r16 >> 2) < NT && cg < cols) {
-      const int qb = cg / RQc;
-      const int r = (cg % RQc) / Qt;
-      const int qi = cg % Qt;
-      atomicMax(hmaxf + qb * qstride + (static_cast<size_t>((g * R + r) * Qt + qi)) * cap + slot,
-                __float_as_uint(mine));
+    if (my_col) hmaxf[(static_cast<size_t>(slot) * kv + g) * colstride + my_cg] = mine;
+  };
+  // Groups of five steps with one exit, at the bottom: steps after the
+  // stream's last tile fold reloaded tiles marked kNoSlot, which emit
+  // nothing (an exit between steps would leave the compiler unable to keep
+  // the rotating tile buffers in place, and it would drain the loads).
+  bool done = false;
+  auto step = [&](Tile& now, Tile& free) {
+    load_next(free);
+    __builtin_amdgcn_sched_barrier(0);
+    fold(now);
+    if (now.fin != kNoSlot && !done) {
+      emit(now.fin & ~kEnd);
+      done = (now.fin & kEnd) != 0u;
     }
   };
-  auto step = [&](Tile& now, Tile& free) -> bool {
-    load_next(free);
-    fold(now);
-    if (now.fin == kNoSlot) return true;
-    emit(now.fin & ~kEnd);
-    return (now.fin & kEnd) == 0u;
-  };
-  while (step(x0, x4) && step(x1, x0) && step(x2, x1) && step(x3, x2) && step(x4, x3)) {
-  }
+  do {
+    step(x0, x4);
+    step(x1, x0);
+    step(x2, x1);
+    step(x3, x2);
+    step(x4, x3);
+  } while (!done);
 }
 
 // Node-score bounds; grid (blocks, queries), 4 wavefronts, lane = slot,
 // grid-stride over groups of 64 slots.  For query qb and slot s, each
-// column's screened maximum m (hmaxf, scaled units) bounds the law's
+// column's screened maximum m (hmaxf[(s*kv + g)*colstride + cg], cg the
+// column of head h = g*R + r and query token qi; scaled units) bounds the
+// law's
 // max_t |dot| / sqrt(hd) of its head and query token from below by
 // max(0, m - E) / scale / denom and from above by (m + E) / scale / denom,
 // E = coef * K + eabs (colinfo), K = kmax[s], or with FACT the bound on
@@ -1224,11 +1263,11 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
 // arithmetic on both sides and rounded outward to float.  Writes
 // lbub[qb*cap + s] = (lb, ub): (0, 0) for a live node without key tokens,
 // NaN for slots that are not ranked (free, non-finite keys, non-finite
-// query); re-zeroes the maxima it reads; the block's k best lower bounds
+// query; their cells are never read); the block's k best lower bounds
 // (tie law) go to block_out[(qb*gridDim.x + blockIdx.x)*k ..).  Also
 // zeroes *zero_counter (the candidates kernel's item count).
 __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
-    unsigned* __restrict__ hmaxf, size_t qstride, size_t cap, int H, int Qt, int R, int cols,
+    const unsigned* __restrict__ hmaxf, int colstride, size_t cap, int H, int Qt, int R, int cols,
     int kv, uint32_t n_slots, const uint32_t* __restrict__ lens,
     const uint32_t* __restrict__ flags, const uint64_t* __restrict__ ids,
     const unsigned* __restrict__ kmax, const float4* __restrict__ colinfo,
@@ -1239,8 +1278,6 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
   const int wave = threadIdx.x / kWave;
   const int qb = blockIdx.y;
   if (blockIdx.x == 0 && qb == 0 && threadIdx.x == 0) *zero_counter = 0u;
-  hmaxf += qb * qstride;
-  const int RQc = R * Qt;
   const double denom = sqrt(static_cast<double>(hd));
   const double kadd = 0x1p-25 * denom;
   bool q_bad = false;
@@ -1260,16 +1297,18 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     const float kmf = in ? __uint_as_float(kmax[slot]) : 0.0f;
     const double K = fact ? (static_cast<double>(kmf) + kadd) / (1.0 - 0x1p-10)
                           : static_cast<double>(kmf);
+    // only ranked nodes with key tokens have screened maxima
+    const bool screened = in && (f & 3u) == 3u && len != 0u && !q_bad;
+    const unsigned* cells = hmaxf + static_cast<size_t>(screened ? slot : 0u) * kv * colstride;
     double lo_sum = 0.0, hi_sum = 0.0;
     for (int h = 0; h < H; ++h) {
       const int g = h / R;
       const int r = h - g * R;
       double lo_h = 0.0, hi_h = 0.0;
       for (int qi = 0; qi < Qt; ++qi) {
-        const size_t cell = static_cast<size_t>(h * Qt + qi) * cap + slot;
-        const float mv = in ? __uint_as_float(hmaxf[cell]) : 0.0f;
-        if (in && mv != 0.0f) hmaxf[cell] = 0u;
-        const float4 ci = colinfo[g * cols + (qb * R + r) * Qt + qi];
+        const int cg = (qb * R + r) * Qt + qi;
+        const float mv = screened ? __uint_as_float(cells[g * colstride + cg]) : 0.0f;
+        const float4 ci = colinfo[g * cols + cg];
         const double e = (static_cast<double>(ci.x) * K + static_cast<double>(ci.y)) * (1.0 + 0x1p-50);
         const double m = static_cast<double>(mv);
         const double inv = 1.0 / static_cast<double>(ci.z);  // a power of two: exact

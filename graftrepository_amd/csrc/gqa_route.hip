@@ -27,6 +27,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <set>
 #include <unordered_map>
 #include <vector>
@@ -76,6 +77,11 @@ struct GqaDeviceArena {
   Item* d_items = nullptr;
   size_t d_items_count = 0;
   uint64_t n_items = 0;
+  // one item per live node with key tokens (all of them), for the
+  // screen-only pass of the bound-and-verify path
+  Item* d_units = nullptr;
+  size_t d_units_count = 0;
+  uint64_t n_units = 0;
   uint64_t items_epoch = ~0ull;
   uint32_t max_len = 0;  // longest live node
   // per-(query, head, slot) maxima, head-major per query (double bits)
@@ -107,6 +113,7 @@ struct GqaDeviceArena {
   Item* d_citems = nullptr;      // exact work items of the candidates
   size_t d_citems_count = 0;
   uint64_t bv_routes = 0;        // passes routed by bound and verify
+  std::map<std::pair<const void*, size_t>, int> resident;  // blocks per CU by (kernel, LDS bytes)
   uint64_t routes = 0;          // route calls
   std::vector<Cand> merged;
   void* d_queries = nullptr;
@@ -186,7 +193,7 @@ void destroy_arena(GqaDeviceArena* a) {
                  a->d_flags,  a->d_nonfinite, a->d_kmax,  a->d_items,  a->d_hmax,
                  a->d_qbad,   a->d_queries, a->d_stage,   a->d_q64,    a->d_hmaxf,
                  a->d_colinfo, a->d_lbub,   a->d_blists,  a->d_cslots, a->d_ccount,
-                 a->d_citems};
+                 a->d_citems, a->d_units};
   for (void* p : dev) {
     if (p) (void)hipFree(p);
   }
@@ -480,21 +487,29 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
 
 int ensure_items(GqaDeviceArena* a) {
   if (a->items_epoch == a->epoch && a->d_items) return 0;
-  std::vector<Item> items;
+  std::vector<Item> items, units;
   items.reserve(a->live * 2);
+  units.reserve(a->live);
   uint32_t max_len = 0;
   for (uint64_t s = 0; s < a->high_water; ++s) {
     if (a->slot_id[s] == kNoId) continue;
     append_items(items, static_cast<uint32_t>(s), a->tok_off[s] * a->kv, a->len[s], a->chunk);
+    if (a->len[s] > 0) {
+      append_items(units, static_cast<uint32_t>(s), a->tok_off[s] * a->kv, a->len[s], a->len[s]);
+    }
     max_len = std::max(max_len, a->len[s]);
   }
   GRM_CHECK_RC(reserve_device(&a->d_items, &a->d_items_count, items.size()));
+  GRM_CHECK_RC(reserve_device(&a->d_units, &a->d_units_count, units.size()));
   if (!items.empty()) {
     GRM_HIP_CHECK(hipMemcpyAsync(a->d_items, items.data(), items.size() * sizeof(Item),
+                                 hipMemcpyHostToDevice, a->stream));
+    GRM_HIP_CHECK(hipMemcpyAsync(a->d_units, units.data(), units.size() * sizeof(Item),
                                  hipMemcpyHostToDevice, a->stream));
     GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
   }
   a->n_items = items.size();
+  a->n_units = units.size();
   a->max_len = max_len;
   a->items_epoch = a->epoch;
   return 0;
@@ -730,12 +745,37 @@ bool use_bound(const GqaDeviceArena* a, const SrPlan& p, int qb) {
   return qb * p.R * p.Qt > 16;
 }
 
+// Grid (P, kv) of the persistent screen kernel `fn`: as many blocks as
+// the device holds resident at once (a block that had to wait for a slot
+// would start its whole share of the items when the others finish), and
+// no more than there are items to give every wave one.
+int persistent_grid(GqaDeviceArena* a, const void* fn, unsigned threads, size_t lds, dim3* grid) {
+  const std::pair<const void*, size_t> key(fn, lds);
+  auto it = a->resident.find(key);
+  int per_cu = 0;
+  if (it == a->resident.end()) {
+    GRM_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, static_cast<int>(threads), lds));
+    per_cu = std::max(1, per_cu);
+    a->resident.emplace(key, per_cu);
+  } else {
+    per_cu = it->second;
+  }
+  int cus = 256;
+  GRM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, a->device));
+  const uint64_t resident = static_cast<uint64_t>(std::max(1, cus)) * static_cast<uint64_t>(per_cu);
+  const uint64_t px = std::max<uint64_t>(
+      1, std::min<uint64_t>((a->n_units + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves,
+                            std::max<uint64_t>(1, resident / a->kv)));
+  *grid = dim3(static_cast<unsigned>(px), a->kv);
+  return 0;
+}
+
 // Device buffers of bound-and-verify passes of up to p.qb_max queries.
 int prepare_bv(GqaDeviceArena* a, const SrPlan& p, int topk, uint32_t fin_blocks) {
   const size_t qbm = static_cast<size_t>(p.qb_max);
   const size_t cap = a->cap_nodes;
-  GRM_CHECK_RC(reserve_device_zero(&a->d_hmaxf, &a->d_hmaxf_count,
-                                   qbm * static_cast<size_t>(p.H) * p.Qt * cap, a->stream));
+  GRM_CHECK_RC(reserve_device(&a->d_hmaxf, &a->d_hmaxf_count,
+                              qbm * static_cast<size_t>(p.H) * p.Qt * cap));
   GRM_CHECK_RC(reserve_device(&a->d_colinfo, &a->d_colinfo_count,
                               static_cast<size_t>(a->kv) * grm::gqa::kMaxCols));
   GRM_CHECK_RC(reserve_device(&a->d_lbub, &a->d_lbub_count, qbm * cap));
@@ -778,45 +818,49 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   }
   const double rho = fact ? ldexp(1.0, -11) + ldexp(1.0, -21) : 0.0;
   const size_t q_elems = static_cast<size_t>(H) * p.Qt * a->hd;
-  const size_t qstride = static_cast<size_t>(H) * p.Qt * a->cap_nodes;
+  // screened maxima: one run of colstride cells per (slot, kv head)
+  const int colstride = p.qb_max * RQ;
   const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
   // 1. query rows as doubles and the query flags (for the exact pass)
   GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt));
   // 2. screened maxima of every (column, node)
-  if (a->n_items > 0) {
-    int cus = 256;
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, a->device);
-    const uint64_t want_blocks = static_cast<uint64_t>(std::max(1, cus)) * 4;
-    const uint64_t px = std::max<uint64_t>(
-        1, std::min<uint64_t>((a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves,
-                              (want_blocks + a->kv - 1) / a->kv));
-    const dim3 grid(static_cast<unsigned>(px), a->kv);
+  if (a->n_units > 0) {
     const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);
-#define GRM_SMAX(KDT, KS, NTT, FACT)                                                              \
-  grm::gqa::gqa_smax_kernel<KDT, KS, NTT, FACT><<<grid, threads, lds, a->stream>>>(              \
-      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                          \
-      static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, qptr, q_dtype, q_elems, qb, emax, gamma,   \
-      delta, rho, sigma_q, sigma_k, sigma_p, a->d_colinfo, a->d_hmaxf, qstride, a->cap_nodes)
-#define GRM_SMAX_NT(KDT, KS, FACT)               \
-  switch (NT) {                                  \
-    case 1: GRM_SMAX(KDT, KS, 1, FACT); break;   \
-    case 2: GRM_SMAX(KDT, KS, 2, FACT); break;   \
-    default: GRM_SMAX(KDT, KS, 4, FACT); break;  \
+#define GRM_SMAX(KDT, KS, NTT, FACT, SF16)                                                        \
+  do {                                                                                            \
+    auto fn = grm::gqa::gqa_smax_kernel<KDT, KS, NTT, FACT, SF16>;                                \
+    dim3 grid;                                                                                    \
+    GRM_CHECK_RC(persistent_grid(a, reinterpret_cast<const void*>(fn), threads, lds, &grid));     \
+    fn<<<grid, threads, lds, a->stream>>>(                                                        \
+        a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_units,                        \
+        static_cast<uint32_t>(a->n_units), kv, p.R, p.Qt, qptr, q_dtype, q_elems, qb, emax,       \
+        gamma, delta, rho, sigma_q, sigma_k, sigma_p, a->d_colinfo, a->d_hmaxf, colstride);       \
+  } while (0)
+#define GRM_SMAX_NT(KDT, KS, FACT, SF16)               \
+  switch (NT) {                                        \
+    case 1: GRM_SMAX(KDT, KS, 1, FACT, SF16); break;   \
+    case 2: GRM_SMAX(KDT, KS, 2, FACT, SF16); break;   \
+    default: GRM_SMAX(KDT, KS, 4, FACT, SF16); break;  \
   }
-#define GRM_SMAX_KS(KDT, FACT)                   \
-  switch (p.KS) {                                \
-    case 2: GRM_SMAX_NT(KDT, 2, FACT); break;    \
-    case 4: GRM_SMAX_NT(KDT, 4, FACT); break;    \
-    default: GRM_SMAX_NT(KDT, 8, FACT); break;   \
+#define GRM_SMAX_KS(KDT, FACT, SF16)                   \
+  switch (p.KS) {                                      \
+    case 2: GRM_SMAX_NT(KDT, 2, FACT, SF16); break;    \
+    case 4: GRM_SMAX_NT(KDT, 4, FACT, SF16); break;    \
+    default: GRM_SMAX_NT(KDT, 8, FACT, SF16); break;   \
   }
+    const bool sf16 = a->scale_dtype == kF16;
     switch (a->key_dtype) {
-      case kBF16: GRM_SMAX_KS(kBF16, false); break;
-      case kF16: GRM_SMAX_KS(kF16, false); break;
+      case kBF16: GRM_SMAX_KS(kBF16, false, false); break;
+      case kF16: GRM_SMAX_KS(kF16, false, false); break;
       default:
-        if (fact) {
-          GRM_SMAX_KS(kI8, true);
+        if (fact && sf16) {
+          GRM_SMAX_KS(kI8, true, true);
+        } else if (fact) {
+          GRM_SMAX_KS(kI8, true, false);
+        } else if (sf16) {
+          GRM_SMAX_KS(kI8, false, true);
         } else {
-          GRM_SMAX_KS(kI8, false);
+          GRM_SMAX_KS(kI8, false, false);
         }
         break;
     }
@@ -830,7 +874,7 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   // tokens and scores 0)
   grm::gqa::gqa_bounds_kernel<<<dim3(fin_blocks, qb), grm::gqa::kFinWaves * grm::kWave, 0,
                                 a->stream>>>(
-      a->d_hmaxf, qstride, a->cap_nodes, H, p.Qt, p.R, cols, kv,
+      a->d_hmaxf, colstride, a->cap_nodes, H, p.Qt, p.R, cols, kv,
       static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags, a->d_ids, a->d_kmax,
       a->d_colinfo, a->d_qbad, fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub,
       a->d_blists, a->d_ccount + p.qb_max);
