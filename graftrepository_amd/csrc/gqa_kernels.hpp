@@ -664,13 +664,14 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
   return fabs(acc);
 }
 
-// Screen and refine; grid (ceil(items / 4), kv heads), one wavefront per
+// Screen and refine; grid (kv heads, ceil(items / 4)) -- or, past the
+// grid's y limit, (ceil(items / 4), kv heads) -- one wavefront per
 // (item, kv head g).
 //
 // Each block first stages kv head g's query columns of the Qb queries
 // (stage_columns: fp32 values for the screen fragments and the exact
-// recomputation, scale and error-bound parameters per column); blocks with
-// blockIdx.x == 0 write qflags[qb*kv + g] = 1 when a value of query qb read
+// recomputation, scale and error-bound parameters per column); the blocks
+// of item block 0 write qflags[qb*kv + g] = 1 when a value of query qb read
 // by kv head g is non-finite (0 otherwise).
 // Columns with a non-finite value take no part in the screen (every score
 // of that query is NaN).  The item's tokens stream in 16-token tiles, two
@@ -692,7 +693,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
     double gamma, double delta, double sigma_q, double sigma_k, double sigma_p,
     unsigned* __restrict__ qflags, const float* __restrict__ kmax, double denom,
-    unsigned long long* __restrict__ hmax, size_t hstride, size_t cap) {
+    unsigned long long* __restrict__ hmax, size_t hstride, size_t cap, int g_fast) {
   using KT = KeyTraits<KDT>;
   constexpr int MT = ScreenTraits<KDT>::kMfma;
   constexpr int HD = 32 * KS;
@@ -702,13 +703,16 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
   __shared__ unsigned s_bad[kMaxCols];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int g = blockIdx.y;
+  // g_fast: grid (kv, item blocks), so consecutive blocks read one node's
+  // neighbouring kv-head blocks; else grid (item blocks, kv)
+  const int g = g_fast ? blockIdx.x : blockIdx.y;
+  const uint32_t item_block = g_fast ? blockIdx.y : blockIdx.x;
   const int RQc = R * Qt;
   const int cols = Qb * RQc;
   // The wave's first tiles are requested before the block prepares its
   // query columns, so the two overlap; a wave without an item issues no
   // loads but joins the block's barriers.
-  const uint32_t item_raw = blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t item_raw = item_block * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const bool has_item = item_raw < n_items;
   const Item it = items[has_item ? item_raw : n_items - 1];
   const uint64_t L = it.len;
@@ -763,7 +767,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
   stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, g, emax, gamma, delta,
                     0.0, sigma_q, sigma_k, sigma_p);
   __syncthreads();
-  if (blockIdx.x == 0 && threadIdx.x < static_cast<unsigned>(Qb)) {
+  if (item_block == 0 && threadIdx.x < static_cast<unsigned>(Qb)) {
     unsigned bad = 0u;
     for (int j = 0; j < RQc; ++j) bad |= s_bad[threadIdx.x * RQc + j];
     qflags[threadIdx.x * kv + g] = bad;
@@ -841,25 +845,20 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     }
   };
 
-  // stream: five tile buffers, four tiles in flight ahead of the fold, in
-  // groups of five steps with the exit at the bottom.  Steps past the
-  // item's last tile fold reloads whose rows all lie past the item (masked
-  // to -inf); an exit between steps would let the compiler sink each load
-  // into the path that continues, behind the fold, and drain the stream.
+  // stream: five tile buffers, four tiles in flight ahead of the fold.
+  // The exits between steps let the compiler move a step's load into the
+  // path that continues, behind the fold, so the wave drains its loads
+  // every few tiles; a single exit (as in gqa_smax_kernel) would fold up
+  // to four reloaded tiles past every item's end instead, which measured
+  // slower here, where items are short and a fold tracks three values.
   int tile = 0;
-  auto step = [&](Tile& now, Tile& free) {
+  auto step = [&](Tile& now, Tile& free) -> bool {
     load_tile(free, tile + 4);  // past the end: reloads the last token
-    __builtin_amdgcn_sched_barrier(0);
     fold(now, tile);
-    ++tile;
+    return ++tile < ntiles;
   };
-  do {
-    step(x0, x4);
-    step(x1, x0);
-    step(x2, x1);
-    step(x3, x2);
-    step(x4, x3);
-  } while (tile < ntiles);
+  while (step(x0, x4) && step(x1, x0) && step(x2, x1) && step(x3, x2) && step(x4, x3)) {
+  }
 
   // thresholds and candidates
   const float km = kmax[it.slot];

@@ -694,8 +694,13 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   // 1. screen and refine every (item, kv head), preparing the query
   // columns in each block
   if (a->n_items > 0) {
-    const dim3 grid(static_cast<unsigned>((a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves),
-                    a->kv);
+    // kv heads fastest, so the resident blocks sweep the bank in address
+    // order (a node's kv-head blocks are contiguous); item blocks on x only
+    // past the grid's y limit
+    const uint64_t item_blocks = (a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves;
+    const int g_fast = item_blocks <= 65535 ? 1 : 0;
+    const dim3 grid = g_fast ? dim3(a->kv, static_cast<unsigned>(item_blocks))
+                             : dim3(static_cast<unsigned>(item_blocks), a->kv);
     const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
     const size_t hstride = a->cap_nodes * static_cast<size_t>(H);
     const double denom = sqrt(static_cast<double>(a->hd));
@@ -705,7 +710,7 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
       a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                        \
       static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, qptr, q_dtype, q_elems, qb, emax, gamma,  \
       delta, sigma_q, sigma_k, sigma_p, a->d_qbad, reinterpret_cast<const float*>(a->d_kmax),     \
-      denom, a->d_hmax, hstride, a->cap_nodes)
+      denom, a->d_hmax, hstride, a->cap_nodes, g_fast)
 #define GRM_SR_NT(KDT, KS)                 \
   switch (NT) {                            \
     case 1: GRM_SR(KDT, KS, 1); break;     \
