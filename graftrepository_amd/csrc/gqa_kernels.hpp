@@ -1247,7 +1247,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
   } while (!done);
 }
 
-// Node-score bounds; grid (blocks, queries), 4 wavefronts, lane = slot,
+// Node-score bounds; grid (queries, blocks), 4 wavefronts, lane = slot,
 // grid-stride over groups of 64 slots.  For query qb and slot s, each
 // column's screened maximum m (hmaxf[(s*kv + g)*colstride + cg], cg the
 // column of head h = g*R + r and query token qi; scaled units) bounds the
@@ -1263,7 +1263,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
 // lbub[qb*cap + s] = (lb, ub): (0, 0) for a live node without key tokens,
 // NaN for slots that are not ranked (free, non-finite keys, non-finite
 // query; their cells are never read); the block's k best lower bounds
-// (tie law) go to block_out[(qb*gridDim.x + blockIdx.x)*k ..).  Also
+// (tie law) go to block_out[(qb*blocks + block)*k ..).  Also
 // zeroes *zero_counter (the candidates kernel's item count).
 __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     const unsigned* __restrict__ hmaxf, int colstride, size_t cap, int H, int Qt, int R, int cols,
@@ -1273,11 +1273,23 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     const unsigned* __restrict__ qbad, int fact, int hd, int k, float2* __restrict__ lbub,
     Cand* __restrict__ block_out, uint32_t* __restrict__ zero_counter) {
   __shared__ Cand s_lists[kFinWaves][kMaxTopK];
+  extern __shared__ float4 s_ci[];  // [H*Qt]: query qb's {coef, eabs, 1/scale, bad}, (h, qi) order
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int qb = blockIdx.y;
-  if (blockIdx.x == 0 && qb == 0 && threadIdx.x == 0) *zero_counter = 0u;
+  // grid (queries, slot blocks): the queries of one group of slots run
+  // back to back and share the cache lines of the slots' maxima
+  const int qb = blockIdx.x;
+  const uint32_t sblk = blockIdx.y, nsblk = gridDim.y;
+  if (sblk == 0 && qb == 0 && threadIdx.x == 0) *zero_counter = 0u;
   const double denom = sqrt(static_cast<double>(hd));
+  const int HQ = H * Qt;
+  for (int i = threadIdx.x; i < HQ; i += blockDim.x) {
+    const int h = i / Qt;
+    float4 ci = colinfo[(h / R) * cols + (qb * R + h % R) * Qt + i % Qt];
+    ci.z = 1.0f / ci.z;  // the scale is a power of two: its inverse is exact
+    s_ci[i] = ci;
+  }
+  __syncthreads();
   const double kadd = 0x1p-25 * denom;
   bool q_bad = false;
   for (int g0 = 0; g0 < kv; g0 += kWave) {
@@ -1286,8 +1298,8 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
   q_bad = __ballot(q_bad) != 0ull;
   WaveList Lw;
   wl_init(Lw);
-  const uint32_t gstride = gridDim.x * kFinWaves * kWave;
-  for (uint32_t base = (blockIdx.x * kFinWaves + wave) * kWave; base < n_slots; base += gstride) {
+  const uint32_t gstride = nsblk * kFinWaves * kWave;
+  for (uint32_t base = (sblk * kFinWaves + wave) * kWave; base < n_slots; base += gstride) {
     const uint32_t slot = base + lane;
     const bool in = slot < n_slots;
     const uint32_t f = in ? flags[slot] : 0u;
@@ -1299,25 +1311,39 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     // only ranked nodes with key tokens have screened maxima
     const bool screened = in && (f & 3u) == 3u && len != 0u && !q_bad;
     const unsigned* cells = hmaxf + static_cast<size_t>(screened ? slot : 0u) * kv * colstride;
-    double lo_sum = 0.0, hi_sum = 0.0;
-    for (int h = 0; h < H; ++h) {
-      const int g = h / R;
-      const int r = h - g * R;
-      double lo_h = 0.0, hi_h = 0.0;
-      for (int qi = 0; qi < Qt; ++qi) {
-        const int cg = (qb * R + r) * Qt + qi;
-        const float mv = screened ? __uint_as_float(cells[g * colstride + cg]) : 0.0f;
-        const float4 ci = colinfo[g * cols + cg];
-        const double e = (static_cast<double>(ci.x) * K + static_cast<double>(ci.y)) * (1.0 + 0x1p-50);
-        const double m = static_cast<double>(mv);
-        const double inv = 1.0 / static_cast<double>(ci.z);  // a power of two: exact
-        const double lo = fmax(0.0, m - e) * inv;
-        const double hi = (m + e) * inv;
-        lo_h = fmax(lo_h, lo);
-        hi_h = (hi > hi_h || isnan(hi)) ? hi : hi_h;
+    // (h, qi) in ascending order, the cells of 16 of them loaded ahead
+    constexpr int kAhead = 16;
+    double lo_sum = 0.0, hi_sum = 0.0, lo_h = 0.0, hi_h = 0.0;
+    for (int j0 = 0; j0 < HQ; j0 += kAhead) {
+      float mv[kAhead];
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j) {
+        const int hq = j0 + j;
+        mv[j] = 0.0f;
+        if (screened && hq < HQ) {
+          const int h = hq / Qt;
+          mv[j] = __uint_as_float(cells[(h / R) * colstride + (qb * R + h % R) * Qt + hq % Qt]);
+        }
       }
-      lo_sum += lo_h;
-      hi_sum += hi_h;
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j) {
+        const int hq = j0 + j;
+        if (hq < HQ) {
+          const float4 ci = s_ci[hq];
+          const double e = (static_cast<double>(ci.x) * K + static_cast<double>(ci.y)) * (1.0 + 0x1p-50);
+          const double m = static_cast<double>(mv[j]);
+          const double inv = static_cast<double>(ci.z);
+          const double lo = fmax(0.0, m - e) * inv;
+          const double hi = (m + e) * inv;
+          lo_h = fmax(lo_h, lo);
+          hi_h = (hi > hi_h || isnan(hi)) ? hi : hi_h;
+          if (hq % Qt == Qt - 1) {  // the head's last query token
+            lo_sum += lo_h;
+            hi_sum += hi_h;
+            lo_h = hi_h = 0.0;
+          }
+        }
+      }
     }
     const double lb = lo_sum / denom / static_cast<double>(H) * (1.0 - 0x1p-40);
     const double ub = hi_sum / denom / static_cast<double>(H) * (1.0 + 0x1p-40);
@@ -1340,7 +1366,7 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
   if (wave == 0) {
     WaveList B;
     block_merge<kFinWaves>(s_lists, k, B);
-    if (lane < k) block_out[(static_cast<size_t>(qb) * gridDim.x + blockIdx.x) * k + lane] = wl_entry(B);
+    if (lane < k) block_out[(static_cast<size_t>(qb) * nsblk + sblk) * k + lane] = wl_entry(B);
   }
 }
 

@@ -877,8 +877,8 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   // 3. score bounds, the k best lower bounds per block (with no key tokens
   // at all the column parameters are never used: every live node has no
   // tokens and scores 0)
-  grm::gqa::gqa_bounds_kernel<<<dim3(fin_blocks, qb), grm::gqa::kFinWaves * grm::kWave, 0,
-                                a->stream>>>(
+  grm::gqa::gqa_bounds_kernel<<<dim3(qb, fin_blocks), grm::gqa::kFinWaves * grm::kWave,
+                                static_cast<size_t>(H) * p.Qt * sizeof(float4), a->stream>>>(
       a->d_hmaxf, colstride, a->cap_nodes, H, p.Qt, p.R, cols, kv,
       static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags, a->d_ids, a->d_kmax,
       a->d_colinfo, a->d_qbad, fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub,
@@ -1117,6 +1117,9 @@ extern "C" int grm_gqa_hip_append(GqaDeviceArena* a, const void* keys_host,
   a->mut_pending = true;
   a->live += count;
   a->epoch += 1;
+  // the route work lists follow the host mirrors; rebuilding them here
+  // keeps the next route from paying for it
+  GRM_CHECK_RC(ensure_items(a));
   if (out_epoch) *out_epoch = a->epoch;
   grm::clear_error();
   return 0;
@@ -1167,6 +1170,7 @@ extern "C" int grm_gqa_hip_evict(GqaDeviceArena* a, const uint64_t* node_ids, ui
   }
   a->live -= count;
   a->epoch += 1;
+  GRM_CHECK_RC(ensure_items(a));  // as after an append
   if (out_epoch) *out_epoch = a->epoch;
   grm::clear_error();
   return 0;
@@ -1221,6 +1225,7 @@ extern "C" int grm_gqa_hip_compact(GqaDeviceArena* a) {
   GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
   a->used_tokens = dst;
   a->epoch += 1;
+  GRM_CHECK_RC(ensure_items(a));  // as after an append
   grm::clear_error();
   return 0;
 }
