@@ -291,3 +291,24 @@ def test_batched_config_parity(hip_lib):
     ids, sc, _ = oracle.mla_route(_f32(rows), _f32(qs), cfg["topk"])
     assert_same(res.ids, res.scores, ids, sc)
     assert stats["passes"] == 1 and stats["fallbacks"] <= 2
+
+
+def test_batched_copies_of_best_rows_far_apart(hip_lib):
+    # Exact copies of the best rows sit in different screen sub-streams
+    # (slots 50.. and 100,000..), so the merge sees tied candidates from
+    # two wavefronts; NaN and zero rows share tiles with the copies.
+    n, dim = 140_000, 288
+    rows = wl.mla_rows(n, dim, seed=65, dtype="bf16")
+    qs = wl.mla_queries(48, dim, seed=65, dtype="bf16")
+    rows[100_000:100_004] = qs[:4]          # near-perfect matches
+    rows[50:54] = qs[:4]                    # their copies, far from them
+    rows[1000] = qs[5]
+    rows[7] = oracle.bf16_bits(np.full(dim, np.nan, np.float32))
+    rows[8] = 0
+    node_ids = np.arange(n, dtype=np.uint64)[::-1].copy()
+    with MlaNodeBank(rows, node_ids, dtype="bf16") as bank:
+        res = bank.route(qs, 8)
+        stats = bank.route_stats()
+    ids, sc, _ = oracle.mla_route(_f32(rows), _f32(qs), 8, node_ids=node_ids)
+    assert_same(res.ids, res.scores, ids, sc)
+    assert stats["batched"] == 48
