@@ -13,6 +13,8 @@ ABI (kernel + top-k + device->host copy of the k results).  Reported:
 * gqa        the ragged GQA route (512 nodes, lengths U[16,512], 4 layers x 8
              kv heads x 128, bf16, 32 query heads, top-3): p50/p99 and its
              roofline (sum(L_i) * 32 * 128 * 2 bytes)
+* bank_bridge  arena-bridge refresh time at about 1% churn per epoch
+             (100k MLA nodes; 512 ragged GQA nodes) against a full rebuild
 * cpu_baseline  the oracle's fp64 route law on the same 1M bank, timed on
              this host's cores for a bounded number of queries
 
@@ -295,6 +297,86 @@ def bench_gqa_int8(steps: int, warmup: int):
     }
 
 
+def bench_bridge(epochs: int):
+    """Arena-bridge refresh cost: a bank that follows its arena's grafts
+    with evictions and appends, against the full rebuild (walk, stack,
+    create and upload) the reference runs on every signature change.
+    Every epoch retires, adds and replaces about 1% of the nodes."""
+    from graftrepository_amd import bank_bridge as bb
+    from graftrepository_amd import workloads as wl
+
+    def run(name, bridge, gs, make, walk, churn):
+        rng = np.random.default_rng(7)
+        nxt = 10_000_000
+        bridge.refresh(gs, 0)
+        bridge.bank.sync()
+        t_ref, t_walk, moved = [], [], []
+        for epoch in range(1, epochs + 1):
+            live = [g for g in gs if not g.get("retired")]
+            pick = rng.choice(len(live), size=2 * churn, replace=False)
+            for j in pick[:churn]:
+                live[int(j)]["retired"] = True
+            for j in pick[churn:]:
+                live[int(j)]["cent"] = make()
+            for _ in range(churn):
+                gs.append({"native_node_id": nxt, "cent": make()})
+                nxt += 1
+            t0 = time.perf_counter()
+            ev = bridge.refresh(gs, epoch)
+            bridge.bank.sync()
+            t_ref.append(time.perf_counter() - t0)
+            moved.append(ev.get("bytes_uploaded", 0))
+            t0 = time.perf_counter()
+            walk(gs)
+            t_walk.append(time.perf_counter() - t0)
+        # full rebuild at the final arena state
+        t_full = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fresh = type(bridge)(dtype=bridge.dtype)
+            fresh.refresh(gs, 0)
+            fresh.bank.sync()
+            t_full.append(time.perf_counter() - t0)
+            full_bytes = fresh.last_event["bytes_uploaded"]
+            fresh.close()
+        nodes = sum(1 for g in gs if not g.get("retired"))
+        r = {"nodes": nodes, "churn_per_epoch": f"{churn} retired + {churn} replaced + {churn} added",
+             "epochs": epochs,
+             "refresh_ms_p50": round(pct(t_ref, 50) * 1e3, 3),
+             # the walk alone in the reference's form (signature tuples):
+             # what the reference pays per epoch before any stacking
+             "reference_walk_ms_p50": round(pct(t_walk, 50) * 1e3, 3),
+             "bytes_uploaded_per_refresh": int(np.median(moved)),
+             "full_rebuild_ms_p50": round(pct(t_full, 50) * 1e3, 3),
+             "full_rebuild_bytes": int(full_bytes),
+             "rebuilds_during_epochs": bridge.totals["rebuilt"]}
+        log(f"[bridge {name}] refresh p50 {r['refresh_ms_p50']:.2f} ms (reference-form walk "
+            f"{r['reference_walk_ms_p50']:.2f}), full rebuild {r['full_rebuild_ms_p50']:.2f} ms, "
+            f"{r['bytes_uploaded_per_refresh'] / 1e6:.2f} MB vs {full_bytes / 1e6:.1f} MB uploaded")
+        bridge.close()
+        return r
+
+    rng = np.random.default_rng(3)
+    n, dim = 100_000, 288
+    rows = wl.mla_rows(n, dim, seed=11)
+    gs = [{"native_node_id": i, "cent": rows[i]} for i in range(n)]
+    mk = lambda: wl.normalise_rows(rng.standard_normal((1, dim), dtype=np.float32))[0]
+    mla = run("mla", bb.MlaRouteBankBridge(), gs, mk, bb.mla_bank_walk, n // 100 // 3)
+
+    cfg = wl.GQA_RAGGED
+    kv, hd = cfg["kv_heads"], cfg["head_dim"]
+    lens = wl.gqa_lengths(cfg["nodes"], cfg["seed"], lo=cfg["lo"], hi=cfg["hi"])
+    gs = [{"native_node_id": i,
+           "cent": rng.standard_normal((kv, int(L), hd), dtype=np.float32)}
+          for i, L in enumerate(lens)]
+    mkg = lambda: rng.standard_normal((kv, int(rng.integers(cfg["lo"], cfg["hi"] + 1)), hd),
+                                      dtype=np.float32)
+    gqa = run("gqa", bb.GqaRouteBankBridge(), gs, mkg, bb.gqa_bank_walk, 2)
+    return {"mla": dict(mla, dim=dim, bank_dtype="f32"),
+            "gqa": dict(gqa, kv_heads=kv, head_dim=hd, lengths="U[16,512]",
+                        bank_dtype="f32")}
+
+
 def cpu_baseline_mla(m, seconds: float):
     """Oracle fp64 route on the host cores, bounded to about `seconds`."""
     import oracle
@@ -327,7 +409,9 @@ def main() -> int:
     ap.add_argument("--gqa-steps", type=int, default=300)
     ap.add_argument("--batched-steps", type=int, default=100)
     ap.add_argument("--int8-steps", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "mla", "gqa", "batched", "int8"], default="all")
+    ap.add_argument("--bridge-epochs", type=int, default=10)
+    ap.add_argument("--only", choices=["all", "mla", "gqa", "batched", "int8", "bridge"],
+                    default="all")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -359,6 +443,9 @@ def main() -> int:
     if args.only in ("all", "batched"):
         b = bench_mla_batched(args.batched_steps, min(args.warmup, 5),
                               0 if args.skip_cpu else 4)
+    br = None
+    if args.only in ("all", "bridge"):
+        br = bench_bridge(args.bridge_epochs)
     cpu = None
     if m is not None and not args.skip_cpu:
         cpu = cpu_baseline_mla(m, args.cpu_seconds)
@@ -436,6 +523,16 @@ def main() -> int:
                    "steps": args.int8_steps, "warmup": 2, "ms_per_step": i8["p50_ms"],
                    "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
                    "dtype": "f64", "data": "synthetic", "config": i8}
+    if br is not None:
+        if out:
+            out["bank_bridge"] = br
+        else:
+            out = {"metric": "arena-bridge refresh p50 (ms) at 1% churn, 100k MLA nodes",
+                   "value": br["mla"]["refresh_ms_p50"], "unit": "ms", "n_gpus": 1,
+                   "steps": args.bridge_epochs, "warmup": 0,
+                   "ms_per_step": br["mla"]["refresh_ms_p50"], "higher_is_better": False,
+                   "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+                   "data": "synthetic", "config": {"workload": "bank_bridge", **br}}
     if cpu is not None:
         out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)

@@ -1,0 +1,487 @@
+"""Arena bridge: epoch-gated device route banks that follow an arena's
+grafts with evictions and appends.
+
+The reference keeps its CUDA route bank in step with the arena like this.
+
+* The arena bumps an epoch on every mutation (core/graft_arena.py:278-291,
+  2922-2931).
+* While the epoch holds, the cached bank is reused with no walk at all.
+* When the epoch moves, a walk over the grafts builds the eligible rows and
+  their signature: one ``(node_id, shape, dtype, id(cent))`` entry per row
+  (MLA core/graft_arena.py:1124-1162, GQA :2933-2977).
+* If the signature is unchanged, the bank stays.
+* Otherwise the whole bank is stacked again and uploaded as a new sidecar
+  bank (:1164-1198, :3055-3160, :1247-1280, :3161-3203; store attach
+  core/grm_native.py:1498-1673), and any route-key mutation on the store
+  drops the bank (:1391-1444).
+
+The bridges here keep the epoch gate, the walk, the signature law and the
+reverse maps.  On a signature change they keep the one device bank
+(``MlaNodeBank`` / ``GqaNodeBank``) and move it to the new row set:
+
+* evict the resident node ids that left, or whose signature entry changed;
+* append the rows that are new or changed;
+* when an append needs more room: a GQA bank first compacts its token
+  arena, and otherwise the bank is rebuilt once with twice the capacity.
+
+Each refresh records an event in the reference's vocabulary
+(``reused``, ``signature_reused``, ``ineligible``, ...) plus the rows moved
+and the bytes uploaded.
+
+A route result depends only on the set of (node id, row) pairs, not on the
+slots that hold them: ties go to the lower node id.  So a bank updated this
+way answers exactly as a bank built from scratch over the same rows.
+"""
+
+from __future__ import annotations
+
+import time
+from typing import NamedTuple
+
+import numpy as np
+
+from .node_bank import GqaNodeBank, MlaNodeBank
+
+MAX_TOPK = 16  # reference ABI cap (scripts/grm_mla_cuda_probe.py:355-358)
+
+
+class RowSet(NamedTuple):
+    """What a walk found, in arrays: row i is node ``node_ids[i]``.  Its
+    centroid object has ``cent_ids[i] = id(cent)``, and its extent is
+    ``extents[i]`` (the dim for MLA, the token count for GQA).  These are
+    the parts of the reference's signature entry
+    ``(node_id, shape, dtype, id(cent))`` that can change.  The dtype after
+    the walk's conversion is always float32, and the other dims are uniform
+    or the walk declines."""
+    node_ids: np.ndarray
+    cent_ids: np.ndarray
+    extents: np.ndarray
+
+    def same(self, other) -> bool:
+        return (other is not None and np.array_equal(self.node_ids, other.node_ids)
+                and np.array_equal(self.cent_ids, other.cent_ids)
+                and np.array_equal(self.extents, other.extents))
+
+
+def _walk_mla(grafts):
+    """The MLA walk (core/graft_arena.py:1124-1162): rows are the grafts
+    that are neither retired nor recall entries (:1139-1140).  Returns
+    ``(RowSet, rows, graft_indices, cents)`` or None."""
+    rows, nids, cids, gidx = [], [], [], []
+    add_row, add_nid, add_cid, add_g = rows.append, nids.append, cids.append, gidx.append
+    dim = None
+    f32 = np.dtype(np.float32)
+    ndarray = np.ndarray
+    for i, g in enumerate(grafts):
+        get = g.get
+        if get("retired") or get("kind", "turn") == "recall":
+            continue
+        if get("child_cents"):
+            return None
+        node_id = get("native_node_id")
+        cent = get("cent")
+        if node_id is None or (cent is None and "cent" not in g):
+            return None
+        if type(cent) is ndarray and cent.dtype == f32 and cent.ndim == 1:
+            key = cent
+        else:
+            key = np.asarray(cent, dtype=np.float32).reshape(-1)
+        n = key.shape[0]
+        if n != dim:
+            if dim is not None:
+                return None
+            dim = n
+        add_row(key)
+        add_nid(node_id if type(node_id) is int else int(node_id))
+        add_cid(id(cent))
+        add_g(i)
+    if not rows:
+        return None
+    rs = RowSet(np.asarray(nids, dtype=np.uint64), np.asarray(cids, dtype=np.int64),
+                np.full(len(rows), dim, dtype=np.int64))
+    cents = [g["cent"] for g in (grafts[i] for i in gidx)]
+    return rs, rows, gidx, cents
+
+
+def _walk_gqa(grafts):
+    """The GQA walk (core/graft_arena.py:2933-2977): keys are
+    ``[kv_heads, tokens, head_dim]``, may differ only in their token
+    extent, and must be finite.  Returns ``(RowSet, rows, graft_indices,
+    cents)`` or None."""
+    rows, nids, cids, lens, gidx, cents = [], [], [], [], [], []
+    geometry = None
+    for i, g in enumerate(grafts):
+        if g.get("retired") or g.get("kind", "turn") == "recall":
+            continue
+        node_id = g.get("native_node_id")
+        if node_id is None or g.get("child_cents") or "cent" not in g:
+            return None
+        cent = g["cent"]
+        key = np.asarray(cent, dtype=np.float32)
+        if key.ndim != 3 or any(int(d) <= 0 for d in key.shape):
+            return None
+        if not np.isfinite(key).all():
+            return None
+        geo = (int(key.shape[0]), int(key.shape[2]))
+        if geometry is None:
+            geometry = geo
+        elif geo != geometry:
+            return None
+        rows.append(key)
+        nids.append(int(node_id))
+        cids.append(id(cent))
+        lens.append(int(key.shape[1]))
+        gidx.append(i)
+        cents.append(cent)
+    if not rows:
+        return None
+    rs = RowSet(np.asarray(nids, dtype=np.uint64), np.asarray(cids, dtype=np.int64),
+                np.asarray(lens, dtype=np.int64))
+    return rs, rows, gidx, cents
+
+
+def _reference_form(walk, shape_of):
+    if walk is None:
+        return None
+    rs, rows, _, _ = walk
+    sig = tuple((int(n), shape_of(r), r.dtype.str, int(c))
+                for n, r, c in zip(rs.node_ids, rows, rs.cent_ids))
+    return rs.node_ids, sig, rows
+
+
+def mla_bank_walk(grafts):
+    """Eligible MLA rows in the reference's form ``(node_ids uint64[N],
+    signature, rows)``, signature entries ``(node_id, dim, dtype,
+    id(cent))`` (core/graft_arena.py:1124-1162).  None when the arena has
+    no attachable bank: a multi-row entry, a missing native id or centroid,
+    mixed dims, or no rows."""
+    return _reference_form(_walk_mla(grafts), lambda r: int(r.shape[0]))
+
+
+def gqa_bank_walk(grafts):
+    """Eligible GQA rows in the reference's form, signature entries
+    ``(node_id, shape, dtype, id(cent))`` (core/graft_arena.py:2933-2977),
+    or None."""
+    return _reference_form(_walk_gqa(grafts), lambda r: tuple(int(d) for d in r.shape))
+
+
+def plan_delta(old, new):
+    """Evictions and appends that take the resident rows ``old`` (a RowSet,
+    or None for an empty bank) to the rows ``new``.
+
+    Returns ``(evict_ids uint64[], append_positions int64[])``.  Evicted
+    are the resident node ids that left, or whose centroid object or
+    extent changed.  Appended are the positions in ``new`` of rows that are
+    new or changed, in row order.  Raises ValueError on a repeated node id
+    in ``new``.
+    """
+    nn = new.node_ids
+    if np.unique(nn).size != nn.size:
+        raise ValueError("a node id appears twice")
+    if old is None or old.node_ids.size == 0:
+        return np.empty(0, dtype=np.uint64), np.arange(nn.size, dtype=np.int64)
+    on = old.node_ids
+    common, io, inew = np.intersect1d(on, nn, assume_unique=True, return_indices=True)
+    changed = ((old.cent_ids[io] != new.cent_ids[inew])
+               | (old.extents[io] != new.extents[inew]))
+    gone = on[~np.isin(on, nn, assume_unique=True)]
+    evict = np.concatenate([gone, common[changed]]).astype(np.uint64)
+    add = ~np.isin(nn, on, assume_unique=True)
+    add[inew[changed]] = True
+    return evict, np.flatnonzero(add).astype(np.int64)
+
+
+class _Bridge:
+    """Shared epoch gate, walk, delta and exclude-aware route order."""
+
+    _full_walk = None
+
+    def __init__(self, *, dtype: str = "f32", headroom: float = 1.25):
+        if headroom < 1.0:
+            raise ValueError("headroom must be >= 1")
+        self.dtype = dtype
+        self.headroom = float(headroom)
+        self.bank = None
+        self._epoch = None
+        self._eligible_bank = False
+        self._resident = None          # RowSet on the device
+        self._pinned: list = []
+        self._sorted_nid = np.empty(0, dtype=np.uint64)
+        self._sorted_gidx = np.empty(0, dtype=np.int64)
+        self._in_bank = np.zeros(0, dtype=bool)
+        self.last_event: dict = {}
+        self.totals = {"appended": 0, "evicted": 0, "rebuilt": 0,
+                       "bytes_uploaded": 0}
+
+    # --------------------------------------------------------- lifecycle
+    def close(self) -> None:
+        if self.bank is not None:
+            self.bank.close()
+            self.bank = None
+        self._resident = None
+        self._pinned = []
+        self._epoch = None
+        self._eligible_bank = False
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def bank_size(self) -> int:
+        if not self._eligible_bank or self._resident is None:
+            return 0
+        return int(self._resident.node_ids.size)
+
+    def refresh(self, grafts, epoch: int) -> dict:
+        """Bring the device bank in step with ``grafts`` at ``epoch``.
+
+        Epoch unchanged: O(1), nothing walked (``reused`` /
+        ``ineligible_reused``).  Otherwise the walk runs; unchanged rows
+        keep the bank (``signature_reused``); changed ones are applied as
+        evictions and appends (``updated``; ``rebuilt`` when the bank had
+        to grow), or as a first upload (``created``).  Returns the event
+        (also ``last_event``).
+        """
+        t0 = time.perf_counter()
+        if self._epoch is not None and epoch == self._epoch:
+            self.last_event = {
+                "status": "reused" if self._eligible_bank else "ineligible_reused",
+                "epoch": int(epoch), "signature_walk": False}
+            return self.last_event
+        walk = type(self)._full_walk(grafts)
+        self._epoch = epoch
+        if walk is None:
+            # The device bank stays allocated: a later epoch may make the
+            # arena eligible again, and the delta then starts from it.
+            self._eligible_bank = False
+            self.last_event = {"status": "ineligible", "epoch": int(epoch),
+                               "signature_walk": True}
+            return self.last_event
+        rs, rows, gidx, cents = walk
+        # Reverse map, native node id -> graft index: row i is the i-th
+        # eligible graft (core/graft_arena.py:1200-1245, 3205-3262).  A
+        # repeated id fails closed.
+        order = np.argsort(rs.node_ids, kind="stable")
+        snid = rs.node_ids[order]
+        if snid.size > 1 and np.any(snid[1:] == snid[:-1]):
+            self._eligible_bank = False
+            self.last_event = {"status": "ineligible", "epoch": int(epoch),
+                               "signature_walk": True,
+                               "reason": "duplicate native id"}
+            return self.last_event
+        g = np.asarray(gidx, dtype=np.int64)
+        self._sorted_nid, self._sorted_gidx = snid, g[order]
+        self._in_bank = np.zeros(len(grafts), dtype=bool)
+        self._in_bank[g] = True
+        if self.bank is not None and rs.same(self._resident):
+            self._eligible_bank = True
+            self._pinned = cents
+            self.last_event = {"status": "signature_reused", "epoch": int(epoch),
+                               "signature_walk": True,
+                               "node_count": int(rs.node_ids.size)}
+            return self.last_event
+        if self.bank is None:
+            moved = self._create(rs.node_ids, rows)
+            status, evicted, appended = "created", 0, int(rs.node_ids.size)
+        else:
+            evict_ids, append_pos = plan_delta(self._resident, rs)
+            moved, rebuilt = self._apply(evict_ids, append_pos, rs.node_ids, rows)
+            status = "rebuilt" if rebuilt else "updated"
+            evicted, appended = int(evict_ids.size), int(append_pos.size)
+            if rebuilt:
+                self.totals["rebuilt"] += 1
+        self._resident = rs
+        # The row set holds id(cent); keeping the resident centroid objects
+        # alive means no later object can take one of those ids while its
+        # row is on the device (a recycled id would read as "unchanged").
+        self._pinned = cents
+        self._eligible_bank = True
+        self.totals["appended"] += appended
+        self.totals["evicted"] += evicted
+        self.totals["bytes_uploaded"] += moved
+        self.last_event = {
+            "status": status, "epoch": int(epoch), "signature_walk": True,
+            "node_count": int(rs.node_ids.size), "appended": appended,
+            "evicted": evicted, "bytes_uploaded": int(moved),
+            "seconds": time.perf_counter() - t0}
+        return self.last_event
+
+    # ------------------------------------------------------------- route
+    def _route_ids(self, query, topk: int):
+        raise NotImplementedError
+
+    def _graft_index(self, nid) -> int | None:
+        i = int(np.searchsorted(self._sorted_nid, np.uint64(nid)))
+        if i < self._sorted_nid.size and int(self._sorted_nid[i]) == int(nid):
+            return int(self._sorted_gidx[i])
+        return None
+
+    def route_order(self, query, limit: int, exclude=(), cand_count=None):
+        """Graft indices of the best ``limit`` rows, excluded indices
+        dropped.  Follows core/graft_arena.py:1282-1364:
+
+        * ask the bank for ``min(16, bank_size, want + excludes in bank)``;
+        * map node ids back through the reverse map and drop excluded
+          indices;
+        * if the ask would be cut below ``want``, or too few rows survive,
+          return None, which sends the caller to its CPU path.
+
+        ``cand_count``, when given, must equal the bank size minus the
+        excludes in the bank, else None (the reference's fail-closed
+        candidate check).
+        """
+        if limit is None or not self._eligible_bank or self.bank is None:
+            return None
+        size = self.bank_size
+        exclude_set = set(exclude) if exclude else None
+        n_g = self._in_bank.size
+        in_bank = (sum(1 for i in exclude_set if 0 <= i < n_g and self._in_bank[i])
+                   if exclude_set else 0)
+        if cand_count is not None and int(cand_count) != size - in_bank:
+            return None
+        want = min(max(0, int(limit)), size - in_bank)
+        if want <= 0:
+            return []
+        topk = min(MAX_TOPK, size, want + in_bank)
+        if topk < want:
+            return None
+        out = []
+        for nid in self._route_ids(query, topk):
+            if nid == np.iinfo(np.uint64).max:
+                continue
+            gi = self._graft_index(nid)
+            if gi is None or (exclude_set is not None and gi in exclude_set):
+                continue
+            out.append(gi)
+            if len(out) >= want:
+                break
+        return out if len(out) >= want else None
+
+
+class MlaRouteBankBridge(_Bridge):
+    """MLA arena bridge (one flat centroid per node)."""
+
+    _full_walk = staticmethod(_walk_mla)
+
+    def _create(self, node_ids, rows):
+        stacked = np.ascontiguousarray(np.stack(rows), dtype=np.float32)
+        cap = int(np.ceil(stacked.shape[0] * self.headroom))
+        self.bank = MlaNodeBank(stacked, node_ids, dtype=self.dtype,
+                                capacity=cap)
+        return self._bytes(stacked.shape[0], stacked.shape[1])
+
+    def _bytes(self, n, dim):
+        return int(n) * int(dim) * (4 if self.dtype == "f32" else 2)
+
+    def _apply(self, evict_ids, append_pos, node_ids, rows):
+        bank = self.bank
+        dim = bank.dim
+        if any(rows[p].shape[0] != dim for p in append_pos):
+            # A new dim cannot share the bank: rebuild over the new rows.
+            self.bank.close()
+            self.bank = None
+            return self._create(node_ids, rows), True
+        info = bank.info()
+        room = info["capacity"] - (info["live"] - len(evict_ids))
+        if len(append_pos) > room:
+            self.bank.close()
+            self.bank = None
+            stacked = np.ascontiguousarray(np.stack(rows), dtype=np.float32)
+            cap = max(int(np.ceil(stacked.shape[0] * self.headroom)),
+                      2 * int(info["capacity"]))
+            self.bank = MlaNodeBank(stacked, node_ids, dtype=self.dtype,
+                                    capacity=cap)
+            return self._bytes(stacked.shape[0], dim), True
+        if evict_ids.size:
+            bank.evict(evict_ids)
+        if append_pos.size:
+            add = np.ascontiguousarray(np.stack([rows[p] for p in append_pos]),
+                                       dtype=np.float32)
+            bank.append(add, node_ids[append_pos])
+        return self._bytes(append_pos.size, dim), False
+
+    def _route_ids(self, query, topk):
+        q = np.ascontiguousarray(query, dtype=np.float32).reshape(1, -1)
+        return self.bank.route(q, topk).ids[0]
+
+
+class GqaRouteBankBridge(_Bridge):
+    """GQA arena bridge (ragged ``[kv_heads, tokens, head_dim]`` keys)."""
+
+    _full_walk = staticmethod(_walk_gqa)
+    _TOK_ALIGN = 8  # the bank pads each node block to a multiple of 8 rows
+
+    def _padded(self, rows):
+        a = self._TOK_ALIGN
+        return sum((int(r.shape[1]) + a - 1) // a * a for r in rows)
+
+    def _flat(self, rows):
+        return np.concatenate([np.ascontiguousarray(r, dtype=np.float32).reshape(-1)
+                               for r in rows])
+
+    def _elem(self):
+        return 4 if self.dtype == "f32" else 2
+
+    def _create(self, node_ids, rows, min_nodes=0, min_tokens=0):
+        kv, _, hd = rows[0].shape
+        counts = np.asarray([r.shape[1] for r in rows], dtype=np.uint64)
+        offs = np.zeros(len(rows) + 1, dtype=np.uint64)
+        offs[1:] = np.cumsum(counts)
+        cap_nodes = max(int(np.ceil(len(rows) * self.headroom)), int(min_nodes))
+        cap_tokens = max(int(np.ceil(self._padded(rows) * self.headroom)),
+                         int(min_tokens))
+        self.bank = GqaNodeBank(self._flat(rows), offs, kv_heads=int(kv),
+                                head_dim=int(hd), node_ids=node_ids,
+                                dtype=self.dtype, capacity_nodes=cap_nodes,
+                                capacity_tokens=cap_tokens)
+        return int(offs[-1]) * int(kv) * int(hd) * self._elem()
+
+    def _apply(self, evict_ids, append_pos, node_ids, rows):
+        bank = self.bank
+        kv, _, hd = rows[0].shape
+        if (kv, hd) != (bank.kv_heads, bank.head_dim):
+            self.bank.close()
+            self.bank = None
+            return self._create(node_ids, rows), True
+        if evict_ids.size:
+            bank.evict(evict_ids)
+        add = [rows[p] for p in append_pos]
+        need_tok = self._padded(add)
+        info = bank.info()
+        node_room = info["capacity_nodes"] - info["live"]
+        if need_tok > info["capacity_tokens"] - info["tokens_in_use"]:
+            bank.compact()
+            info = bank.info()
+        if (len(add) > node_room
+                or need_tok > info["capacity_tokens"] - info["tokens_in_use"]):
+            old = info
+            self.bank.close()
+            self.bank = None
+            moved = self._create(node_ids, rows,
+                                 min_nodes=2 * int(old["capacity_nodes"]),
+                                 min_tokens=2 * int(old["capacity_tokens"]))
+            return moved, True
+        if add:
+            counts = np.asarray([r.shape[1] for r in add], dtype=np.uint64)
+            bank.append(self._flat(add), counts, node_ids[append_pos])
+            return int(counts.sum()) * int(kv) * int(hd) * self._elem(), False
+        return 0, False
+
+    def _route_ids(self, query, topk):
+        q = np.ascontiguousarray(query, dtype=np.float32)
+        if q.ndim == 3:
+            q = q[None]
+        return self.bank.route(q, topk, query_dtype="f32").ids[0]
+
+
+__all__ = ["MlaRouteBankBridge", "GqaRouteBankBridge", "RowSet", "mla_bank_walk",
+           "gqa_bank_walk", "plan_delta"]

@@ -1,0 +1,194 @@
+"""Arena bridge logic on the CPU: walk laws, deltas, the epoch gate and the
+exclude-aware route order.
+
+The walks follow core/graft_arena.py:1124-1162 (MLA) and :2933-2977 (GQA).
+The route order follows :1282-1364.  The bank behind the bridge here is an
+in-memory row store routed by the oracle, so every case runs without a GPU.
+The GPU file drives the same bridge over real device banks.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from graftrepository_amd import bank_bridge as bb
+
+NO_ID = np.iinfo(np.uint64).max
+
+
+class _RowStore:
+    """Stands in for a device bank: node id -> row."""
+
+    def __init__(self, node_ids, rows):
+        self.rows = {int(n): np.asarray(r, np.float32) for n, r in zip(node_ids, rows)}
+        self.ops = [("create", len(self.rows))]
+
+    def close(self):
+        self.rows = {}
+
+
+class CpuMlaBridge(bb._Bridge):
+    _full_walk = staticmethod(bb._walk_mla)
+
+    def _create(self, node_ids, rows):
+        self.bank = _RowStore(node_ids, rows)
+        return len(rows)
+
+    def _apply(self, evict_ids, append_pos, node_ids, rows):
+        for nid in evict_ids:
+            del self.bank.rows[int(nid)]
+        for p in append_pos:
+            nid = int(node_ids[p])
+            assert nid not in self.bank.rows, "append of a live id"
+            self.bank.rows[nid] = np.asarray(rows[p], np.float32)
+        self.bank.ops.append(("delta", len(evict_ids), len(append_pos)))
+        return len(append_pos), False
+
+    def _route_ids(self, query, topk):
+        ids = np.asarray(sorted(self.bank.rows), dtype=np.uint64)
+        rows = np.stack([self.bank.rows[int(i)] for i in ids])
+        got, _, _ = oracle.mla_route(rows, np.asarray(query, np.float32)[None],
+                                     topk, node_ids=ids)
+        return got[0]
+
+
+def graft(nid, cent, **kw):
+    g = {"native_node_id": nid, "cent": cent}
+    g.update(kw)
+    return g
+
+
+def test_mla_walk_law():
+    rng = np.random.default_rng(1)
+    c = [rng.standard_normal(8).astype(np.float32) for _ in range(4)]
+    gs = [graft(10, c[0]), graft(11, c[1], retired=True),
+          graft(12, c[2], kind="recall"), graft(13, c[3])]
+    ids, sig, rows = bb.mla_bank_walk(gs)
+    assert ids.tolist() == [10, 13]
+    assert sig == ((10, 8, "<f4", id(c[0])), (13, 8, "<f4", id(c[3])))
+    assert np.array_equal(rows[1], c[3])
+    # Each of these declines the whole bank (fail closed to the CPU path).
+    assert bb.mla_bank_walk(gs + [graft(14, c[0], child_cents=[c[1]])]) is None
+    assert bb.mla_bank_walk(gs + [{"cent": c[0]}]) is None
+    assert bb.mla_bank_walk(gs + [{"native_node_id": 15}]) is None
+    assert bb.mla_bank_walk(gs + [graft(16, np.zeros(9, np.float32))]) is None
+    assert bb.mla_bank_walk([graft(1, c[0], retired=True)]) is None
+    # A retired multi-row entry is skipped before the hierarchy check.
+    assert bb.mla_bank_walk(gs + [graft(17, c[0], child_cents=[1], retired=True)]) is not None
+
+
+def test_gqa_walk_law():
+    rng = np.random.default_rng(2)
+    k1 = rng.standard_normal((2, 5, 4)).astype(np.float32)
+    k2 = rng.standard_normal((2, 9, 4)).astype(np.float32)
+    ids, sig, rows = bb.gqa_bank_walk([graft(1, k1), graft(2, k2)])
+    assert ids.tolist() == [1, 2] and sig[1] == (2, (2, 9, 4), "<f4", id(k2))
+    bad = k2.copy()
+    bad[0, 3, 1] = np.inf
+    assert bb.gqa_bank_walk([graft(1, k1), graft(2, bad)]) is None
+    assert bb.gqa_bank_walk([graft(1, k1), graft(2, np.zeros((3, 5, 4)))]) is None
+    assert bb.gqa_bank_walk([graft(1, k1), graft(2, np.zeros((2, 5, 8)))]) is None
+    assert bb.gqa_bank_walk([graft(1, k1), graft(2, np.zeros((2, 0, 4)))]) is None
+    assert bb.gqa_bank_walk([graft(1, k1.reshape(-1))]) is None
+
+
+def rowset(nids, cids, ext):
+    return bb.RowSet(np.asarray(nids, np.uint64), np.asarray(cids, np.int64),
+                     np.asarray(ext, np.int64))
+
+
+def test_plan_delta():
+    old = rowset([1, 2, 3], [101, 102, 103], [8, 8, 8])
+    ev, ap = bb.plan_delta(old, rowset([1, 3, 4], [101, 203, 104], [8, 8, 8]))
+    assert sorted(ev.tolist()) == [2, 3] and ap.tolist() == [1, 2]
+    ev, ap = bb.plan_delta(old, rowset([3, 2, 1], [103, 102, 101], [8, 8, 8]))
+    assert ev.size == 0 and ap.size == 0
+    ev, ap = bb.plan_delta(old, rowset([1, 2, 3], [101, 102, 103], [8, 9, 8]))
+    assert ev.tolist() == [2] and ap.tolist() == [1]       # extent changed
+    ev, ap = bb.plan_delta(None, rowset([7, 8], [1, 2], [4, 4]))
+    assert ev.size == 0 and ap.tolist() == [0, 1]
+    with pytest.raises(ValueError):
+        bb.plan_delta(None, rowset([7, 7], [1, 2], [4, 4]))
+
+
+class NoWalk(list):
+    def __iter__(self):
+        raise AssertionError("walked the grafts under an unchanged epoch")
+
+
+def test_epoch_gate_and_events():
+    rng = np.random.default_rng(3)
+    gs = [graft(100 + i, rng.standard_normal(6).astype(np.float32)) for i in range(20)]
+    br = CpuMlaBridge()
+    ev = br.refresh(gs, 1)
+    assert ev["status"] == "created" and ev["node_count"] == 20
+    assert br.refresh(NoWalk(gs), 1)["status"] == "reused"
+    gs[4]["note"] = "metadata only"
+    assert br.refresh(gs, 2)["status"] == "signature_reused"
+    gs[5]["retired"] = True
+    gs.append(graft(500, rng.standard_normal(6).astype(np.float32)))
+    gs[7]["cent"] = rng.standard_normal(6).astype(np.float32)
+    ev = br.refresh(gs, 3)
+    assert ev["status"] == "updated" and ev["evicted"] == 2 and ev["appended"] == 2
+    gs.append(graft(600, gs[0]["cent"], child_cents=[gs[1]["cent"]]))
+    assert br.refresh(gs, 4)["status"] == "ineligible"
+    assert br.refresh(NoWalk(gs), 4)["status"] == "ineligible_reused"
+    assert br.route_order(gs[0]["cent"], 3) is None
+    gs.pop()
+    ev = br.refresh(gs, 5)
+    assert ev["status"] == "signature_reused"
+    assert sorted(br.bank.rows) == sorted(int(g["native_node_id"]) for g in gs
+                                          if not g.get("retired"))
+
+
+def test_random_mutations_keep_the_rows_in_step():
+    rng = np.random.default_rng(4)
+    gs = [graft(i, rng.standard_normal(5).astype(np.float32)) for i in range(60)]
+    nxt = 60
+    br = CpuMlaBridge()
+    br.refresh(gs, 0)
+    for epoch in range(1, 80):
+        for _ in range(rng.integers(0, 6)):
+            op = rng.integers(0, 4)
+            live = [g for g in gs if not g.get("retired")]
+            if op == 0 and len(live) > 10:
+                live[rng.integers(len(live))]["retired"] = True
+            elif op == 1:
+                gs.append(graft(nxt, rng.standard_normal(5).astype(np.float32)))
+                nxt += 1
+            elif op == 2 and live:
+                live[rng.integers(len(live))]["cent"] = rng.standard_normal(5).astype(np.float32)
+            elif live:
+                live[rng.integers(len(live))]["kind"] = "turn"  # metadata only
+        br.refresh(gs, epoch)
+        want = {int(g["native_node_id"]): g["cent"] for g in gs if not g.get("retired")}
+        assert sorted(br.bank.rows) == sorted(want)
+        for nid, row in want.items():
+            assert np.array_equal(br.bank.rows[nid], row)
+    assert br.bank.ops[0] == ("create", 60) and len(br.bank.ops) > 1
+
+
+def test_route_order_with_excludes():
+    rng = np.random.default_rng(5)
+    gs = [graft(1000 - i, rng.standard_normal(12).astype(np.float32)) for i in range(40)]
+    gs[3]["retired"] = True
+    gs[9]["kind"] = "recall"
+    br = CpuMlaBridge()
+    br.refresh(gs, 1)
+    q = rng.standard_normal(12).astype(np.float32)
+    elig = [i for i, g in enumerate(gs) if not g.get("retired") and g.get("kind") != "recall"]
+    rows = np.stack([gs[i]["cent"] for i in elig])
+    ids = np.asarray([gs[i]["native_node_id"] for i in elig], np.uint64)
+    full, _, _ = oracle.mla_route(rows, q[None], 16, node_ids=ids)
+    by_id = {int(gs[i]["native_node_id"]): i for i in elig}
+    order = [by_id[int(n)] for n in full[0]]
+    assert br.route_order(q, 5) == order[:5]
+    excl = {order[0], order[2], 3, 9}            # two in the bank, two not
+    assert br.route_order(q, 5, exclude=excl) == [i for i in order if i not in excl][:5]
+    size = len(elig)
+    assert br.route_order(q, 5, exclude=excl, cand_count=size - 2) is not None
+    assert br.route_order(q, 5, exclude=excl, cand_count=size) is None
+    assert br.route_order(q, 0) == []
+    # 16 wanted with 2 excludes in the bank: the capped ask (16) holds the
+    # excluded rows, so too few survive and the caller falls back.
+    assert br.route_order(q, 16, exclude={order[0], order[1]}) is None
