@@ -13,6 +13,8 @@ ABI (kernel + top-k + device->host copy of the k results).  Reported:
 * gqa        the ragged GQA route (512 nodes, lengths U[16,512], 4 layers x 8
              kv heads x 128, bf16, 32 query heads, top-3): p50/p99 and its
              roofline (sum(L_i) * 32 * 128 * 2 bytes)
+* payload    packed graft payload unpack on the device: kernel roofline and
+             one node mount against host dequant + fp16 upload
 * bank_bridge  arena-bridge refresh time at about 1% churn per epoch
              (100k MLA nodes; 512 ragged GQA nodes) against a full rebuild
 * cpu_baseline  the oracle's fp64 route law on the same 1M bank, timed on
@@ -377,6 +379,93 @@ def bench_bridge(epochs: int):
                         bank_dtype="f32")}
 
 
+def bench_payload(reps: int):
+    """Packed graft payloads: the device unpack kernel against its HBM
+    roofline, and mounting one packed node payload (device unpack) against
+    the reference's route (host dequant, then the fp16 upload)."""
+    import ctypes
+
+    import oracle
+    from graftrepository_amd import _lib, payload as pl
+
+    lib = _lib.load()
+    gs = 32
+    # kernel: 1 Gi values, codes + scales + fp16 out = 3.125 B per value
+    n = 1 << 30
+    block = np.random.default_rng(1).integers(-128, 128, size=64 << 20, dtype=np.int8)
+    d_c, d_s, d_o = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    for ptr, nbytes in ((d_c, n), (d_s, n // gs * 4), (d_o, 2 * n)):
+        _lib.check(lib.grm_hip_device_alloc(nbytes, ctypes.byref(ptr)), "alloc")
+    try:
+        for off in range(0, n, block.size):
+            _lib.check(lib.grm_hip_copy_to_device(d_c.value + off, block.ctypes.data,
+                                                  block.size), "h2d")
+        sc = (np.random.default_rng(2).random(n // gs) * 0.05).astype(np.float32)
+        _lib.check(lib.grm_hip_copy_to_device(d_s.value, sc.ctypes.data, sc.nbytes), "h2d")
+        ms = ctypes.c_float()
+        times = []
+        for i in range(reps + 2):
+            _lib.check(lib.grm_hip_payload_dequant(d_c, d_s, n, gs, d_o, ctypes.byref(ms)),
+                       "dequant")
+            if i >= 2:
+                times.append(ms.value)
+    finally:
+        for ptr in (d_c, d_s, d_o):
+            lib.grm_hip_device_free(ptr)
+    bytes_per_launch = n * (1 + 4 / gs + 2)
+    kms = float(np.mean(times))
+    achieved = bytes_per_launch / (kms * 1e-3) / 1e9
+    log(f"[payload] unpack kernel {kms:.3f} ms for {n} values: {achieved:.0f} GB/s")
+
+    # mount of one packed node payload (L, H, S, D) = (28, 4, 512, 128), k and v
+    rng = np.random.default_rng(3)
+    shape = (28, 4, 512, 128)
+    arrays = {nm: (rng.standard_normal(shape) * 2).astype(np.float16) for nm in ("k", "v")}
+    z = {"format_version": np.asarray(1, np.int64), "storage_bits": np.asarray(8, np.int64),
+         "group_size": np.asarray(gs, np.int64)}
+    for nm, a in arrays.items():
+        c, s_ = oracle.quantize_symmetric(a, 8, gs)
+        z[f"{nm}_codes"], z[f"{nm}_scales"] = c, s_
+        z[f"{nm}_shape"] = np.asarray(a.shape, np.int64)
+    dev, host = [], []
+    for i in range(reps + 2):
+        t0 = time.perf_counter()
+        out = pl.unpack_node_device(z)
+        t1 = time.perf_counter()
+        for a in out.values():
+            a.close()
+        # the reference's route: numpy dequant (core/graft_quant.py:136-144),
+        # then the fp16 arrays uploaded
+        t2 = time.perf_counter()
+        ups = []
+        for nm in ("k", "v"):
+            h = (z[f"{nm}_codes"].astype(np.float32) * z[f"{nm}_scales"]).reshape(shape)
+            h = h.astype(np.float16)
+            d = pl.DeviceArray(shape)
+            _lib.check(lib.grm_hip_copy_to_device(d.ptr, h.ctypes.data, h.nbytes), "h2d")
+            ups.append(d)
+        t3 = time.perf_counter()
+        for d in ups:
+            d.close()
+        if i >= 2:
+            dev.append(t1 - t0)
+            host.append(t3 - t2)
+    vals = 2 * int(np.prod(shape))
+    r = {"unpack_kernel": {"values": n, "group_size": gs, "device_ms_mean": round(kms, 4),
+                           "bytes_per_launch": int(bytes_per_launch),
+                           "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
+                                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                        "frac": round(achieved / HBM_PEAK_GBS, 4)}},
+         "node_mount": {"shape_each": list(shape), "tensors": ["k", "v"], "storage_bits": 8,
+                        "device_unpack_ms_p50": round(pct(dev, 50) * 1e3, 3),
+                        "host_dequant_then_fp16_upload_ms_p50": round(pct(host, 50) * 1e3, 3),
+                        "bytes_crossing_pcie_packed": int(vals * (1 + 4 / gs)),
+                        "bytes_crossing_pcie_fp16": 2 * vals}}
+    log(f"[payload] node mount {r['node_mount']['device_unpack_ms_p50']:.2f} ms packed "
+        f"vs {r['node_mount']['host_dequant_then_fp16_upload_ms_p50']:.2f} ms host dequant + fp16")
+    return r
+
+
 def cpu_baseline_mla(m, seconds: float):
     """Oracle fp64 route on the host cores, bounded to about `seconds`."""
     import oracle
@@ -410,8 +499,9 @@ def main() -> int:
     ap.add_argument("--batched-steps", type=int, default=100)
     ap.add_argument("--int8-steps", type=int, default=20)
     ap.add_argument("--bridge-epochs", type=int, default=10)
-    ap.add_argument("--only", choices=["all", "mla", "gqa", "batched", "int8", "bridge"],
-                    default="all")
+    ap.add_argument("--payload-reps", type=int, default=10)
+    ap.add_argument("--only", choices=["all", "mla", "gqa", "batched", "int8", "bridge",
+                                       "payload"], default="all")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -446,6 +536,9 @@ def main() -> int:
     br = None
     if args.only in ("all", "bridge"):
         br = bench_bridge(args.bridge_epochs)
+    pay = None
+    if args.only in ("all", "payload"):
+        pay = bench_payload(args.payload_reps)
     cpu = None
     if m is not None and not args.skip_cpu:
         cpu = cpu_baseline_mla(m, args.cpu_seconds)
@@ -533,6 +626,17 @@ def main() -> int:
                    "ms_per_step": br["mla"]["refresh_ms_p50"], "higher_is_better": False,
                    "scaling": "weak", "vs_baseline": None, "dtype": "f32",
                    "data": "synthetic", "config": {"workload": "bank_bridge", **br}}
+    if pay is not None:
+        if out:
+            out["payload"] = pay
+        else:
+            out = {"metric": "packed payload unpack kernel GB/s (1 Gi values, group 32)",
+                   "value": pay["unpack_kernel"]["roofline"]["achieved"], "unit": "GB/s",
+                   "n_gpus": 1, "steps": args.payload_reps, "warmup": 2,
+                   "ms_per_step": pay["unpack_kernel"]["device_ms_mean"],
+                   "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                   "dtype": "int8->f16", "data": "synthetic",
+                   "config": {"workload": "payload_unpack", **pay}}
     if cpu is not None:
         out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)

@@ -76,6 +76,12 @@ SIGNATURES = {
     "grm_gqa_hip_compact": (i32, [vp]),
     "grm_gqa_hip_sync": (i32, [vp]),
     "grm_gqa_hip_bank_info": (i32, [vp, vp]),
+    "grm_hip_payload_dequant": (i32, [vp, vp, u64, ctypes.c_uint32, vp, vp]),
+    "grm_hip_payload_upload": (i32, [vp, vp, u64, ctypes.c_uint32, vp, vp]),
+    "grm_hip_device_alloc": (i32, [u64, ctypes.POINTER(vp)]),
+    "grm_hip_device_free": (i32, [vp]),
+    "grm_hip_copy_to_host": (i32, [vp, vp, u64]),
+    "grm_hip_copy_to_device": (i32, [vp, vp, u64]),
 }
 
 _libs: dict[str, ctypes.CDLL] = {}

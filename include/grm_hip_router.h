@@ -232,6 +232,34 @@ int grm_gqa_hip_sync(GqaDeviceArena* arena);
  * capacity, epoch, kv_heads, head_dim, key dtype].  No counterpart. */
 int grm_gqa_hip_bank_info(GqaDeviceArena* arena, uint64_t* out8);
 
+/* ---- Packed graft payloads (core/graft_quant.py:177-268) ----------------
+ * A packed tensor is int8 codes (values in row-major order, grouped along
+ * the last axis) and one fp32 scale per group of group_size values.  It
+ * unpacks as fp16(fp32(code) * scale) (core/graft_quant.py:136-144; any
+ * storage depth <= 8).  The reference dequantises on the host and uploads
+ * fp16 (unpack_node, core/graft_arena.py:3479-3492); these entry points
+ * take the packed form to the device and write the fp16 bit patterns there.
+ * n_values must be a multiple of group_size.  Both wait for completion;
+ * elapsed_ms (may be NULL) receives the device time. */
+
+/* Device codes and scales to device fp16.  No counterpart (the reference
+ * has no device unpack). */
+int grm_hip_payload_dequant(const void* d_codes, const void* d_scales, uint64_t n_values,
+                            uint32_t group_size, void* d_out_f16, float* elapsed_ms);
+
+/* Host codes and scales uploaded in chunks and unpacked to device fp16.
+ * Replaces the host dequant + fp16 upload of unpack_node
+ * (core/graft_arena.py:3479-3492). */
+int grm_hip_payload_upload(const void* h_codes, const void* h_scales, uint64_t n_values,
+                           uint32_t group_size, void* d_out_f16, float* elapsed_ms);
+
+/* Device memory for payload outputs (no counterpart; the reference's
+ * equivalents are the sidecars' upload_queries / free_device_ptr). */
+int grm_hip_device_alloc(uint64_t bytes, void** out_ptr);
+int grm_hip_device_free(void* ptr);
+int grm_hip_copy_to_host(void* host, const void* device, uint64_t bytes);
+int grm_hip_copy_to_device(void* device, const void* host, uint64_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -184,6 +184,38 @@ def dequantize_int8(codes: np.ndarray, scales: np.ndarray, group_size: int,
     return f16_to_f32(f16_bits(prod))
 
 
+def quantize_symmetric(x: np.ndarray, bits: int, group_size: int = 32):
+    """Packed-format quantiser, core/graft_quant.py:93-131, any depth 2..8.
+
+    ``qmax = 2^(bits-1) - 1``; per group of ``group_size`` values along
+    the last axis, ``scale = max|g| / qmax`` in fp32 (0 -> 1.0) and
+    ``codes = clip(round_half_even(g / scale), -qmax-1, qmax)`` as int8.
+    Returns ``codes (..., groups, group_size)`` and ``scales (..., groups,
+    1)`` fp32, the shapes pack_kv_arrays stores.
+    """
+    if not 2 <= bits <= 8:
+        raise ValueError("bits must be in 2..8")
+    xf = np.ascontiguousarray(x, dtype=np.float32)
+    d = xf.shape[-1]
+    if d % group_size:
+        raise ValueError("last axis not divisible by group_size")
+    g = xf.reshape(*xf.shape[:-1], d // group_size, group_size)
+    qmax = (1 << (bits - 1)) - 1
+    scale = np.abs(g).max(axis=-1, keepdims=True) / np.float32(qmax)
+    scale = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
+    codes = np.clip(np.round(g / scale), -qmax - 1, qmax).astype(np.int8)
+    return codes, scale
+
+
+def dequant_payload_bits(codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """Unpack law core/graft_quant.py:136-144 as fp16 bit patterns (uint16,
+    codes' shape): the fp32 product of each code and its group's scale,
+    rounded to fp16 (nearest even)."""
+    c = np.ascontiguousarray(codes, dtype=np.int8)
+    s = np.ascontiguousarray(scales, dtype=np.float32).reshape(*c.shape[:-1], 1)
+    return f16_bits(c.astype(np.float32) * s)
+
+
 # ------------------------------------------------------------------ MLA
 
 def mla_row_norms(rows: np.ndarray, threads: int = 0) -> np.ndarray:
