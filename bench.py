@@ -77,6 +77,40 @@ def load_traffic() -> dict:
         return {}
 
 
+def bench_latent_entry(bank, dim: int, k: int, steps: int) -> dict:
+    """Route key from a device-resident latent block (512 tokens x dim
+    fp16, what a forward pass leaves on the GPU), routed in one call,
+    against the host round trip the reference makes: copy the latent
+    back, form latent_centroid with numpy (core/kv_graft.py:131-142) and
+    route the host query."""
+    from graftrepository_amd.payload import DeviceArray
+
+    rng = np.random.default_rng(5)
+    lat = rng.standard_normal((512, dim)).astype(np.float16)
+    dev_ms, host_ms = [], []
+    with DeviceArray.from_host(lat) as d_lat:
+        for i in range(steps + 3):
+            t0 = time.perf_counter()
+            r1 = bank.route_latent(d_lat, 512, k, dtype="f16")
+            t1 = time.perf_counter()
+            back = d_lat.to_host()
+            c = back.astype(np.float32).mean(0)
+            key = c / (np.linalg.norm(c) + 1e-8)
+            r2 = bank.route(key[None], k)
+            t2 = time.perf_counter()
+            if i >= 3:
+                dev_ms.append((t1 - t0) * 1e3)
+                host_ms.append((t2 - t1) * 1e3)
+    same = bool(np.array_equal(r1.ids, r2.ids))
+    out = {"latent_tokens": 512, "latent_dtype": "f16",
+           "device_key_route_ms_p50": round(pct(dev_ms, 50), 4),
+           "host_round_trip_route_ms_p50": round(pct(host_ms, 50), 4),
+           "same_ids": same}
+    log(f"[mla latent] device key + route {out['device_key_route_ms_p50']:.3f} ms, "
+        f"host round trip {out['host_round_trip_route_ms_p50']:.3f} ms, same ids {same}")
+    return out
+
+
 def bench_mla(steps: int, warmup: int):
     from graftrepository_amd import MlaNodeBank, workloads as wl
     from graftrepository_amd.mla_probe import HipProbe
@@ -100,13 +134,14 @@ def bench_mla(steps: int, warmup: int):
     ids = r.ids[0].copy()
     scores = r.scores[0].copy()
     dq.close()
+    latent = bench_latent_entry(bank, d, k, max(20, steps // 10))
     bank.close()
     bytes_per_launch = n * d * 4 + n * 4
     mean_dev = float(np.mean(devs))
     achieved = bytes_per_launch / (mean_dev * 1e-3) / 1e9
     log(f"[mla] p50 {pct(walls, 50):.4f} ms  p99 {pct(walls, 99):.4f} ms  "
         f"kernel {mean_dev:.4f} ms  {achieved:.0f} GB/s")
-    return dict(rows=rows, q=q, ids=ids, scores=scores, walls=walls,
+    return dict(rows=rows, q=q, ids=ids, scores=scores, walls=walls, latent=latent,
                 devs=devs, bytes=bytes_per_launch, achieved=achieved,
                 mean_dev=mean_dev, cfg=cfg)
 
@@ -563,6 +598,7 @@ def main() -> int:
                        "queries_per_call": 1, "query_resident": "hbm"},
             "p99_ms": round(pct(m["walls"], 99), 5),
             "kernel_ms_mean": round(m["mean_dev"], 5),
+            "latent_entry": m["latent"],
             "roofline": {"bound": "hbm", "achieved": round(m["achieved"], 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(m["achieved"] / HBM_PEAK_GBS, 4),

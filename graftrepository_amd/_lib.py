@@ -67,6 +67,8 @@ SIGNATURES = {
     "grm_mla_hip_bank_info": (i32, [vp, vp]),
     "grm_mla_hip_route_stats": (i32, [vp, vp]),
     "grm_mla_hip_screen_ms": (i32, [vp, vp]),
+    "grm_mla_hip_latent_query": (i32, [vp, vp, i32, u64, u64, i32, vp]),
+    "grm_mla_hip_route_latent": (i32, [vp, vp, i32, u64, u64, i32, vp, vp, vp]),
     "grm_gqa_hip_bank_create": (i32, [vp, i32, vp, i32, i32, vp, u64, i32, i32,
                                       vp, u64, u64, ctypes.POINTER(vp)]),
     "grm_gqa_hip_route": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, i32, vp,

@@ -351,6 +351,7 @@ __global__ void mla_evict_kernel(const uint64_t* __restrict__ slots,
 
 using grm::Cand;
 using grm::kBF16;
+using grm::kF16;
 using grm::kF32;
 using grm::kNoId;
 using grm::mla::u32x4;
@@ -376,6 +377,7 @@ struct MlaDeviceArena {
   std::set<uint64_t> free_slots;  // freed slots below high_water
   void* d_queries = nullptr;
   size_t d_queries_bytes = 0;
+  float* d_latent_q = nullptr;  // route key formed from a device latent (dim floats)
   grm::MappedCands blocks_out;  // per-query, per-block top-k (host mapped)
   std::vector<Cand> merged;
   void* h_stage = nullptr;
@@ -424,6 +426,7 @@ void destroy_arena(MlaDeviceArena* a) {
   if (a->d_norms) (void)hipFree(a->d_norms);
   if (a->d_ids) (void)hipFree(a->d_ids);
   if (a->d_queries) (void)hipFree(a->d_queries);
+  if (a->d_latent_q) (void)hipFree(a->d_latent_q);
   if (a->d_stage) (void)hipFree(a->d_stage);
   if (a->d_min_norm) (void)hipFree(a->d_min_norm);
   if (a->d_qpad) (void)hipFree(a->d_qpad);
@@ -903,6 +906,131 @@ int stage_upload(MlaDeviceArena* a, size_t bytes, void** host, void** dev) {
   return 0;
 }
 
+// Route key of one latent block, core/kv_graft.py:131-142
+// (latent_centroid):
+//   c = latent.astype(float32).mean(0);  key = c / (||c|| + 1e-8).
+// The mean follows numpy's float32 reduce over axis 0 as mean() runs it
+// (with a where mask, so from the identity): the accumulator starts at
+// +0.0 (an all -0 column sums to +0), rows add in order, and one fp32
+// division by the token count follows.  The norm is taken in
+// fp64 and rounded to fp32.  The reference's comes from a BLAS dot in fp32
+// whose summation order depends on the host CPU, so the key agrees with it
+// to that dot's rounding (up to dim * 2^-24 of |c|^2), not bit for bit.
+// normalize = 0 writes the mean alone.
+//
+// Columns are split over blocks, kLatentCols per block.  A block stages
+// its strip of up to kLatentRows tokens in LDS at once (16-byte loads when
+// rows allow them), then thread c adds column c over those tokens in order.
+// The adds of a column stay one serial chain, as the law has them.  A
+// one-block kernel then takes the norm and scales the key.
+constexpr int kLatentThreads = 256;
+constexpr uint32_t kLatentCols = 32;
+constexpr uint32_t kLatentRows = 512;  // 64 KiB of fp32 strip per pass
+
+__global__ __launch_bounds__(kLatentThreads) void latent_mean_kernel(
+    const void* __restrict__ latent, int dtype, uint64_t tokens, uint32_t dim,
+    uint64_t row_stride, float* __restrict__ out) {
+  __shared__ float s_strip[kLatentRows * kLatentCols];  // [row][column]
+  const uint32_t c0 = blockIdx.x * kLatentCols;
+  const uint32_t width = min(kLatentCols, dim - c0);
+  const uint32_t esize = dtype == kF32 ? 4u : 2u;
+  const uint32_t epv = 16u / esize;  // values per 16-byte load
+  const bool vec = width % epv == 0 && row_stride % epv == 0 && c0 % epv == 0 &&
+                   reinterpret_cast<uintptr_t>(latent) % 16 == 0;
+  auto cvt = [&](uint16_t b) -> float {
+    return dtype == kBF16 ? grm::bf16_to_f32(b) : static_cast<float>(__builtin_bit_cast(_Float16, b));
+  };
+  float acc = 0.0f;  // column c0 + threadIdx.x (threads below width)
+  for (uint64_t t0 = 0; t0 < tokens; t0 += kLatentRows) {
+    const uint32_t rows = static_cast<uint32_t>(min<uint64_t>(kLatentRows, tokens - t0));
+    if (vec) {
+      const uint32_t per_row = width / epv;
+      const uint32_t nv = rows * per_row;
+      constexpr int kBatch = 8;
+      for (uint32_t base = 0; base < nv; base += kBatch * kLatentThreads) {
+        u32x4 v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const uint32_t i = base + k * kLatentThreads + threadIdx.x;
+          const uint64_t e = (t0 + i / per_row) * row_stride + c0 + (i % per_row) * epv;
+          v[k] = i < nv ? *reinterpret_cast<const u32x4*>(
+                              static_cast<const unsigned char*>(latent) + e * esize)
+                        : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const uint32_t i = base + k * kLatentThreads + threadIdx.x;
+          if (i >= nv) continue;
+          float* dst = s_strip + (i / per_row) * kLatentCols + (i % per_row) * epv;
+          if (dtype == kF32) {
+            dst[0] = __uint_as_float(v[k].x);
+            dst[1] = __uint_as_float(v[k].y);
+            dst[2] = __uint_as_float(v[k].z);
+            dst[3] = __uint_as_float(v[k].w);
+          } else {
+            const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) dst[q] = cvt(static_cast<uint16_t>(w[q / 2] >> (16 * (q % 2))));
+          }
+        }
+      }
+    } else {
+      for (uint32_t i = threadIdx.x; i < rows * width; i += kLatentThreads) {
+        const uint32_t r = i / width, c = i % width;
+        const uint64_t e = (t0 + r) * row_stride + c0 + c;
+        s_strip[r * kLatentCols + c] =
+            dtype == kF32 ? static_cast<const float*>(latent)[e]
+                          : cvt(static_cast<const uint16_t*>(latent)[e]);
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < width) {
+      float a = acc;
+#pragma unroll 8
+      for (uint32_t r = 0; r < rows; ++r) a += s_strip[r * kLatentCols + threadIdx.x];
+      acc = a;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < width) out[c0 + threadIdx.x] = acc / static_cast<float>(tokens);
+}
+
+__global__ __launch_bounds__(kLatentThreads) void latent_normalize_kernel(uint32_t dim,
+                                                                          float* __restrict__ out) {
+  __shared__ double s_ss[kLatentThreads / grm::kWave];
+  double ss = 0.0;
+  for (uint32_t d = threadIdx.x; d < dim; d += kLatentThreads) {
+    ss += static_cast<double>(out[d]) * static_cast<double>(out[d]);
+  }
+  for (int off = grm::kWave / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  if ((threadIdx.x & (grm::kWave - 1)) == 0) s_ss[threadIdx.x / grm::kWave] = ss;
+  __syncthreads();
+  double total = 0.0;
+  for (int w = 0; w < kLatentThreads / grm::kWave; ++w) total += s_ss[w];
+  const float denom = static_cast<float>(sqrt(total)) + 1e-8f;
+  for (uint32_t d = threadIdx.x; d < dim; d += kLatentThreads) out[d] = out[d] / denom;
+}
+
+int enqueue_latent_query(MlaDeviceArena* a, const void* d_latent, int dtype, uint64_t tokens,
+                         uint64_t row_stride, int normalize, float* d_out) {
+  if (!d_latent || !d_out) return grm::fail(-1, "null pointer");
+  if (dtype != kF32 && dtype != kBF16 && dtype != kF16) {
+    return grm::fail(-1, "latent dtype must be F32, BF16 or F16");
+  }
+  if (tokens == 0) return grm::fail(-1, "latent has no tokens");
+  if (tokens >= (1ull << 24)) return grm::fail(-1, "token count above 2^24");
+  if (row_stride == 0) row_stride = a->dim;
+  if (row_stride < a->dim) return grm::fail(-1, "row stride below the bank dim");
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  const uint32_t dim = static_cast<uint32_t>(a->dim);
+  latent_mean_kernel<<<(dim + kLatentCols - 1) / kLatentCols, kLatentThreads, 0, a->stream>>>(
+      d_latent, dtype, tokens, dim, row_stride, d_out);
+  GRM_HIP_CHECK(hipGetLastError());
+  if (normalize) latent_normalize_kernel<<<1, kLatentThreads, 0, a->stream>>>(dim, d_out);
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
 }  // namespace
 
 // ============================================================ reference ABI
@@ -1003,6 +1131,36 @@ extern "C" int grm_mla_hip_route(MlaDeviceArena* arena, const void* queries,
   return route_impl(arena, queries, query_dtype, queries_on_device != 0,
                     query_count, dim, warmup, topk, out_ids_host,
                     out_scores_host, elapsed_ms_host);
+}
+
+extern "C" int grm_mla_hip_latent_query(MlaDeviceArena* arena, const void* d_latent,
+                                        int latent_dtype, uint64_t tokens,
+                                        uint64_t row_stride, int normalize, float* d_out) {
+  if (!arena) return grm::fail(-1, "null arena");
+  GRM_CHECK_RC(enqueue_latent_query(arena, d_latent, latent_dtype, tokens, row_stride,
+                                    normalize, d_out));
+  GRM_HIP_CHECK(hipStreamSynchronize(arena->stream));
+  grm::clear_error();
+  return 0;
+}
+
+extern "C" int grm_mla_hip_route_latent(MlaDeviceArena* arena, const void* d_latent,
+                                        int latent_dtype, uint64_t tokens,
+                                        uint64_t row_stride, int topk,
+                                        uint64_t* out_ids_host, float* out_scores_host,
+                                        float* elapsed_ms_host) {
+  if (!arena) return grm::fail(-1, "null arena");
+  if (!arena->d_latent_q) {
+    GRM_HIP_CHECK(hipSetDevice(arena->device));
+    GRM_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&arena->d_latent_q),
+                            static_cast<size_t>(arena->dim) * sizeof(float)));
+  }
+  // The key is formed on the route stream; the route that follows on the
+  // same stream reads it there, with no copy to the host in between.
+  GRM_CHECK_RC(enqueue_latent_query(arena, d_latent, latent_dtype, tokens, row_stride, 1,
+                                    arena->d_latent_q));
+  return route_impl(arena, arena->d_latent_q, kF32, true, 1, static_cast<int>(arena->dim), 0,
+                    topk, out_ids_host, out_scores_host, elapsed_ms_host);
 }
 
 extern "C" int grm_mla_hip_append(MlaDeviceArena* a, const void* rows_host,

@@ -178,6 +178,33 @@ class MlaNodeBank(_Bank):
         _lib.check(rc, "MLA route")
         return RouteResult(ids, scores, float(ms.value), wall)
 
+    def latent_query(self, latent, tokens: int, *, dtype: str = "f16",
+                     row_stride: int = 0, normalize: bool = True, out=None) -> int:
+        """Write the route key of a device latent block [tokens][dim]
+        (core/kv_graft.py:131-142) to device memory ``out`` (a device
+        address or an object with ``data_ptr()``; dim floats)."""
+        self._need_open()
+        _lib.check(self._lib.grm_mla_hip_latent_query(
+            self._h, _device_ptr(latent), _dtype_code(dtype), int(tokens), int(row_stride),
+            1 if normalize else 0, _device_ptr(out)), "MLA latent query")
+        return _device_ptr(out)
+
+    def route_latent(self, latent, tokens: int, topk: int, *, dtype: str = "f16",
+                     row_stride: int = 0) -> RouteResult:
+        """Route the key of a device latent block without a host round
+        trip: the key is formed on the route stream and routed there."""
+        self._need_open()
+        ids = np.empty((1, topk), dtype=np.uint64)
+        scores = np.empty((1, topk), dtype=np.float32)
+        ms = ctypes.c_float(0.0)
+        t0 = time.perf_counter_ns()
+        rc = self._lib.grm_mla_hip_route_latent(
+            self._h, _device_ptr(latent), _dtype_code(dtype), int(tokens), int(row_stride),
+            int(topk), _ptr(ids), _ptr(scores), ctypes.byref(ms))
+        wall = (time.perf_counter_ns() - t0) / 1e6
+        _lib.check(rc, "MLA latent route")
+        return RouteResult(ids, scores, float(ms.value), wall)
+
     def append(self, rows, node_ids) -> int:
         self._need_open()
         r = self._rows(rows, self.dim)

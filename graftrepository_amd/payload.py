@@ -36,15 +36,17 @@ class PayloadFormatError(ValueError):
 
 
 class DeviceArray:
-    """fp16 values in device memory owned by this object (row-major
-    ``shape``).  ``ptr`` is the device address; ``to_host()`` copies them
-    back as numpy float16.  ``sub(i)`` is the address of entry i along the
+    """Values in device memory owned by this object (row-major ``shape``,
+    numpy ``dtype``, fp16 by default).  ``ptr`` is the device address;
+    ``to_host()`` copies them back, ``from_host(a)`` makes one holding a
+    copy of a host array.  ``sub(i)`` is the address of entry i along the
     first axis, e.g. one layer of an (L, H, S, D) node payload."""
 
-    def __init__(self, shape):
+    def __init__(self, shape, dtype=np.float16):
         self.shape = tuple(int(d) for d in shape)
+        self.dtype = np.dtype(dtype)
         self.size = int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1
-        self.nbytes = 2 * self.size
+        self.nbytes = self.dtype.itemsize * self.size
         self._lib = _lib.load()
         p = ctypes.c_void_p()
         _lib.check(self._lib.grm_hip_device_alloc(max(self.nbytes, 2), ctypes.byref(p)),
@@ -52,10 +54,18 @@ class DeviceArray:
         self.ptr = int(p.value)
 
     def to_host(self) -> np.ndarray:
-        out = np.empty(self.shape, dtype=np.float16)
+        out = np.empty(self.shape, dtype=self.dtype)
         _lib.check(self._lib.grm_hip_copy_to_host(out.ctypes.data, self.ptr, self.nbytes),
                    "device to host copy")
         return out
+
+    @classmethod
+    def from_host(cls, a) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        _lib.check(d._lib.grm_hip_copy_to_device(d.ptr, a.ctypes.data, a.nbytes),
+                   "host to device copy")
+        return d
 
     def sub(self, i: int) -> int:
         if not self.shape or not 0 <= i < self.shape[0]:
@@ -167,11 +177,7 @@ def unpack_node_device(payload, names=("k", "v")) -> dict[str, DeviceArray]:
         return unpack_kv_arrays_device(payload, list(names))
     out: dict[str, DeviceArray] = {}
     for name in names:
-        a = np.ascontiguousarray(payload[name], dtype=np.float16)
-        d = DeviceArray(a.shape)
-        _lib.check(d._lib.grm_hip_copy_to_device(d.ptr, a.ctypes.data, a.nbytes),
-                   "fp16 upload")
-        out[name] = d
+        out[name] = DeviceArray.from_host(np.ascontiguousarray(payload[name], dtype=np.float16))
     return out
 
 

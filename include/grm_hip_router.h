@@ -181,6 +181,23 @@ int grm_mla_hip_route_stats(MlaDeviceArena* arena, uint64_t* out4);
  * the last route was not batched.  No counterpart. */
 int grm_mla_hip_screen_ms(MlaDeviceArena* arena, float* ms);
 
+/* MLA route key from a device-resident latent block [tokens][dim] (row
+ * stride row_stride elements, 0 = dim; latent_dtype F32, BF16 or F16): the
+ * unit-norm token mean of core/kv_graft.py:131-142 (latent_centroid), written
+ * as dim floats to d_out (normalize = 0 writes the plain mean).  Replaces
+ * the forward pass's host round trip before route_topk_device
+ * (core/grm_cuda_router.py:491-539).  Waits for completion.  No counterpart. */
+int grm_mla_hip_latent_query(MlaDeviceArena* arena, const void* d_latent, int latent_dtype,
+                             uint64_t tokens, uint64_t row_stride, int normalize,
+                             float* d_out);
+
+/* Form that key on the bank's route stream and route it (one query) in the
+ * same call: ids and scores as grm_mla_hip_route.  No counterpart. */
+int grm_mla_hip_route_latent(MlaDeviceArena* arena, const void* d_latent, int latent_dtype,
+                             uint64_t tokens, uint64_t row_stride, int topk,
+                             uint64_t* out_ids_host, float* out_scores_host,
+                             float* elapsed_ms_host);
+
 /* Ragged GQA node bank over CSR token offsets (no counterpart: the reference
  * zero-pads every node to the longest, core/graft_arena.py:2979-3042).
  * keys_host: node i's block [kv_heads][L_i][head_dim] starts at value

@@ -1,0 +1,82 @@
+"""Device-resident MLA route keys: the latent centroid of core/kv_graft.py:
+131-142, formed on the device and routed without a host round trip.
+
+Bars:
+* the token mean, bit-exact against numpy's float32 reduce over axis 0;
+* the unit-norm key, within the rounding of numpy's own norm.  That norm
+  is a BLAS fp32 dot whose summation order depends on the host CPU, with
+  error up to dim * 2^-24 of |c|^2 (Higham's bound for an n-term dot).  The
+  device takes it in fp64, so the keys agree to (dim/2 + 2) * 2^-24
+  relative;
+* the route on that key, bit-exact against the oracle's route on the same
+  key.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from graftrepository_amd import MlaNodeBank, workloads as wl
+from graftrepository_amd.node_bank import as_bf16_bits, bf16_bits_to_f32
+from graftrepository_amd.payload import DeviceArray
+
+pytestmark = pytest.mark.gpu
+DIM = 256
+
+
+def numpy_key(c32):
+    c = c32.mean(0)
+    return c, c / (np.linalg.norm(c) + 1e-8)
+
+
+def assert_key_close(got, want):
+    bound = np.abs(want).astype(np.float64) * (DIM / 2 + 2) * 2.0 ** -24 + 1e-30
+    assert np.all(np.abs(got.astype(np.float64) - want) <= bound)
+
+
+@pytest.fixture(scope="module")
+def bank(hip_lib):
+    rows = wl.mla_rows(20_000, DIM, seed=31)
+    with MlaNodeBank(rows, np.arange(20_000, dtype=np.uint64) * 3 + 1) as b:
+        yield b, rows
+
+
+@pytest.mark.parametrize("dtype,tokens,stride", [("f16", 300, DIM), ("f16", 1, DIM),
+                                                 ("bf16", 777, DIM), ("f32", 64, 288),
+                                                 ("f16", 4096, 288), ("f16", 50, 261)])
+def test_latent_key_and_route(bank, dtype, tokens, stride):
+    b, rows = bank
+    rng = np.random.default_rng(tokens + stride)
+    full = (rng.standard_normal((tokens, stride)) * 1.5).astype(np.float32)
+    full[:, 3] = -0.0                                  # an all -0 column: numpy gives +0
+    if dtype == "f16":
+        host, c32 = full.astype(np.float16), full.astype(np.float16)[:, :DIM].astype(np.float32)
+    elif dtype == "bf16":
+        host = as_bf16_bits(full)
+        c32 = bf16_bits_to_f32(host)[:, :DIM]
+    else:
+        host, c32 = full, full[:, :DIM]
+    mean, key = numpy_key(np.ascontiguousarray(c32))
+    with DeviceArray.from_host(host) as lat, DeviceArray((DIM,), np.float32) as out:
+        b.latent_query(lat, tokens, dtype=dtype, row_stride=stride, normalize=False, out=out)
+        got_mean = out.to_host()
+        np.testing.assert_array_equal(got_mean.view(np.uint32), mean.view(np.uint32))
+        b.latent_query(lat, tokens, dtype=dtype, row_stride=stride, out=out)
+        got_key = out.to_host()
+        assert_key_close(got_key, key)
+        res = b.route_latent(lat, tokens, 8, dtype=dtype, row_stride=stride)
+    want_ids, want_sc, _ = oracle.mla_route(rows, got_key[None], 8,
+                                            node_ids=np.arange(20_000, dtype=np.uint64) * 3 + 1)
+    np.testing.assert_array_equal(res.ids, want_ids)
+    np.testing.assert_array_equal(res.scores.view(np.uint32), want_sc.view(np.uint32))
+
+
+def test_bad_latent_arguments(bank):
+    b, _ = bank
+    with DeviceArray((4, DIM), np.float16) as lat, DeviceArray((DIM,), np.float32) as out:
+        for kw in (dict(tokens=0), dict(tokens=4, row_stride=DIM - 1), dict(tokens=4, dtype="i8")):
+            args = dict(dtype="f16", row_stride=0)
+            args.update(kw)
+            t = args.pop("tokens")
+            with pytest.raises(RuntimeError):
+                b.latent_query(lat, t, out=out, **args)
