@@ -13,6 +13,8 @@ ABI (kernel + top-k + device->host copy of the k results).  Reported:
 * gqa        the ragged GQA route (512 nodes, lengths U[16,512], 4 layers x 8
              kv heads x 128, bf16, 32 query heads, top-3): p50/p99 and its
              roofline (sum(L_i) * 32 * 128 * 2 bytes)
+* store_route  the store's route law (lexical bonus + route filters) on
+             the device, 1M nodes, against the plain route
 * payload    packed graft payload unpack on the device: kernel roofline and
              one node mount against host dequant + fp16 upload
 * bank_bridge  arena-bridge refresh time at about 1% churn per epoch
@@ -414,6 +416,49 @@ def bench_bridge(epochs: int):
                         bank_dtype="f32")}
 
 
+def bench_store(steps: int):
+    """The store route on the device (lexical bonus + route filters,
+    grm_store_route_filtered's law) on a 1M x 288 fp32 store, against the
+    plain route of the same bank."""
+    from graftrepository_amd import workloads as wl
+    from graftrepository_amd.store_route import DeviceRouteStore, _KNOWN
+
+    n, d = 1_000_000, 288
+    rng = np.random.default_rng(17)
+    rows = wl.mla_rows(n, d, seed=23)
+    vocab = [f"w{i}" for i in range(1000)]
+    lex = [[] for _ in range(n)]
+    for i in rng.choice(n, size=n // 100, replace=False):
+        lex[int(i)] = list(rng.choice(vocab, size=3, replace=False))
+    kinds = np.asarray(_KNOWN["kind"])[rng.integers(0, 8, size=n)]
+    meta = [(str(k), "", "", "") for k in kinds]
+    t0 = time.perf_counter()
+    st = DeviceRouteStore(d, capacity=n)
+    st.set_routes(np.arange(n, dtype=np.uint64), rows, lex, meta)
+    build_s = time.perf_counter() - t0
+    q = wl.mla_queries(1, d, seed=29)[0]
+    qlex = ["w1", "w2", "w3"]
+    walls, plain = [], []
+    for i in range(steps + 5):
+        t0 = time.perf_counter()
+        st.route_filtered(q, qlex, kinds=["turn", "doc"], topk=8)
+        t1 = time.perf_counter()
+        st.bank.route(q[None], 8)
+        t2 = time.perf_counter()
+        if i >= 5:
+            walls.append((t1 - t0) * 1e3)
+            plain.append((t2 - t1) * 1e3)
+    st.close()
+    r = {"nodes": n, "dim": d, "lexical_nodes": n // 100, "query_lexical": 3,
+         "filter": "kind in {turn, doc}", "topk": 8,
+         "store_route_ms_p50": round(pct(walls, 50), 4),
+         "plain_route_ms_p50": round(pct(plain, 50), 4),
+         "build_s": round(build_s, 2)}
+    log(f"[store] filtered + lexical route p50 {r['store_route_ms_p50']:.3f} ms "
+        f"(plain route {r['plain_route_ms_p50']:.3f} ms), bulk build {build_s:.1f}s")
+    return r
+
+
 def bench_payload(reps: int):
     """Packed graft payloads: the device unpack kernel against its HBM
     roofline, and mounting one packed node payload (device unpack) against
@@ -535,8 +580,9 @@ def main() -> int:
     ap.add_argument("--int8-steps", type=int, default=20)
     ap.add_argument("--bridge-epochs", type=int, default=10)
     ap.add_argument("--payload-reps", type=int, default=10)
+    ap.add_argument("--store-steps", type=int, default=100)
     ap.add_argument("--only", choices=["all", "mla", "gqa", "batched", "int8", "bridge",
-                                       "payload"], default="all")
+                                       "payload", "store"], default="all")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -574,6 +620,9 @@ def main() -> int:
     pay = None
     if args.only in ("all", "payload"):
         pay = bench_payload(args.payload_reps)
+    sto = None
+    if args.only in ("all", "store"):
+        sto = bench_store(args.store_steps)
     cpu = None
     if m is not None and not args.skip_cpu:
         cpu = cpu_baseline_mla(m, args.cpu_seconds)
@@ -673,6 +722,16 @@ def main() -> int:
                    "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                    "dtype": "int8->f16", "data": "synthetic",
                    "config": {"workload": "payload_unpack", **pay}}
+    if sto is not None:
+        if out:
+            out["store_route"] = sto
+        else:
+            out = {"metric": "p50 store route latency (ms), lexical + filters, 1M MLA nodes",
+                   "value": sto["store_route_ms_p50"], "unit": "ms", "n_gpus": 1,
+                   "steps": args.store_steps, "warmup": 5,
+                   "ms_per_step": sto["store_route_ms_p50"], "higher_is_better": False,
+                   "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+                   "data": "synthetic", "config": {"workload": "store_route", **sto}}
     if cpu is not None:
         out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)

@@ -69,6 +69,10 @@ SIGNATURES = {
     "grm_mla_hip_screen_ms": (i32, [vp, vp]),
     "grm_mla_hip_latent_query": (i32, [vp, vp, i32, u64, u64, i32, vp]),
     "grm_mla_hip_route_latent": (i32, [vp, vp, i32, u64, u64, i32, vp, vp, vp]),
+    "grm_mla_hip_set_filter_bits": (i32, [vp, vp, vp, u64]),
+    "grm_mla_hip_route_filtered": (i32, [vp, vp, i32, i32, i32, u64, ctypes.c_uint32, vp, vp,
+                                         vp]),
+    "grm_mla_hip_score_nodes": (i32, [vp, vp, i32, vp, u64, vp]),
     "grm_gqa_hip_bank_create": (i32, [vp, i32, vp, i32, i32, vp, u64, i32, i32,
                                       vp, u64, u64, ctypes.POINTER(vp)]),
     "grm_gqa_hip_route": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, i32, vp,

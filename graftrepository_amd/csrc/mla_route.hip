@@ -378,6 +378,10 @@ struct MlaDeviceArena {
   void* d_queries = nullptr;
   size_t d_queries_bytes = 0;
   float* d_latent_q = nullptr;  // route key formed from a device latent (dim floats)
+  uint64_t* d_fbits = nullptr;  // per-slot route filter bits (capacity), 0 until set
+  float* d_fnorms = nullptr;    // per-route norms with filtered-out slots NaN (capacity)
+  const float* route_norms = nullptr;  // set around a filtered route: norms it reads
+  bool no_batch = false;               // set around a filtered route: single-query path only
   grm::MappedCands blocks_out;  // per-query, per-block top-k (host mapped)
   std::vector<Cand> merged;
   void* h_stage = nullptr;
@@ -427,6 +431,8 @@ void destroy_arena(MlaDeviceArena* a) {
   if (a->d_ids) (void)hipFree(a->d_ids);
   if (a->d_queries) (void)hipFree(a->d_queries);
   if (a->d_latent_q) (void)hipFree(a->d_latent_q);
+  if (a->d_fbits) (void)hipFree(a->d_fbits);
+  if (a->d_fnorms) (void)hipFree(a->d_fnorms);
   if (a->d_stage) (void)hipFree(a->d_stage);
   if (a->d_min_norm) (void)hipFree(a->d_min_norm);
   if (a->d_qpad) (void)hipFree(a->d_qpad);
@@ -665,8 +671,9 @@ int launch_single(MlaDeviceArena* a, const SingleGeom& g, const void* q, int q_d
                   Cand* bout) {
   const size_t lds = static_cast<size_t>(a->dim_pad) * sizeof(double);
   const dim3 grid(g.blocks), block(g.nw * grm::kWave);
+  const float* nrm = a->route_norms ? a->route_norms : a->d_norms;
 #define GRM_MLA_ARGS                                                                  \
-  a->d_tiles, a->d_norms, a->d_ids, g.num_tiles, a->chunks, a->capacity, a->dim, a->dim_pad, q, \
+  a->d_tiles, nrm, a->d_ids, g.num_tiles, a->chunks, a->capacity, a->dim, a->dim_pad, q, \
       q_dtype, topk, bout
   constexpr int PW = grm::mla::kPipeWaves;
   constexpr int RW = grm::mla::kRouteWaves;
@@ -807,7 +814,7 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
   if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
   const size_t qstride = static_cast<size_t>(a->dim) * elem_size(q_dtype);
   BatchPlan bp;
-  const bool batched = batch_plan(a, q_count - warmup, &bp);
+  const bool batched = !a->no_batch && batch_plan(a, q_count - warmup, &bp);
   a->screen_ms = 0.0f;
   std::vector<int> redo;  // queries for the single-query kernel
   if (batched) {
@@ -1011,6 +1018,79 @@ __global__ __launch_bounds__(kLatentThreads) void latent_normalize_kernel(uint32
   for (uint32_t d = threadIdx.x; d < dim; d += kLatentThreads) out[d] = out[d] / denom;
 }
 
+// Route filters (cpp/grm_runtime.cpp:3074-3104, every filter value known,
+// bits as route_filter_bits :2793-2838): a node passes when, for each
+// category c with filters (bit c of cats), its bits meet that category's
+// 16-bit mask, held at shift 16c in fmask.  Slots that do not pass get a
+// NaN norm, the marker the route kernels already skip; the filtered route
+// reads this copy in place of the bank's norms.
+__global__ void mla_filter_norms_kernel(const float* __restrict__ norms,
+                                        const uint64_t* __restrict__ fbits, uint64_t n,
+                                        uint64_t fmask, uint32_t cats, float* __restrict__ out) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride) {
+    const uint64_t hit = fbits[i] & fmask;
+    bool ok = true;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if ((cats >> c) & 1u) ok = ok && ((hit >> (16 * c)) & 0xffffull) != 0;
+    }
+    out[i] = ok ? norms[i] : __builtin_nanf("");
+  }
+}
+
+__global__ void mla_zero_bits_kernel(const uint64_t* __restrict__ slots, uint64_t n,
+                                     uint64_t* __restrict__ fbits) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride) {
+    fbits[slots[i]] = 0ull;
+  }
+}
+
+__global__ void mla_scatter_bits_kernel(const uint64_t* __restrict__ slot_bits, uint64_t n,
+                                        uint64_t* __restrict__ fbits) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) fbits[slot_bits[2 * i]] = slot_bits[2 * i + 1];
+}
+
+// Law scores (cpp/grm_runtime.cpp:3518-3545) of listed slots: the query
+// staged in fp64, its norm summed in d order (as the route kernels), and
+// per slot the fp64 dot in d order, then float(dot / (qnorm * norm_f +
+// 1e-8)); NaN where that is not finite or the slot is empty.  One block;
+// thread i scores slots i, i + blockDim.x, ...
+template <int DT>
+__global__ __launch_bounds__(256) void mla_score_slots_kernel(
+    const u32x4* __restrict__ tiles, const float* __restrict__ norms, size_t plane,
+    uint32_t chunks, uint32_t dim, uint32_t dim_pad, const void* __restrict__ query,
+    int query_dtype, const uint64_t* __restrict__ slots, uint64_t n, float* __restrict__ out) {
+  constexpr int EPC = DT == kF32 ? 4 : 8;
+  extern __shared__ double qd[];
+  __shared__ double s_qnorm;
+  grm::mla::stage_query(qd, query, query_dtype, dim, dim_pad);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double acc = 0.0;
+    for (uint32_t d = 0; d < dim; ++d) acc = fma(qd[d], qd[d], acc);
+    s_qnorm = sqrt(acc);
+  }
+  __syncthreads();
+  const double qnorm = s_qnorm;
+  for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const uint64_t slot = slots[i];
+    // the route kernels' own chunk fold, chunks in order (zero past dim)
+    double acc = 0.0;
+    for (uint32_t c = 0; c < chunks; ++c) {
+      acc = grm::mla::chunk_dot<DT>(tiles[static_cast<size_t>(c) * plane + slot], qd + c * EPC,
+                                    acc);
+    }
+    const float nrm = norms[slot];
+    const float sc = static_cast<float>(acc / (qnorm * static_cast<double>(nrm) + 1.0e-8));
+    out[i] = isfinite(sc) ? sc : __builtin_nanf("");
+  }
+}
+
 int enqueue_latent_query(MlaDeviceArena* a, const void* d_latent, int dtype, uint64_t tokens,
                          uint64_t row_stride, int normalize, float* d_out) {
   if (!d_latent || !d_out) return grm::fail(-1, "null pointer");
@@ -1163,6 +1243,129 @@ extern "C" int grm_mla_hip_route_latent(MlaDeviceArena* arena, const void* d_lat
                     topk, out_ids_host, out_scores_host, elapsed_ms_host);
 }
 
+extern "C" int grm_mla_hip_set_filter_bits(MlaDeviceArena* a, const uint64_t* node_ids,
+                                           const uint64_t* bits, uint64_t count) {
+  if (!a || (count > 0 && (!node_ids || !bits))) return grm::fail(-1, "invalid arguments");
+  std::vector<uint64_t> pairs;
+  pairs.reserve(2 * count);
+  for (uint64_t i = 0; i < count; ++i) {
+    auto it = a->slot_of.find(node_ids[i]);
+    if (it == a->slot_of.end()) return grm::fail(-1, "filter bits for an id that is not live");
+    pairs.push_back(it->second);
+    pairs.push_back(bits[i]);
+  }
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  GRM_CHECK_RC(wait_mutations(a));
+  if (!a->d_fbits) {
+    GRM_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&a->d_fbits),
+                            a->capacity * sizeof(uint64_t)));
+    GRM_HIP_CHECK(hipMemsetAsync(a->d_fbits, 0, a->capacity * sizeof(uint64_t), a->stream));
+  }
+  if (count > 0) {
+    void* h = nullptr;
+    void* d = nullptr;
+    GRM_CHECK_RC(stage_upload(a, pairs.size() * sizeof(uint64_t), &h, &d));
+    memcpy(h, pairs.data(), pairs.size() * sizeof(uint64_t));
+    GRM_HIP_CHECK(hipMemcpyAsync(d, h, pairs.size() * sizeof(uint64_t), hipMemcpyHostToDevice,
+                                 a->stream));
+    mla_scatter_bits_kernel<<<static_cast<unsigned>((count + 255) / 256), 256, 0, a->stream>>>(
+        static_cast<const uint64_t*>(d), count, a->d_fbits);
+    GRM_HIP_CHECK(hipGetLastError());
+  }
+  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  grm::clear_error();
+  return 0;
+}
+
+extern "C" int grm_mla_hip_route_filtered(MlaDeviceArena* a, const void* query, int query_dtype,
+                                          int query_on_device, int topk, uint64_t filter_mask,
+                                          uint32_t filter_categories, uint64_t* out_ids_host,
+                                          float* out_scores_host, float* elapsed_ms_host) {
+  if (!a) return grm::fail(-1, "null arena");
+  if (filter_categories & ~0xfu) return grm::fail(-1, "filter categories are bits 0..3");
+  if (filter_categories == 0) {
+    return route_impl(a, query, query_dtype, query_on_device != 0, 1, static_cast<int>(a->dim), 0,
+                      topk, out_ids_host, out_scores_host, elapsed_ms_host);
+  }
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  if (!a->d_fnorms) {
+    GRM_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&a->d_fnorms), a->capacity * sizeof(float)));
+  }
+  if (!a->d_fbits) {
+    // no bits set on any node: every node fails an active category
+    GRM_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&a->d_fbits),
+                            a->capacity * sizeof(uint64_t)));
+    GRM_HIP_CHECK(hipMemsetAsync(a->d_fbits, 0, a->capacity * sizeof(uint64_t), a->stream));
+  }
+  if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
+  // every slot the route scans: whole 64-slot tiles up to the high water
+  // (capacity is a multiple of 64; the tail slots stay NaN)
+  const uint64_t n = (a->high_water + grm::kWave - 1) / grm::kWave * grm::kWave;
+  if (n > 0) {
+    const unsigned blocks =
+        static_cast<unsigned>(std::min<uint64_t>((n + 255) / 256, static_cast<uint64_t>(a->cus) * 16));
+    mla_filter_norms_kernel<<<blocks, 256, 0, a->stream>>>(a->d_norms, a->d_fbits, n, filter_mask,
+                                                          filter_categories, a->d_fnorms);
+    GRM_HIP_CHECK(hipGetLastError());
+  }
+  a->route_norms = a->d_fnorms;
+  a->no_batch = true;
+  const int rc = route_impl(a, query, query_dtype, query_on_device != 0, 1,
+                            static_cast<int>(a->dim), 0, topk, out_ids_host, out_scores_host,
+                            elapsed_ms_host);
+  a->route_norms = nullptr;
+  a->no_batch = false;
+  return rc;
+}
+
+extern "C" int grm_mla_hip_score_nodes(MlaDeviceArena* a, const void* query_host,
+                                       int query_dtype, const uint64_t* node_ids, uint64_t count,
+                                       float* out_scores_host) {
+  if (!a || !query_host || (count > 0 && (!node_ids || !out_scores_host))) {
+    return grm::fail(-1, "invalid arguments");
+  }
+  if (query_dtype != kF32 && query_dtype != kBF16) return grm::fail(-1, "query dtype must be F32 or BF16");
+  if (count == 0) return 0;
+  std::vector<uint64_t> slots(count);
+  for (uint64_t i = 0; i < count; ++i) {
+    auto it = a->slot_of.find(node_ids[i]);
+    if (it == a->slot_of.end()) return grm::fail(-1, "score of an id that is not live");
+    slots[i] = it->second;
+  }
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  GRM_CHECK_RC(wait_mutations(a));
+  const size_t qbytes = static_cast<size_t>(a->dim) * (query_dtype == kF32 ? 4 : 2);
+  const size_t sbytes = count * sizeof(uint64_t);
+  const size_t obytes = count * sizeof(float);
+  const size_t q_off = 0, s_off = (qbytes + 255) / 256 * 256, o_off = s_off + (sbytes + 255) / 256 * 256;
+  void* h = nullptr;
+  void* d = nullptr;
+  GRM_CHECK_RC(stage_upload(a, o_off + obytes, &h, &d));
+  memcpy(static_cast<unsigned char*>(h) + q_off, query_host, qbytes);
+  memcpy(static_cast<unsigned char*>(h) + s_off, slots.data(), sbytes);
+  GRM_HIP_CHECK(hipMemcpyAsync(d, h, o_off, hipMemcpyHostToDevice, a->stream));
+  auto* dq = static_cast<unsigned char*>(d) + q_off;
+  auto* ds = reinterpret_cast<const uint64_t*>(static_cast<unsigned char*>(d) + s_off);
+  auto* dout = reinterpret_cast<float*>(static_cast<unsigned char*>(d) + o_off);
+  const size_t lds = static_cast<size_t>(a->dim_pad) * sizeof(double);
+  if (a->dtype == kF32) {
+    mla_score_slots_kernel<kF32><<<1, 256, lds, a->stream>>>(a->d_tiles, a->d_norms, a->capacity,
+                                                             a->chunks, a->dim, a->dim_pad, dq,
+                                                             query_dtype, ds, count, dout);
+  } else {
+    mla_score_slots_kernel<kBF16><<<1, 256, lds, a->stream>>>(a->d_tiles, a->d_norms, a->capacity,
+                                                              a->chunks, a->dim, a->dim_pad, dq,
+                                                              query_dtype, ds, count, dout);
+  }
+  GRM_HIP_CHECK(hipGetLastError());
+  GRM_HIP_CHECK(hipMemcpyAsync(static_cast<unsigned char*>(h) + o_off, dout, obytes,
+                               hipMemcpyDeviceToHost, a->stream));
+  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  memcpy(out_scores_host, static_cast<unsigned char*>(h) + o_off, obytes);
+  grm::clear_error();
+  return 0;
+}
+
 extern "C" int grm_mla_hip_append(MlaDeviceArena* a, const void* rows_host,
                                   int row_dtype, uint64_t count,
                                   const uint64_t* node_ids,
@@ -1258,6 +1461,12 @@ extern "C" int grm_mla_hip_evict(MlaDeviceArena* a, const uint64_t* node_ids,
   grm::mla::mla_evict_kernel<<<blocks, threads, 0, a->side>>>(
       static_cast<const uint64_t*>(d), count, a->d_norms, a->d_ids);
   GRM_HIP_CHECK(hipGetLastError());
+  if (a->d_fbits) {
+    // a slot reused by a later append starts with no filter bits
+    mla_zero_bits_kernel<<<blocks, threads, 0, a->side>>>(static_cast<const uint64_t*>(d), count,
+                                                          a->d_fbits);
+    GRM_HIP_CHECK(hipGetLastError());
+  }
   GRM_HIP_CHECK(hipEventRecord(a->ev_mut, a->side));
   a->mut_pending = true;
   for (uint64_t s : slots) {

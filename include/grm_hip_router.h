@@ -191,6 +191,32 @@ int grm_mla_hip_latent_query(MlaDeviceArena* arena, const void* d_latent, int la
                              uint64_t tokens, uint64_t row_stride, int normalize,
                              float* d_out);
 
+/* ---- Store route on the device (cpp/grm_runtime_c.h:176-181, 381-424) ----
+ * Per-node route filter bits, as route_filter_bits (cpp/grm_runtime.cpp:
+ * 2793-2838: kind at bit 0, scope 16, durability 32, mutability 48, one
+ * bit per known value).  A slot reused by a later append starts at 0.
+ * Ids must be live.  Counterpart of the filter bits kept by
+ * grm_store_set_route_metadata. */
+int grm_mla_hip_set_filter_bits(MlaDeviceArena* arena, const uint64_t* node_ids,
+                                const uint64_t* bits, uint64_t count);
+
+/* One query routed over the nodes that pass the route filters
+ * (cpp/grm_runtime.cpp:3074-3104 with known values): for each category c
+ * set in filter_categories (bits 0..3), a node's bits must meet the 16-bit
+ * mask at shift 16c of filter_mask.  Ids and scores as grm_mla_hip_route.
+ * The lexical bonus is added above this call (graftrepository_amd.
+ * store_route), giving grm_store_route_filtered's law. */
+int grm_mla_hip_route_filtered(MlaDeviceArena* arena, const void* query, int query_dtype,
+                               int query_on_device, int topk, uint64_t filter_mask,
+                               uint32_t filter_categories, uint64_t* out_ids_host,
+                               float* out_scores_host, float* elapsed_ms_host);
+
+/* Exact law scores (cpp/grm_runtime.cpp:3518-3545) of listed live nodes for
+ * one host query (F32 or BF16): float, NaN where not finite.  No
+ * counterpart (the store scores every entry on the CPU). */
+int grm_mla_hip_score_nodes(MlaDeviceArena* arena, const void* query_host, int query_dtype,
+                            const uint64_t* node_ids, uint64_t count, float* out_scores_host);
+
 /* Form that key on the bank's route stream and route it (one query) in the
  * same call: ids and scores as grm_mla_hip_route.  No counterpart. */
 int grm_mla_hip_route_latent(MlaDeviceArena* arena, const void* d_latent, int latent_dtype,

@@ -216,6 +216,64 @@ def dequant_payload_bits(codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
     return f16_bits(c.astype(np.float32) * s)
 
 
+# ------------------------------------------------------------ store route
+
+_FILTER_SHIFTS = (0, 16, 32, 48)
+_FILTER_DEFAULT = ("turn", "conversation", "session", "ephemeral")
+_FILTER_KNOWN = (
+    ("turn", "doc", "digest", "era", "fact", "task_state", "recall", "cull_span"),
+    ("conversation", "project", "user", "task", "global", "session"),
+    ("volatile", "session", "project", "permanent"),
+    ("ephemeral", "stable", "mutable", "immutable"),
+)
+
+
+def store_route(rows: np.ndarray, node_ids, lexical: list, meta: list, query: np.ndarray,
+                query_lexical=(), filters=((), (), (), ()), topk: int = 3):
+    """The store's MLA route law, route_mla_arena (cpp/grm_runtime.cpp:
+    4299-4361), single-row entries.
+
+    * meta[i] holds the values passed to set_route_metadata after the
+      route was set (:2922-2946): an empty value keeps the entry's default,
+      turn / conversation / session / ephemeral (cpp/grm_runtime.hpp:
+      483-494).
+    * Filters (:3053-3104): per category with filter values, the node's
+      known-value bit (:2797-2838) must be among the filters' bits, or,
+      when any filter value is unknown, the node's string must be listed.
+    * The exact score must be finite; the route score is
+      float(score) + float(hits) / float(|query lexical|) in fp32, where
+      hits counts the query keys found among the node's keys (:3107-3170).
+    * A non-finite sum drops the node; the order is (score desc, node id
+      asc).
+
+    Returns (node ids, route scores fp32) of the best topk."""
+    base = mla_scores(rows, np.asarray(query, np.float32)[None])[0]
+    ids = np.asarray(node_ids, dtype=np.uint64)
+    qlex = [s for s in query_lexical if s]
+    out = []
+    for i in range(base.size):
+        ok = True
+        for c in range(4):
+            fl = [v for v in filters[c] if v]
+            if not fl:
+                continue
+            val = meta[i][c] or _FILTER_DEFAULT[c]
+            if all(v in _FILTER_KNOWN[c] for v in fl):
+                ok = ok and val in fl and val in _FILTER_KNOWN[c]
+            else:
+                ok = ok and val in fl
+        if not ok or not np.isfinite(base[i]):
+            continue
+        hits = sum(1 for s in qlex if s in lexical[i])
+        bonus = (np.float32(hits) / np.float32(len(qlex))) if qlex else np.float32(0.0)
+        total = np.float32(base[i]) + bonus
+        if np.isfinite(total):
+            out.append((-float(total), int(ids[i]), total))
+    out.sort()
+    top = out[:topk]
+    return [n for _, n, _ in top], np.asarray([t for _, _, t in top], dtype=np.float32)
+
+
 # ------------------------------------------------------------------ MLA
 
 def mla_row_norms(rows: np.ndarray, threads: int = 0) -> np.ndarray:

@@ -8,6 +8,8 @@ and for pinning the oracle restatement.
 
 Route entry points used:
   grm_store_route      cpp/grm_runtime.cpp:6767-6825 -> route_mla_arena (fp64)
+  grm_store_route_filtered  cpp/grm_runtime.cpp:6840-6897 -> route_mla_arena
+                       with lexical bonus and route filters
   grm_store_route_gqa  cpp/grm_runtime.cpp:6898-6961 -> route_gqa_raw
 ``route_gqa_raw`` takes its fp32 arena path when every route key's length is
 a multiple of kv_heads*head_dim, and the fp64 ``gqa_raw_score`` path
@@ -63,6 +65,11 @@ def lib() -> ctypes.CDLL:
         L.grm_store_route_gqa.restype = i32
         L.grm_store_last_error.argtypes = [vp]
         L.grm_store_last_error.restype = cp
+        L.grm_store_set_route_metadata.argtypes = [vp, u64, cp, cp, cp, cp]
+        L.grm_store_set_route_metadata.restype = i32
+        L.grm_store_route_filtered.argtypes = [vp, vp, u64, cp, cp, cp, cp, cp, u64, vp, u64,
+                                               ctypes.POINTER(u64)]
+        L.grm_store_route_filtered.restype = i32
         _ref = L
     return _ref
 
@@ -110,6 +117,38 @@ class _Store:
         self._check(lib().grm_store_set_route_list(
             self.h, node_id, values.ctypes.data, values.size,
             offs.ctypes.data, len(flat), b""))
+
+
+def _blob(items) -> bytes:
+    return "\n".join(items).encode("utf-8")
+
+
+def store_route(rows: np.ndarray, lexical: list, meta: list, query: np.ndarray,
+                query_lexical=(), filters=((), (), (), ()), topk: int = 3) -> list[int]:
+    """Route order from the reference ``grm_store_route_filtered``
+    (cpp/grm_runtime.cpp:6840-6897 -> route_mla_arena): node i has route
+    key rows[i], lexical keys lexical[i] and route metadata meta[i] =
+    (kind, scope, durability, mutability).  filters = (kinds, scopes,
+    durabilities, mutabilities), each a list of values."""
+    r = np.ascontiguousarray(rows, dtype=np.float32)
+    q = np.ascontiguousarray(query, dtype=np.float32).reshape(-1)
+    d = r.shape[1]
+    h = lib().grm_store_create_mla(b"MiniCPM3_TC", 62, 2560, d, 0, d, 0)
+    with _Store(h) as st:
+        for i in range(r.shape[0]):
+            nid = st.add_node()
+            assert nid == i
+            k = np.ascontiguousarray(r[i])
+            st._check(lib().grm_store_set_route(st.h, nid, k.ctypes.data, k.size,
+                                                _blob(lexical[i])))
+            st._check(lib().grm_store_set_route_metadata(
+                st.h, nid, *[str(v).encode("utf-8") for v in meta[i]]))
+        out = np.empty(max(1, topk), dtype=np.uint64)
+        count = ctypes.c_uint64()
+        st._check(lib().grm_store_route_filtered(
+            st.h, q.ctypes.data, q.size, _blob(query_lexical), *[_blob(f) for f in filters],
+            topk, out.ctypes.data, topk, ctypes.byref(count)))
+        return [int(x) for x in out[:count.value]]
 
 
 def mla_route(rows: np.ndarray, query: np.ndarray, topk: int) -> list[int]:

@@ -1,0 +1,82 @@
+"""The store route law (lexical bonus and route filters) on the CPU: the
+oracle's restatement pinned against the reference store itself.
+
+The reference store is ``cpp/grm_runtime.cpp``, built into oracle/_ref.
+The cases are random stores with a small shared lexical vocabulary
+(collisions and repeated query keys), duplicate rows (score ties), route
+metadata drawn from known values, unknown values and empty values, and
+filters of known and unknown values.  Law: route_mla_arena
+(cpp/grm_runtime.cpp:4299-4361).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import ref
+from graftrepository_amd import store_route as sr
+
+pytestmark = pytest.mark.skipif(not ref.available(), reason="reference CPU store not built")
+
+VOCAB = ["alpha", "beta", "gamma", "delta", "eps", "zeta", "eta", "theta", "iota", "kappa"]
+META = [
+    ["turn", "doc", "fact", "recall", "weird-kind", ""],
+    ["conversation", "project", "global", "elsewhere", ""],
+    ["volatile", "permanent", "session", ""],
+    ["stable", "mutable", "odd", ""],
+]
+
+
+def random_store(rng, n, dim):
+    rows = rng.standard_normal((n, dim)).astype(np.float32)
+    rows[5] = rows[4]                              # exact ties
+    rows[9] = rows[4]
+    lexical = [list(rng.choice(VOCAB, size=rng.integers(0, 4), replace=False)) for _ in range(n)]
+    meta = [tuple(str(rng.choice(m)) for m in META) for _ in range(n)]
+    return rows, lexical, meta
+
+
+def random_query(rng, rows, dim):
+    q = rng.standard_normal(dim).astype(np.float32)
+    if rng.random() < 0.3:
+        q = rows[4].copy()
+    qlex = list(rng.choice(VOCAB, size=rng.integers(0, 5), replace=True))
+    filters = tuple(list(rng.choice(m, size=rng.integers(0, 3), replace=False))
+                    if rng.random() < 0.5 else [] for m in META)
+    return q, qlex, tuple([v for v in f if v] for f in filters)
+
+
+def test_oracle_store_law_matches_the_reference_store():
+    rng = np.random.default_rng(41)
+    n, dim = 120, 12
+    rows, lexical, meta = random_store(rng, n, dim)
+    for case in range(60):
+        q, qlex, filters = random_query(rng, rows, dim)
+        k = int(rng.integers(1, 17))
+        want = ref.store_route(rows, lexical, meta, q, qlex, filters, k)
+        got, _ = oracle.store_route(rows, np.arange(n), lexical, meta, q, qlex, filters, k)
+        assert got == want, (case, qlex, filters, k)
+
+
+def test_lexical_bonus_reorders_and_filters_bind():
+    rng = np.random.default_rng(42)
+    rows, lexical, meta = random_store(rng, 80, 8)
+    q = rng.standard_normal(8).astype(np.float32)
+    plain, _ = oracle.store_route(rows, np.arange(80), lexical, meta, q, (), ((), (), (), ()), 5)
+    boosted, _ = oracle.store_route(rows, np.arange(80), lexical, meta, q,
+                                    ["alpha", "beta"], ((), (), (), ()), 5)
+    assert plain != boosted
+    assert boosted == ref.store_route(rows, lexical, meta, q, ["alpha", "beta"],
+                                      ((), (), (), ()), 5)
+    only_docs, _ = oracle.store_route(rows, np.arange(80), lexical, meta, q, (),
+                                      (["doc"], (), (), ()), 16)
+    assert only_docs and all(meta[i][0] == "doc" for i in only_docs)
+
+
+def test_split_and_bits_follow_the_reference():
+    assert sr.split_keys("a\n\nb\n") == ["a", "b"]
+    assert sr.split_keys(b"x\ny") == ["x", "y"]
+    assert sr.split_keys(["a", "", "b"]) == ["a", "b"]
+    assert sr.filter_bits("doc", "project", "permanent", "stable") == (
+        (1 << 1) | (1 << 17) | (1 << 35) | (1 << 49))
+    assert sr.filter_bits("weird", "", "", "") == 0

@@ -1,0 +1,81 @@
+"""The store route on the device: DeviceRouteStore against the oracle's
+store law (pinned against the reference store in test_store_route.py).
+Bar: node ids and fp32 route scores bit-exact.
+
+Covered:
+
+* lexical bonus from a small shared vocabulary, with repeated query keys;
+* filters of known values, and of unknown values (the per-query
+  string-match bit);
+* metadata updates that keep unset fields (cpp/grm_runtime.cpp:2922-2946);
+* route replacement (set_route on a live node) and clear_route;
+* score ties from duplicate rows.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from graftrepository_amd.store_route import DeviceRouteStore
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = ["alpha", "beta", "gamma", "delta", "eps", "zeta", "eta", "theta", "iota", "kappa"]
+META = [
+    ["turn", "doc", "fact", "recall", "weird-kind", ""],
+    ["conversation", "project", "global", "elsewhere", ""],
+    ["volatile", "permanent", "session", ""],
+    ["stable", "mutable", "odd", ""],
+]
+DEFAULT = ("turn", "conversation", "session", "ephemeral")
+
+
+def test_device_store_route_matches_the_law(hip_lib):
+    rng = np.random.default_rng(51)
+    n, dim = 3000, 64
+    rows = {1000 + i: rng.standard_normal(dim).astype(np.float32) for i in range(n)}
+    rows[1005] = rows[1004].copy()                  # ties
+    rows[1009] = rows[1004].copy()
+    lex, meta = {}, {}
+    with DeviceRouteStore(dim, capacity=4096) as st:
+        def set_meta(nid, vals):
+            st.set_route_metadata(nid, *vals)
+            meta[nid] = tuple(v if v else o for v, o in zip(vals, meta[nid]))
+
+        for nid, r in rows.items():
+            lex[nid] = list(rng.choice(VOCAB, size=rng.integers(0, 4), replace=False))
+            st.set_route(nid, r, "\n".join(lex[nid]))
+            meta[nid] = DEFAULT
+            set_meta(nid, tuple(str(rng.choice(m)) for m in META))
+        for step in range(40):
+            if step % 5 == 4:                       # mutations between queries
+                for nid in rng.choice(list(rows), size=20, replace=False):
+                    nid = int(nid)
+                    op = rng.integers(0, 3)
+                    if op == 0:
+                        rows[nid] = rng.standard_normal(dim).astype(np.float32)
+                        lex[nid] = list(rng.choice(VOCAB, size=rng.integers(0, 3), replace=False))
+                        st.set_route(nid, rows[nid], lex[nid])
+                    elif op == 1:
+                        set_meta(nid, tuple(str(rng.choice(m)) for m in META))
+                    else:
+                        st.clear_route(nid)
+                        del rows[nid], lex[nid], meta[nid]
+            ids = np.asarray(sorted(rows), dtype=np.uint64)
+            R = np.stack([rows[int(i)] for i in ids])
+            q = rng.standard_normal(dim).astype(np.float32)
+            if rng.random() < 0.3:
+                q = rows[int(ids[4])].copy()
+            qlex = list(rng.choice(VOCAB, size=rng.integers(0, 5), replace=True))
+            filters = tuple([str(v) for v in rng.choice(m, size=rng.integers(0, 3), replace=False) if v]
+                            if rng.random() < 0.5 else [] for m in META)
+            k = int(rng.integers(1, 17))
+            want_ids, want_sc = oracle.store_route(R, ids, [lex[int(i)] for i in ids],
+                                                   [meta[int(i)] for i in ids], q, qlex, filters, k)
+            got_ids, got_sc = st.route_scored(q, qlex, k, kinds=filters[0], scopes=filters[1],
+                                              durabilities=filters[2], mutabilities=filters[3])
+            assert got_ids == want_ids, (step, qlex, filters, k)
+            np.testing.assert_array_equal(np.asarray(got_sc, np.float32).view(np.uint32),
+                                          want_sc.view(np.uint32))
+            assert st.route_filtered(q, "\n".join(qlex), *["\n".join(f) for f in filters],
+                                     topk=k) == want_ids
