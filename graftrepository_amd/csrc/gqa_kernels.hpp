@@ -347,7 +347,10 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
 // the cache -- and re-zero them; wave 0 sums each slot's heads in order,
 // keeps the block's k best and writes them to
 // block_out[(qb*gridDim.x + blockIdx.x)*k ..).  qbad[qb*kv + g] are the
-// query's non-finite flags.
+// query's non-finite flags.  With done (host-mapped memory) the block then
+// stores seq at done[qb*gridDim.x + blockIdx.x] once all of its stores are
+// complete, so a host that sees every flag of a launch holds its lists
+// without waiting for the stream.
 constexpr int kFinSlots = 64;    // slots per finalize group (one per lane)
 constexpr int kFinHeads = 128;   // heads staged per pass
 
@@ -356,7 +359,8 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
     const uint32_t* __restrict__ lens, const uint32_t* __restrict__ flags,
     const uint64_t* __restrict__ ids, const unsigned* __restrict__ qbad, int kv,
     int k, Cand* __restrict__ block_out, const uint32_t* __restrict__ slot_list,
-    const uint32_t* __restrict__ list_count, size_t list_stride) {
+    const uint32_t* __restrict__ list_count, size_t list_stride, unsigned* __restrict__ done,
+    unsigned seq) {
   __shared__ double s_h[kFinHeads][kFinSlots];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -444,6 +448,13 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
   }
   if (wave == 0 && lane < k) {
     block_out[(static_cast<size_t>(qb) * gridDim.x + blockIdx.x) * k + lane] = wl_entry(L);
+  }
+  if (done) {
+    // every wave's stores (the list, the re-zeroed maxima) are complete
+    // before the flag
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) done[static_cast<size_t>(qb) * gridDim.x + blockIdx.x] = seq;
   }
 }
 

@@ -88,6 +88,10 @@ struct GqaDeviceArena {
   unsigned long long* d_hmax = nullptr;
   size_t d_hmax_count = 0;
   grm::MappedCands blocks_out;  // per-query, per-block top-k (host mapped)
+  // per-(query, finalize block) completion flags (host mapped) and the
+  // number the last route stored there
+  grm::MappedBuf done_flags;
+  unsigned route_seq = 0;
   unsigned* d_qbad = nullptr;   // per (query, kv head): non-finite query value
   size_t d_qbad_count = 0;
   // exact path
@@ -198,6 +202,7 @@ void destroy_arena(GqaDeviceArena* a) {
     if (p) (void)hipFree(p);
   }
   grm::release_mapped(&a->blocks_out);
+  grm::release_mapped_bytes(&a->done_flags);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
@@ -531,12 +536,14 @@ int ensure_hmax(GqaDeviceArena* a, int H, int qb) {
 // Exact scores and per-block top-k of every slot, or (slot_list given) of
 // the listed candidate slots of each query.
 int launch_finalize(GqaDeviceArena* a, int H, int qb, int topk, uint32_t fin_blocks, Cand* bout,
-                    const uint32_t* slot_list = nullptr, const uint32_t* list_count = nullptr) {
+                    const uint32_t* slot_list = nullptr, const uint32_t* list_count = nullptr,
+                    unsigned* done = nullptr) {
   const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
   grm::gqa::gqa_finalize_kernel<<<dim3(fin_blocks, qb), per_block, 0, a->stream>>>(
       a->d_hmax, a->cap_nodes * static_cast<size_t>(H), a->cap_nodes, H,
       static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags, a->d_ids, a->d_qbad,
-      static_cast<int>(a->kv), topk, bout, slot_list, list_count, a->cap_nodes);
+      static_cast<int>(a->kv), topk, bout, slot_list, list_count, a->cap_nodes, done,
+      a->route_seq);
   GRM_HIP_CHECK(hipGetLastError());
   return 0;
 }
@@ -662,10 +669,11 @@ int prepare_sr(GqaDeviceArena* a, const SrPlan& p) {
 }
 
 // Enqueue one screen-and-refine pass over queries [0, qb) at qptr (device,
-// `qstride` bytes apart); their per-block top-k lands at bout.  Launches
-// only (prepare_sr allocates), so the pass can be captured in a graph.
+// `qstride` bytes apart); their per-block top-k lands at bout, and with
+// `done` the finalize blocks' completion flags at done[0, qb*fin_blocks).
+// Launches only (prepare_sr allocates).
 int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
-               int topk, uint32_t fin_blocks, Cand* bout) {
+               int topk, uint32_t fin_blocks, Cand* bout, unsigned* done) {
   const int kv = static_cast<int>(a->kv);
   const int RQ = p.R * p.Qt;
   const int cols = qb * RQ;
@@ -737,7 +745,7 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
     GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt));
   }
   // 2. exact scores and per-block top-k
-  return launch_finalize(a, H, qb, topk, fin_blocks, bout);
+  return launch_finalize(a, H, qb, topk, fin_blocks, bout, nullptr, nullptr, done);
 }
 
 // ------------------------------------------------------ bound-and-verify path
@@ -898,6 +906,9 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
                          a->d_ccount);
 }
 
+// Completion flags a route may wait on (one per query and finalize block).
+constexpr size_t kMaxDoneFlags = 4096;
+
 int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_device, int q_count,
                int H, int Qt, int warmup, int topk, uint64_t* out_ids, float* out_scores,
                float* elapsed_ms) {
@@ -934,6 +945,16 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   SrPlan plan;
   const bool use_sr = sr_plan(a, H, Qt, &plan);
   if (use_sr) GRM_CHECK_RC(prepare_sr(a, plan));
+  // Without a timing request, screen-and-refine routes report completion
+  // through per-block flags in host memory, which the host sees as soon as
+  // the last finalize block stores its flag (no stream event on the path).
+  const size_t n_flags = static_cast<size_t>(q_count) * fin_blocks;
+  bool flags = !elapsed_ms && use_sr && n_flags <= kMaxDoneFlags && !grm::blocking_sync();
+  unsigned* d_done = nullptr;
+  if (flags) {
+    GRM_CHECK_RC(grm::begin_flags(&a->done_flags, kMaxDoneFlags, &a->route_seq));
+    d_done = static_cast<unsigned*>(a->done_flags.dev);
+  }
   // where each query's per-block lists are, and how many entries they hold
   std::vector<uint32_t> q_entries(q_count, static_cast<uint32_t>(per_q));
   std::vector<size_t> q_off(q_count);
@@ -943,11 +964,12 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   const int segments[2][2] = {{0, warmup}, {warmup, q_count}};
   for (int si = 0; si < 2; ++si) {
     const auto& seg = segments[si];
-    if (si == 1) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+    if (si == 1 && elapsed_ms) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
     if (use_sr) {
       for (int q0 = seg[0]; q0 < seg[1]; q0 += plan.qb_max) {
         const int qb = std::min(plan.qb_max, seg[1] - q0);
         if (use_bound(a, plan, qb)) {
+          flags = false;
           if (!bv_ready) {
             GRM_CHECK_RC(prepare_bv(a, plan, topk, fin_blocks));
             bv_ready = true;
@@ -964,7 +986,8 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
           a->bv_routes += 1;
         } else {
           GRM_CHECK_RC(enqueue_sr(a, plan, qbase + static_cast<size_t>(q0) * qstride, q_dtype, qb, topk,
-                                  fin_blocks, a->blocks_out.dev + static_cast<size_t>(q0) * per_q));
+                                  fin_blocks, a->blocks_out.dev + static_cast<size_t>(q0) * per_q,
+                                  d_done ? d_done + static_cast<size_t>(q0) * fin_blocks : nullptr));
         }
       }
     } else {
@@ -975,7 +998,11 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
     }
   }
   GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
-  GRM_CHECK_RC(grm::wait_event(a->ev_stop));
+  if (flags) {
+    GRM_CHECK_RC(grm::wait_flags(a->done_flags, a->route_seq, n_flags, a->ev_stop));
+  } else {
+    GRM_CHECK_RC(grm::wait_event(a->ev_stop));
+  }
   for (int qi = 0; qi < q_count; ++qi) {
     grm::host_topk_merge(a->blocks_out.host + q_off[qi], q_entries[qi], topk, a->merged.data());
     write_result(a->merged.data(), topk, out_ids + static_cast<size_t>(qi) * topk,

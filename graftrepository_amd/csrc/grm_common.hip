@@ -6,6 +6,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+
 namespace grm {
 
 static thread_local std::string g_last_error;
@@ -65,12 +67,16 @@ int reserve_mapped(MappedCands* m, size_t count) {
   return 0;
 }
 
-int wait_event(hipEvent_t ev) {
+bool blocking_sync() {
   static const bool blocking = [] {
     const char* env = getenv("GRM_HIP_BLOCKING_SYNC");
     return env && env[0] == '1';
   }();
-  if (blocking) {
+  return blocking;
+}
+
+int wait_event(hipEvent_t ev) {
+  if (blocking_sync()) {
     GRM_HIP_CHECK(hipEventSynchronize(ev));
     return 0;
   }
@@ -79,6 +85,36 @@ int wait_event(hipEvent_t ev) {
     if (e == hipSuccess) return 0;
     if (e != hipErrorNotReady) return fail_hip(e, "hipEventQuery");
   }
+}
+
+int begin_flags(MappedBuf* buf, size_t max, unsigned* seq) {
+  if (buf->bytes < max * sizeof(unsigned)) {
+    GRM_CHECK_RC(reserve_mapped_bytes(buf, max * sizeof(unsigned)));
+    memset(buf->host, 0, max * sizeof(unsigned));
+    *seq = 0;
+  }
+  if (++*seq == 0) *seq = 1;  // 0 is what a fresh buffer holds
+  return 0;
+}
+
+int wait_flags(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev) {
+  const volatile unsigned* f = static_cast<const volatile unsigned*>(buf.host);
+  size_t i = 0;
+  for (uint64_t spin = 1;; ++spin) {
+    while (i < n && f[i] == seq) ++i;
+    if (i == n) break;
+    if (spin % 256 == 0) {
+      const hipError_t e = hipEventQuery(ev);
+      if (e == hipSuccess) {
+        while (i < n && f[i] == seq) ++i;
+        if (i == n) break;
+        return fail(-1, "route finished without its completion flags");
+      }
+      if (e != hipErrorNotReady) return fail_hip(e, "hipEventQuery");
+    }
+  }
+  std::atomic_thread_fence(std::memory_order_acquire);
+  return 0;
 }
 
 int reserve_mapped_bytes(MappedBuf* m, size_t bytes) {

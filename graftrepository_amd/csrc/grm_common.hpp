@@ -240,6 +240,16 @@ __device__ inline void block_topk_write(WaveList& L, int k,
   }
 }
 
+// Completion flag of a block whose list went to host-mapped memory (after
+// block_topk_write, where wave 0 wrote the list): once wave 0's stores are
+// complete it stores seq at done[blockIdx.x].  No-op when done is null.
+__device__ inline void block_done_flag(unsigned* __restrict__ done, unsigned seq) {
+  if (done && threadIdx.x < kWave) {
+    __threadfence_system();
+    if (threadIdx.x == 0) done[blockIdx.x] = seq;
+  }
+}
+
 constexpr int kMergeWaves = 4;
 
 // Host side: keep the best k of `count` candidates (tie law above) in out,
@@ -250,6 +260,9 @@ void host_topk_merge(const Cand* in, size_t count, int k, Cand* out);
 // the moment its last kernel ends instead of after a blocking wake-up.
 // With GRM_HIP_BLOCKING_SYNC=1 in the environment the wait blocks instead.
 int wait_event(hipEvent_t ev);
+// True when GRM_HIP_BLOCKING_SYNC=1 asks for blocking waits.
+bool blocking_sync();
+
 
 // Pinned host buffer of raw bytes that the device reads and writes directly
 // (mapped, coherent).
@@ -260,6 +273,17 @@ struct MappedBuf {
 };
 int reserve_mapped_bytes(MappedBuf* m, size_t bytes);
 void release_mapped_bytes(MappedBuf* m);
+
+// Completion flags in host-mapped memory: a route kernel's blocks store
+// the route's number there once their results are in host memory
+// (block_done_flag), and the host waits on the flags instead of a stream
+// event.  begin_flags puts a buffer of `max` flags in place (zeroed when
+// new) and advances *seq to the route's number (never 0); wait_flags
+// polls flags [0, n) until all hold seq, checking `ev` (recorded after the
+// route's kernels) now and then, so a route whose kernels fail or store no
+// flags returns an error instead of spinning.
+int begin_flags(MappedBuf* buf, size_t max, unsigned* seq);
+int wait_flags(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev);
 
 // Pinned host buffer the device writes directly (mapped, coherent): the
 // route kernels leave their per-block results there so the final merge

@@ -100,14 +100,14 @@ __device__ inline double tile_dot(const u32x4* __restrict__ p, uint32_t chunks,
 }
 
 // One query against every slot; each block writes its k best entries to
-// block_out[blockIdx.x*k ..) for topk_merge_kernel.
+// block_out[blockIdx.x*k ..), then (with done) seq to done[blockIdx.x].
 template <int DT, int NW>
 __global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
     const u32x4* __restrict__ tiles, const float* __restrict__ norms,
     const uint64_t* __restrict__ ids, uint32_t num_tiles, uint32_t chunks,
     size_t plane, uint32_t dim, uint32_t dim_pad,
     const void* __restrict__ query, int query_dtype, int k,
-    Cand* __restrict__ block_out) {
+    Cand* __restrict__ block_out, unsigned* __restrict__ done, unsigned seq) {
   extern __shared__ double qd[];
   __shared__ double s_qnorm;
   __shared__ Cand s_lists[NW][kMaxTopK];
@@ -149,6 +149,7 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
   }
 
   block_topk_write<NW>(L, k, s_lists, block_out);
+  block_done_flag(done, seq);
 }
 
 // Stage the query as doubles in LDS (zero beyond dim).
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_pipe_kernel(
     const uint64_t* __restrict__ ids, uint32_t num_tiles, uint32_t chunks,
     size_t plane, uint32_t dim, uint32_t dim_pad,
     const void* __restrict__ query, int query_dtype, int k,
-    Cand* __restrict__ block_out) {
+    Cand* __restrict__ block_out, unsigned* __restrict__ done, unsigned seq) {
   constexpr int EPC = DT == kF32 ? 4 : 8;
   extern __shared__ double qd[];
   __shared__ double s_qnorm;
@@ -272,6 +273,7 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_pipe_kernel(
     b = bn;
   }
   block_topk_write<NW>(L, k, s_lists, block_out);
+  block_done_flag(done, seq);
 }
 
 // Place staged row-major rows into their tile slots and compute row norms
@@ -383,6 +385,10 @@ struct MlaDeviceArena {
   const float* route_norms = nullptr;  // set around a filtered route: norms it reads
   bool no_batch = false;               // set around a filtered route: single-query path only
   grm::MappedCands blocks_out;  // per-query, per-block top-k (host mapped)
+  // per-(query, block) completion flags (host mapped) and the number the
+  // last flag-waiting route stored there
+  grm::MappedBuf done_flags;
+  unsigned route_seq = 0;
   std::vector<Cand> merged;
   void* h_stage = nullptr;
   size_t h_stage_bytes = 0;
@@ -441,6 +447,7 @@ void destroy_arena(MlaDeviceArena* a) {
   grm::release_mapped(&a->batch_out);
   grm::release_mapped_bytes(&a->batch_status);
   grm::release_mapped(&a->blocks_out);
+  grm::release_mapped_bytes(&a->done_flags);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
@@ -666,15 +673,16 @@ SingleGeom single_geom(const MlaDeviceArena* a) {
 }
 
 // One query (device pointer q) through the single-query kernel; its
-// per-block top-k lands at bout (g.blocks * topk entries).
+// per-block top-k lands at bout (g.blocks * topk entries), and with done
+// its blocks' completion flags at done[0, g.blocks).
 int launch_single(MlaDeviceArena* a, const SingleGeom& g, const void* q, int q_dtype, int topk,
-                  Cand* bout) {
+                  Cand* bout, unsigned* done = nullptr) {
   const size_t lds = static_cast<size_t>(a->dim_pad) * sizeof(double);
   const dim3 grid(g.blocks), block(g.nw * grm::kWave);
   const float* nrm = a->route_norms ? a->route_norms : a->d_norms;
 #define GRM_MLA_ARGS                                                                  \
   a->d_tiles, nrm, a->d_ids, g.num_tiles, a->chunks, a->capacity, a->dim, a->dim_pad, q, \
-      q_dtype, topk, bout
+      q_dtype, topk, bout, done, a->route_seq
   constexpr int PW = grm::mla::kPipeWaves;
   constexpr int RW = grm::mla::kRouteWaves;
   if (a->dtype == kF32) {
@@ -787,6 +795,9 @@ int enqueue_batch_pass(MlaDeviceArena* a, const BatchPlan& p, const unsigned cha
   return 0;
 }
 
+// Completion flags a route may wait on (one per query and route block).
+constexpr size_t kMaxDoneFlags = 8192;
+
 int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
                bool on_device, int q_count, int dim, int warmup, int topk,
                uint64_t* out_ids, float* out_scores, float* elapsed_ms) {
@@ -872,19 +883,34 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
   if (!redo.empty()) {
     a->single_queries += redo.size();
     GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * redo.size()));
+    // Without a timing request the host sees completion through per-block
+    // flags in host memory, as soon as the last block stores its flag (no
+    // stream event on the path).
+    const size_t n_flags = static_cast<size_t>(g.blocks) * redo.size();
+    const bool flags = !elapsed_ms && n_flags <= kMaxDoneFlags && !grm::blocking_sync();
+    unsigned* d_done = nullptr;
+    if (flags) {
+      GRM_CHECK_RC(grm::begin_flags(&a->done_flags, kMaxDoneFlags, &a->route_seq));
+      d_done = static_cast<unsigned*>(a->done_flags.dev);
+    }
     // Uncertified batched queries add their time to the timed segment.
     bool started = false;
     for (size_t j = 0; j < redo.size(); ++j) {
       const int qi = redo[j];
-      if (!started && (batched || qi == warmup)) {
+      if (!started && elapsed_ms && (batched || qi == warmup)) {
         GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
         started = true;
       }
       GRM_CHECK_RC(launch_single(a, g, qbase + qi * qstride, q_dtype, topk,
-                                 a->blocks_out.dev + j * per_q));
+                                 a->blocks_out.dev + j * per_q,
+                                 d_done ? d_done + j * g.blocks : nullptr));
     }
     GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
-    GRM_CHECK_RC(grm::wait_event(a->ev_stop));
+    if (flags) {
+      GRM_CHECK_RC(grm::wait_flags(a->done_flags, a->route_seq, n_flags, a->ev_stop));
+    } else {
+      GRM_CHECK_RC(grm::wait_event(a->ev_stop));
+    }
     if (elapsed_ms) {
       float ms = 0.0f;
       GRM_HIP_CHECK(hipEventElapsedTime(&ms, a->ev_start, a->ev_stop));

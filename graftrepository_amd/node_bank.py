@@ -143,8 +143,10 @@ class MlaNodeBank(_Bank):
 
     def route(self, queries, topk: int, *, warmup: int = 0,
               on_device: bool = False, query_dtype: str | None = None,
-              query_count: int | None = None) -> RouteResult:
-        """Route queries [Q, dim] (or [dim]); returns ids/scores [Q, topk]."""
+              query_count: int | None = None, timed: bool = True) -> RouteResult:
+        """Route queries [Q, dim] (or [dim]); returns ids/scores [Q, topk].
+        With ``timed=False`` no device time is taken (``device_ms`` is NaN)
+        and the library may report completion without a stream event."""
         self._need_open()
         qd = self.dtype if query_dtype is None else _dtype_code(query_dtype)
         if on_device:
@@ -172,11 +174,12 @@ class MlaNodeBank(_Bank):
         t0 = time.perf_counter_ns()
         rc = self._lib.grm_mla_hip_route(
             self._h, qptr, qd, 1 if on_device else 0, q_count, self.dim,
-            int(warmup), int(topk), _ptr(ids), _ptr(scores), ctypes.byref(ms))
+            int(warmup), int(topk), _ptr(ids), _ptr(scores),
+            ctypes.byref(ms) if timed else None)
         wall = (time.perf_counter_ns() - t0) / 1e6
         del keep
         _lib.check(rc, "MLA route")
-        return RouteResult(ids, scores, float(ms.value), wall)
+        return RouteResult(ids, scores, float(ms.value) if timed else float("nan"), wall)
 
     def latent_query(self, latent, tokens: int, *, dtype: str = "f16",
                      row_stride: int = 0, normalize: bool = True, out=None) -> int:
@@ -319,9 +322,11 @@ class GqaNodeBank(_Bank):
 
     def route(self, queries, topk: int, *, warmup: int = 0,
               on_device: bool = False, query_dtype: str = "f32",
-              query_shape: tuple[int, int, int, int] | None = None
-              ) -> RouteResult:
-        """Route queries [Q, H, Qt, hd] (or [H, Qt, hd])."""
+              query_shape: tuple[int, int, int, int] | None = None,
+              timed: bool = True) -> RouteResult:
+        """Route queries [Q, H, Qt, hd] (or [H, Qt, hd]).  With
+        ``timed=False`` no device time is taken (``device_ms`` is NaN) and
+        the library may report completion without a stream event."""
         self._need_open()
         qd = _dtype_code(query_dtype)
         if on_device:
@@ -350,11 +355,11 @@ class GqaNodeBank(_Bank):
         t0 = time.perf_counter_ns()
         rc = self._lib.grm_gqa_hip_route(
             self._h, qptr, qd, 1 if on_device else 0, qc, H, Qt, int(warmup),
-            int(topk), _ptr(ids), _ptr(scores), ctypes.byref(ms))
+            int(topk), _ptr(ids), _ptr(scores), ctypes.byref(ms) if timed else None)
         wall = (time.perf_counter_ns() - t0) / 1e6
         del keep
         _lib.check(rc, "GQA route")
-        return RouteResult(ids, scores, float(ms.value), wall)
+        return RouteResult(ids, scores, float(ms.value) if timed else float("nan"), wall)
 
     def append(self, keys, tok_counts, node_ids, scales=None) -> int:
         self._need_open()

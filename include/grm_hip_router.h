@@ -143,7 +143,10 @@ int grm_mla_hip_bank_create(const void* rows_host, int row_dtype,
 /* MLA route returning node ids and scores (no counterpart: the reference
  * returns row ids only).  queries [query_count][dim] of query_dtype
  * (F32 or BF16 bits); queries_on_device selects a device pointer.
- * out_ids_host / out_scores_host are [query_count][topk]; scores may be NULL. */
+ * out_ids_host / out_scores_host are [query_count][topk]; scores may be NULL.
+ * elapsed_ms_host may be NULL: no device time is taken then, and the call
+ * sees its kernel's completion through per-block flags in host memory
+ * rather than a stream event (the same results, sooner). */
 int grm_mla_hip_route(MlaDeviceArena* arena, const void* queries,
                       int query_dtype, int queries_on_device, int query_count,
                       int dim, int warmup, int topk, uint64_t* out_ids_host,
@@ -244,7 +247,10 @@ int grm_gqa_hip_bank_create(const void* keys_host, int key_dtype,
 /* GQA route returning node ids and scores (no counterpart).  queries
  * [query_count][query_heads][query_tokens][head_dim] of query_dtype
  * (F32 or BF16 bits).  Stacked routing layers are expressed by folding the
- * layer axis into the head axes of both bank and query. */
+ * layer axis into the head axes of both bank and query.  elapsed_ms_host
+ * may be NULL: no device time is taken then, and screen-and-refine routes
+ * see completion through the finalize blocks' flags in host memory rather
+ * than a stream event (the same results, sooner). */
 int grm_gqa_hip_route(GqaDeviceArena* arena, const void* queries,
                       int query_dtype, int queries_on_device, int query_count,
                       int query_heads, int query_tokens, int warmup, int topk,

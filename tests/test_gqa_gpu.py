@@ -348,3 +348,40 @@ def test_repeated_routes_follow_query_and_bank_changes(hip_lib):
         ids, sc, _ = want(qs[1], live)
         for _ in range(2):
             assert_same(bank.route(dq, 4, on_device=True), ids, sc)
+
+
+@pytest.mark.parametrize("bound", [None, "0"])
+def test_untimed_routes_wait_on_completion_flags(hip_lib, monkeypatch, bound):
+    # Routes that ask for no device time wait on the finalize blocks'
+    # completion flags instead of a stream event: the same results as timed
+    # routes, for one query, several, several screen passes (bound "0"
+    # keeps every batch on the screen-and-refine path, 16 queries a pass)
+    # and batches that take the bound-and-verify path, across bank changes.
+    if bound is not None:
+        monkeypatch.setenv("GRM_HIP_GQA_BOUND", bound)
+    lens = wl.gqa_lengths(300, seed=83, lo=1, hi=400)
+    keys, offs = wl.gqa_bank(lens, 8, 128, seed=83, dtype="bf16")
+    node_ids = np.arange(300, dtype=np.uint64) * 3 + 1
+    qs = wl.gqa_queries(20, 32, 1, 128, seed=83, dtype="bf16")
+    qf = bf16_bits_to_f32(qs).reshape(qs.shape)
+
+    def want(q, live):
+        blocks = [keys[int(offs[j]) * 8 * 128:int(offs[j + 1]) * 8 * 128] for j in live]
+        o = np.zeros(len(live) + 1, np.uint64)
+        o[1:] = np.cumsum([lens[j] for j in live])
+        return oracle.gqa_route(np.concatenate(blocks), oracle.BF16, o, 8, 128, q, 5,
+                                node_ids=node_ids[live])
+
+    live = list(range(300))
+    with GqaNodeBank(keys, offs, kv_heads=8, head_dim=128, dtype="bf16",
+                     node_ids=node_ids) as bank:
+        for step in range(2):
+            for n, warm in ((1, 0), (3, 0), (2, 1), (6, 0), (20, 2)):
+                ids, sc, _ = want(qf[:n], live)
+                for timed in (False, True, False):
+                    r = bank.route(qs[:n], 5, query_dtype="bf16", warmup=warm, timed=timed)
+                    assert_same(r, ids, sc)
+                    assert np.isnan(r.device_ms) != timed
+            if step == 0:
+                bank.evict(node_ids[10:40])
+                live = live[:10] + live[40:]

@@ -312,3 +312,29 @@ def test_batched_copies_of_best_rows_far_apart(hip_lib):
     ids, sc, _ = oracle.mla_route(_f32(rows), _f32(qs), 8, node_ids=node_ids)
     assert_same(res.ids, res.scores, ids, sc)
     assert stats["batched"] == 48
+
+
+@pytest.mark.parametrize("dim,dtype", [(288, "f32"), (96, "f32"), (256, "bf16")])
+def test_untimed_routes_wait_on_completion_flags(hip_lib, dim, dtype):
+    # Routes that ask for no device time wait on the route blocks'
+    # completion flags instead of a stream event: the same results as timed
+    # routes, for the pipelined kernel (288 values), the plain kernel (96),
+    # several queries with warmup, batched bf16 queries, and across bank
+    # changes.
+    rng = np.random.default_rng(dim)
+    rows = wl.mla_rows(120_000, dim, seed=dim, dtype=dtype)
+    ids0 = np.arange(120_000, dtype=np.uint64) * 5 + 2
+    qs = wl.mla_queries(24, dim, seed=dim + 1, dtype=dtype)
+    f = _f32 if dtype == "bf16" else (lambda x: x)
+    live = np.ones(120_000, bool)
+    with MlaNodeBank(rows, ids0, dtype=dtype) as bank:
+        for step in range(2):
+            for n, warm in ((1, 0), (3, 1), (24, 0)):
+                want, wsc, _ = oracle.mla_route(f(rows[live]), f(qs[:n]), 7, node_ids=ids0[live])
+                for timed in (False, True, False):
+                    r = bank.route(qs[:n], 7, warmup=warm, timed=timed)
+                    assert_same(r.ids, r.scores, want, wsc)
+                    assert np.isnan(r.device_ms) != timed
+            ev = rng.choice(np.flatnonzero(live), size=500, replace=False)
+            bank.evict(ids0[ev])
+            live[ev] = False
