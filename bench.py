@@ -93,12 +93,12 @@ def bench_latent_entry(bank, dim: int, k: int, steps: int) -> dict:
     with DeviceArray.from_host(lat) as d_lat:
         for i in range(steps + 3):
             t0 = time.perf_counter()
-            r1 = bank.route_latent(d_lat, 512, k, dtype="f16")
+            r1 = bank.route_latent(d_lat, 512, k, dtype="f16", timed=False)
             t1 = time.perf_counter()
             back = d_lat.to_host()
             c = back.astype(np.float32).mean(0)
             key = c / (np.linalg.norm(c) + 1e-8)
-            r2 = bank.route(key[None], k)
+            r2 = bank.route(key[None], k, timed=False)
             t2 = time.perf_counter()
             if i >= 3:
                 dev_ms.append((t1 - t0) * 1e3)
@@ -464,7 +464,7 @@ def bench_store(steps: int):
         t0 = time.perf_counter()
         st.route_filtered(q, qlex, kinds=["turn", "doc"], topk=8)
         t1 = time.perf_counter()
-        st.bank.route(q[None], 8)
+        st.bank.route(q[None], 8, timed=False)
         t2 = time.perf_counter()
         if i >= 5:
             walls.append((t1 - t0) * 1e3)

@@ -193,9 +193,10 @@ class MlaNodeBank(_Bank):
         return _device_ptr(out)
 
     def route_latent(self, latent, tokens: int, topk: int, *, dtype: str = "f16",
-                     row_stride: int = 0) -> RouteResult:
+                     row_stride: int = 0, timed: bool = True) -> RouteResult:
         """Route the key of a device latent block without a host round
-        trip: the key is formed on the route stream and routed there."""
+        trip: the key is formed on the route stream and routed there.
+        ``timed=False`` as in ``route``."""
         self._need_open()
         ids = np.empty((1, topk), dtype=np.uint64)
         scores = np.empty((1, topk), dtype=np.float32)
@@ -203,10 +204,10 @@ class MlaNodeBank(_Bank):
         t0 = time.perf_counter_ns()
         rc = self._lib.grm_mla_hip_route_latent(
             self._h, _device_ptr(latent), _dtype_code(dtype), int(tokens), int(row_stride),
-            int(topk), _ptr(ids), _ptr(scores), ctypes.byref(ms))
+            int(topk), _ptr(ids), _ptr(scores), ctypes.byref(ms) if timed else None)
         wall = (time.perf_counter_ns() - t0) / 1e6
         _lib.check(rc, "MLA latent route")
-        return RouteResult(ids, scores, float(ms.value), wall)
+        return RouteResult(ids, scores, float(ms.value) if timed else float("nan"), wall)
 
     def append(self, rows, node_ids) -> int:
         self._need_open()

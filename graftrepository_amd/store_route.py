@@ -264,10 +264,10 @@ class DeviceRouteStore:
             kk = min(k, live)
             ids = np.empty((1, kk), dtype=np.uint64)
             sc = np.empty((1, kk), dtype=np.float32)
-            ms = ctypes.c_float(0.0)
+            # no device time asked for: the library waits on completion flags
             _lib.check(self._lib.grm_mla_hip_route_filtered(
                 self.bank._h, _ptr(q), 0, 0, kk, ctypes.c_uint64(fmask), ctypes.c_uint32(cats),
-                _ptr(ids), _ptr(sc), ctypes.byref(ms)), "store route")
+                _ptr(ids), _ptr(sc), None), "store route")
         finally:
             if temp:
                 self._set_bits(list(temp), [self._bits.get(n, 0) for n in temp])

@@ -64,11 +64,13 @@ def test_latent_key_and_route(bank, dtype, tokens, stride):
         b.latent_query(lat, tokens, dtype=dtype, row_stride=stride, out=out)
         got_key = out.to_host()
         assert_key_close(got_key, key)
-        res = b.route_latent(lat, tokens, 8, dtype=dtype, row_stride=stride)
+        results = [b.route_latent(lat, tokens, 8, dtype=dtype, row_stride=stride, timed=t)
+                   for t in (True, False)]
     want_ids, want_sc, _ = oracle.mla_route(rows, got_key[None], 8,
                                             node_ids=np.arange(20_000, dtype=np.uint64) * 3 + 1)
-    np.testing.assert_array_equal(res.ids, want_ids)
-    np.testing.assert_array_equal(res.scores.view(np.uint32), want_sc.view(np.uint32))
+    for res in results:
+        np.testing.assert_array_equal(res.ids, want_ids)
+        np.testing.assert_array_equal(res.scores.view(np.uint32), want_sc.view(np.uint32))
 
 
 def test_bad_latent_arguments(bank):
