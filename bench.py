@@ -264,18 +264,36 @@ def bench_gqa(steps: int, warmup: int):
         devs.append(r.device_ms)
         timed_walls.append(r.wall_ms)
     dq.close()
+    # the same bank with 4 query tokens per head (16 query columns per kv
+    # head instead of 4)
+    q4 = wl.gqa_queries(1, H, 4, hd, cfg["seed"] + 1)
+    dq4 = probe.upload_queries(q4.view(np.float32))
+    for _ in range(warmup):
+        bank.route(dq4, cfg["topk"], on_device=True, query_dtype="bf16", query_shape=q4.shape)
+    walls4 = [bank.route(dq4, cfg["topk"], on_device=True, query_dtype="bf16",
+                         query_shape=q4.shape, timed=False).wall_ms
+              for _ in range(max(1, steps // 2))]
+    devs4 = [bank.route(dq4, cfg["topk"], on_device=True, query_dtype="bf16",
+                        query_shape=q4.shape).device_ms
+             for _ in range(min(steps, 100))]
+    dq4.close()
     bank.close()
     sum_l = int(offs[-1])
     bytes_per_call = sum_l * kv * hd * 2
     mean_dev = float(np.mean(devs))
     achieved = bytes_per_call / (mean_dev * 1e-3) / 1e9
+    qt4 = {"query_tokens": 4, "p50_ms": round(pct(walls4, 50), 5),
+           "device_ms_mean": round(float(np.mean(devs4)), 5),
+           "achieved_gbs": round(bytes_per_call / (float(np.mean(devs4)) * 1e-3) / 1e9, 1)}
+    log(f"[gqa qt4] p50 {qt4['p50_ms']:.4f} ms  device {qt4['device_ms_mean']:.4f} ms"
+        f"  {qt4['achieved_gbs']:.0f} GB/s")
     log(f"[gqa] sumL {sum_l}  p50 {pct(walls, 50):.4f} ms  p99 {pct(walls, 99):.4f} ms"
         f"  device {mean_dev:.4f} ms  {achieved:.0f} GB/s"
         f"  (timed calls p50 {pct(timed_walls, 50):.4f} ms)")
     return dict(keys=keys, offs=offs, q=q, ids=r.ids[0].copy(),
                 scores=r.scores[0].copy(), walls=walls, devs=devs,
                 bytes=bytes_per_call, achieved=achieved, mean_dev=mean_dev,
-                timed_p50=pct(timed_walls, 50),
+                timed_p50=pct(timed_walls, 50), qt4=qt4,
                 sum_l=sum_l, cfg=cfg, kv=kv, H=H)
 
 
@@ -688,6 +706,7 @@ def main() -> int:
             "p99_ms": round(pct(g["walls"], 99), 5),
             "device_ms_mean": round(g["mean_dev"], 5),
             "timed_calls_p50_ms": round(g["timed_p50"], 5),
+            "query_tokens_4": g["qt4"],
             "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(g["achieved"] / HBM_PEAK_GBS, 4),

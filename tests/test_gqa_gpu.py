@@ -185,20 +185,23 @@ def test_append_evict_compact(hip_lib):
         assert bank.info()["live"] == len(blocks)
 
 
-def test_ragged_config_parity(hip_lib):
+@pytest.mark.parametrize("Qt", [1, 4])
+def test_ragged_config_parity(hip_lib, Qt):
     cfg = wl.GQA_RAGGED
     kv = cfg["layers"] * cfg["kv_heads"]
     H = cfg["layers"] * cfg["heads"]
     lens = wl.gqa_lengths(cfg["nodes"], cfg["seed"], lo=cfg["lo"], hi=cfg["hi"])
     keys, offs = wl.gqa_bank(lens, kv, cfg["head_dim"], cfg["seed"])
-    qs = wl.gqa_queries(2, H, cfg["tokens"], cfg["head_dim"], cfg["seed"])
+    qs = wl.gqa_queries(2, H, Qt, cfg["head_dim"], cfg["seed"] + Qt - 1)
     with GqaNodeBank(keys, offs, kv_heads=kv, head_dim=cfg["head_dim"],
                      dtype="bf16") as bank:
         res = bank.route(qs, cfg["topk"], query_dtype="bf16")
+        one = bank.route(qs[:1], cfg["topk"], query_dtype="bf16", timed=False)
     ids, sc, _ = oracle.gqa_route(keys, oracle.BF16, offs, kv, cfg["head_dim"],
                                   bf16_bits_to_f32(qs).reshape(qs.shape),
                                   cfg["topk"])
     assert_same(res, ids, sc)
+    assert_same(one, ids[:1], sc[:1])
 
 
 @pytest.mark.parametrize("Qt", [1, 4])
