@@ -258,8 +258,8 @@ class _Bridge:
                 "epoch": int(epoch), "signature_walk": False}
             return self.last_event
         walk = type(self)._full_walk(grafts)
-        self._epoch = epoch
         if walk is None:
+            self._epoch = epoch
             # The device bank stays allocated: a later epoch may make the
             # arena eligible again, and the delta then starts from it.
             self._eligible_bank = False
@@ -273,6 +273,7 @@ class _Bridge:
         order = np.argsort(rs.node_ids, kind="stable")
         snid = rs.node_ids[order]
         if snid.size > 1 and np.any(snid[1:] == snid[:-1]):
+            self._epoch = epoch
             self._eligible_bank = False
             self.last_event = {"status": "ineligible", "epoch": int(epoch),
                                "signature_walk": True,
@@ -283,22 +284,34 @@ class _Bridge:
         self._in_bank = np.zeros(len(grafts), dtype=bool)
         self._in_bank[g] = True
         if self.bank is not None and rs.same(self._resident):
+            self._epoch = epoch
             self._eligible_bank = True
             self._pinned = cents
             self.last_event = {"status": "signature_reused", "epoch": int(epoch),
                                "signature_walk": True,
                                "node_count": int(rs.node_ids.size)}
             return self.last_event
-        if self.bank is None:
-            moved = self._create(rs.node_ids, rows)
-            status, evicted, appended = "created", 0, int(rs.node_ids.size)
-        else:
-            evict_ids, append_pos = plan_delta(self._resident, rs)
-            moved, rebuilt = self._apply(evict_ids, append_pos, rs.node_ids, rows)
-            status = "rebuilt" if rebuilt else "updated"
-            evicted, appended = int(evict_ids.size), int(append_pos.size)
-            if rebuilt:
-                self.totals["rebuilt"] += 1
+        # Fail closed (core/graft_arena.py:1270-1281): until the device bank
+        # holds exactly this row set the route is unavailable, and an error
+        # part-way through an update leaves no epoch that a retry could
+        # take as current; the bank, in an unknown state, is dropped.
+        self._eligible_bank = False
+        self._epoch = None
+        try:
+            if self.bank is None:
+                moved = self._create(rs.node_ids, rows)
+                status, evicted, appended = "created", 0, int(rs.node_ids.size)
+            else:
+                evict_ids, append_pos = plan_delta(self._resident, rs)
+                moved, rebuilt = self._apply(evict_ids, append_pos, rs.node_ids, rows)
+                status = "rebuilt" if rebuilt else "updated"
+                evicted, appended = int(evict_ids.size), int(append_pos.size)
+                if rebuilt:
+                    self.totals["rebuilt"] += 1
+        except BaseException:
+            self.close()
+            raise
+        self._epoch = epoch
         self._resident = rs
         # The row set holds id(cent); keeping the resident centroid objects
         # alive means no later object can take one of those ids while its

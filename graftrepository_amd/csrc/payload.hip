@@ -125,8 +125,9 @@ int enqueue(DeviceCtx* c, const void* codes, const void* scales, uint64_t n, uin
   // One step per thread: a grid that covers the data measures 6.7 TB/s on
   // 1 Gi values, against 5.1 TB/s for a grid-stride loop over 32 blocks
   // per CU (each thread's load-convert-store chain then serialises).  The
-  // stride loop stays for counts beyond the cap.
-  const uint64_t max_blocks = 1ull << 30;
+  // stride loop stays for counts beyond the cap, which keeps blocks x
+  // threads within the 2^32 - 1 work items a grid dimension may hold.
+  const uint64_t max_blocks = 0xffffffffull / kThreads;
   (void)c->cus;
   const bool vec = gs % 8 == 0 && (reinterpret_cast<uintptr_t>(codes) % 8) == 0 &&
                    (reinterpret_cast<uintptr_t>(out) % 16) == 0;

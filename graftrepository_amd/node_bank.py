@@ -63,6 +63,20 @@ def _device_ptr(obj) -> int:
     raise TypeError("device queries need data_ptr(), .handle or an address")
 
 
+def _device_nbytes(obj) -> int | None:
+    """Bytes a device query object holds, when it says (``nbytes``, or a
+    torch tensor's element count and size); None for a bare address."""
+    if isinstance(obj, int):
+        return None
+    nb = getattr(obj, "nbytes", None)
+    if isinstance(nb, int):
+        return nb
+    numel, esz = getattr(obj, "numel", None), getattr(obj, "element_size", None)
+    if callable(numel) and callable(esz):
+        return int(numel()) * int(esz())
+    return None
+
+
 @dataclass(frozen=True)
 class RouteResult:
     """Top-k per query: node ids (UINT64_MAX = unfilled), scores (NaN =
@@ -155,6 +169,10 @@ class MlaNodeBank(_Bank):
                 shape = getattr(queries, "shape", None)
                 query_count = int(shape[0]) if shape is not None and len(shape) == 2 else 1
             q_count = int(query_count)
+            need = q_count * self.dim * (4 if qd == DTYPE_F32 else 2)
+            have = _device_nbytes(queries)
+            if have is not None and have < need:
+                raise ValueError(f"device queries hold {have} bytes, {q_count} queries need {need}")
             keep = None
         else:
             q = np.asarray(queries)
@@ -335,6 +353,12 @@ class GqaNodeBank(_Bank):
                 query_shape = tuple(int(x) for x in queries.shape)
             if len(query_shape) == 3:
                 query_shape = (1, *query_shape)
+            if len(query_shape) != 4 or query_shape[3] != self.head_dim:
+                raise ValueError("query_shape must be (Q, H, Qt, head_dim)")
+            need = int(np.prod(query_shape, dtype=np.int64)) * (4 if qd == DTYPE_F32 else 2)
+            have = _device_nbytes(queries)
+            if have is not None and have < need:
+                raise ValueError(f"device queries hold {have} bytes, the shape needs {need}")
             qptr = _device_ptr(queries)
             keep = None
         else:

@@ -192,3 +192,39 @@ def test_route_order_with_excludes():
     # 16 wanted with 2 excludes in the bank: the capped ask (16) holds the
     # excluded rows, so too few survive and the caller falls back.
     assert br.route_order(q, 16, exclude={order[0], order[1]}) is None
+
+
+def test_failed_update_fails_closed_and_retries_from_scratch():
+    # An error part-way through applying a delta (here the append, after
+    # the evictions ran) must not leave a route on a half-updated bank, and
+    # a retry at the same epoch must not take the bank as current
+    # (core/graft_arena.py:1270-1281 marks the route unavailable).
+    rng = np.random.default_rng(6)
+    gs = [graft(i, rng.standard_normal(8).astype(np.float32)) for i in range(30)]
+    br = CpuMlaBridge()
+    br.refresh(gs, 1)
+    q = gs[3]["cent"]
+    assert br.route_order(q, 3) is not None
+    gs[2]["retired"] = True
+    gs.append(graft(99, rng.standard_normal(8).astype(np.float32)))
+
+    real_apply = CpuMlaBridge._apply
+
+    def failing_apply(self, evict_ids, append_pos, node_ids, rows):
+        for nid in evict_ids:
+            del self.bank.rows[int(nid)]
+        raise RuntimeError("append failed")
+
+    CpuMlaBridge._apply = failing_apply
+    try:
+        with pytest.raises(RuntimeError, match="append failed"):
+            br.refresh(gs, 2)
+    finally:
+        CpuMlaBridge._apply = real_apply
+    assert br.bank is None and br.bank_size == 0
+    assert br.route_order(q, 3) is None
+    ev = br.refresh(gs, 2)                       # same epoch: walks again
+    assert ev["status"] == "created"
+    want = sorted(int(g["native_node_id"]) for g in gs if not g.get("retired"))
+    assert sorted(br.bank.rows) == want
+    assert br.route_order(q, 3) is not None

@@ -83,3 +83,108 @@ def test_gqa_workload_shapes():
     keys, offs = wl.gqa_bank(lens[:8], 4, 32, seed=1)
     assert offs[0] == 0 and offs[-1] == lens[:8].sum()
     assert keys.size == int(offs[-1]) * 4 * 32 and keys.dtype == np.uint16
+
+
+class _NoComputeLib:
+    """Stands in for the library: any route call is a test failure."""
+
+    def __getattr__(self, name):
+        if "route" in name:
+            raise AssertionError(f"{name} called with bad arguments")
+        return lambda *a: 0
+
+
+def _bank_without_device(cls, **attrs):
+    import ctypes
+    b = cls.__new__(cls)
+    b._lib = _NoComputeLib()
+    b._h = ctypes.c_void_p(1)
+    for k, v in attrs.items():
+        setattr(b, k, v)
+    return b
+
+
+def test_device_query_shapes_are_checked_before_the_call():
+    from graftrepository_amd.node_bank import GqaNodeBank, MlaNodeBank
+
+    class Dev:  # a device buffer that states its size
+        def __init__(self, nbytes):
+            self.nbytes = nbytes
+
+        def data_ptr(self):
+            return 0x1000
+
+    g = _bank_without_device(GqaNodeBank, head_dim=128, dtype=0)
+    with pytest.raises(ValueError, match="head_dim"):
+        g.route(Dev(1 << 20), 3, on_device=True, query_shape=(1, 32, 1, 64))
+    with pytest.raises(ValueError, match="bytes"):
+        g.route(Dev(32 * 128 * 4 - 4), 3, on_device=True, query_shape=(1, 32, 1, 128))
+    with pytest.raises(ValueError, match="bytes"):
+        g.route(Dev(2 * 32 * 4 * 128 * 2 - 2), 3, on_device=True, query_dtype="bf16",
+                query_shape=(2, 32, 4, 128))
+    m = _bank_without_device(MlaNodeBank, dim=288, dtype=0)
+    with pytest.raises(ValueError, match="bytes"):
+        m.route(Dev(288 * 4 * 3 - 4), 3, on_device=True, query_count=3)
+
+
+class _RecordingLib:
+    """Records each C call's arguments and returns 0 (no device work)."""
+
+    def __init__(self):
+        self.calls = []
+
+    def __getattr__(self, name):
+        def fn(*args):
+            self.calls.append((name, args))
+            if name.endswith(("_create", "_upload_queries")):
+                args[-1]._obj.value = 0x1000   # the handle out-parameter
+            return 0
+        return fn
+
+
+@pytest.mark.parametrize("mod", ["mla_probe", "gqa_probe"])
+def test_probe_layer_argument_order(monkeypatch, mod):
+    import importlib
+
+    from graftrepository_amd import _lib, probe
+    m = importlib.import_module(f"graftrepository_amd.{mod}")
+    fake = _RecordingLib()
+    monkeypatch.setattr(probe._lib, "load", lambda path=None: fake)
+    gqa = mod == "gqa_probe"
+    bank = np.zeros((5, 2, 7, 16) if gqa else (5, 16), np.float32)
+    qs = np.zeros((3, 8, 4, 16) if gqa else (3, 16), np.float32)
+    p = m.HipProbe()
+    assert m.CudaProbe is m.HipProbe
+    ids, ms, wall = p.route_topk(bank, qs, warmup=1, topk=2)
+    assert ids.shape == (3, 2) and ids.dtype == np.uint64 and wall >= 0.0
+    arena = p.create_arena(bank)
+    arena.route_topk(qs, warmup=1, topk=2)
+    dq = p.upload_queries(qs)
+    arena.route_topk_device(dq, warmup=0, topk=2)
+    pre = "grm_gqa" if gqa else "grm_mla"
+    names = [c[0] for c in fake.calls]
+    assert names == [f"{pre}_cublas_route", f"{pre}_cuda_arena_create",
+                     f"{pre}_cuda_arena_route", f"{pre}_cuda_upload_queries",
+                     f"{pre}_cuda_arena_route_device"]
+    for name, args in fake.calls:
+        assert len(args) == len(_lib.SIGNATURES[name][1]), name
+    ints = [a for a in fake.calls[0][1] if isinstance(a, int)]
+    if gqa:   # keys, q, nodes, kv, T, Q, H, Qt, hd, warmup, topk, out, ms
+        assert fake.calls[0][1][2:11] == (5, 2, 7, 3, 8, 4, 16, 1, 2)
+        assert fake.calls[2][1][2:7] == (3, 8, 4, 1, 2)
+        assert (arena.nodes, arena.kv_heads, arena.key_tokens, arena.head_dim) == (5, 2, 7, 16)
+    else:     # rows, q, nodes, dim, Q, warmup, topk, out, ms
+        assert fake.calls[0][1][2:7] == (5, 16, 3, 1, 2)
+        assert fake.calls[2][1][2:6] == (3, 16, 1, 2)
+        assert (arena.nodes, arena.dim) == (5, 16)
+    assert ints
+    with pytest.raises(ValueError):
+        arena.route_topk(qs[..., :8], warmup=0, topk=2)
+    with pytest.raises(ValueError):
+        arena.route_topk(qs, warmup=0, topk=6)
+    arena.close()
+    with pytest.raises(RuntimeError, match="closed"):
+        arena.route_topk(qs, warmup=0, topk=2)
+    dq.close()
+    assert names.count(f"{pre}_cuda_free_device_ptr") == 0
+    assert fake.calls[-1][0] == f"{pre}_cuda_free_device_ptr"
