@@ -61,6 +61,7 @@ SIGNATURES = {
                                       ctypes.POINTER(vp)]),
     "grm_mla_hip_route": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp,
                                 vp]),
+    "grm_mla_hip_route_noalloc": (i32, [vp, vp, i32, i32, i32, i32, vp, vp]),
     "grm_mla_hip_append": (i32, [vp, vp, i32, u64, vp, vp]),
     "grm_mla_hip_evict": (i32, [vp, vp, u64, vp]),
     "grm_mla_hip_sync": (i32, [vp]),

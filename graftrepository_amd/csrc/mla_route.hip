@@ -35,6 +35,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <set>
 #include <unordered_map>
 #include <vector>
@@ -422,6 +423,10 @@ struct MlaDeviceArena {
   uint32_t cus = 256;       // compute units of the device
   uint32_t max_blocks = 0;  // plain-kernel grid cap (4 blocks per CU)
 };
+
+// Per-block top-k lists of the allocation-free route (see route_noalloc).
+constexpr size_t kScratchCands = 16384;  // 256 KiB
+static __device__ __align__(256) Cand scratch[kScratchCands];
 
 namespace {
 
@@ -1137,6 +1142,97 @@ int enqueue_latent_query(MlaDeviceArena* a, const void* d_latent, int dtype, uin
   return 0;
 }
 
+// ------------------------------------------------ allocation-free route
+//
+// grm_mla_hip_route_noalloc keeps the single-query kernel's per-block top-k
+// lists in `scratch`, a file-scope device array, instead of memory the
+// library allocates; a merge kernel then writes the k best of those lists
+// straight to the caller's device outputs.  Each GPU holds its own copy of
+// the array from load to process end, and host code reaches it only through
+// the address hipGetSymbolAddress returns for the current device (the
+// array's name in host code is a host-side stand-in, not a device address).
+// Every call on one GPU shares that GPU's array: calls that overlap on a
+// GPU race.  Queries run one after another on the bank's stream, so one
+// query's lists fit the array: up to kScratchCands entries (grid blocks x
+// topk; 1024 blocks x 16 at most with the default grid cap).  Each block
+// writes all k of its entries before the merge reads them, so nothing in
+// the array has to start at zero.
+constexpr int kScratchDevices = 64;
+
+std::mutex g_scratch_mu;
+Cand* g_scratch_ptr[kScratchDevices] = {};
+
+// Device address of this device's scratch (the device must be current).
+int scratch_for(int device, Cand** out) {
+  if (device < 0 || device >= kScratchDevices) return grm::fail(-1, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    GRM_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return grm::fail(-1, "scratch symbol has no device address");
+    g_scratch_ptr[device] = static_cast<Cand*>(p);
+  }
+  *out = g_scratch_ptr[device];
+  return 0;
+}
+
+// k best of `count` per-block entries, written as ids and scores (unfilled:
+// UINT64_MAX and NaN); one block.
+__global__ __launch_bounds__(grm::kMergeWaves * grm::kWave) void mla_merge_out_kernel(
+    const Cand* __restrict__ in, uint32_t count, int k, uint64_t* __restrict__ out_ids,
+    float* __restrict__ out_scores) {
+  __shared__ Cand s_lists[grm::kMergeWaves][grm::kMaxTopK];
+  const int lane = threadIdx.x & (grm::kWave - 1);
+  const int wave = threadIdx.x / grm::kWave;
+  grm::WaveList G;
+  grm::wl_init(G);
+  grm::wl_consume_global(G, k, in, count, static_cast<uint32_t>(wave), grm::kMergeWaves);
+  if (lane < grm::kMaxTopK) s_lists[wave][lane] = grm::wl_entry(G);
+  __syncthreads();
+  if (wave == 0) {
+    grm::WaveList B;
+    grm::block_merge<grm::kMergeWaves>(s_lists, k, B);
+    if (lane < k) {
+      const bool ok = isfinite(B.s) && B.id != kNoId;
+      out_ids[lane] = ok ? B.id : kNoId;
+      if (out_scores) out_scores[lane] = ok ? B.s : __builtin_nanf("");
+    }
+  }
+}
+
+int route_noalloc(MlaDeviceArena* a, const void* d_queries, int q_dtype, int q_count, int dim,
+                  int topk, uint64_t* d_out_ids, float* d_out_scores) {
+  if (!a || !d_queries || !d_out_ids) return grm::fail(-1, "null argument");
+  if (dim != static_cast<int>(a->dim)) return grm::fail(-1, "query dim does not match bank");
+  if (q_dtype != kF32 && q_dtype != kBF16) return grm::fail(-1, "query dtype must be F32 or BF16");
+  if (q_count <= 0) return grm::fail(-1, "need query_count > 0");
+  if (topk <= 0 || topk > grm::kMaxTopK || static_cast<uint64_t>(topk) > a->live) {
+    return grm::fail(-1, "topk must be in [1, 16] and <= live nodes");
+  }
+  const SingleGeom g = single_geom(a);
+  const size_t per_q = static_cast<size_t>(g.blocks) * topk;
+  if (per_q > kScratchCands) {
+    return grm::fail(-1, "route grid blocks x topk exceed the 16384-entry scratch");
+  }
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  Cand* lists = nullptr;
+  GRM_CHECK_RC(scratch_for(a->device, &lists));
+  if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
+  const size_t qstride = static_cast<size_t>(a->dim) * elem_size(q_dtype);
+  const unsigned char* qbase = static_cast<const unsigned char*>(d_queries);
+  for (int qi = 0; qi < q_count; ++qi) {
+    GRM_CHECK_RC(launch_single(a, g, qbase + qi * qstride, q_dtype, topk, lists));
+    mla_merge_out_kernel<<<1, grm::kMergeWaves * grm::kWave, 0, a->stream>>>(
+        lists, static_cast<uint32_t>(per_q), topk, d_out_ids + static_cast<size_t>(qi) * topk,
+        d_out_scores ? d_out_scores + static_cast<size_t>(qi) * topk : nullptr);
+    GRM_HIP_CHECK(hipGetLastError());
+  }
+  a->single_queries += static_cast<uint64_t>(q_count);
+  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  grm::clear_error();
+  return 0;
+}
+
 }  // namespace
 
 // ============================================================ reference ABI
@@ -1237,6 +1333,13 @@ extern "C" int grm_mla_hip_route(MlaDeviceArena* arena, const void* queries,
   return route_impl(arena, queries, query_dtype, queries_on_device != 0,
                     query_count, dim, warmup, topk, out_ids_host,
                     out_scores_host, elapsed_ms_host);
+}
+
+extern "C" int grm_mla_hip_route_noalloc(MlaDeviceArena* arena, const void* d_queries,
+                                         int query_dtype, int query_count, int dim, int topk,
+                                         uint64_t* d_out_ids, float* d_out_scores) {
+  return route_noalloc(arena, d_queries, query_dtype, query_count, dim, topk, d_out_ids,
+                       d_out_scores);
 }
 
 extern "C" int grm_mla_hip_latent_query(MlaDeviceArena* arena, const void* d_latent,

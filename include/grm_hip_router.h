@@ -152,6 +152,23 @@ int grm_mla_hip_route(MlaDeviceArena* arena, const void* queries,
                       int dim, int warmup, int topk, uint64_t* out_ids_host,
                       float* out_scores_host, float* elapsed_ms_host);
 
+/* Allocation-free variant of grm_mla_hip_route for callers that cannot
+ * allocate device or host memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Queries are device memory [query_count][dim] (F32 or BF16
+ * bits); results go to device memory: d_out_ids [query_count][topk] and
+ * d_out_scores (may be NULL), unfilled slots UINT64_MAX / NaN.  Every query
+ * runs the single-query kernel (the batched matrix-core path is not used).
+ * The per-block lists live in a fixed 256 KiB device array inside the
+ * library (one per GPU, held until the process ends); a route whose grid
+ * blocks x topk exceed its 16384 entries is refused with -1.  The call
+ * allocates nothing and returns once the outputs are written.  Calls that
+ * overlap on one GPU share that array and race. */
+int grm_mla_hip_route_noalloc(MlaDeviceArena* arena, const void* d_queries,
+                              int query_dtype, int query_count, int dim,
+                              int topk, uint64_t* d_out_ids,
+                              float* d_out_scores);
+
 /* Append `count` rows with node ids (no counterpart).  The upload and the
  * device-side placement run on the bank's side stream; the next route waits
  * for them.  out_epoch (may be NULL) receives the bank epoch after the call.
