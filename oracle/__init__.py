@@ -37,10 +37,17 @@ F32, BF16, F16, I8 = 0, 1, 2, 3
 PINNING = {
     "mla_route": "reference C++ grm_store_route goldens (tests/golden) + "
                  "orthonormal closed form + duplicate-row tie blocks + NaN rows",
+    "mla_route_numpy": "closed forms (basis rows, scaled rows: a dot, not a "
+                       "cosine), stable tie order, NaN rows dropped, and its "
+                       "distance from the fp64 law within the fp32 dot's "
+                       "rounding bound",
+    "mla_route_normed": "equal to mla_route (ids and score bits) on random banks",
     "mla_row_norms": "closed form (unit vectors, Pythagorean triples) + "
                      "reference goldens via route order",
     "gqa_route": "reference C++ grm_store_route_gqa goldens on its fp64 path "
-                 "(tests/golden) + hand cases [1,2,0], ties [0,1,2], multi-key",
+                 "(tests/golden) + hand cases [1,2,0], ties [0,1,2] + "
+                 "single-token closed form (one key per node; multi-key "
+                 "nodes are not modelled)",
     "f16 conversion": "exhaustive agreement with numpy astype(float16)",
     "bf16 rounding": "agreement with torch.bfloat16 conversion",
     "int8 quantise/dequant": "round-trip invariants of "
@@ -82,6 +89,9 @@ def lib() -> ctypes.CDLL:
         L.grm_oracle_mla_route.argtypes = [
             vp, u64, u64, vp, vp, vp, u64, u64, i32, vp, vp, vp]
         L.grm_oracle_mla_route.restype = i32
+        L.grm_oracle_mla_route_normed.argtypes = [
+            vp, u64, u64, vp, vp, u64, u64, i32, vp, vp, vp]
+        L.grm_oracle_mla_route_normed.restype = i32
         L.grm_oracle_gqa_scores.argtypes = [
             vp, i32, vp, i32, u64, vp, u64, u64, u64, vp, u64, u64, u64, vp,
             i32]
@@ -299,6 +309,46 @@ def mla_scores(rows: np.ndarray, queries: np.ndarray, threads: int = 0):
     return out
 
 
+def mla_route_numpy(rows: np.ndarray, queries: np.ndarray, topk: int):
+    """The reference's Python MLA route law, in numpy, for the CPU baseline.
+
+    ``ArenaCache._vector_route_scores`` (core/graft_arena.py:778-801)
+    scores ``np.stack(rows).astype(float32) @ q`` -- an fp32 dot, no
+    norms (the centroids are unit-norm) -- and keeps the finite scores;
+    the route (:733-768) then sorts the candidates by ``-score`` with
+    Python's stable sort, so ties keep ascending graft order.  With no
+    lexical keys and the default length/normalisation hooks off (:813,
+    :847-862) the first ``topk`` entries are the route.
+
+    Returns (row indices [Q,k] int64, scores [Q,k] f32, counts [Q]);
+    unfilled slots hold -1 / NaN.  The dot's summation order is numpy's
+    BLAS sgemv and is not fixed by the reference; the tests pin the law
+    by closed forms and by its distance from the fp64 law, not bit for
+    bit."""
+    r = np.ascontiguousarray(rows, dtype=np.float32)
+    q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, r.shape[1])
+    out_ids = np.full((q.shape[0], topk), -1, dtype=np.int64)
+    out_sc = np.full((q.shape[0], topk), np.nan, dtype=np.float32)
+    counts = np.zeros(q.shape[0], dtype=np.int64)
+    for j in range(q.shape[0]):
+        s = r @ q[j]
+        keep = np.flatnonzero(np.isfinite(s))
+        sk = s[keep]
+        kk = min(topk, keep.size)
+        if kk < keep.size:
+            # the stable sort's first kk entries: every score at or above the
+            # kk-th largest (ties at that value included), in row order,
+            # then sorted stably by -score
+            part = np.argpartition(-sk, kk - 1)[:kk]
+            keep = keep[sk >= sk[part].min()]
+            sk = s[keep]
+        order = keep[np.argsort(-sk, kind="stable")][:topk]
+        out_ids[j, :order.size] = order
+        out_sc[j, :order.size] = s[order]
+        counts[j] = order.size
+    return out_ids, out_sc, counts
+
+
 def mla_route(rows: np.ndarray, queries: np.ndarray, topk: int, *,
               node_ids: np.ndarray | None = None,
               live: np.ndarray | None = None, threads: int = 0):
@@ -315,6 +365,27 @@ def mla_route(rows: np.ndarray, queries: np.ndarray, topk: int, *,
         topk, threads, _p(out_ids), _p(out_scores), _p(counts))
     if rc != 0:
         raise RuntimeError(f"oracle mla_route failed: {rc}")
+    return out_ids, out_scores, counts
+
+
+def mla_route_normed(rows: np.ndarray, norms: np.ndarray, queries: np.ndarray,
+                     topk: int, threads: int = 0):
+    """fp64 MLA law route over precomputed row norms (``mla_row_norms``):
+    the reference route's per-call work, with the norms held by its arena
+    as the reference's arena holds them.  Same returns as ``mla_route``."""
+    r = np.ascontiguousarray(rows, dtype=np.float32)
+    nr = np.ascontiguousarray(norms, dtype=np.float32)
+    q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, r.shape[1])
+    if nr.shape != (r.shape[0],):
+        raise ValueError("norms must have one value per row")
+    out_ids = np.empty((q.shape[0], topk), dtype=np.uint64)
+    out_scores = np.empty((q.shape[0], topk), dtype=np.float32)
+    counts = np.empty(q.shape[0], dtype=np.uint64)
+    rc = lib().grm_oracle_mla_route_normed(
+        _p(r), r.shape[0], r.shape[1], _p(nr), _p(q), q.shape[0], topk,
+        threads, _p(out_ids), _p(out_scores), _p(counts))
+    if rc != 0:
+        raise RuntimeError(f"oracle mla_route_normed failed: {rc}")
     return out_ids, out_scores, counts
 
 

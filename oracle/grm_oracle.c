@@ -313,6 +313,32 @@ GRM_ORACLE_EXPORT int grm_oracle_mla_route(const float* rows, uint64_t n,
   return 0;
 }
 
+/* The per-call part of route_mla_arena (cpp/grm_runtime.cpp:4299-4361):
+ * the arena build computes the row norms once (:3232-3241), so a route
+ * reads them; `norms` holds grm_oracle_mla_row_norms' output.  Used to time
+ * the CPU baseline at the reference's per-call cost. */
+GRM_ORACLE_EXPORT int grm_oracle_mla_route_normed(
+    const float* rows, uint64_t n, uint64_t dim, const float* norms,
+    const float* queries, uint64_t q_count, uint64_t topk, int threads,
+    uint64_t* out_ids, float* out_scores, uint64_t* out_counts) {
+  if (!rows || !norms || !queries || !out_ids || dim == 0 || topk == 0) {
+    return -1;
+  }
+  float* scores = (float*)malloc(sizeof(float) * (n ? n : 1));
+  if (!scores) {
+    return -2;
+  }
+  for (uint64_t qi = 0; qi < q_count; ++qi) {
+    grm_oracle_mla_scores(rows, n, dim, norms, queries + qi * dim, 1, scores,
+                          threads);
+    select_topk(scores, NULL, NULL, n, topk, out_ids + qi * topk,
+                out_scores ? out_scores + qi * topk : NULL,
+                out_counts ? out_counts + qi : NULL);
+  }
+  free(scores);
+  return 0;
+}
+
 /* ----------------------------------------------------------------- GQA */
 
 /* cpp/grm_runtime.cpp:2980-3029 (gqa_raw_score) over f32 values.

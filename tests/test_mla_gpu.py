@@ -39,6 +39,29 @@ def test_small_config_parity(hip_lib):
             assert_same(res.ids, res.scores, ids, sc)
 
 
+def test_small_config_against_python_numpy_law(hip_lib):
+    """The 10,000 x 288 workload against the reference's Python route
+    (numpy fp32 dot, stable sort; core/graft_arena.py:733-801): ids equal
+    wherever the fp32 dot's rounding bound cannot reorder the top k,
+    scores within 1e-5 relative."""
+    d, k = 288, 3
+    rows = wl.mla_rows(10_000, d, seed=1)
+    qs = wl.mla_queries(32, d, seed=1)
+    gamma = d * 2.0 ** -24 / (1 - d * 2.0 ** -24)
+    with MlaNodeBank(rows) as bank:
+        res = bank.route(qs, k)
+    ids_np, sc_np, _ = oracle.mla_route_numpy(rows, qs, k + 1)
+    absdot = np.abs(rows.astype(np.float64)) @ np.abs(qs.astype(np.float64)).T
+    compared = 0
+    for j in range(qs.shape[0]):
+        assert np.allclose(res.scores[j], sc_np[j, :k], rtol=1e-5, atol=0)
+        gaps = -np.diff(sc_np[j].astype(np.float64))
+        if np.all(gaps > 2 * gamma * absdot[:, j].max()):
+            assert res.ids[j].astype(np.int64).tolist() == ids_np[j, :k].tolist()
+            compared += 1
+    assert compared >= qs.shape[0] // 2
+
+
 @pytest.mark.parametrize("dim", [1, 3, 4, 5, 64, 127, 128, 256, 288, 300, 1000])
 def test_dims_and_ragged_tiles(hip_lib, dim):
     rng = np.random.default_rng(dim)
