@@ -37,7 +37,18 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kUnitWaves = 4;     // wavefronts per work-item block
 constexpr int kFinWaves = 4;      // wavefronts per finalize block
-constexpr int kMaxRQ = 32;        // R * Qt supported by the exact kernels
+constexpr int kMaxRQ = 32;        // query columns per kv head of one exact pass
+
+// Query passes.  A route's query has H = kv * R heads of Qt tokens; the
+// kernels below read one pass of it: heads g*R + r0 + rr (rr < Rc) of every
+// kv head g and tokens t0 + tt (tt < Qc).  The host hands a pass over as a
+// query pointer advanced by (r0 * Qt + t0) * hd values and a maxima pointer
+// advanced by r0 * cap, so the kernels index with the full R and Qt as
+// strides and with Rc and Qc as counts: the value (rr, tt, d) of kv head g
+// is element ((g*R + rr) * Qt + tt) * hd + d, and its head's maximum is at
+// (g*R + rr) * cap.  best_h is a maximum over (query token, key token), so
+// passes over disjoint parts of the query fold into one maximum with the
+// same atomicMax, in any order.
 constexpr uint32_t kMaxHeadDim = 512;
 
 // Key chunk planes.  A key row of head_dim values is C 16-byte pieces
@@ -139,18 +150,20 @@ __device__ inline void decode_chunk(u32x4 v, float scale, float* out) {
 
 // ----------------------------------------------------------------- exact
 
-// Query rows as doubles for the exact kernels: q64[((qb * kv + g) * hd + d)
-// * RQP + j] = q[qb][g*R + j/Qt][j%Qt][d] for j < R*Qt, 0 for the padding
-// rows j < RQP.  The d-major order lets a wave read the RQP values of one
-// d as one wave-uniform (scalar) load.  qflags[qb * kv + g] = 1 when a
-// value of query qb read by kv head g is non-finite, else 0.  grid (kv, Qb).
+// Query rows of one pass as doubles for the exact kernels:
+// q64[((qb * kv + g) * hd + d) * RQP + j] = value (j / Qc, j % Qc, d) of kv
+// head g for j < Rc*Qc, 0 for the padding rows j < RQP.  The d-major order
+// lets a wave read the RQP values of one d as one wave-uniform (scalar)
+// load.  qflags[qb * kv + g] = 1 when a value of query qb read by kv head g
+// is non-finite; the first pass (flags_or = 0) writes 0 otherwise, later
+// passes leave the flag as it is.  grid (kv, Qb).
 __global__ __launch_bounds__(256) void gqa_q64_kernel(
-    const void* __restrict__ query, int q_dtype, size_t q_elems, int Qt,
-    int hd, int kv, int R, int RQP, double* __restrict__ q64,
-    unsigned* __restrict__ qflags) {
+    const void* __restrict__ query, int q_dtype, size_t q_elems, int Qt, int Qc,
+    int hd, int kv, int R, int Rc, int RQP, double* __restrict__ q64,
+    unsigned* __restrict__ qflags, int flags_or) {
   const int g = blockIdx.x;
   const int qb = blockIdx.y;
-  const int rq = R * Qt;
+  const int rq = Rc * Qc;
   bool bad = false;
   for (int idx = threadIdx.x; idx < RQP * hd; idx += blockDim.x) {
     const int d = idx / RQP;
@@ -158,7 +171,7 @@ __global__ __launch_bounds__(256) void gqa_q64_kernel(
     double v = 0.0;
     if (j < rq) {
       const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
-                           (static_cast<uint64_t>(g * R + j / Qt) * Qt + j % Qt) * hd + d;
+                           (static_cast<uint64_t>(g * R + j / Qc) * Qt + j % Qc) * hd + d;
       const float f = q_dtype == kBF16
                           ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
                           : static_cast<const float*>(query)[src];
@@ -168,7 +181,7 @@ __global__ __launch_bounds__(256) void gqa_q64_kernel(
     q64[(static_cast<size_t>(qb * kv + g) * hd + d) * RQP + idx % RQP] = v;
   }
   bad = __syncthreads_or(bad);
-  if (threadIdx.x == 0) qflags[qb * kv + g] = bad ? 1u : 0u;
+  if (threadIdx.x == 0 && (bad || !flags_or)) qflags[qb * kv + g] = bad ? 1u : 0u;
 }
 
 // Chunks per stage of the pipelined exact kernel (two stages live in
@@ -196,7 +209,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
     const unsigned char* __restrict__ keys,
     const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
     const Item* __restrict__ items, uint32_t n_items, const uint32_t* __restrict__ n_items_dev,
-    int kv, int hd, int sS, int R, int Qt, const double* __restrict__ q64, double denom,
+    int kv, int hd, int sS, int R, int Rc, int Qc, const double* __restrict__ q64, double denom,
     unsigned long long* __restrict__ hmax, size_t hstride, size_t cap) {
   using T = KeyTraits<KDT>;
   const int lane = threadIdx.x & (kWave - 1);
@@ -255,12 +268,12 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
     }
   };
   auto emit = [&](const Item& it, int g) {
-    const int rq_used = R * Qt;
-    for (int r = 0; r < R; ++r) {
+    const int rq_used = Rc * Qc;
+    for (int r = 0; r < Rc; ++r) {
       double m = 0.0;
 #pragma unroll
       for (int j = 0; j < RQ; ++j) {
-        if (j / Qt == r && j < rq_used) m = (best[j] > m || isnan(best[j])) ? best[j] : m;
+        if (j / Qc == r && j < rq_used) m = (best[j] > m || isnan(best[j])) ? best[j] : m;
       }
       // max(|dot|)/denom equals the law's max(|dot|/denom): division by a
       // positive constant is monotone under rounding to nearest
@@ -502,9 +515,10 @@ constexpr int kMaxCols = 64;  // query columns (Qb * R * Qt) per screen pass
 
 // ------------------------------------------------------- query columns
 //
-// A screen pass reads kv head g's query columns: column cg = (qb*R + r)*Qt
-// + qi (cg < cols) is query qb's row of head g*R + r at query token qi,
-// q_elems values after query qb-1's.
+// A screen pass reads kv head g's query columns: column cg = (qb*Rc + rr)*Qc
+// + tt (cg < cols) is query qb's row of head g*R + rr at query token tt of
+// the pass (strides R and Qt, see "Query passes"), q_elems values after
+// query qb-1's.
 
 // Block-wide: stage the columns in s_q[cg][HD] as fp32 (exact: queries are
 // fp32 or bf16) and derive each column's screen parameters
@@ -525,19 +539,19 @@ constexpr int kMaxCols = 64;  // query columns (Qb * R * Qt) per screen pass
 template <int HD>
 __device__ inline void stage_columns(float* __restrict__ s_q, float4* __restrict__ s_ec,
                                      unsigned* __restrict__ s_bad, const void* __restrict__ query,
-                                     int q_dtype, size_t q_elems, int cols, int R, int Qt, int g,
-                                     int emax, double gamma, double delta, double rho,
-                                     double sigma_q, double sigma_k, double sigma_p) {
+                                     int q_dtype, size_t q_elems, int cols, int R, int Qt, int Rc,
+                                     int Qc, int g, int emax, double gamma, double delta,
+                                     double rho, double sigma_q, double sigma_k, double sigma_p) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nwaves = blockDim.x / kWave;
-  const int RQc = R * Qt;
+  const int RQc = Rc * Qc;
   for (int i = threadIdx.x; i < cols * HD; i += blockDim.x) {
     const int cg = i / HD;
     const int qb = cg / RQc;
-    const int r = (cg % RQc) / Qt;
+    const int r = (cg % RQc) / Qc;
     const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
-                         (static_cast<uint64_t>(g * R + r) * Qt + cg % Qt) * HD + (i - cg * HD);
+                         (static_cast<uint64_t>(g * R + r) * Qt + cg % Qc) * HD + (i - cg * HD);
     s_q[i] = q_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
                               : static_cast<const float*>(query)[src];
   }
@@ -679,11 +693,12 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
 // grid's y limit, (ceil(items / 4), kv heads) -- one wavefront per
 // (item, kv head g).
 //
-// Each block first stages kv head g's query columns of the Qb queries
-// (stage_columns: fp32 values for the screen fragments and the exact
-// recomputation, scale and error-bound parameters per column); the blocks
-// of item block 0 write qflags[qb*kv + g] = 1 when a value of query qb read
-// by kv head g is non-finite (0 otherwise).
+// Each block first stages kv head g's query columns of the Qb queries for
+// the pass (stage_columns: fp32 values for the screen fragments and the
+// exact recomputation, scale and error-bound parameters per column); the
+// blocks of item block 0 write qflags[qb*kv + g] = 1 when a value of query
+// qb read by kv head g is non-finite (0 otherwise on the first pass,
+// flags_or = 0; later passes only raise it).
 // Columns with a non-finite value take no part in the screen (every score
 // of that query is NaN).  The item's tokens stream in 16-token tiles, two
 // tiles ahead of the one being screened.  Lane l sees column
@@ -694,16 +709,16 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
 // candidates are among the kept two and are recomputed exactly, otherwise
 // the item is screened again tile by tile and every token at or above the
 // threshold is recomputed.  The per-column exact maxima, divided by
-// sqrt(hd) (monotone), fold into hmax[qb*hstride + (g*R + r)*cap + slot]
+// sqrt(hd) (monotone), fold into hmax[qb*hstride + (g*R + rr)*cap + slot]
 // (double bits, atomicMax).
 template <int KDT, int KS, int NT>
 __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     const unsigned char* __restrict__ keys,
     const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
-    const Item* __restrict__ items, uint32_t n_items, int kv, int R, int Qt,
+    const Item* __restrict__ items, uint32_t n_items, int kv, int R, int Qt, int Rc, int Qc,
     const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
     double gamma, double delta, double sigma_q, double sigma_k, double sigma_p,
-    unsigned* __restrict__ qflags, const float* __restrict__ kmax, double denom,
+    unsigned* __restrict__ qflags, int flags_or, const float* __restrict__ kmax, double denom,
     unsigned long long* __restrict__ hmax, size_t hstride, size_t cap, int g_fast) {
   using KT = KeyTraits<KDT>;
   constexpr int MT = ScreenTraits<KDT>::kMfma;
@@ -718,7 +733,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
   // neighbouring kv-head blocks; else grid (item blocks, kv)
   const int g = g_fast ? blockIdx.x : blockIdx.y;
   const uint32_t item_block = g_fast ? blockIdx.y : blockIdx.x;
-  const int RQc = R * Qt;
+  const int RQc = Rc * Qc;
   const int cols = Qb * RQc;
   // The wave's first tiles are requested before the block prepares its
   // query columns, so the two overlap; a wave without an item issues no
@@ -775,13 +790,13 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     load_tile(x2, 2);
     load_tile(x3, 3);
   }
-  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, g, emax, gamma, delta,
-                    0.0, sigma_q, sigma_k, sigma_p);
+  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, Rc, Qc, g, emax,
+                    gamma, delta, 0.0, sigma_q, sigma_k, sigma_p);
   __syncthreads();
   if (item_block == 0 && threadIdx.x < static_cast<unsigned>(Qb)) {
     unsigned bad = 0u;
     for (int j = 0; j < RQc; ++j) bad |= s_bad[threadIdx.x * RQc + j];
-    qflags[threadIdx.x * kv + g] = bad;
+    if (bad || !flags_or) qflags[threadIdx.x * kv + g] = bad;
   }
   if (!has_item) return;
 
@@ -953,7 +968,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     const int cg = nt * 16 + lane;
     if (lane < 16 && cg < cols && bits != 0ull) {
       const int qb = cg / RQc;
-      const int r = (cg % RQc) / Qt;
+      const int r = (cg % RQc) / Qc;
       atomicMax(hmax + qb * hstride + static_cast<size_t>(g * R + r) * cap + it.slot, bits);
     }
   }
@@ -1128,8 +1143,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     load_next(x2);
     load_next(x3);
   }
-  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, g, emax, gamma, delta,
-                    rho, sigma_q, sigma_k, sigma_p);
+  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, R, Qt, g, emax,
+                    gamma, delta, rho, sigma_q, sigma_k, sigma_p);
   if (blockIdx.x == 0) {
     for (int cg = threadIdx.x; cg < cols; cg += blockDim.x) {
       float4 e = s_ec[cg];

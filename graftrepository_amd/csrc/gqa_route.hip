@@ -526,6 +526,36 @@ int rq_pad_of(int rq) {
   return p;
 }
 
+// One pass over part of a route's query: heads g*R + r0 .. +rc of every kv
+// head g, tokens t0 .. +qc (see "Query passes" in gqa_kernels.hpp).
+struct QPass {
+  int r0 = 0, rc = 0, t0 = 0, qc = 0;
+};
+
+// Passes that cover R heads per kv head x Qt tokens with at most `cmax`
+// query columns (rc * qc) each: the whole query when it fits, else runs of
+// tokens of all R heads, else (R > cmax) runs of heads of one token.
+std::vector<QPass> query_passes(int R, int Qt, int cmax) {
+  std::vector<QPass> out;
+  if (R * Qt <= cmax) {
+    out.push_back({0, R, 0, Qt});
+  } else if (R <= cmax) {
+    const int qc = cmax / R;
+    for (int t0 = 0; t0 < Qt; t0 += qc) out.push_back({0, R, t0, std::min(qc, Qt - t0)});
+  } else {
+    for (int t0 = 0; t0 < Qt; ++t0) {
+      for (int r0 = 0; r0 < R; r0 += cmax) out.push_back({r0, std::min(cmax, R - r0), t0, 1});
+    }
+  }
+  return out;
+}
+
+// Byte offset of a pass's first query value (head r0, token t0 of kv head
+// 0) from the query's start.
+size_t pass_query_offset(const GqaDeviceArena* a, int Qt, const QPass& ps, int q_dtype) {
+  return (static_cast<size_t>(ps.r0) * Qt + ps.t0) * a->hd * (q_dtype == kF32 ? 4 : 2);
+}
+
 // Maxima for up to qb queries; all zero between routes (the finalize
 // kernel re-zeroes what it reads).
 int ensure_hmax(GqaDeviceArena* a, int H, int qb) {
@@ -550,25 +580,28 @@ int launch_finalize(GqaDeviceArena* a, int H, int qb, int topk, uint32_t fin_blo
 
 // --------------------------------------------------------------- exact path
 
-// Query rows of queries [0, qb) at q as doubles in d_q64; d_qbad records
-// non-finite values.
-int launch_q64(GqaDeviceArena* a, const void* q, int q_dtype, int qb, int H, int Qt) {
+// Query rows of pass `ps` of queries [0, qb) at q (the query's start) as
+// doubles in d_q64; d_qbad records non-finite values (written by the first
+// pass, raised by later ones: flags_or).
+int launch_q64(GqaDeviceArena* a, const void* q, int q_dtype, int qb, int H, int Qt,
+               const QPass& ps, bool flags_or) {
   const int R = H / static_cast<int>(a->kv);
-  const int rq_pad = rq_pad_of(R * Qt);
+  const int rq_pad = rq_pad_of(ps.rc * ps.qc);
   GRM_CHECK_RC(reserve_device(&a->d_q64, &a->d_q64_count,
                               static_cast<size_t>(qb) * a->kv * a->hd * rq_pad));
   GRM_CHECK_RC(reserve_device(&a->d_qbad, &a->d_qbad_count, static_cast<size_t>(qb) * a->kv));
   grm::gqa::gqa_q64_kernel<<<dim3(a->kv, qb), 256, 0, a->stream>>>(
-      q, q_dtype, static_cast<size_t>(H) * Qt * a->hd, Qt, static_cast<int>(a->hd),
-      static_cast<int>(a->kv), R, rq_pad, a->d_q64, a->d_qbad);
+      static_cast<const unsigned char*>(q) + pass_query_offset(a, Qt, ps, q_dtype), q_dtype,
+      static_cast<size_t>(H) * Qt * a->hd, Qt, ps.qc, static_cast<int>(a->hd),
+      static_cast<int>(a->kv), R, ps.rc, rq_pad, a->d_q64, a->d_qbad, flags_or ? 1 : 0);
   GRM_HIP_CHECK(hipGetLastError());
   return 0;
 }
 
-// Exact maxima of the bank's items against query 0, or (n_items_dev given)
-// of the device-built list `items` (at most max_items), each item against
-// its own query.
-int launch_exact(GqaDeviceArena* a, int H, int Qt, const Item* items = nullptr,
+// Exact maxima of pass `ps` (rows in d_q64, launch_q64) of the bank's items
+// against query 0, or (n_items_dev given) of the device-built list `items`
+// (at most max_items), each item against its own query.
+int launch_exact(GqaDeviceArena* a, int H, const QPass& ps, const Item* items = nullptr,
                  uint64_t max_items = 0, const uint32_t* n_items_dev = nullptr) {
   if (!n_items_dev) {
     items = a->d_items;
@@ -576,7 +609,8 @@ int launch_exact(GqaDeviceArena* a, int H, int Qt, const Item* items = nullptr,
   }
   if (max_items == 0) return 0;
   const int R = H / static_cast<int>(a->kv);
-  const int rq_pad = rq_pad_of(R * Qt);
+  const int rq_pad = rq_pad_of(ps.rc * ps.qc);
+  if (rq_pad > grm::gqa::kMaxRQ) return grm::fail(-1, "exact pass wider than 32 columns");
   // Persistent stream: about exact_waves wavefronts, each walking the
   // (kv head, item) pairs w, w+W, ...; device-built lists get a fixed
   // number of waves, since their length is known only on the device
@@ -591,7 +625,8 @@ int launch_exact(GqaDeviceArena* a, int H, int Qt, const Item* items = nullptr,
   grm::gqa::gqa_exact_kernel<KDT, RQ, grm::gqa::exact_stage_chunks<KDT, RQ>()><<<grid, threads, 0, a->stream>>>( \
       a->d_keys, a->d_scales, a->scale_dtype, a->group_size, items,                         \
       static_cast<uint32_t>(max_items), n_items_dev, static_cast<int>(a->kv),                 \
-      static_cast<int>(a->hd), a->piece_shift, R, Qt, a->d_q64, denom, a->d_hmax,             \
+      static_cast<int>(a->hd), a->piece_shift, R, ps.rc, ps.qc, a->d_q64, denom,              \
+      a->d_hmax + static_cast<size_t>(ps.r0) * a->cap_nodes,                                   \
       a->cap_nodes * static_cast<size_t>(H), a->cap_nodes)
 #define GRM_EXACT_RQ(KDT)                       \
   switch (rq_pad) {                             \
@@ -614,12 +649,16 @@ int launch_exact(GqaDeviceArena* a, int H, int Qt, const Item* items = nullptr,
   return 0;
 }
 
-// Enqueue the exact route of one query; its per-block top-k lands at bout.
+// Enqueue the exact route of one query, in passes of at most 32 query
+// columns per kv head; its per-block top-k lands at bout.
 int enqueue_exact(GqaDeviceArena* a, const void* q, int q_dtype, int H, int Qt, int topk,
                   uint32_t fin_blocks, Cand* bout) {
   GRM_CHECK_RC(ensure_hmax(a, H, 1));
-  GRM_CHECK_RC(launch_q64(a, q, q_dtype, 1, H, Qt));
-  GRM_CHECK_RC(launch_exact(a, H, Qt));
+  const auto passes = query_passes(H / static_cast<int>(a->kv), Qt, grm::gqa::kMaxRQ);
+  for (size_t i = 0; i < passes.size(); ++i) {
+    GRM_CHECK_RC(launch_q64(a, q, q_dtype, 1, H, Qt, passes[i], i > 0));
+    GRM_CHECK_RC(launch_exact(a, H, passes[i]));
+  }
   return launch_finalize(a, H, 1, topk, fin_blocks, bout);
 }
 
@@ -639,6 +678,7 @@ struct SrPlan {
   int KS = 0;        // head_dim / 32
   int qb_max = 0;    // queries per pass (<= 64 columns)
   int mfma = kBF16;  // MFMA operand type
+  std::vector<QPass> passes;  // query passes of one query (one unless R*Qt > 64)
 };
 
 // Maxima memory per pass is bounded by this many bytes (when one query
@@ -650,14 +690,18 @@ bool sr_plan(const GqaDeviceArena* a, int H, int Qt, SrPlan* p) {
   if (a->hd != 64 && a->hd != 128 && a->hd != 256) return false;
   if (a->piece_shift != 2) return false;  // the screen reads 64-byte chunks
   const int R = H / static_cast<int>(a->kv);
-  if (R * Qt > grm::gqa::kMaxCols) return false;
   p->R = R;
   p->Qt = Qt;
   p->H = H;
   p->KS = static_cast<int>(a->hd / 32);
+  p->passes = query_passes(R, Qt, grm::gqa::kMaxCols);
   const size_t per_q = a->cap_nodes * static_cast<size_t>(H) * sizeof(unsigned long long);
-  p->qb_max = std::max(1, std::min(grm::gqa::kMaxCols / (R * Qt),
-                                   static_cast<int>(std::max<size_t>(1, kMaxHmaxBytes / per_q))));
+  // a query wider than one pass is routed alone, its passes one after another
+  const int cols1 = p->passes.size() == 1 ? R * Qt : grm::gqa::kMaxCols;
+  p->qb_max = p->passes.size() == 1
+                  ? std::max(1, std::min(grm::gqa::kMaxCols / cols1,
+                                         static_cast<int>(std::max<size_t>(1, kMaxHmaxBytes / per_q))))
+                  : 1;
   p->mfma = a->key_dtype == kBF16 ? kBF16 : kF16;
   return true;
 }
@@ -668,57 +712,69 @@ int prepare_sr(GqaDeviceArena* a, const SrPlan& p) {
   return ensure_hmax(a, p.H, p.qb_max);
 }
 
-// Enqueue one screen-and-refine pass over queries [0, qb) at qptr (device,
-// `qstride` bytes apart); their per-block top-k lands at bout, and with
-// `done` the finalize blocks' completion flags at done[0, qb*fin_blocks).
-// Launches only (prepare_sr allocates).
-int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
-               int topk, uint32_t fin_blocks, Cand* bout, unsigned* done) {
+// Screen-bound constants of one route (per query column, see
+// gqa_sr_kernel and gqa_smax_kernel):
+//   gamma  fp32 accumulation of hd products, MFMA internal order unknown
+//   delta  rounding of an fp32 query value to the MFMA type
+//   sigma_q, sigma_k  a query / key value near zero flushed or rounded
+//   sigma_p  a product lost to fp32 underflow
+//   emax   the exponent under which scaled query values stay
+struct ScreenBound {
+  double gamma = 0, delta = 0, sigma_q = 0, sigma_k = 0, sigma_p = 0;
+  int emax = 0;
+};
+
+ScreenBound screen_bound(const GqaDeviceArena* a, const SrPlan& p, int q_dtype) {
+  ScreenBound b;
+  b.gamma = 2.0 * (a->hd + 2.0 * p.KS) * ldexp(1.0, -24);
+  if (p.mfma == kBF16) {
+    b.delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
+    b.sigma_q = b.sigma_k = b.sigma_p = ldexp(1.0, -125);
+    b.emax = 126;
+  } else {
+    b.delta = q_dtype == kF32 ? ldexp(1.0, -11) : 0.0;
+    b.sigma_q = b.sigma_k = ldexp(1.0, -14);
+    b.sigma_p = 0.0;
+    b.emax = 15;
+  }
+  return b;
+}
+
+// One screen-and-refine launch: query pass `pi` of queries [0, qb) at qptr
+// (the queries' start) against every (item, kv head), folding into the
+// maxima; the first pass writes the query flags, later ones raise them.
+int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
+                   const unsigned char* qptr, int q_dtype, int qb, size_t pi) {
   const int kv = static_cast<int>(a->kv);
-  const int RQ = p.R * p.Qt;
-  const int cols = qb * RQ;
+  const QPass& ps = p.passes[pi];
+  if (a->n_items == 0) {
+    // no key tokens at all: only the query flags are needed
+    return launch_q64(a, qptr, q_dtype, qb, p.H, p.Qt, ps, pi > 0);
+  }
+  const int cols = qb * ps.rc * ps.qc;
   const int nt_need = (cols + 15) / 16;
   const int NT = nt_need <= 1 ? 1 : (nt_need <= 2 ? 2 : 4);
-  const int H = p.H;
-  // Error-bound constants (per query column, see gqa_sr_kernel):
-  //   gamma  fp32 accumulation of hd products, MFMA internal order unknown
-  //   delta  rounding of an fp32 query value to the MFMA type
-  //   sigma_q, sigma_k  a query / key value near zero flushed or rounded
-  //   sigma_p  a product lost to fp32 underflow
-  const double gamma = 2.0 * (a->hd + 2.0 * p.KS) * ldexp(1.0, -24);
-  double delta, sigma_q, sigma_k, sigma_p;
-  int emax;
-  if (p.mfma == kBF16) {
-    delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
-    sigma_q = sigma_k = sigma_p = ldexp(1.0, -125);
-    emax = 126;
-  } else {
-    delta = q_dtype == kF32 ? ldexp(1.0, -11) : 0.0;
-    sigma_q = sigma_k = ldexp(1.0, -14);
-    sigma_p = 0.0;
-    emax = 15;
-  }
-  const size_t q_elems = static_cast<size_t>(H) * p.Qt * a->hd;
-  // 1. screen and refine every (item, kv head), preparing the query
-  // columns in each block
-  if (a->n_items > 0) {
-    // kv heads fastest, so the resident blocks sweep the bank in address
-    // order (a node's kv-head blocks are contiguous); item blocks on x only
-    // past the grid's y limit
-    const uint64_t item_blocks = (a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves;
-    const int g_fast = item_blocks <= 65535 ? 1 : 0;
-    const dim3 grid = g_fast ? dim3(a->kv, static_cast<unsigned>(item_blocks))
-                             : dim3(static_cast<unsigned>(item_blocks), a->kv);
-    const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
-    const size_t hstride = a->cap_nodes * static_cast<size_t>(H);
-    const double denom = sqrt(static_cast<double>(a->hd));
-    const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);  // <= 64 KiB
+  const unsigned char* qpass = qptr + pass_query_offset(a, p.Qt, ps, q_dtype);
+  unsigned long long* hpass = a->d_hmax + static_cast<size_t>(ps.r0) * a->cap_nodes;
+  const size_t q_elems = static_cast<size_t>(p.H) * p.Qt * a->hd;
+  // kv heads fastest, so the resident blocks sweep the bank in address
+  // order (a node's kv-head blocks are contiguous); item blocks on x only
+  // past the grid's y limit
+  const uint64_t item_blocks = (a->n_items + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves;
+  const int g_fast = item_blocks <= 65535 ? 1 : 0;
+  const dim3 grid = g_fast ? dim3(a->kv, static_cast<unsigned>(item_blocks))
+                           : dim3(static_cast<unsigned>(item_blocks), a->kv);
+  const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
+  const size_t hstride = a->cap_nodes * static_cast<size_t>(p.H);
+  const double denom = sqrt(static_cast<double>(a->hd));
+  const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);  // <= 64 KiB
 #define GRM_SR(KDT, KS, NTT)                                                                    \
   grm::gqa::gqa_sr_kernel<KDT, KS, NTT><<<grid, threads, lds, a->stream>>>(                     \
       a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                        \
-      static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, qptr, q_dtype, q_elems, qb, emax, gamma,  \
-      delta, sigma_q, sigma_k, sigma_p, a->d_qbad, reinterpret_cast<const float*>(a->d_kmax),     \
-      denom, a->d_hmax, hstride, a->cap_nodes, g_fast)
+      static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, ps.rc, ps.qc, qpass, q_dtype, q_elems,  \
+      qb, eb.emax, eb.gamma, eb.delta, eb.sigma_q, eb.sigma_k, eb.sigma_p, a->d_qbad,           \
+      pi > 0 ? 1 : 0, reinterpret_cast<const float*>(a->d_kmax), denom, hpass, hstride,          \
+      a->cap_nodes, g_fast)
 #define GRM_SR_NT(KDT, KS)                 \
   switch (NT) {                            \
     case 1: GRM_SR(KDT, KS, 1); break;     \
@@ -731,29 +787,41 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
     case 4: GRM_SR_NT(KDT, 4); break;      \
     default: GRM_SR_NT(KDT, 8); break;     \
   }
-    switch (a->key_dtype) {
-      case kBF16: GRM_SR_KS(kBF16); break;
-      case kF16: GRM_SR_KS(kF16); break;
-      default: GRM_SR_KS(kI8); break;
-    }
+  switch (a->key_dtype) {
+    case kBF16: GRM_SR_KS(kBF16); break;
+    case kF16: GRM_SR_KS(kF16); break;
+    default: GRM_SR_KS(kI8); break;
+  }
 #undef GRM_SR_KS
 #undef GRM_SR_NT
 #undef GRM_SR
-    GRM_HIP_CHECK(hipGetLastError());
-  } else {
-    // no key tokens at all: only the query flags are needed
-    GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt));
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
+// Enqueue the screen-and-refine route of queries [0, qb) at qptr (device,
+// `qstride` bytes apart): its query passes one after another, all folding
+// into the same maxima, then the finalize.  Their per-block top-k lands at
+// bout, and with `done` the finalize blocks' completion flags at
+// done[0, qb*fin_blocks).  Launches only (prepare_sr allocates).
+int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
+               int topk, uint32_t fin_blocks, Cand* bout, unsigned* done) {
+  const ScreenBound eb = screen_bound(a, p, q_dtype);
+  for (size_t pi = 0; pi < p.passes.size(); ++pi) {
+    GRM_CHECK_RC(launch_sr_pass(a, p, eb, qptr, q_dtype, qb, pi));
   }
-  // 2. exact scores and per-block top-k
-  return launch_finalize(a, H, qb, topk, fin_blocks, bout, nullptr, nullptr, done);
+  return launch_finalize(a, p.H, qb, topk, fin_blocks, bout, nullptr, nullptr, done);
 }
 
 // ------------------------------------------------------ bound-and-verify path
 
 constexpr uint32_t kCandFinBlocks = 16;  // finalize blocks per query over candidates
 
+// Bound and verify keeps per-column maxima of one pass and verifies in one
+// exact pass: routes whose query has at most 32 columns per kv head.
 bool use_bound(const GqaDeviceArena* a, const SrPlan& p, int qb) {
   if (a->bound_mode == 0) return false;
+  if (p.passes.size() != 1 || p.R * p.Qt > grm::gqa::kMaxRQ) return false;
   if (a->bound_mode == 1) return true;
   return qb * p.R * p.Qt > 16;
 }
@@ -816,26 +884,17 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   // error-bound constants as in enqueue_sr; rho: the INT8 row scale
   // factored out of the dot product (fp32 product then fp16 rounding of
   // code*scale, and the fp32 product of the screened value by the scale)
-  const double gamma = 2.0 * (a->hd + 2.0 * p.KS) * ldexp(1.0, -24);
-  double delta, sigma_q, sigma_k, sigma_p;
-  int emax;
-  if (p.mfma == kBF16) {
-    delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
-    sigma_q = sigma_k = sigma_p = ldexp(1.0, -125);
-    emax = 126;
-  } else {
-    delta = q_dtype == kF32 ? ldexp(1.0, -11) : 0.0;
-    sigma_q = sigma_k = ldexp(1.0, -14);
-    sigma_p = 0.0;
-    emax = 15;
-  }
+  const ScreenBound eb = screen_bound(a, p, q_dtype);
+  const double gamma = eb.gamma, delta = eb.delta, sigma_q = eb.sigma_q, sigma_k = eb.sigma_k,
+               sigma_p = eb.sigma_p;
+  const int emax = eb.emax;
   const double rho = fact ? ldexp(1.0, -11) + ldexp(1.0, -21) : 0.0;
   const size_t q_elems = static_cast<size_t>(H) * p.Qt * a->hd;
   // screened maxima: one run of colstride cells per (slot, kv head)
   const int colstride = p.qb_max * RQ;
   const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
   // 1. query rows as doubles and the query flags (for the exact pass)
-  GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt));
+  GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, p.passes[0], false));
   // 2. screened maxima of every (column, node)
   if (a->n_units > 0) {
     const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);
@@ -899,8 +958,8 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
       a->d_ccount + p.qb_max);
   GRM_HIP_CHECK(hipGetLastError());
   // 5. the law on the candidates, then their exact scores and top-k
-  GRM_CHECK_RC(launch_exact(a, H, p.Qt, a->d_citems, static_cast<uint64_t>(qb) * a->n_items,
-                            a->d_ccount + p.qb_max));
+  GRM_CHECK_RC(launch_exact(a, H, p.passes[0], a->d_citems,
+                            static_cast<uint64_t>(qb) * a->n_items, a->d_ccount + p.qb_max));
   (void)per_q;
   return launch_finalize(a, H, qb, topk, std::min(kCandFinBlocks, fin_blocks), bout, a->d_cslots,
                          a->d_ccount);
@@ -921,8 +980,6 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   if (topk <= 0 || topk > grm::kMaxTopK || static_cast<uint64_t>(topk) > a->live) {
     return grm::fail(-1, "topk must be in [1, 16] and <= live nodes");
   }
-  const int R = H / static_cast<int>(a->kv);
-  if (R * Qt > grm::gqa::kMaxRQ) return grm::fail(-1, "(heads / kv_heads) * query_tokens above 32");
   GRM_HIP_CHECK(hipSetDevice(a->device));
   if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
   GRM_CHECK_RC(ensure_items(a));
