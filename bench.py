@@ -487,6 +487,19 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
                         query_shape=q4.shape).device_ms
              for _ in range(min(steps, 100))]
     dq4.close()
+    # a 64-token query (a prompt-length probe key): 256 query columns per
+    # kv head, routed in four passes of 64
+    q64 = wl.gqa_queries(1, H, 64, hd, cfg["seed"] + 2)
+    dq64 = probe.upload_queries(q64.view(np.float32))
+    for _ in range(3):
+        bank.route(dq64, cfg["topk"], on_device=True, query_dtype="bf16", query_shape=q64.shape)
+    walls64 = [bank.route(dq64, cfg["topk"], on_device=True, query_dtype="bf16",
+                          query_shape=q64.shape, timed=False).wall_ms
+               for _ in range(max(1, steps // 4))]
+    devs64 = [bank.route(dq64, cfg["topk"], on_device=True, query_dtype="bf16",
+                         query_shape=q64.shape).device_ms
+              for _ in range(min(steps, 50))]
+    dq64.close()
     bank.close()
     sum_l = int(offs[-1])
     bytes_per_call = sum_l * kv * hd * 2
@@ -495,6 +508,20 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
     qt4 = {"query_tokens": 4, "p50_ms": round(pct(walls4, 50), 5),
            "device_ms_mean": round(float(np.mean(devs4)), 5),
            "achieved_gbs": round(bytes_per_call / (float(np.mean(devs4)) * 1e-3) / 1e9, 1)}
+    d64 = float(np.mean(devs64))
+    flops64 = 2.0 * sum_l * kv * (H // kv) * 64 * hd
+    t_floor = max(bytes_per_call / (HBM_PEAK_GBS * 1e9), flops64 / 2.5e15)
+    qt64 = {"query_tokens": 64, "query_columns_per_kv_head": (H // kv) * 64,
+            "p50_ms": round(pct(walls64, 50), 5), "device_ms_mean": round(d64, 5),
+            "roofline": {"bound": "hbm", "achieved": round(bytes_per_call / (d64 * 1e-3) / 1e9, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(bytes_per_call / (d64 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "bytes_per_call": bytes_per_call, "flops_per_call": flops64,
+                         "mfma_tflops": round(flops64 / (d64 * 1e-3) / 1e12, 1),
+                         "floor_ms": round(t_floor * 1e3, 5),
+                         "frac_of_floor": round(t_floor * 1e3 / d64, 4)}}
+    log(f"[gqa qt64] p50 {qt64['p50_ms']:.4f} ms  device {d64:.4f} ms  "
+        f"floor {t_floor * 1e3:.4f} ms ({qt64['roofline']['frac_of_floor']:.2f} of it)")
     log(f"[gqa qt4] p50 {qt4['p50_ms']:.4f} ms  device {qt4['device_ms_mean']:.4f} ms"
         f"  {qt4['achieved_gbs']:.0f} GB/s")
     log(f"[gqa] sumL {sum_l}  p50 {pct(walls, 50):.4f} ms  p99 {pct(walls, 99):.4f} ms"
@@ -508,7 +535,7 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
                 scores=r.scores[0].copy(), walls=walls, devs=devs,
                 bytes=bytes_per_call, achieved=achieved, mean_dev=mean_dev,
                 timed_p50=pct(timed_walls, 50), qt4=qt4,
-                sum_l=sum_l, cfg=cfg, kv=kv, H=H)
+                sum_l=sum_l, cfg=cfg, kv=kv, H=H, qt64=qt64)
 
 
 def cpu_baseline_gqa_int8(codes, scales, offs, kv, hd, q_bits, k):
@@ -994,6 +1021,7 @@ def main() -> int:
             "device_ms_mean": round(g["mean_dev"], 5),
             "timed_calls_p50_ms": round(g["timed_p50"], 5),
             "query_tokens_4": g["qt4"],
+            "query_tokens_64": g["qt64"],
             "cpu_baseline": g["cpu"],
             "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",

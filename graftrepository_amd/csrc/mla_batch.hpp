@@ -10,12 +10,19 @@
 //
 //  * screen  -- every node tile (32 slots) against every query of a pass
 //               (up to 256, staged in LDS).  The screened score
-//               s~ = acc * (1/norm_f) * (1/qnorm) obeys |s~ - score| <= B,
-//               B a per-query constant (see mla_batch_merge_kernel).
-//               Each lane follows one query over half of every tile its
-//               wavefront walks and keeps the two best (s~, slot) and the
-//               largest s~ it did not keep; the two halves of a query are
+//               s~ = u * (1/qnorm), u = acc * (1/norm_f) with the slot's
+//               index written into the low `ibits` mantissa bits of u,
+//               obeys |s~ - score| <= B, B a per-query constant (see
+//               mla_batch_merge_kernel).  Each lane follows one query over
+//               half of every tile its wavefront walks and keeps the three
+//               largest u: the two best (each carrying its slot) and the
+//               largest it did not keep; the two halves of a query are
 //               merged at the end, one sub-stream per (wavefront, query).
+//               "Largest" is the order of u's bits as a signed integer,
+//               which is the float order on values >= +0 and puts every
+//               negative value (and -0) below them; the merge certifies a
+//               query only when its threshold t is positive, so only
+//               positive values decide.
 //  * merge   -- one block per query over the sub-streams' kept entries:
 //               v_k = the k-th best kept s~, t = v_k - 2B.  A node whose
 //               s~ lies below t scores below v_k - B, so if every
@@ -36,17 +43,37 @@ namespace mla {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// v_med3_i32 and v_and_or_b32: the compiler forms neither from the
+// equivalent min/max and and/or expressions, and the screen's per-score
+// work is these two instructions and a maximum.
+// b = med3(a, b, c), in place
+__device__ __forceinline__ void med3_i32_into(int a, int& b, int c) {
+  asm("v_med3_i32 %0, %1, %0, %2" : "+v"(b) : "v"(a), "v"(c));
+}
+__device__ __forceinline__ uint32_t and_or_b32(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 constexpr int kBatchWaves = 8;       // wavefronts per screen block (one block per CU)
 constexpr int kBatchMaxCols = 256;   // queries per screen pass
-constexpr int kEntryPlanes = 5;      // s1, s2, nk, i1, i2
+constexpr int kEntryPlanes = 3;      // u1, u2, nk
 
 // Screen results, one row of n_sub values per (plane, query): plane p of
 // query q at planes + (p*QP + q)*n_sub, sub-stream i = the wavefront:
-//   s1, s2  the two best s~ a sub-stream kept (float bits), i1, i2 their
-//   slots, nk the largest s~ it did not keep.
+//   u1, u2  the two best u a sub-stream kept (float bits, slot code in
+//   the low ibits bits), nk the largest u it did not keep.
+//
+// Slot code of a value: (half << (ibits - 1)) | ((t - t_begin) << 4) | r
+// for result register r of lane half `half` in tile t of a wavefront
+// whose tiles start at t_begin; ibits - 5 bits hold the tile offset, so
+// the host picks ibits from the longest run of tiles a wavefront walks.
+// Writing the code moves u by less than 2^(ibits-23) |u| (2^(ibits-149)
+// near zero), which the merge adds to B.
 // Screen; grid = one block of kBatchWaves wavefronts per CU, LDS holds the
 // pass's queries: qpad[QP][stride] bf16 (row d of query j at j*stride + d,
-// stride = dim_pad + 8 so the 16-byte reads of 32 rows hit distinct
+// stride = 16*KS + 8 so the 16-byte reads of 32 rows hit distinct
 // banks).  Wavefront w walks 32-slot tiles [w*T/W, (w+1)*T/W).  For K-step
 // ks the A fragment of lane l is chunk 2*ks + l/32 (8 values) of slot
 // tile*32 + l%32 -- two 512-byte runs per load -- and the B fragment is
@@ -55,9 +82,11 @@ constexpr int kEntryPlanes = 5;      // s1, s2, nk, i1, i2
 template <int KS, int CT>
 __global__ __launch_bounds__(kBatchWaves * kWave) void mla_batch_screen_kernel(
     const u32x4* __restrict__ tiles, const float* __restrict__ norms, uint64_t cap,
-    uint32_t chunks, uint32_t n_tiles32, const uint16_t* __restrict__ qpad, int stride,
-    const float* __restrict__ inv_qn, uint32_t* __restrict__ planes) {
+    uint32_t chunks, uint32_t n_tiles32, const uint16_t* __restrict__ qpad, int stride_arg,
+    int ibits, uint32_t* __restrict__ planes) {
   constexpr int QP = 32 * CT;
+  constexpr int stride = 16 * KS + 8;  // the host's row stride (stride_arg)
+  (void)stride_arg;
   extern __shared__ uint16_t s_qb[];  // [QP][stride]
   {
     const u32x4* src = reinterpret_cast<const u32x4*>(qpad);
@@ -73,94 +102,114 @@ __global__ __launch_bounds__(kBatchWaves * kWave) void mla_batch_screen_kernel(
   const uint32_t w = blockIdx.x * kBatchWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t t_begin = static_cast<uint32_t>(static_cast<uint64_t>(w) * n_tiles32 / W);
   const uint32_t t_end = static_cast<uint32_t>(static_cast<uint64_t>(w + 1) * n_tiles32 / W);
-  float iq[CT], b1[CT], b2[CT], nk[CT];
-  uint32_t i1[CT], i2[CT];
+  // per column tile: the three largest coded u as signed-integer bits
+  // (b1 >= b2 >= b3)
+  int b1[CT], b2[CT], b3[CT];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) {
-    iq[ct] = inv_qn[ct * 32 + col];
-    b1[ct] = b2[ct] = nk[ct] = -INFINITY;
-    i1[ct] = i2[ct] = 0u;
-  }
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  auto load_a = [&](u32x4 (&a)[KS], uint32_t t) {
-    const uint64_t slot = static_cast<uint64_t>(t) * 32 + col;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const uint32_t c = 2 * ks + half;
-      a[ks] = c < chunks ? __builtin_nontemporal_load(tiles + c * cap + slot) : zero;
-    }
+  for (int ct = 0; ct < CT; ++ct) b1[ct] = b2[ct] = b3[ct] = INT32_MIN;
+  const uint32_t keep_mask = ~((1u << ibits) - 1u);
+  // A fragment ks of tile t: chunk 2*ks + half of slot t*32 + col (the
+  // bank holds 2*KS planes, zero past its chunks)
+  const u32x4* lane_base = tiles + static_cast<uint64_t>(half) * cap + col;
+  auto load_frag = [&](u32x4 (&a)[KS], uint32_t t, int ks) {
+    a[ks] = __builtin_nontemporal_load(lane_base + static_cast<uint64_t>(2 * ks) * cap +
+                                       static_cast<uint64_t>(t) * 32);
   };
   const uint16_t* qrow = s_qb + col * stride + 8 * half;
-  // Lanes track u = acc * (1/norm_f); s~ = u * (1/qnorm) is formed at the
-  // end (rounding is monotone, so the two best and the largest dropped u
-  // give the two best and the largest dropped s~).
-  // Per (lane, column tile): the two best u = acc * (1/norm_f) with their
-  // slots and the largest u not kept.
-  auto update = [&](float accv, float w, int ct, uint32_t slot) {
-    const float v = accv * w;  // NaN compares false: never kept
-    const bool gt1 = v > b1[ct];
-    const bool gt2 = v > b2[ct];
-    nk[ct] = fmaxf(nk[ct], gt2 ? b2[ct] : v);
-    const float nb2 = gt1 ? b1[ct] : v;
-    const uint32_t ni2 = gt1 ? i1[ct] : slot;
-    b2[ct] = gt2 ? nb2 : b2[ct];
-    i2[ct] = gt2 ? ni2 : i2[ct];
-    b1[ct] = gt1 ? v : b1[ct];
-    i1[ct] = gt1 ? slot : i1[ct];
+  // Lanes track u = acc * (1/norm_f); s~ = u * (1/qnorm) is formed by the
+  // merge (rounding is monotone, so the largest u give the largest s~).
+  // A slot that never ranks (tombstone, unused slot, non-finite row: the
+  // bank stores its row as zeros) has 1/norm_f = -0, so u is a zero and
+  // never outranks a positive value.  The accumulation cannot overflow
+  // where the merge certifies (it checks ||q|| * max norm_f), so a u that
+  // is not finite comes from a non-finite query, which the merge never
+  // certifies.  u's low bits take the slot code, and the three largest
+  // move by two medians and a maximum of the integer bits:
+  // b3 = med3(b2, b3, v), b2 = med3(b1, b2, v), b1 = max(b1, v) keep
+  // b1 >= b2 >= b3 the three largest values seen.
+  auto update = [&](float accv, float w, int ct, uint32_t code) {
+    const int v = static_cast<int>(and_or_b32(__float_as_uint(accv * w), keep_mask, code));
+    med3_i32_into(b2[ct], b3[ct], v);
+    med3_i32_into(b1[ct], b2[ct], v);
+    b1[ct] = max(b1[ct], v);
   };
-  // Column tile ct's matrix-core chain runs while the vector units reduce
-  // column tile ct-1: after step ks of the chain come the updates of result
-  // registers [ks*kUp, ks*kUp + kUp) of the previous accumulator, in that
-  // order (a scheduling barrier per step), so the matrix cores and the
-  // vector units work at once.  Query fragments are read kPre steps ahead.
+  // Matrix-core chains: one dependent accumulation chain per wavefront
+  // issues a 32x32x16 MFMA only about every fourth slot of the matrix
+  // core (a result feeds the next step's accumulator after several times
+  // the issue interval), so the column tiles advance in groups of kG
+  // independent chains -- step ks issues the kG MFMAs of a[ks] with the
+  // group's kG query fragments -- and the group's 16*kG results are
+  // reduced once its chains end.  Query fragments stream from LDS kPre
+  // fragments ahead, across step and group boundaries.  In the tile's last
+  // group each a[ks] is reloaded with the next tile's fragment as soon as
+  // its last MFMA has issued, so the next tile's loads are in flight
+  // during the rest of the group and the reductions (no second tile
+  // buffer is needed).  The reload is unconditional: after a wavefront's
+  // last tile it reads that tile again (cached, and never folded).
+  constexpr int kG = CT < 4 ? CT : 4;
+  constexpr int kGroups = CT / kG;
   constexpr int kPre = 4;
-  constexpr int kUp = (16 + KS - 1) / KS;  // updates per chain step
-  auto fold = [&](const u32x4 (&a)[KS], const float (&wr)[16], uint32_t t) {
-    const uint32_t sbase = t * 32 + 4 * half;  // slot of result register r: sbase + 8*(r/4) + r%4
-    f32x16 prev;
+  constexpr int kSteps = CT * KS;  // fragment stream: (group, ks, chain)
+  auto bfrag = [&](int step) -> u32x4 {
+    const int g = step / (KS * kG);
+    const int ks = (step / kG) % KS;
+    const int ct = g * kG + step % kG;
+    return *reinterpret_cast<const u32x4*>(qrow + ct * 32 * stride + 16 * ks);
+  };
+  auto fold = [&](u32x4 (&a)[KS], const float (&wr)[16], uint32_t t, uint32_t t_next) {
+    // code of result register r (slot t*32 + 8*(r/4) + 4*half + r%4): tcode | r
+    const uint32_t tcode = (static_cast<uint32_t>(half) << (ibits - 1)) | ((t - t_begin) << 4);
+    u32x4 bw[kPre];
 #pragma unroll
-    for (int ct = 0; ct <= CT; ++ct) {
-      f32x16 acc;
+    for (int j = 0; j < kPre; ++j) bw[j] = bfrag(j);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-      u32x4 bw[kPre];
-      const uint16_t* qc = qrow + (ct < CT ? ct : 0) * 32 * stride;
-      if (ct < CT) {
+    for (int g = 0; g < kGroups; ++g) {
+      f32x16 acc[kG];
 #pragma unroll
-        for (int j = 0; j < kPre; ++j) bw[j] = *reinterpret_cast<const u32x4*>(qc + 16 * j);
+      for (int c = 0; c < kG; ++c) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[c][r] = 0.0f;
       }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        if (ct < CT) {
-          const u32x4 b = bw[ks % kPre];
-          if (ks + kPre < KS) bw[ks % kPre] = *reinterpret_cast<const u32x4*>(qc + 16 * (ks + kPre));
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[ks]),
-                                                        __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
-        }
 #pragma unroll
-        for (int j = 0; j < kUp; ++j) {
-          const int r = ks * kUp + j;
-          if (ct > 0 && r < 16) update(prev[r], wr[r], ct - 1, sbase + 8 * (r / 4) + (r % 4));
+        for (int c = 0; c < kG; ++c) {
+          const int step = (g * KS + ks) * kG + c;
+          const u32x4 b = bw[step % kPre];
+          if (step + kPre < kSteps) bw[step % kPre] = bfrag(step + kPre);
+          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[ks]),
+                                                           __builtin_bit_cast(bf16x8, b), acc[c],
+                                                           0, 0, 0);
         }
+        if (g == kGroups - 1) load_frag(a, t_next, ks);
         __builtin_amdgcn_sched_barrier(0);
       }
-      prev = acc;
+#pragma unroll
+      for (int c = 0; c < kG; ++c) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) update(acc[c][r], wr[r], g * kG + c, tcode | static_cast<uint32_t>(r));
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   // Row norms of a tile are wave-uniform loads, fetched one tile ahead.
-  // 1/norm_f: NaN for a tombstone or an unused slot (never kept), 0 for an
-  // all-zero row (score 0, exact).
+  // 1/norm_f: -0 for a slot that never ranks (norm NaN: tombstone, unused
+  // slot, non-finite row) and for a norm that overflowed (its law score is
+  // a zero), 0 for an all-zero row (score 0, exact).
   float ns[32];
   auto load_norms = [&](uint32_t t) {
 #pragma unroll
     for (int j = 0; j < 32; ++j) ns[j] = norms[static_cast<size_t>(t) * 32 + j];
   };
-  if (t_begin < t_end) load_norms(t_begin);
-  // One tile buffer per wavefront (the two wavefronts of a SIMD take turns
-  // waiting for their tiles and running the matrix cores).
+  // One tile buffer per wavefront, refilled for the next tile during the
+  // current tile's last group (see fold).
+  u32x4 a[KS];
+  if (t_begin < t_end) {
+    load_norms(t_begin);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) load_frag(a, t_begin, ks);
+  }
   for (uint32_t t = t_begin; t < t_end; ++t) {
-    u32x4 a[KS];
-    load_a(a, t);
     float wr[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -168,42 +217,35 @@ __global__ __launch_bounds__(kBatchWaves * kWave) void mla_batch_screen_kernel(
       const float n0 = ns[j];
       const float n1 = ns[j + 4];
       const float nf = __builtin_bit_cast(float, half ? __float_as_uint(n1) : __float_as_uint(n0));
-      wr[r] = nf == 0.0f ? 0.0f : __builtin_amdgcn_rcpf(nf);
+      wr[r] = nf == 0.0f ? 0.0f : (nf < INFINITY ? __builtin_amdgcn_rcpf(nf) : -0.0f);
     }
     if (t + 1 < t_end) load_norms(t + 1);
-    fold(a, wr, t);
+    fold(a, wr, t, t + 1 < t_end ? t + 1 : t);
   }
   // The two lane halves of a column hold disjoint slots: merge their lists
-  // (top two of four, the third joins the dropped maximum), then the
-  // block's 8 sub-streams per query go out through LDS so that every
+  // (each half's three values go through the same update as a score), then
+  // the block's 8 sub-streams per query go out through LDS so that every
   // (plane, query) row receives one 32-byte run.
   __syncthreads();  // every wavefront is done with the staged queries
   uint32_t* s_out = reinterpret_cast<uint32_t*>(s_qb);  // [kEntryPlanes][QP][kBatchWaves]
   const int wv = threadIdx.x / kWave;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    const float o1 = __shfl_xor(b1[ct], 32);
-    const float o2 = __shfl_xor(b2[ct], 32);
-    const float onk = __shfl_xor(nk[ct], 32);
-    const uint32_t oi1 = __shfl_xor(i1[ct], 32);
-    const uint32_t oi2 = __shfl_xor(i2[ct], 32);
-    const bool mine = b1[ct] >= o1;
-    const float w1 = mine ? b1[ct] : o1, w2 = mine ? b2[ct] : o2;
-    const float l1 = mine ? o1 : b1[ct], l2 = mine ? o2 : b2[ct];
-    const uint32_t wi1 = mine ? i1[ct] : oi1, wi2 = mine ? i2[ct] : oi2;
-    const uint32_t li1 = mine ? oi1 : i1[ct];
-    const bool keep_w2 = w2 >= l1;
-    const float s2 = keep_w2 ? w2 : l1;
-    const uint32_t si2 = keep_w2 ? wi2 : li1;
-    const float third = keep_w2 ? l1 : fmaxf(w2, l2);
-    const float nkm = fmaxf(fmaxf(nk[ct], onk), third);
+    const int o1 = __shfl_xor(b1[ct], 32);
+    const int o2 = __shfl_xor(b2[ct], 32);
+    const int o3 = __shfl_xor(b3[ct], 32);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int v = j == 0 ? o1 : (j == 1 ? o2 : o3);
+      med3_i32_into(b2[ct], b3[ct], v);
+      med3_i32_into(b1[ct], b2[ct], v);
+      b1[ct] = max(b1[ct], v);
+    }
     if (half == 0) {
       const int q = ct * 32 + col;
-      s_out[(0 * QP + q) * kBatchWaves + wv] = __float_as_uint(w1 * iq[ct]);
-      s_out[(1 * QP + q) * kBatchWaves + wv] = __float_as_uint(s2 * iq[ct]);
-      s_out[(2 * QP + q) * kBatchWaves + wv] = __float_as_uint(nkm * iq[ct]);
-      s_out[(3 * QP + q) * kBatchWaves + wv] = wi1;
-      s_out[(4 * QP + q) * kBatchWaves + wv] = si2;
+      s_out[(0 * QP + q) * kBatchWaves + wv] = static_cast<uint32_t>(b1[ct]);
+      s_out[(1 * QP + q) * kBatchWaves + wv] = static_cast<uint32_t>(b2[ct]);
+      s_out[(2 * QP + q) * kBatchWaves + wv] = static_cast<uint32_t>(b3[ct]);
     }
   }
   __syncthreads();
@@ -265,18 +307,24 @@ __device__ inline float wave_sort_desc(float v) {
 }
 
 // Merge, certificate and exact rescore; grid = one block of kMergeThreads
-// per query of the pass.  planes: the screen's rows (n_sub sub-streams,
-// QP queries); query qi (pass column) has its `dim` values at query +
-// qi*qstride elements (F32 or BF16).  The screen bound for the query
+// per query of the pass.  planes: the screen's rows (n_sub sub-streams =
+// the screen's wavefronts, QP queries; wavefront i walked tiles from
+// i * n_tiles32 / n_sub); query qi (pass column) has its `dim` values at
+// query + qi*qstride elements (F32 or BF16) and 1/||q|| at inv_qn[qi].
+// The screened score of a kept value u is s~ = u * inv_qn[qi], its slot
+// the code in u's low ibits bits.  The screen bound for the query
 // (|s~ - score|):
-//   B = (gamma + delta) * (1 + 2^-20) + 8 * 2^-24
-//       + 1.01e-8 / (qn * nmin) + sqrt(dim) * 2^-125 * (1/qn + 1/nmin)
-//       + dim * 2^-125 / (qn * nmin),
+//   B0 = (gamma + delta) * (1 + 2^-20) + 8 * 2^-24
+//        + 1.01e-8 / (qn * nmin) + sqrt(dim) * 2^-125 * (1/qn + 1/nmin)
+//        + dim * 2^-125 / (qn * nmin),
+//   B  = B0 + 2^(ibits-23) * (1 + B0) * (1 + 2^-20) + 2^(ibits-148) / qn,
 // gamma bounding the fp32 accumulation, delta the rounding of an fp32
 // query to bf16, 8 * 2^-24 the reciprocals and products of the screened
 // score and the score's own rounding, the 1e-8 term the law's
-// denominator, the last terms bf16 values or products flushed near zero;
-// qn is the law's query norm and nmin the smallest positive row norm.
+// denominator, the next terms bf16 values or products flushed near zero;
+// the last two the slot code written into u (relative to |u|, with
+// |score| <= 1, and absolute near zero).  qn is the law's query norm and
+// nmin the smallest positive row norm.
 //
 // Steps: the last wavefront stages the query and one of its lanes forms
 // the law's qnorm while the others load the sub-streams' entries.  Each
@@ -300,10 +348,11 @@ constexpr int kSurvMax = kMergeThreads;
 constexpr uint32_t kBatchMaxDim = 288;
 
 __global__ __launch_bounds__(kMergeThreads) void mla_batch_merge_kernel(
-    const uint32_t* __restrict__ planes, uint32_t n_sub, int QP, const u32x4* __restrict__ tiles,
+    const uint32_t* __restrict__ planes, uint32_t n_sub, int QP, uint32_t n_tiles32, int ibits,
+    const float* __restrict__ inv_qn, const u32x4* __restrict__ tiles,
     const float* __restrict__ norms, const uint64_t* __restrict__ ids, uint64_t cap,
     uint32_t dim, const void* __restrict__ query, int q_dtype, size_t qstride, double gamma,
-    double delta, const unsigned* __restrict__ min_norm, int k, Cand* __restrict__ out,
+    double delta, const unsigned* __restrict__ norm_range, int k, Cand* __restrict__ out,
     unsigned* __restrict__ status) {
   __shared__ double s_q[kBatchMaxDim];      // the query, zero past dim
   __shared__ float s_lw[kMergeWavesB];      // per wavefront: k-th largest lane maximum
@@ -324,11 +373,22 @@ __global__ __launch_bounds__(kMergeThreads) void mla_batch_merge_kernel(
   const int qi = blockIdx.x;
   const size_t plane = static_cast<size_t>(QP) * n_sub;
   const size_t row = static_cast<size_t>(qi) * n_sub;
-  const float* p_s1 = reinterpret_cast<const float*>(planes) + row;
-  const float* p_s2 = p_s1 + plane;
-  const float* p_nk = p_s2 + plane;
-  const uint32_t* p_i1 = planes + 3 * plane + row;
-  const uint32_t* p_i2 = p_i1 + plane;
+  const float* p_u1 = reinterpret_cast<const float*>(planes) + row;
+  const float* p_u2 = p_u1 + plane;
+  const float* p_nk = p_u2 + plane;
+  const float iq = inv_qn[qi];
+  const uint32_t cmask = (1u << ibits) - 1u;
+  // slot of coded value u kept by sub-stream i (see the screen's slot code)
+  auto slot_of = [&](float u, uint32_t i) -> uint32_t {
+    const uint32_t c = __float_as_uint(u) & cmask;
+    const uint32_t t_begin = static_cast<uint32_t>(static_cast<uint64_t>(i) * n_tiles32 / n_sub);
+    const uint32_t r = c & 15u;
+    const uint32_t t = t_begin + ((c >> 4) & ((1u << (ibits - 5)) - 1u));
+    const uint32_t slot = t * 32u + 8u * (r >> 2) + 4u * (c >> (ibits - 1)) + (r & 3u);
+    // every code the screen writes names a slot of a tile it walked; the
+    // clamp only keeps a corrupted value from reading past the bank
+    return slot < cap ? slot : static_cast<uint32_t>(cap - 1);
+  };
 
   float v1[kMergePer], v2[kMergePer];
   uint32_t j1[kMergePer], j2[kMergePer];
@@ -339,11 +399,12 @@ __global__ __launch_bounds__(kMergeThreads) void mla_batch_merge_kernel(
     v1[j] = v2[j] = -INFINITY;
     j1[j] = j2[j] = 0u;
     if (tid < kMergeLoaders && i < n_sub) {
-      v1[j] = p_s1[i];
-      v2[j] = p_s2[i];
-      j1[j] = p_i1[i];
-      j2[j] = p_i2[i];
-      nk = fmaxf(nk, p_nk[i]);
+      const float u1 = p_u1[i], u2 = p_u2[i];
+      v1[j] = u1 * iq;
+      v2[j] = u2 * iq;
+      j1[j] = slot_of(u1, i);
+      j2[j] = slot_of(u2, i);
+      nk = fmaxf(nk, p_nk[i] * iq);
     }
   }
   if (wave == kMergeWavesB - 1) {
@@ -388,11 +449,14 @@ __global__ __launch_bounds__(kMergeThreads) void mla_batch_merge_kernel(
   const int any_pinf = __syncthreads_or(pinf ? 1 : 0);
 
   const double qn = s_qn;
-  const double nmin = static_cast<double>(__uint_as_float(*min_norm));
-  const double bound = (gamma + delta) * (1.0 + 0x1p-20) + 8.0 * 0x1p-24 +
-                       1.01e-8 / (qn * nmin) +
-                       sqrt(static_cast<double>(dim)) * 0x1p-125 * (1.0 / qn + 1.0 / nmin) +
-                       dim * 0x1p-125 / (qn * nmin);
+  const double nmin = static_cast<double>(__uint_as_float(norm_range[0]));
+  const double nmax = static_cast<double>(__uint_as_float(norm_range[1]));
+  const double bound0 = (gamma + delta) * (1.0 + 0x1p-20) + 8.0 * 0x1p-24 +
+                        1.01e-8 / (qn * nmin) +
+                        sqrt(static_cast<double>(dim)) * 0x1p-125 * (1.0 / qn + 1.0 / nmin) +
+                        dim * 0x1p-125 / (qn * nmin);
+  const double bound = bound0 + ldexp(1.0 + bound0, ibits - 23) * (1.0 + 0x1p-20) +
+                       ldexp(1.0, ibits - 148) / qn;
   float L = -INFINITY, nk_all = -INFINITY;
 #pragma unroll
   for (int w = 0; w < kMergeWavesB - 1; ++w) {
@@ -476,8 +540,13 @@ __global__ __launch_bounds__(kMergeThreads) void mla_batch_merge_kernel(
   const int n_el = __syncthreads_count(sup ? 1 : 0);
   const float vk = n >= k ? s_sv[s_byrank[k - 1]] : -INFINITY;
   const double t = static_cast<double>(vk) - 2.0 * bound - 0x1p-40;
+  // t > 0: the screen kept its values by their integer bits, the float
+  // order only from +0 up.  qn * nmax < 2^125: no product or partial sum
+  // of the bf16 query (norm at most qn * (1 + 2^-8)) and a row can reach
+  // the fp32 overflow threshold (Cauchy-Schwarz, with the accumulation's
+  // rounding), so the bound B holds for every screened value.
   const bool pre = any_pinf == 0 && count <= static_cast<unsigned>(kSurvMax) && n >= k &&
-                   static_cast<double>(nk_all) < t;
+                   static_cast<double>(nk_all) < t && t > 0.0 && qn * nmax < 0x1p125;
   // the rescored prefix: ranks [0, n_el)
   if (sup) {
     const float sc = static_cast<float>(dot / (qn * static_cast<double>(nf) + 1e-8));

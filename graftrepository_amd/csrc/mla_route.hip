@@ -279,8 +279,13 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_pipe_kernel(
 
 // Place staged row-major rows into their tile slots and compute row norms
 // (cpp/grm_runtime.cpp:3232-3241).  rows: [count][dim] of DT; slots/ids may be
-// null (contiguous slots from slot0 / ids = slot).  min_norm tracks the
-// smallest positive norm ever placed (float bits, atomicMin).
+// null (contiguous slots from slot0 / ids = slot).  norm_range[0] tracks the
+// smallest positive norm ever placed, norm_range[1] the largest finite one
+// (float bits, atomicMin / atomicMax).  A row holding a non-finite value
+// has a NaN or infinite dot product with every query, so the law scores it
+// NaN whatever its norm; such a row is stored as zeros with a NaN norm,
+// which every route scores NaN as well (0 / NaN), and which the batched
+// screen's products can then never overflow on.
 template <int DT>
 __global__ void mla_place_rows_kernel(const void* __restrict__ rows,
                                       uint64_t count, uint32_t dim,
@@ -290,7 +295,7 @@ __global__ void mla_place_rows_kernel(const void* __restrict__ rows,
                                       uint64_t slot0, u32x4* __restrict__ tiles,
                                       float* __restrict__ norms,
                                       uint64_t* __restrict__ slot_ids,
-                                      unsigned* __restrict__ min_norm) {
+                                      unsigned* __restrict__ norm_range) {
   constexpr int EPC = DT == kF32 ? 4 : 8;
   for (uint64_t r = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
        r < count; r += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
@@ -328,11 +333,20 @@ __global__ void mla_place_rows_kernel(const void* __restrict__ rows,
       v.w = w[3];
       dst[static_cast<size_t>(c) * plane] = v;
     }
-    const float nf = static_cast<float>(sqrt(acc));
+    // squares of finite fp32 / bf16 values cannot overflow fp64
+    const bool finite_row = isfinite(acc);
+    if (!finite_row) {
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      for (uint32_t c = 0; c < chunks; ++c) dst[static_cast<size_t>(c) * plane] = zero;
+    }
+    const float nf = finite_row ? static_cast<float>(sqrt(acc)) : __builtin_nanf("");
     norms[slot] = nf;
     slot_ids[slot] = ids ? ids[r] : slot;
-    // smallest positive row norm (positive floats order like their bits)
-    if (nf > 0.0f && isfinite(nf)) atomicMin(min_norm, __float_as_uint(nf));
+    // norm range (non-negative floats order like their bits)
+    if (nf > 0.0f && isfinite(nf)) {
+      atomicMin(norm_range, __float_as_uint(nf));
+      atomicMax(norm_range + 1, __float_as_uint(nf));
+    }
   }
 }
 
@@ -368,6 +382,7 @@ struct MlaDeviceArena {
   uint32_t dim_pad = 0;
   uint32_t epc = 4;
   uint32_t chunks = 0;
+  uint32_t planes = 0;      // chunk planes allocated: chunks, or (bf16) the batched screen's 2*KS
   uint64_t capacity = 0;    // slots, multiple of 64
   uint64_t high_water = 0;  // slots [0, high_water) may hold live rows
   uint64_t live = 0;
@@ -401,7 +416,7 @@ struct MlaDeviceArena {
   hipEvent_t ev_stop = nullptr;
   hipEvent_t ev_mut = nullptr;
   bool mut_pending = false;
-  unsigned* d_min_norm = nullptr;  // smallest positive row norm placed (float bits)
+  unsigned* d_min_norm = nullptr;  // [smallest positive, largest finite] row norm placed (float bits)
   // batched route (bf16 banks): pass buffers and per-query results
   uint16_t* d_qpad = nullptr;
   size_t d_qpad_count = 0;
@@ -546,6 +561,17 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
   a->epc = dtype == kF32 ? 4 : 8;
   a->dim_pad = (a->dim + a->epc - 1) / a->epc * a->epc;
   a->chunks = a->dim_pad / a->epc;
+  // bf16 banks get zero planes up to the batched screen's 16-dimension
+  // K-steps (16, 32 or 36 planes), which it then reads unconditionally
+  a->planes = a->chunks;
+  if (dtype == kBF16) {
+    for (uint32_t p : {16u, 32u, 36u}) {
+      if (a->chunks <= p) {
+        a->planes = p;
+        break;
+      }
+    }
+  }
   a->capacity = (capacity + grm::kWave - 1) / grm::kWave * grm::kWave;
   {
     int cus = 0;
@@ -592,7 +618,7 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
       a->slot_id[i] = i;
     }
   }
-  const size_t tile_bytes = static_cast<size_t>(a->chunks) * grm::kWave * 16;
+  const size_t tile_bytes = static_cast<size_t>(a->planes) * grm::kWave * 16;
   const size_t tiles = a->capacity / grm::kWave;
 #define BAIL_HIP(expr)                                  \
   do {                                                  \
@@ -610,10 +636,10 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
   BAIL_HIP(hipMemsetAsync(a->d_tiles, 0, tiles * tile_bytes, a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_norms, 0xff, a->capacity * sizeof(float), a->stream));
   BAIL_HIP(hipMemsetAsync(a->d_ids, 0xff, a->capacity * sizeof(uint64_t), a->stream));
-  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_min_norm), sizeof(unsigned)));
+  BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_min_norm), 2 * sizeof(unsigned)));
   {
-    const unsigned inf_bits = 0x7f800000u;
-    BAIL_HIP(hipMemcpyAsync(a->d_min_norm, &inf_bits, sizeof(unsigned), hipMemcpyHostToDevice,
+    const unsigned range0[2] = {0x7f800000u, 0u};
+    BAIL_HIP(hipMemcpyAsync(a->d_min_norm, range0, sizeof(range0), hipMemcpyHostToDevice,
                             a->stream));
     BAIL_HIP(hipStreamSynchronize(a->stream));
   }
@@ -723,14 +749,24 @@ struct BatchPlan {
   int ks = 0;        // 8, 16 or 18
   int stride = 0;    // bf16 elements per staged query row
   int qp_max = 0;    // queries per pass (multiple of 32, <= 256)
+  int ibits = 0;     // width of the slot code the screen writes into its values
 };
+
+// Slot code width of the batched screen: 4 bits of result register, the
+// lane half, and enough bits for the longest run of tiles one screen
+// wavefront walks.  The code costs the screen bound 2^(ibits-23) relative,
+// so banks whose runs would need more than 16 bits route on the
+// single-query path instead.
+constexpr int kMaxSlotCodeBits = 16;
 
 bool batch_plan(const MlaDeviceArena* a, int q_timed, BatchPlan* p) {
   if (a->dtype != kBF16 || q_timed < a->batch_min) return false;
   const uint32_t ks_need = (a->chunks + 1) / 2;
   p->ks = ks_need <= 8 ? 8 : (ks_need <= 16 ? 16 : (ks_need <= 18 ? 18 : 0));
-  if (p->ks == 0) return false;
-  p->stride = static_cast<int>(std::max<uint32_t>(a->dim_pad, 16u * p->ks)) + 8;
+  if (p->ks == 0 || a->planes < 2u * p->ks) return false;
+  // 16*ks >= dim_pad always (ks covers the row's chunks); the screen
+  // kernel takes this stride as a compile-time constant of its KS
+  p->stride = 16 * p->ks + 8;
   const size_t row = std::max(static_cast<size_t>(p->stride) * 2,
                               static_cast<size_t>(grm::mla::kEntryPlanes) * grm::mla::kBatchWaves * 4);
   int qp = grm::mla::kBatchMaxCols;
@@ -742,12 +778,19 @@ bool batch_plan(const MlaDeviceArena* a, int q_timed, BatchPlan* p) {
     return false;
   }
   if (a->dim > grm::mla::kBatchMaxDim) return false;
+  const uint32_t n_tiles32 = static_cast<uint32_t>((a->high_water + 31) / 32);
+  const uint32_t n_waves = static_cast<uint32_t>(a->cus) * grm::mla::kBatchWaves;
+  const uint32_t max_run = (n_tiles32 + n_waves - 1) / n_waves;
+  int ibits = 5;
+  while ((1u << (ibits - 5)) < max_run) ++ibits;
+  if (ibits > kMaxSlotCodeBits) return false;
+  p->ibits = ibits;
   p->qp_max = qp;
   return true;
 }
 
 template <int KS, int CT>
-int launch_screen(MlaDeviceArena* a, uint32_t n_tiles32, int stride, size_t lds) {
+int launch_screen(MlaDeviceArena* a, uint32_t n_tiles32, int stride, int ibits, size_t lds) {
   auto kern = grm::mla::mla_batch_screen_kernel<KS, CT>;
   if (lds > 65536) {
     GRM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -755,7 +798,7 @@ int launch_screen(MlaDeviceArena* a, uint32_t n_tiles32, int stride, size_t lds)
                                       static_cast<int>(lds)));
   }
   kern<<<a->cus, grm::mla::kBatchWaves * grm::kWave, lds, a->stream>>>(
-      a->d_tiles, a->d_norms, a->capacity, a->chunks, n_tiles32, a->d_qpad, stride, a->d_inv_qn,
+      a->d_tiles, a->d_norms, a->capacity, a->chunks, n_tiles32, a->d_qpad, stride, ibits,
       a->d_entries);
   GRM_HIP_CHECK(hipGetLastError());
   return 0;
@@ -773,16 +816,18 @@ int enqueue_batch_pass(MlaDeviceArena* a, const BatchPlan& p, const unsigned cha
       q, q_dtype, qc, a->dim, p.stride, a->d_qpad, a->d_inv_qn);
   GRM_HIP_CHECK(hipGetLastError());
   const uint32_t n_tiles32 = static_cast<uint32_t>((a->high_water + 31) / 32);
+  const uint32_t n_waves = static_cast<uint32_t>(a->cus) * grm::mla::kBatchWaves;
+  const int ibits = p.ibits;
   // LDS: the staged queries, later the block's result rows
   const size_t lds = std::max(static_cast<size_t>(qp) * p.stride * 2,
                               static_cast<size_t>(grm::mla::kEntryPlanes) * qp * grm::mla::kBatchWaves * 4);
   if (ev) GRM_HIP_CHECK(hipEventRecord(ev[0], a->stream));
 #define GRM_SCREEN_CT(KS)                                                   \
   switch (ct) {                                                             \
-    case 1: GRM_CHECK_RC((launch_screen<KS, 1>(a, n_tiles32, p.stride, lds))); break; \
-    case 2: GRM_CHECK_RC((launch_screen<KS, 2>(a, n_tiles32, p.stride, lds))); break; \
-    case 4: GRM_CHECK_RC((launch_screen<KS, 4>(a, n_tiles32, p.stride, lds))); break; \
-    default: GRM_CHECK_RC((launch_screen<KS, 8>(a, n_tiles32, p.stride, lds))); break; \
+    case 1: GRM_CHECK_RC((launch_screen<KS, 1>(a, n_tiles32, p.stride, ibits, lds))); break; \
+    case 2: GRM_CHECK_RC((launch_screen<KS, 2>(a, n_tiles32, p.stride, ibits, lds))); break; \
+    case 4: GRM_CHECK_RC((launch_screen<KS, 4>(a, n_tiles32, p.stride, ibits, lds))); break; \
+    default: GRM_CHECK_RC((launch_screen<KS, 8>(a, n_tiles32, p.stride, ibits, lds))); break; \
   }
   switch (p.ks) {
     case 8: GRM_SCREEN_CT(8); break;
@@ -794,7 +839,7 @@ int enqueue_batch_pass(MlaDeviceArena* a, const BatchPlan& p, const unsigned cha
   const double gamma = 2.0 * (16.0 * p.ks + 2.0 * p.ks) * ldexp(1.0, -24);
   const double delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
   grm::mla::mla_batch_merge_kernel<<<qc, grm::mla::kMergeThreads, 0, a->stream>>>(
-      a->d_entries, a->cus * grm::mla::kBatchWaves, qp, a->d_tiles, a->d_norms, a->d_ids,
+      a->d_entries, n_waves, qp, n_tiles32, ibits, a->d_inv_qn, a->d_tiles, a->d_norms, a->d_ids,
       a->capacity, a->dim, q, q_dtype, a->dim, gamma, delta, a->d_min_norm, topk, out, status);
   GRM_HIP_CHECK(hipGetLastError());
   return 0;

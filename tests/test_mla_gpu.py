@@ -269,6 +269,35 @@ def test_batched_ties_zero_and_nan_rows(hip_lib):
     assert_same(res.ids, res.scores, ids, sc)
 
 
+def test_batched_negative_tops_huge_rows_and_infinities(hip_lib):
+    # Where the screen cannot certify, the single-query path answers:
+    # every score negative (a non-positive threshold), a query whose
+    # products with the largest row could overflow fp32, and rows holding
+    # an infinity (the law scores them NaN) beside ordinary rows.
+    rng = np.random.default_rng(65)
+    rows = np.abs(rng.standard_normal((3000, 64))).astype(np.float32)
+    qs = -np.abs(rng.standard_normal((8, 64))).astype(np.float32)
+    bits, qbits = oracle.bf16_bits(rows), oracle.bf16_bits(qs)
+    with MlaNodeBank(bits, dtype="bf16") as bank:
+        res = bank.route(qbits, 6)
+    ids, sc, _ = oracle.mla_route(_f32(bits), _f32(qbits), 6)
+    assert_same(res.ids, res.scores, ids, sc)
+
+    rows = rng.standard_normal((3000, 64)).astype(np.float32)
+    rows[7] *= np.float32(1e30)
+    rows[9, 2] = np.inf
+    rows[11, 5] = -np.inf
+    qs = rng.standard_normal((8, 64)).astype(np.float32)
+    qs[0] *= np.float32(1e10)
+    qs[1] = rows[7] / np.float32(1e30)
+    bits, qbits = oracle.bf16_bits(rows), oracle.bf16_bits(qs)
+    with MlaNodeBank(bits, dtype="bf16") as bank:
+        res = bank.route(qbits, 6)
+    ids, sc, _ = oracle.mla_route(_f32(bits), _f32(qbits), 6)
+    assert_same(res.ids, res.scores, ids, sc)
+    assert not {9, 11} & set(res.ids.ravel().tolist())
+
+
 def test_batched_f32_queries_on_bf16_bank(hip_lib):
     # fp32 queries are rounded to bf16 for the matrix cores; the bound
     # covers the rounding and the law uses the fp32 values.
