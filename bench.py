@@ -742,7 +742,7 @@ def bench_bridge(epochs: int):
 def bench_store(steps: int):
     """The store route on the device (lexical bonus + route filters,
     grm_store_route_filtered's law) on a 1M x 288 fp32 store, against the
-    plain route of the same bank."""
+    same store's route without lexical keys or filters."""
     from graftrepository_amd import workloads as wl
     from graftrepository_amd.store_route import DeviceRouteStore, _KNOWN
 
@@ -766,7 +766,7 @@ def bench_store(steps: int):
         t0 = time.perf_counter()
         st.route_filtered(q, qlex, kinds=["turn", "doc"], topk=8)
         t1 = time.perf_counter()
-        st.bank.route(q[None], 8, timed=False)
+        st.route_scored(q, (), 8)
         t2 = time.perf_counter()
         if i >= 5:
             walls.append((t1 - t0) * 1e3)

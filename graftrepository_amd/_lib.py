@@ -83,6 +83,30 @@ SIGNATURES = {
     "grm_gqa_hip_compact": (i32, [vp]),
     "grm_gqa_hip_sync": (i32, [vp]),
     "grm_gqa_hip_bank_info": (i32, [vp, vp]),
+    "grm_gqa_hip_set_filter_bits": (i32, [vp, vp, vp, u64]),
+    "grm_gqa_hip_route_filtered": (i32, [vp, vp, i32, i32, i32, i32, i32, u64, ctypes.c_uint32,
+                                         vp, vp, vp]),
+    "grm_gqa_hip_score_nodes": (i32, [vp, vp, i32, i32, i32, vp, u64, vp]),
+    # the store's route calls over a device bank (cpp/grm_runtime_c.h:176-181,
+    # 381-436, 499) and their extensions
+    "grm_hip_store_create_mla": (i32, [i32, u64, i32, ctypes.POINTER(vp)]),
+    "grm_hip_store_create_gqa": (i32, [i32, i32, u64, u64, ctypes.POINTER(vp)]),
+    "grm_hip_store_destroy": (None, [vp]),
+    "grm_store_set_route": (i32, [vp, u64, vp, u64, ctypes.c_char_p]),
+    "grm_store_set_route_multi": (i32, [vp, u64, vp, u64, u64, ctypes.c_char_p]),
+    "grm_store_set_route_list": (i32, [vp, u64, vp, u64, vp, u64, ctypes.c_char_p]),
+    "grm_store_clear_route": (i32, [vp, u64]),
+    "grm_store_set_route_metadata": (i32, [vp, u64] + [ctypes.c_char_p] * 4),
+    "grm_store_route": (i32, [vp, vp, u64, ctypes.c_char_p, u64, vp, u64, vp]),
+    "grm_store_route_filtered": (i32, [vp, vp, u64] + [ctypes.c_char_p] * 5
+                                 + [u64, vp, u64, vp]),
+    "grm_store_route_gqa": (i32, [vp, vp, u64, u64, u64] + [ctypes.c_char_p] * 5
+                            + [u64, vp, u64, vp]),
+    "grm_store_last_error": (ctypes.c_char_p, [vp]),
+    "grm_hip_store_set_routes": (i32, [vp, u64, vp, vp, vp, vp, vp]),
+    "grm_hip_store_route_scored": (i32, [vp, vp, u64, u64] + [ctypes.c_char_p] * 5
+                                   + [u64, vp, vp, u64, vp]),
+    "grm_hip_store_info": (i32, [vp, vp]),
     "grm_hip_payload_dequant": (i32, [vp, vp, u64, ctypes.c_uint32, vp, vp]),
     "grm_hip_payload_upload": (i32, [vp, vp, u64, ctypes.c_uint32, vp, vp]),
     "grm_hip_device_alloc": (i32, [u64, ctypes.POINTER(vp)]),

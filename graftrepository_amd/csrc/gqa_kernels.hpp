@@ -1600,5 +1600,60 @@ __global__ void gqa_clear_flags_kernel(unsigned* __restrict__ flags, int n) {
   if (i < n) flags[i] = 0u;
 }
 
+// Route filters (cpp/grm_runtime.cpp:3074-3104; bits as route_filter_bits,
+// :2793-2838): slot i passes when, for each category c with filters (bit c
+// of cats), its bits meet that category's 16-bit mask at shift 16c.  A
+// failing slot loses its live bit in the route's copy of the flags, which
+// every score path reads, so it scores NaN and never ranks.
+__global__ void gqa_filter_flags_kernel(const uint32_t* __restrict__ flags,
+                                        const uint64_t* __restrict__ fbits, uint64_t n,
+                                        uint64_t fmask, uint32_t cats,
+                                        uint32_t* __restrict__ out) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride) {
+    const uint64_t hit = fbits[i] & fmask;
+    bool ok = true;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if ((cats >> c) & 1u) ok = ok && ((hit >> (16 * c)) & 0xffffull) != 0;
+    }
+    out[i] = ok ? flags[i] : (flags[i] & ~1u);
+  }
+}
+
+// Scores of listed slots from their per-head maxima (query 0; the exact
+// kernel filled them): the finalize kernel's law -- heads summed in order
+// in fp64, / H, 0.0 for a slot without key tokens, NaN for a slot that is
+// not live, holds a non-finite key value, or meets a non-finite query
+// value -- one thread per listed slot, which then re-zeroes its maxima.
+__global__ void gqa_slot_scores_kernel(unsigned long long* __restrict__ hmax, size_t cap, int H,
+                                       const uint32_t* __restrict__ slots, uint64_t n,
+                                       const uint32_t* __restrict__ lens,
+                                       const uint32_t* __restrict__ flags,
+                                       const unsigned* __restrict__ qbad, int kv,
+                                       float* __restrict__ out) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  bool q_bad = false;
+  for (int g = 0; g < kv; ++g) q_bad = q_bad || qbad[g] != 0u;
+  const uint32_t slot = slots[i];
+  double total = 0.0;
+  for (int h = 0; h < H; ++h) {
+    total += __longlong_as_double(hmax[static_cast<size_t>(h) * cap + slot]);
+    hmax[static_cast<size_t>(h) * cap + slot] = 0ull;
+  }
+  const uint32_t f = flags[slot];
+  float sc = __builtin_nanf("");
+  if (f & 1u) {
+    if (lens[slot] == 0) {
+      sc = 0.0f;
+    } else if ((f & 2u) && !q_bad) {
+      sc = static_cast<float>(total / static_cast<double>(H));
+    }
+  }
+  out[i] = sc;
+}
+
 }  // namespace gqa
 }  // namespace grm

@@ -64,6 +64,23 @@ struct GqaDeviceArena {
   uint32_t* d_len = nullptr;
   uint64_t* d_ids = nullptr;
   uint32_t* d_flags = nullptr;  // bit 0 live, bit 1 all key values finite
+  // store route: per-slot route filter bits (host copy uploaded when it
+  // changed), a filtered route's copy of the flags, and the flags a route
+  // reads (d_flags unless a filtered route set its copy)
+  std::vector<uint64_t> fbits;
+  bool fbits_dirty = false;
+  uint64_t* d_fbits = nullptr;
+  size_t d_fbits_count = 0;
+  uint32_t* d_fflags = nullptr;
+  size_t d_fflags_count = 0;
+  const uint32_t* route_flags = nullptr;
+  // listed-slot scoring (grm_gqa_hip_score_nodes)
+  Item* d_sitems = nullptr;
+  size_t d_sitems_count = 0;
+  uint32_t* d_sslots = nullptr;
+  size_t d_sslots_count = 0;
+  float* d_sout = nullptr;
+  size_t d_sout_count = 0;
   uint32_t* d_nonfinite = nullptr;
   unsigned* d_kmax = nullptr;   // float bits: max key norm per slot
   // host mirrors
@@ -197,7 +214,8 @@ void destroy_arena(GqaDeviceArena* a) {
                  a->d_flags,  a->d_nonfinite, a->d_kmax,  a->d_items,  a->d_hmax,
                  a->d_qbad,   a->d_queries, a->d_stage,   a->d_q64,    a->d_hmaxf,
                  a->d_colinfo, a->d_lbub,   a->d_blists,  a->d_cslots, a->d_ccount,
-                 a->d_citems, a->d_units};
+                 a->d_citems, a->d_units,   a->d_fbits,   a->d_fflags,  a->d_sitems,
+                 a->d_sslots, a->d_sout};
   for (void* p : dev) {
     if (p) (void)hipFree(p);
   }
@@ -571,7 +589,8 @@ int launch_finalize(GqaDeviceArena* a, int H, int qb, int topk, uint32_t fin_blo
   const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
   grm::gqa::gqa_finalize_kernel<<<dim3(fin_blocks, qb), per_block, 0, a->stream>>>(
       a->d_hmax, a->cap_nodes * static_cast<size_t>(H), a->cap_nodes, H,
-      static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags, a->d_ids, a->d_qbad,
+      static_cast<uint32_t>(a->high_water), a->d_len,
+      a->route_flags ? a->route_flags : a->d_flags, a->d_ids, a->d_qbad,
       static_cast<int>(a->kv), topk, bout, slot_list, list_count, a->cap_nodes, done,
       a->route_seq);
   GRM_HIP_CHECK(hipGetLastError());
@@ -947,7 +966,8 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   grm::gqa::gqa_bounds_kernel<<<dim3(qb, fin_blocks), grm::gqa::kFinWaves * grm::kWave,
                                 static_cast<size_t>(H) * p.Qt * sizeof(float4), a->stream>>>(
       a->d_hmaxf, colstride, a->cap_nodes, H, p.Qt, p.R, cols, kv,
-      static_cast<uint32_t>(a->high_water), a->d_len, a->d_flags, a->d_ids, a->d_kmax,
+      static_cast<uint32_t>(a->high_water), a->d_len,
+      a->route_flags ? a->route_flags : a->d_flags, a->d_ids, a->d_kmax,
       a->d_colinfo, a->d_qbad, fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub,
       a->d_blists, a->d_ccount + p.qb_max);
   GRM_HIP_CHECK(hipGetLastError());
@@ -1201,6 +1221,15 @@ extern "C" int grm_gqa_hip_append(GqaDeviceArena* a, const void* keys_host,
   a->mut_pending = true;
   a->live += count;
   a->epoch += 1;
+  // a slot taken by an append starts with no route filter bits
+  if (!a->fbits.empty()) {
+    for (uint64_t sl : slots) {
+      if (sl < a->fbits.size() && a->fbits[sl] != 0) {
+        a->fbits[sl] = 0;
+        a->fbits_dirty = true;
+      }
+    }
+  }
   // the route work lists follow the host mirrors; rebuilding them here
   // keeps the next route from paying for it
   GRM_CHECK_RC(ensure_items(a));
@@ -1318,6 +1347,142 @@ extern "C" int grm_gqa_hip_sync(GqaDeviceArena* a) {
   if (!a) return grm::fail(-1, "null arena");
   GRM_HIP_CHECK(hipSetDevice(a->device));
   return wait_mutations(a);
+}
+
+// ---------------------------------------------------------------- store route
+
+namespace {
+
+// Upload the host copy of the route filter bits when it changed.
+int sync_filter_bits(GqaDeviceArena* a) {
+  if (a->fbits.size() < a->cap_nodes) {
+    a->fbits.resize(a->cap_nodes, 0);
+    a->fbits_dirty = true;
+  }
+  if (!a->d_fbits || a->fbits_dirty) {
+    GRM_CHECK_RC(reserve_device(&a->d_fbits, &a->d_fbits_count, a->cap_nodes));
+    GRM_HIP_CHECK(hipMemcpyAsync(a->d_fbits, a->fbits.data(), a->cap_nodes * sizeof(uint64_t),
+                                 hipMemcpyHostToDevice, a->stream));
+    a->fbits_dirty = false;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int grm_gqa_hip_set_filter_bits(GqaDeviceArena* a, const uint64_t* node_ids,
+                                           const uint64_t* bits, uint64_t count) {
+  if (!a || (count > 0 && (!node_ids || !bits))) return grm::fail(-1, "invalid arguments");
+  if (a->fbits.size() < a->cap_nodes) a->fbits.resize(a->cap_nodes, 0);
+  std::vector<uint64_t> slots(count);
+  for (uint64_t i = 0; i < count; ++i) {
+    auto it = a->slot_of.find(node_ids[i]);
+    if (it == a->slot_of.end()) return grm::fail(-1, "filter bits for an id that is not live");
+    slots[i] = it->second;
+  }
+  for (uint64_t i = 0; i < count; ++i) a->fbits[slots[i]] = bits[i];
+  if (count > 0) a->fbits_dirty = true;
+  grm::clear_error();
+  return 0;
+}
+
+extern "C" int grm_gqa_hip_route_filtered(GqaDeviceArena* a, const void* query, int query_dtype,
+                                          int query_on_device, int query_heads, int query_tokens,
+                                          int topk, uint64_t filter_mask, uint32_t filter_categories,
+                                          uint64_t* out_ids_host, float* out_scores_host,
+                                          float* elapsed_ms_host) {
+  if (!a) return grm::fail(-1, "null arena");
+  if (filter_categories & ~0xfu) return grm::fail(-1, "filter categories are bits 0..3");
+  if (filter_categories == 0) {
+    return route_impl(a, query, query_dtype, query_on_device != 0, 1, query_heads, query_tokens,
+                      0, topk, out_ids_host, out_scores_host, elapsed_ms_host);
+  }
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  GRM_CHECK_RC(sync_filter_bits(a));
+  GRM_CHECK_RC(reserve_device(&a->d_fflags, &a->d_fflags_count, a->cap_nodes));
+  if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
+  const uint64_t n = a->high_water;
+  if (n > 0) {
+    const unsigned blocks = static_cast<unsigned>(std::min<uint64_t>((n + 255) / 256, 4096));
+    grm::gqa::gqa_filter_flags_kernel<<<blocks, 256, 0, a->stream>>>(
+        a->d_flags, a->d_fbits, n, filter_mask, filter_categories, a->d_fflags);
+    GRM_HIP_CHECK(hipGetLastError());
+  }
+  a->route_flags = a->d_fflags;
+  const int rc = route_impl(a, query, query_dtype, query_on_device != 0, 1, query_heads,
+                            query_tokens, 0, topk, out_ids_host, out_scores_host, elapsed_ms_host);
+  a->route_flags = nullptr;
+  return rc;
+}
+
+extern "C" int grm_gqa_hip_score_nodes(GqaDeviceArena* a, const void* query_host, int query_dtype,
+                                       int query_heads, int query_tokens, const uint64_t* node_ids,
+                                       uint64_t count, float* out_scores_host) {
+  if (!a || !query_host || (count > 0 && (!node_ids || !out_scores_host))) {
+    return grm::fail(-1, "invalid arguments");
+  }
+  if (query_dtype != kF32 && query_dtype != kBF16) return grm::fail(-1, "query dtype must be F32 or BF16");
+  if (query_heads <= 0 || query_tokens <= 0 || query_heads % static_cast<int>(a->kv) != 0) {
+    return grm::fail(-1, "need heads, tokens > 0 and heads % kv_heads == 0");
+  }
+  if (count == 0) return 0;
+  // distinct slots (a slot's maxima are read once), results mapped back
+  std::vector<uint32_t> slots;
+  std::unordered_map<uint64_t, uint32_t> pos;
+  std::vector<uint32_t> where(count);
+  for (uint64_t i = 0; i < count; ++i) {
+    auto it = a->slot_of.find(node_ids[i]);
+    if (it == a->slot_of.end()) return grm::fail(-1, "score of an id that is not live");
+    auto ins = pos.emplace(it->second, static_cast<uint32_t>(slots.size()));
+    if (ins.second) slots.push_back(static_cast<uint32_t>(it->second));
+    where[i] = ins.first->second;
+  }
+  std::vector<Item> items;
+  for (uint32_t sl : slots) {
+    if (a->len[sl] > 0) append_items(items, sl, a->tok_off[sl] * a->kv, a->len[sl], a->chunk);
+  }
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  GRM_CHECK_RC(wait_mutations(a));
+  const int H = query_heads;
+  const int Qt = query_tokens;
+  const size_t qbytes = static_cast<size_t>(H) * Qt * a->hd * (query_dtype == kF32 ? 4 : 2);
+  GRM_CHECK_RC(reserve_device(reinterpret_cast<unsigned char**>(&a->d_queries), &a->d_queries_bytes,
+                              qbytes));
+  GRM_CHECK_RC(reserve_device(&a->d_sitems, &a->d_sitems_count, items.size() + 1));
+  GRM_CHECK_RC(reserve_device(&a->d_sslots, &a->d_sslots_count, slots.size() + 1));
+  GRM_CHECK_RC(reserve_device(&a->d_sout, &a->d_sout_count, slots.size()));
+  GRM_CHECK_RC(ensure_hmax(a, H, 1));
+  GRM_HIP_CHECK(hipMemcpyAsync(a->d_queries, query_host, qbytes, hipMemcpyHostToDevice, a->stream));
+  // slot list, then the item count behind it (the exact kernel reads its
+  // item count from the device)
+  std::vector<uint32_t> sl_and_count(slots);
+  sl_and_count.push_back(static_cast<uint32_t>(items.size()));
+  GRM_HIP_CHECK(hipMemcpyAsync(a->d_sslots, sl_and_count.data(), sl_and_count.size() * sizeof(uint32_t),
+                               hipMemcpyHostToDevice, a->stream));
+  if (!items.empty()) {
+    GRM_HIP_CHECK(hipMemcpyAsync(a->d_sitems, items.data(), items.size() * sizeof(Item),
+                                 hipMemcpyHostToDevice, a->stream));
+  }
+  const auto passes = query_passes(H / static_cast<int>(a->kv), Qt, grm::gqa::kMaxRQ);
+  for (size_t i = 0; i < passes.size(); ++i) {
+    GRM_CHECK_RC(launch_q64(a, a->d_queries, query_dtype, 1, H, Qt, passes[i], i > 0));
+    if (!items.empty()) {
+      GRM_CHECK_RC(launch_exact(a, H, passes[i], a->d_sitems, items.size(),
+                                a->d_sslots + slots.size()));
+    }
+  }
+  const unsigned blocks = static_cast<unsigned>((slots.size() + 255) / 256);
+  grm::gqa::gqa_slot_scores_kernel<<<blocks, 256, 0, a->stream>>>(
+      a->d_hmax, a->cap_nodes, H, a->d_sslots, slots.size(), a->d_len, a->d_flags, a->d_qbad,
+      static_cast<int>(a->kv), a->d_sout);
+  GRM_HIP_CHECK(hipGetLastError());
+  std::vector<float> out(slots.size());
+  GRM_HIP_CHECK(hipMemcpyAsync(out.data(), a->d_sout, out.size() * sizeof(float), hipMemcpyDeviceToHost,
+                               a->stream));
+  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  for (uint64_t i = 0; i < count; ++i) out_scores_host[i] = out[where[i]];
+  grm::clear_error();
+  return 0;
 }
 
 extern "C" int grm_gqa_hip_bank_info(GqaDeviceArena* a, uint64_t* out8) {

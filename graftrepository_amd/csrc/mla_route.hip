@@ -1153,7 +1153,8 @@ __global__ __launch_bounds__(256) void mla_score_slots_kernel(
   }
   __syncthreads();
   const double qnorm = s_qnorm;
-  for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) {
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
     const uint64_t slot = slots[i];
     // the route kernels' own chunk fold, chunks in order (zero past dim)
     double acc = 0.0;
@@ -1522,12 +1523,16 @@ extern "C" int grm_mla_hip_score_nodes(MlaDeviceArena* a, const void* query_host
   auto* ds = reinterpret_cast<const uint64_t*>(static_cast<unsigned char*>(d) + s_off);
   auto* dout = reinterpret_cast<float*>(static_cast<unsigned char*>(d) + o_off);
   const size_t lds = static_cast<size_t>(a->dim_pad) * sizeof(double);
+  // one thread per listed node, spread over the compute units; each block
+  // stages the query itself
+  const unsigned blocks = static_cast<unsigned>(
+      std::min<uint64_t>((count + 255) / 256, static_cast<uint64_t>(a->cus) * 4));
   if (a->dtype == kF32) {
-    mla_score_slots_kernel<kF32><<<1, 256, lds, a->stream>>>(a->d_tiles, a->d_norms, a->capacity,
+    mla_score_slots_kernel<kF32><<<blocks, 256, lds, a->stream>>>(a->d_tiles, a->d_norms, a->capacity,
                                                              a->chunks, a->dim, a->dim_pad, dq,
                                                              query_dtype, ds, count, dout);
   } else {
-    mla_score_slots_kernel<kBF16><<<1, 256, lds, a->stream>>>(a->d_tiles, a->d_norms, a->capacity,
+    mla_score_slots_kernel<kBF16><<<blocks, 256, lds, a->stream>>>(a->d_tiles, a->d_norms, a->capacity,
                                                               a->chunks, a->dim, a->dim_pad, dq,
                                                               query_dtype, ds, count, dout);
   }

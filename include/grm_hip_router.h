@@ -298,6 +298,117 @@ int grm_gqa_hip_sync(GqaDeviceArena* arena);
  * capacity, epoch, kv_heads, head_dim, key dtype].  No counterpart. */
 int grm_gqa_hip_bank_info(GqaDeviceArena* arena, uint64_t* out8);
 
+/* ---- GQA store route on the device (cpp/grm_runtime.cpp:6898-6961) ----
+ * Per-node route filter bits, as grm_mla_hip_set_filter_bits (a slot taken
+ * by a later append starts at 0).  Ids must be live. */
+int grm_gqa_hip_set_filter_bits(GqaDeviceArena* arena, const uint64_t* node_ids,
+                                const uint64_t* bits, uint64_t count);
+
+/* One query [query_heads][query_tokens][head_dim] routed over the nodes that
+ * pass the route filters (semantics of grm_mla_hip_route_filtered): node
+ * ids and raw law scores (cpp/grm_runtime.cpp:2980-3029), (score desc, id
+ * asc).  route_gqa_raw's filtered ranking before any lexical bonus. */
+int grm_gqa_hip_route_filtered(GqaDeviceArena* arena, const void* query, int query_dtype,
+                               int query_on_device, int query_heads, int query_tokens, int topk,
+                               uint64_t filter_mask, uint32_t filter_categories,
+                               uint64_t* out_ids_host, float* out_scores_host,
+                               float* elapsed_ms_host);
+
+/* Exact raw law scores of listed live nodes for one host query (F32 or
+ * BF16): float, NaN where not finite.  No counterpart (the store scores
+ * every entry on the CPU). */
+int grm_gqa_hip_score_nodes(GqaDeviceArena* arena, const void* query_host, int query_dtype,
+                            int query_heads, int query_tokens, const uint64_t* node_ids,
+                            uint64_t count, float* out_scores_host);
+
+/* ---- The store's route calls over a device bank ---------------------------
+ * A device store holds route entries (one route key, lexical keys, route
+ * metadata per node) in an MLA or a GQA bank of this library and answers
+ * the reference store's route calls with their names, argument lists and
+ * output conventions (cpp/grm_runtime_c.h:176-181, 381-436, 499): 0 on
+ * success, nonzero with grm_store_last_error() on failure; out_count
+ * receives min(results, out_cap).  Nodes need no grm_store_add_node here:
+ * the CPU store keeps nodes and payloads, this store their route entries.
+ * Limits: topk <= 16; one key per entry (set_route_multi / set_route_list
+ * take key_count 1); MLA keys of the store's dim, GQA keys of whole
+ * [kv_heads][L][head_dim] blocks; calls on one handle are serialized. */
+typedef struct grm_store_handle grm_store_handle;
+
+/* Create an MLA store of `dim`-value fp32 route keys with room for
+ * `capacity` entries (row_dtype GRM_DTYPE_F32), or a GQA store with room
+ * for capacity_nodes entries and capacity_tokens key tokens.  Replace the
+ * reference's grm_store_create_mla / _gqa (cpp/grm_runtime_c.h:70-106) for
+ * the route path. */
+int grm_hip_store_create_mla(int dim, uint64_t capacity, int row_dtype,
+                             grm_store_handle** out_handle);
+int grm_hip_store_create_gqa(int kv_heads, int head_dim, uint64_t capacity_nodes,
+                             uint64_t capacity_tokens, grm_store_handle** out_handle);
+/* cpp/grm_runtime_c.h:108 (grm_store_destroy) */
+void grm_hip_store_destroy(grm_store_handle* handle);
+
+/* cpp/grm_runtime_c.h:381-385 */
+int grm_store_set_route(grm_store_handle* handle, uint64_t node_id, const float* route_key,
+                        uint64_t route_len, const char* lexical_keys);
+/* cpp/grm_runtime_c.h:386-391 (key_count 1 only) */
+int grm_store_set_route_multi(grm_store_handle* handle, uint64_t node_id,
+                              const float* route_keys, uint64_t key_count, uint64_t route_len,
+                              const char* lexical_keys);
+/* cpp/grm_runtime_c.h:392-399 (key_count 1 only) */
+int grm_store_set_route_list(grm_store_handle* handle, uint64_t node_id,
+                             const float* route_values, uint64_t value_count,
+                             const uint64_t* route_offsets, uint64_t key_count,
+                             const char* lexical_keys);
+/* cpp/grm_runtime_c.h:400-401 */
+int grm_store_clear_route(grm_store_handle* handle, uint64_t node_id);
+/* cpp/grm_runtime_c.h:176-181 */
+int grm_store_set_route_metadata(grm_store_handle* handle, uint64_t node_id, const char* kind,
+                                 const char* scope, const char* durability,
+                                 const char* mutability);
+/* cpp/grm_runtime_c.h:402-409 */
+int grm_store_route(grm_store_handle* handle, const float* query, uint64_t query_len,
+                    const char* lexical_keys, uint64_t topk, uint64_t* out_node_ids,
+                    uint64_t out_cap, uint64_t* out_count);
+/* cpp/grm_runtime_c.h:410-421 */
+int grm_store_route_filtered(grm_store_handle* handle, const float* query, uint64_t query_len,
+                             const char* lexical_keys, const char* kind_filters,
+                             const char* scope_filters, const char* durability_filters,
+                             const char* mutability_filters, uint64_t topk,
+                             uint64_t* out_node_ids, uint64_t out_cap, uint64_t* out_count);
+/* cpp/grm_runtime_c.h:422-435 */
+int grm_store_route_gqa(grm_store_handle* handle, const float* query, uint64_t query_heads,
+                        uint64_t query_tokens, uint64_t head_dim, const char* lexical_keys,
+                        const char* kind_filters, const char* scope_filters,
+                        const char* durability_filters, const char* mutability_filters,
+                        uint64_t topk, uint64_t* out_node_ids, uint64_t out_cap,
+                        uint64_t* out_count);
+/* cpp/grm_runtime_c.h:499 (the calling thread's last message) */
+const char* grm_store_last_error(grm_store_handle* handle);
+
+/* Many new entries at once (no counterpart: the reference sets routes one
+ * node at a time): keys back to back, key_lens[i] values for node i;
+ * lexical_keys[i] '\n'-joined (NULL array: none); metadata[4*i + c] the
+ * kind, scope, durability, mutability of node i (NULL array or empty
+ * values: the entry defaults). */
+int grm_hip_store_set_routes(grm_store_handle* handle, uint64_t count, const uint64_t* node_ids,
+                             const float* keys, const uint64_t* key_lens,
+                             const char* const* lexical_keys, const char* const* metadata);
+
+/* The store route with its fp32 route scores (no counterpart: the reference
+ * returns ids only).  MLA stores ignore query_heads / query_tokens (the
+ * query holds the store's dim values); GQA stores take
+ * [query_heads][query_tokens][head_dim]. */
+int grm_hip_store_route_scored(grm_store_handle* handle, const float* query,
+                               uint64_t query_heads, uint64_t query_tokens,
+                               const char* lexical_keys, const char* kind_filters,
+                               const char* scope_filters, const char* durability_filters,
+                               const char* mutability_filters, uint64_t topk,
+                               uint64_t* out_node_ids, float* out_scores, uint64_t out_cap,
+                               uint64_t* out_count);
+
+/* [dialect (0 MLA, 1 GQA), entries, dim or kv_heads, 0 or head_dim].
+ * No counterpart. */
+int grm_hip_store_info(grm_store_handle* handle, uint64_t* out4);
+
 /* ---- Packed graft payloads (core/graft_quant.py:177-268) ----------------
  * A packed tensor is int8 codes (values in row-major order, grouped along
  * the last axis) and one fp32 scale per group of group_size values.  It

@@ -48,6 +48,9 @@ PINNING = {
                  "(tests/golden) + hand cases [1,2,0], ties [0,1,2] + "
                  "single-token closed form (one key per node; multi-key "
                  "nodes are not modelled)",
+    "store_route_gqa": "the reference store's grm_store_route_gqa (oracle/_ref, fp64 "
+                       "law path) on random stores with lexical keys, metadata and "
+                       "filters (tests/test_store_route.py)",
     "f16 conversion": "exhaustive agreement with numpy astype(float16)",
     "bf16 rounding": "agreement with torch.bfloat16 conversion",
     "int8 quantise/dequant": "round-trip invariants of "
@@ -279,6 +282,61 @@ def store_route(rows: np.ndarray, node_ids, lexical: list, meta: list, query: np
         total = np.float32(base[i]) + bonus
         if np.isfinite(total):
             out.append((-float(total), int(ids[i]), total))
+    out.sort()
+    top = out[:topk]
+    return [n for _, n, _ in top], np.asarray([t for _, _, t in top], dtype=np.float32)
+
+
+def _route_allowed(meta_i, filters) -> bool:
+    """Route filters (cpp/grm_runtime.cpp:3053-3104) for one entry whose
+    metadata values are meta_i (empty: the entry default)."""
+    for c in range(4):
+        fl = [v for v in filters[c] if v]
+        if not fl:
+            continue
+        val = meta_i[c] or _FILTER_DEFAULT[c]
+        if all(v in _FILTER_KNOWN[c] for v in fl):
+            if not (val in fl and val in _FILTER_KNOWN[c]):
+                return False
+        elif val not in fl:
+            return False
+    return True
+
+
+def store_route_gqa(keys, tok_offsets, kv_heads: int, head_dim: int, node_ids, lexical: list,
+                    meta: list, query, query_lexical=(), filters=((), (), (), ()),
+                    topk: int = 3):
+    """The store's GQA route law, route_gqa_raw (cpp/grm_runtime.cpp:
+    4498-4881), single-key entries over fp32 keys in CSR layout (node i's
+    [kv][L_i][hd] block at tok_offsets[i] * kv * hd).
+
+    * raw = the fp64 GQA law (gqa_raw_score, :2980-3029) as float; entries
+      that fail the route filters or whose raw score is not finite drop out;
+    * no query lexical keys: order (raw desc, node id asc) (:4796-4821);
+    * with them: norm = float(max |raw| over the entries left) + 1e-8f and
+      score = raw / norm + float(hits) / float(|query lexical|) in fp32,
+      order (score desc, node id asc) (:4823-4880).
+
+    Returns (node ids, route scores fp32) of the best topk."""
+    q = np.ascontiguousarray(query, dtype=np.float32)
+    raw = gqa_scores(keys, F32, tok_offsets, kv_heads, head_dim, q[None])[0]
+    ids = np.asarray(node_ids, dtype=np.uint64)
+    qlex = [s for s in query_lexical if s]
+    have = [i for i in range(raw.size)
+            if _route_allowed(meta[i], filters) and np.isfinite(raw[i])]
+    if not qlex:
+        order = sorted(have, key=lambda i: (-float(raw[i]), int(ids[i])))[:topk]
+        return [int(ids[i]) for i in order], np.asarray([raw[i] for i in order], np.float32)
+    max_abs = np.float32(0.0)
+    for i in have:
+        max_abs = max(max_abs, np.float32(abs(raw[i])))
+    norm = np.float32(max_abs + np.float32(1.0e-8))
+    den = np.float32(len(qlex))
+    out = []
+    for i in have:
+        hits = sum(1 for s in qlex if s in lexical[i])
+        score = np.float32(np.float32(raw[i]) / norm) + np.float32(np.float32(hits) / den)
+        out.append((-float(score), int(ids[i]), np.float32(score)))
     out.sort()
     top = out[:topk]
     return [n for _, n, _ in top], np.asarray([t for _, _, t in top], dtype=np.float32)

@@ -201,3 +201,35 @@ def gqa_route(node_keys: list, query: np.ndarray, kv_heads: int, topk: int,
         if sentinel is not None:
             order = [x for x in order if x != sentinel]
         return order[:topk]
+
+
+def store_route_gqa(blocks: list, lexical: list, meta: list, query: np.ndarray, kv_heads: int,
+                    query_lexical=(), filters=((), (), (), ()), topk: int = 3) -> list[int]:
+    """Route order from the reference ``grm_store_route_gqa`` with lexical
+    keys and route filters: node i (id i) has key blocks[i] [kv, L, hd],
+    lexical keys lexical[i] and metadata meta[i].  A sentinel node with a
+    one-value key keeps the store on its fp64 law path (see gqa_route) and
+    is dropped from the order."""
+    q = np.ascontiguousarray(query, dtype=np.float32)
+    H, Qt, hd = q.shape
+    h = lib().grm_store_create_gqa(b"Qwen3_TC", 36, 2560, 2 * kv_heads * hd, 0, kv_heads, hd)
+    with _Store(h) as st:
+        for i, key in enumerate(blocks):
+            nid = st.add_node()
+            assert nid == i
+            k = np.ascontiguousarray(key, dtype=np.float32).reshape(-1)
+            offs = np.asarray([0, k.size], dtype=np.uint64)
+            st._check(lib().grm_store_set_route_list(st.h, nid, k.ctypes.data, k.size,
+                                                     offs.ctypes.data, 1, _blob(lexical[i])))
+            st._check(lib().grm_store_set_route_metadata(
+                st.h, nid, *[str(v).encode("utf-8") for v in meta[i]]))
+        sentinel = st.add_node()
+        st.set_route(sentinel, np.zeros(1, dtype=np.float32))
+        want = topk + 1
+        out = np.empty(want, dtype=np.uint64)
+        count = ctypes.c_uint64()
+        st._check(lib().grm_store_route_gqa(
+            st.h, q.ctypes.data, H, Qt, hd, _blob(query_lexical), *[_blob(f) for f in filters],
+            want, out.ctypes.data, want, ctypes.byref(count)))
+        order = [int(x) for x in out[:count.value] if int(x) != sentinel]
+        return order[:topk]

@@ -23,6 +23,10 @@ REFERENCE_SYMBOLS = {
     "grm_gqa_cuda_arena_route", "grm_gqa_cuda_arena_route_device",
     "grm_gqa_cuda_upload_queries", "grm_gqa_cuda_free_device_ptr",
     "grm_gqa_cuda_arena_destroy", "grm_gqa_cublas_route",
+    # the CPU store's route calls (cpp/grm_runtime_c.h:176-181, 381-436, 499)
+    "grm_store_set_route", "grm_store_set_route_multi", "grm_store_set_route_list",
+    "grm_store_clear_route", "grm_store_set_route_metadata", "grm_store_route",
+    "grm_store_route_filtered", "grm_store_route_gqa", "grm_store_last_error",
 }
 
 

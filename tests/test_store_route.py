@@ -80,3 +80,36 @@ def test_split_and_bits_follow_the_reference():
     assert sr.filter_bits("doc", "project", "permanent", "stable") == (
         (1 << 1) | (1 << 17) | (1 << 35) | (1 << 49))
     assert sr.filter_bits("weird", "", "", "") == 0
+
+
+def random_gqa_store(rng, n, kv, hd):
+    lens = rng.integers(0, 20, size=n)
+    blocks = [rng.standard_normal((kv, int(L), hd)).astype(np.float32) for L in lens]
+    blocks[5] = blocks[4].copy()                   # exact ties
+    blocks[9] = blocks[4].copy()
+    lexical = [list(rng.choice(VOCAB, size=rng.integers(0, 4), replace=False)) for _ in range(n)]
+    meta = [tuple(str(rng.choice(m)) for m in META) for _ in range(n)]
+    return blocks, lexical, meta
+
+
+def test_oracle_gqa_store_law_matches_the_reference_store():
+    rng = np.random.default_rng(43)
+    n, kv, hd, H = 80, 2, 8, 4
+    blocks, lexical, meta = random_gqa_store(rng, n, kv, hd)
+    lens = np.asarray([b.shape[1] for b in blocks], dtype=np.uint64)
+    offs = np.zeros(n + 1, dtype=np.uint64)
+    offs[1:] = np.cumsum(lens)
+    keys = np.concatenate([b.reshape(-1) for b in blocks])
+    for case in range(60):
+        Qt = int(rng.integers(1, 4))
+        q = rng.standard_normal((H, Qt, hd)).astype(np.float32)
+        if rng.random() < 0.3 and blocks[4].shape[1] > 0:
+            q[:, 0, :] = np.repeat(blocks[4][:, 0, :], H // kv, axis=0)
+        qlex = list(rng.choice(VOCAB, size=rng.integers(0, 5), replace=True))
+        filters = tuple([v for v in (list(rng.choice(m, size=rng.integers(0, 3), replace=False))
+                                     if rng.random() < 0.5 else []) if v] for m in META)
+        k = int(rng.integers(1, 17))
+        want = ref.store_route_gqa(blocks, lexical, meta, q, kv, qlex, filters, k)
+        got, _ = oracle.store_route_gqa(keys, offs, kv, hd, np.arange(n), lexical, meta, q,
+                                        qlex, filters, k)
+        assert got == want, (case, qlex, filters, k)

@@ -79,3 +79,87 @@ def test_device_store_route_matches_the_law(hip_lib):
                                           want_sc.view(np.uint32))
             assert st.route_filtered(q, "\n".join(qlex), *["\n".join(f) for f in filters],
                                      topk=k) == want_ids
+
+
+def test_device_gqa_store_route_matches_the_law(hip_lib):
+    # grm_store_route_gqa's law (route_gqa_raw, cpp/grm_runtime.cpp:4498-4881)
+    # over the device store: raw order without lexical keys, normalised raw
+    # plus the lexical bonus with them; filters of known and unknown values;
+    # replacements, clears and metadata updates between queries.
+    from graftrepository_amd.store_route import DeviceGqaRouteStore
+
+    rng = np.random.default_rng(53)
+    n, kv, hd, H = 400, 4, 64, 16
+    blocks = {500 + i: rng.standard_normal((kv, int(rng.integers(0, 40)), hd)).astype(np.float32)
+              for i in range(n)}
+    blocks[505] = blocks[504].copy()                # ties
+    lex, meta = {}, {}
+    with DeviceGqaRouteStore(kv, hd, capacity_nodes=512, capacity_tokens=40_000) as st:
+        ids0 = sorted(blocks)
+        for nid in ids0:
+            lex[nid] = list(rng.choice(VOCAB, size=rng.integers(0, 4), replace=False))
+            meta[nid] = tuple(str(rng.choice(m)) or d for m, d in zip(META, DEFAULT))
+        st.set_routes(ids0, [blocks[i] for i in ids0], [lex[i] for i in ids0],
+                      [meta[i] for i in ids0])
+        for step in range(30):
+            if step % 5 == 4:
+                for nid in rng.choice(sorted(blocks), size=15, replace=False):
+                    nid = int(nid)
+                    op = rng.integers(0, 3)
+                    if op == 0:
+                        blocks[nid] = rng.standard_normal(
+                            (kv, int(rng.integers(0, 40)), hd)).astype(np.float32)
+                        lex[nid] = list(rng.choice(VOCAB, size=rng.integers(0, 3), replace=False))
+                        st.set_route(nid, blocks[nid], lex[nid])
+                    elif op == 1:
+                        vals = tuple(str(rng.choice(m)) for m in META)
+                        st.set_route_metadata(nid, *vals)
+                        meta[nid] = tuple(v if v else o for v, o in zip(vals, meta[nid]))
+                    else:
+                        st.clear_route(nid)
+                        del blocks[nid], lex[nid], meta[nid]
+            ids = sorted(blocks)
+            lens = np.asarray([blocks[i].shape[1] for i in ids], dtype=np.uint64)
+            offs = np.zeros(len(ids) + 1, dtype=np.uint64)
+            offs[1:] = np.cumsum(lens)
+            keys = np.concatenate([blocks[i].reshape(-1) for i in ids])
+            Qt = int(rng.integers(1, 6))
+            q = rng.standard_normal((H, Qt, hd)).astype(np.float32)
+            qlex = list(rng.choice(VOCAB, size=rng.integers(0, 5), replace=True))
+            filters = tuple([str(v) for v in rng.choice(m, size=rng.integers(0, 3), replace=False)
+                             if v] if rng.random() < 0.5 else [] for m in META)
+            k = int(rng.integers(1, 16))
+            want_ids, want_sc = oracle.store_route_gqa(
+                keys, offs, kv, hd, ids, [lex[i] for i in ids], [meta[i] for i in ids], q, qlex,
+                filters, k)
+            got_ids, got_sc = st.route_scored(q, qlex, k, kinds=filters[0], scopes=filters[1],
+                                              durabilities=filters[2], mutabilities=filters[3])
+            assert got_ids == want_ids, (step, qlex, filters, k)
+            np.testing.assert_array_equal(np.asarray(got_sc, np.float32).view(np.uint32),
+                                          want_sc.view(np.uint32))
+            assert st.route_gqa(q, "\n".join(qlex), *["\n".join(f) for f in filters],
+                                topk=k) == want_ids
+
+
+def test_device_store_refuses_what_it_does_not_serve(hip_lib):
+    from graftrepository_amd import _lib
+    from graftrepository_amd.store_route import DeviceGqaRouteStore
+
+    lib = _lib.load()
+    with DeviceRouteStore(8, capacity=64) as st:
+        with pytest.raises(RuntimeError):
+            st.set_route(1, np.zeros(7, np.float32))          # wrong length
+        keys = np.zeros((2, 8), np.float32)
+        rc = lib.grm_store_set_route_multi(st._h, 3, keys.ctypes.data, 2, 8, b"")
+        assert rc != 0 and b"multi-row" in lib.grm_store_last_error(st._h)
+        st.set_route(1, np.ones(8, np.float32), "a")
+        with pytest.raises(RuntimeError):
+            st.route_scored(np.ones(8, np.float32), topk=17)   # above the device list
+        st.clear_route(99)                                     # no entry: nothing to clear
+        assert len(st) == 1
+    with DeviceGqaRouteStore(2, 8, capacity_nodes=8, capacity_tokens=64) as st:
+        with pytest.raises(RuntimeError):
+            st.set_route(1, np.zeros(17, np.float32))         # not whole [kv][L][hd] blocks
+        q = np.zeros((3, 1, 8), np.float32)
+        with pytest.raises(RuntimeError):
+            st.route_gqa(q, topk=2)                             # heads not a multiple of kv
