@@ -534,8 +534,14 @@ constexpr int kMaxCols = 64;  // query columns (Qb * R * Qt) per screen pass
 //    product (0 elsewhere), sigma_q a scaled query value flushed or rounded
 //    near zero, sigma_k a key value flushed near zero, sigma_p a product
 //    lost to underflow, and 2^-40 the law's own fp64 rounding;
-// into s_ec[cg] = {coef, eabs, scale, 0} and s_bad[cg] = 1 when the column
-// holds a non-finite value.  Ends with a barrier.
+// into s_ec[cg] = {coef, eabs, scale, kcap} and s_bad[cg] = 1 when the
+// column holds a non-finite value.  kcap = 2^127 / (scale * ||q|| *
+// (1 + 2^-6)), rounded down: for a node whose key norm bound K stays below
+// it, every product and partial sum of the screen's fp32 accumulation stays
+// below 2^127 in magnitude (Cauchy-Schwarz; 1 + 2^-6 covers the roundings
+// of query, key and sums), so no screened value overflows; for K >= kcap
+// the bound is not established and the screen's users take E = +inf.
+// Ends with a barrier.
 template <int HD>
 __device__ inline void stage_columns(float* __restrict__ s_q, float4* __restrict__ s_ec,
                                      unsigned* __restrict__ s_bad, const void* __restrict__ query,
@@ -587,9 +593,10 @@ __device__ inline void stage_columns(float* __restrict__ s_q, float4* __restrict
       const double up = 1.0 + 0x1p-20;
       c *= up * scale * up;
       ea *= up * scale * up;
+      const double kcap = 0x1p127 / (static_cast<double>(scale) * norm * (1.0 + 0x1p-6)) * (1.0 - 0x1p-20);
       s_ec[cg] = make_float4(isfinite(c) ? static_cast<float>(c) * 1.000001f : INFINITY,
                              isfinite(ea) ? static_cast<float>(ea) * 1.000001f : INFINITY, scale,
-                             0.0f);
+                             kcap < 0x1p127 ? static_cast<float>(kcap) : INFINITY);
       s_bad[cg] = bad ? 1u : 0u;
     }
   }
@@ -725,10 +732,9 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
   constexpr int HD = 32 * KS;
   constexpr int C = HD / KT::kEpc;  // chunks per key row
   extern __shared__ float s_q[];  // [cols][HD]: the block's query columns
-  __shared__ float4 s_ec[kMaxCols];  // {coef, eabs, scale, 0} per column
+  __shared__ float4 s_ec[kMaxCols];  // {coef, eabs, scale, kcap} per column
   __shared__ unsigned s_bad[kMaxCols];
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
   // g_fast: grid (kv, item blocks), so consecutive blocks read one node's
   // neighbouring kv-head blocks; else grid (item blocks, kv)
   const int g = g_fast ? blockIdx.x : blockIdx.y;
@@ -899,7 +905,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     const int cg = nt * 16 + r16;
     live[nt] = cg < cols && s_bad[min(cg, cols - 1)] == 0u;
     const float4 ec = s_ec[min(cg, cols - 1)];
-    const double e = static_cast<double>(ec.x) * static_cast<double>(km) + static_cast<double>(ec.y);
+    const double e = km < ec.w ? static_cast<double>(ec.x) * static_cast<double>(km) + static_cast<double>(ec.y)
+                               : static_cast<double>(INFINITY);
     thr[nt] = static_cast<double>(m) - 2.0 * e;
     if (live[nt]) {
       amb = amb || !(thr[nt] > -INFINITY) || !isfinite(e) ||
@@ -1006,7 +1013,7 @@ __device__ inline void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 // four tiles in flight ahead of the one being screened, across item
 // boundaries.  The block stages kv head g's query columns once
 // (stage_columns); blocks with blockIdx.x == 0 write colinfo[g*cols + cg]
-// = {coef, eabs, scale, bad} for the bounds kernel.
+// = {coef, eabs, scale, kcap} for the bounds kernel.
 //
 // The MFMA runs with the query columns as the row operand, so lane l holds
 // columns nt*16 + (l/16)*4 + v (v < 4) of token l%16, the token whose key
@@ -1146,11 +1153,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
   stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, R, Qt, g, emax,
                     gamma, delta, rho, sigma_q, sigma_k, sigma_p);
   if (blockIdx.x == 0) {
-    for (int cg = threadIdx.x; cg < cols; cg += blockDim.x) {
-      float4 e = s_ec[cg];
-      e.w = s_bad[cg] ? 1.0f : 0.0f;
-      colinfo[g * cols + cg] = e;
-    }
+    for (int cg = threadIdx.x; cg < cols; cg += blockDim.x) colinfo[g * cols + cg] = s_ec[cg];
   }
   if (!has_item) return;
 
@@ -1273,6 +1276,15 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
   } while (!done);
 }
 
+// Norm bound K of a node's keys as the screen used them: its largest key
+// norm kmax, or with FACT (INT8 rows with one scale each, screened as
+// scale * codes) the bound on ||code * scale||,
+// (kmax + 2^-25 sqrt(hd)) / (1 - 2^-10).
+__host__ __device__ inline double screen_key_norm(float kmax, bool fact, int hd) {
+  return fact ? (static_cast<double>(kmax) + 0x1p-25 * sqrt(static_cast<double>(hd))) / (1.0 - 0x1p-10)
+              : static_cast<double>(kmax);
+}
+
 // Node-score bounds; grid (queries, blocks), 4 wavefronts, lane = slot,
 // grid-stride over groups of 64 slots.  For query qb and slot s, each
 // column's screened maximum m (hmaxf[(s*kv + g)*colstride + cg], cg the
@@ -1280,16 +1292,18 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
 // law's
 // max_t |dot| / sqrt(hd) of its head and query token from below by
 // max(0, m - E) / scale / denom and from above by (m + E) / scale / denom,
-// E = coef * K + eabs (colinfo), K = kmax[s], or with FACT the bound on
-// ||code * scale|| the screen used: (kmax + 2^-25 sqrt(hd)) / (1 - 2^-10).
+// E = coef * K + eabs (colinfo), K = screen_key_norm(kmax[s]), and
+// E = +inf where K >= kcap (the screen may have overflowed).
 // best_h is the max over the head's query tokens, so its bounds are the
 // max of theirs; the score (sum_h best_h) / H lies in [lb, ub] with
 // lb = sum_h lo_h / H, ub = sum_h hi_h / H, widened by 2^-40 for the fp64
 // arithmetic on both sides and rounded outward to float.  Writes
 // lbub[qb*cap + s] = (lb, ub): (0, 0) for a live node without key tokens,
 // NaN for slots that are not ranked (free, non-finite keys, non-finite
-// query; their cells are never read); the block's k best lower bounds
-// (tie law) go to block_out[(qb*blocks + block)*k ..).  Also
+// query; their cells are never read) or certainly unranked (a lower bound
+// past the float range: the law's score is +inf); the block's k best
+// lower bounds among nodes with a finite upper bound (tie law) go to
+// block_out[(qb*blocks + block)*k ..).  Also
 // zeroes *zero_counter (the candidates kernel's item count).
 __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     const unsigned* __restrict__ hmaxf, int colstride, size_t cap, int H, int Qt, int R, int cols,
@@ -1299,7 +1313,7 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     const unsigned* __restrict__ qbad, int fact, int hd, int k, float2* __restrict__ lbub,
     Cand* __restrict__ block_out, uint32_t* __restrict__ zero_counter) {
   __shared__ Cand s_lists[kFinWaves][kMaxTopK];
-  extern __shared__ float4 s_ci[];  // [H*Qt]: query qb's {coef, eabs, 1/scale, bad}, (h, qi) order
+  extern __shared__ float4 s_ci[];  // [H*Qt]: query qb's {coef, eabs, 1/scale, kcap}, (h, qi) order
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   // grid (queries, slot blocks): the queries of one group of slots run
@@ -1316,7 +1330,6 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     s_ci[i] = ci;
   }
   __syncthreads();
-  const double kadd = 0x1p-25 * denom;
   bool q_bad = false;
   for (int g0 = 0; g0 < kv; g0 += kWave) {
     q_bad = q_bad || (g0 + lane < kv && qbad[qb * kv + g0 + lane] != 0u);
@@ -1332,8 +1345,7 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     const uint32_t len = in ? lens[slot] : 0u;
     const uint64_t id = in ? ids[slot] : kNoId;
     const float kmf = in ? __uint_as_float(kmax[slot]) : 0.0f;
-    const double K = fact ? (static_cast<double>(kmf) + kadd) / (1.0 - 0x1p-10)
-                          : static_cast<double>(kmf);
+    const double K = screen_key_norm(kmf, fact != 0, hd);
     // only ranked nodes with key tokens have screened maxima
     const bool screened = in && (f & 3u) == 3u && len != 0u && !q_bad;
     const unsigned* cells = hmaxf + static_cast<size_t>(screened ? slot : 0u) * kv * colstride;
@@ -1356,7 +1368,9 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
         const int hq = j0 + j;
         if (hq < HQ) {
           const float4 ci = s_ci[hq];
-          const double e = (static_cast<double>(ci.x) * K + static_cast<double>(ci.y)) * (1.0 + 0x1p-50);
+          const double e = K < static_cast<double>(ci.w)
+                               ? (static_cast<double>(ci.x) * K + static_cast<double>(ci.y)) * (1.0 + 0x1p-50)
+                               : static_cast<double>(INFINITY);
           const double m = static_cast<double>(mv[j]);
           const double inv = static_cast<double>(ci.z);
           const double lo = fmax(0.0, m - e) * inv;
@@ -1377,7 +1391,9 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     if (in && (f & 1u)) {
       if (len == 0) {
         lbf = ubf = 0.0f;
-      } else if ((f & 2u) && !q_bad) {
+      } else if ((f & 2u) && !q_bad && !isinf(static_cast<float>(lb))) {
+        // (a lower bound that rounds to +inf means the law's float score
+        // is +inf too: the node is certainly not ranked and stays NaN)
         lbf = static_cast<float>(lb);
         if (static_cast<double>(lbf) > lb) lbf = nextafterf(lbf, -INFINITY);
         ubf = static_cast<float>(ub);
@@ -1385,7 +1401,10 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
       }
     }
     if (in) lbub[static_cast<size_t>(qb) * cap + slot] = make_float2(lbf, ubf);
-    wl_consume(Lw, k, lbf, id, slot, isfinite(lbf) && lbf >= Lw.th_s);
+    // a lower bound counts towards the k best only when the node's score
+    // is certainly finite (ub below the float range), as only finite
+    // scores are ranked
+    wl_consume(Lw, k, lbf, id, slot, isfinite(lbf) && isfinite(ubf) && lbf >= Lw.th_s);
   }
   if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(Lw);
   __syncthreads();

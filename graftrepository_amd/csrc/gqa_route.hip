@@ -890,15 +890,15 @@ int prepare_bv(GqaDeviceArena* a, const SrPlan& p, int topk, uint32_t fin_blocks
   return 0;
 }
 
-// Enqueue one bound-and-verify pass over queries [0, qb) at qptr; query
-// j's top-k candidates (kCandFinBlocks lists of k) land at bout + j*per_q.
-int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
-               int topk, uint32_t fin_blocks, Cand* bout, size_t per_q) {
+// Screen-only pass of queries [0, qb) at qptr over every (node, kv head)
+// work unit: the largest screened |q~.k| per column and node into
+// d_hmaxf (one run of colstride cells per (slot, kv head)), the columns'
+// bound parameters into d_colinfo.
+int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
+                int colstride) {
   const int kv = static_cast<int>(a->kv);
-  const int RQ = p.R * p.Qt;
-  const int cols = qb * RQ;
+  const int cols = qb * p.R * p.Qt;
   const int NT = (cols + 15) / 16 <= 1 ? 1 : ((cols + 15) / 16 <= 2 ? 2 : 4);
-  const int H = p.H;
   const bool fact = a->key_dtype == kI8 && static_cast<uint32_t>(a->group_size) == a->hd;
   // error-bound constants as in enqueue_sr; rho: the INT8 row scale
   // factored out of the dot product (fp32 product then fp16 rounding of
@@ -908,13 +908,8 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
                sigma_p = eb.sigma_p;
   const int emax = eb.emax;
   const double rho = fact ? ldexp(1.0, -11) + ldexp(1.0, -21) : 0.0;
-  const size_t q_elems = static_cast<size_t>(H) * p.Qt * a->hd;
-  // screened maxima: one run of colstride cells per (slot, kv head)
-  const int colstride = p.qb_max * RQ;
+  const size_t q_elems = static_cast<size_t>(p.H) * p.Qt * a->hd;
   const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
-  // 1. query rows as doubles and the query flags (for the exact pass)
-  GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, p.passes[0], false));
-  // 2. screened maxima of every (column, node)
   if (a->n_units > 0) {
     const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);
 #define GRM_SMAX(KDT, KS, NTT, FACT, SF16)                                                        \
@@ -960,6 +955,24 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
 #undef GRM_SMAX
     GRM_HIP_CHECK(hipGetLastError());
   }
+  return 0;
+}
+
+// Enqueue one bound-and-verify pass over queries [0, qb) at qptr; query
+// j's top-k candidates (kCandFinBlocks lists of k) land at bout + j*per_q.
+int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
+               int topk, uint32_t fin_blocks, Cand* bout, size_t per_q) {
+  const int kv = static_cast<int>(a->kv);
+  const int RQ = p.R * p.Qt;
+  const int cols = qb * RQ;
+  const int H = p.H;
+  const bool fact = a->key_dtype == kI8 && static_cast<uint32_t>(a->group_size) == a->hd;
+  // screened maxima: one run of colstride cells per (slot, kv head)
+  const int colstride = p.qb_max * RQ;
+  // 1. query rows as doubles and the query flags (for the exact pass)
+  GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, p.passes[0], false));
+  // 2. screened maxima of every (column, node)
+  GRM_CHECK_RC(launch_smax(a, p, qptr, q_dtype, qb, colstride));
   // 3. score bounds, the k best lower bounds per block (with no key tokens
   // at all the column parameters are never used: every live node has no
   // tokens and scores 0)
@@ -1495,5 +1508,79 @@ extern "C" int grm_gqa_hip_bank_info(GqaDeviceArena* a, uint64_t* out8) {
   out8[5] = a->kv;
   out8[6] = a->hd;
   out8[7] = static_cast<uint64_t>(a->key_dtype);
+  return 0;
+}
+
+// ------------------------------------------------------- screen-bound probe
+//
+// Test entry: runs the screen-only kernel of the bound-and-verify path (one
+// query, one pass: heads/kv_heads x query_tokens <= 64 columns per kv head)
+// over every node with key tokens and returns, per (slot < node capacity,
+// kv head g,
+// column cg = r*Qt + t of head g*R + r at query token t), the largest
+// screened value over the node's tokens in the screen's scaled units,
+// out_maxima[(slot*kv + g)*R*Qt + cg] (0 for nodes without tokens); per
+// column the bound parameters {coef, eabs, scale, kcap},
+// out_colinfo[(g*R*Qt + cg)*4 ..]; per slot the key norm bound K the
+// bound uses, out_knorm[slot]; and the slots' node ids.  For every node
+// with K < kcap the screen obeys |m - scale * max_t |q.k_t|| <= coef * K +
+// eabs.  Not on any route path; allocates its own query buffer.
+extern "C" int grm_gqa_hip_probe_screen(GqaDeviceArena* a, const void* query_host, int query_dtype,
+                                        int query_heads, int query_tokens, float* out_maxima_host,
+                                        float* out_colinfo_host, double* out_knorm_host,
+                                        uint64_t* out_slot_ids_host) {
+  if (!a || !query_host || !out_maxima_host || !out_colinfo_host || !out_knorm_host) {
+    return grm::fail(-1, "null argument");
+  }
+  if (query_dtype != kF32 && query_dtype != kBF16) return grm::fail(-1, "query dtype must be F32 or BF16");
+  if (query_heads <= 0 || query_tokens <= 0 || query_heads % static_cast<int>(a->kv) != 0) {
+    return grm::fail(-1, "need heads, tokens > 0 and heads % kv_heads == 0");
+  }
+  SrPlan p;
+  if (!sr_plan(a, query_heads, query_tokens, &p) || p.passes.size() != 1) {
+    return grm::fail(-1, "bank or query has no screen pass (bf16/f16/int8 keys, head_dim 64/128/256, <= 64 columns)");
+  }
+  const uint64_t n = a->cap_nodes;
+  const int colstride = p.R * p.Qt;
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  struct Buf {
+    void* p = nullptr;
+    ~Buf() {
+      if (p) (void)hipFree(p);
+    }
+  } d_q;
+  const size_t qbytes = static_cast<size_t>(query_heads) * query_tokens * a->hd * (query_dtype == kF32 ? 4 : 2);
+  GRM_HIP_CHECK(hipMalloc(&d_q.p, qbytes));
+  const size_t cells = static_cast<size_t>(a->cap_nodes) * a->kv * colstride;
+  GRM_CHECK_RC(reserve_device(&a->d_hmaxf, &a->d_hmaxf_count, cells));
+  GRM_CHECK_RC(reserve_device(&a->d_colinfo, &a->d_colinfo_count,
+                              static_cast<size_t>(a->kv) * grm::gqa::kMaxCols));
+  if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
+  GRM_CHECK_RC(ensure_items(a));
+  if (a->n_units == 0) return grm::fail(-1, "no node has key tokens");
+  GRM_HIP_CHECK(hipMemcpyAsync(d_q.p, query_host, qbytes, hipMemcpyHostToDevice, a->stream));
+  GRM_HIP_CHECK(hipMemsetAsync(a->d_hmaxf, 0, cells * sizeof(unsigned), a->stream));
+  GRM_CHECK_RC(launch_smax(a, p, static_cast<const unsigned char*>(d_q.p), query_dtype, 1, colstride));
+  const size_t out_cells = static_cast<size_t>(n) * a->kv * colstride;
+  GRM_HIP_CHECK(hipMemcpyAsync(out_maxima_host, a->d_hmaxf, out_cells * sizeof(float),
+                               hipMemcpyDeviceToHost, a->stream));
+  GRM_HIP_CHECK(hipMemcpyAsync(out_colinfo_host, a->d_colinfo,
+                               static_cast<size_t>(a->kv) * colstride * sizeof(float4),
+                               hipMemcpyDeviceToHost, a->stream));
+  std::vector<unsigned> km(n);
+  GRM_HIP_CHECK(hipMemcpyAsync(km.data(), a->d_kmax, n * sizeof(unsigned), hipMemcpyDeviceToHost,
+                               a->stream));
+  if (out_slot_ids_host) {
+    GRM_HIP_CHECK(hipMemcpyAsync(out_slot_ids_host, a->d_ids, n * sizeof(uint64_t),
+                                 hipMemcpyDeviceToHost, a->stream));
+  }
+  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  const bool fact = a->key_dtype == kI8 && static_cast<uint32_t>(a->group_size) == a->hd;
+  for (uint64_t s = 0; s < n; ++s) {
+    float f;
+    memcpy(&f, &km[s], sizeof(f));
+    out_knorm_host[s] = grm::gqa::screen_key_norm(f, fact, static_cast<int>(a->hd));
+  }
+  grm::clear_error();
   return 0;
 }

@@ -79,7 +79,10 @@ constexpr int kEntryPlanes = 3;      // u1, u2, nk
 // tile*32 + l%32 -- two 512-byte runs per load -- and the B fragment is
 // query ct*32 + l%32 at dims 16*ks + 8*(l/32) .. +8; result register r of
 // lane l is slot tile*32 + 8*(r/4) + 4*(l/32) + r%4 against that query.
-template <int KS, int CT>
+//
+// kProbe (tests of the screen bound only): every coded u goes to
+// planes[q*cap + slot] instead of the lists, and nothing else is written.
+template <int KS, int CT, bool kProbe = false>
 __global__ __launch_bounds__(kBatchWaves * kWave) void mla_batch_screen_kernel(
     const u32x4* __restrict__ tiles, const float* __restrict__ norms, uint64_t cap,
     uint32_t chunks, uint32_t n_tiles32, const uint16_t* __restrict__ qpad, int stride_arg,
@@ -187,7 +190,16 @@ __global__ __launch_bounds__(kBatchWaves * kWave) void mla_batch_screen_kernel(
 #pragma unroll
       for (int c = 0; c < kG; ++c) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) update(acc[c][r], wr[r], g * kG + c, tcode | static_cast<uint32_t>(r));
+        for (int r = 0; r < 16; ++r) {
+          if constexpr (kProbe) {
+            const uint32_t slot = t * 32u + 8u * (r / 4) + 4u * half + (r % 4);
+            const uint32_t q = (g * kG + c) * 32u + col;
+            planes[static_cast<size_t>(q) * cap + slot] =
+                and_or_b32(__float_as_uint(acc[c][r] * wr[r]), keep_mask, tcode | static_cast<uint32_t>(r));
+          } else {
+            update(acc[c][r], wr[r], g * kG + c, tcode | static_cast<uint32_t>(r));
+          }
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -222,6 +234,7 @@ __global__ __launch_bounds__(kBatchWaves * kWave) void mla_batch_screen_kernel(
     if (t + 1 < t_end) load_norms(t + 1);
     fold(a, wr, t, t + 1 < t_end ? t + 1 : t);
   }
+  if constexpr (kProbe) return;
   // The two lane halves of a column hold disjoint slots: merge their lists
   // (each half's three values go through the same update as a score), then
   // the block's 8 sub-streams per query go out through LDS so that every
@@ -340,12 +353,53 @@ __device__ inline float wave_sort_desc(float v) {
 // below t as well changes nothing: they are real nodes with law scores.
 // Writes out[qi*k ..) (the law's top-k, host mapped) and status[qi] = 1
 // when certified (0: route qi again on the exact path).
+constexpr uint32_t kBatchMaxDim = 288;
+
+// The law's query norm (d ascending, fp64): one wavefront stages query qi
+// (`dim` values, F32 or BF16, qstride elements apart) as doubles in
+// s_q[kBatchMaxDim], zero past dim; its lane 0 sums the squares and
+// returns the norm (other lanes return 0).
+__device__ inline double stage_query_norm(double* __restrict__ s_q, const void* __restrict__ query,
+                                          int q_dtype, size_t qstride, int qi, uint32_t dim,
+                                          int lane) {
+  const unsigned char* qbase = static_cast<const unsigned char*>(query) +
+                               static_cast<size_t>(qi) * qstride * (q_dtype == kBF16 ? 2 : 4);
+  for (uint32_t d = lane; d < kBatchMaxDim; d += kWave) {
+    double x = 0.0;
+    if (d < dim) {
+      x = q_dtype == kBF16
+              ? static_cast<double>(bf16_to_f32(reinterpret_cast<const uint16_t*>(qbase)[d]))
+              : static_cast<double>(reinterpret_cast<const float*>(qbase)[d]);
+    }
+    s_q[d] = x;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  double acc = 0.0;
+  if (lane == 0) {
+#pragma unroll
+    for (uint32_t d = 0; d < kBatchMaxDim; ++d) acc = fma(s_q[d], s_q[d], acc);
+  }
+  return sqrt(acc);
+}
+
+// The screen bound B of a query (|s~ - score|, see mla_batch_merge_kernel)
+// from the law's query norm qn and the smallest positive row norm nmin;
+// it holds where qn * nmax < 2^125 (nmax the largest row norm).
+__device__ inline double batch_screen_bound(double gamma, double delta, double qn, double nmin,
+                                            uint32_t dim, int ibits) {
+  const double bound0 = (gamma + delta) * (1.0 + 0x1p-20) + 8.0 * 0x1p-24 + 1.01e-8 / (qn * nmin) +
+                        sqrt(static_cast<double>(dim)) * 0x1p-125 * (1.0 / qn + 1.0 / nmin) +
+                        dim * 0x1p-125 / (qn * nmin);
+  return bound0 + ldexp(1.0 + bound0, ibits - 23) * (1.0 + 0x1p-20) + ldexp(1.0, ibits - 148) / qn;
+}
+
 constexpr int kMergeThreads = 512;
 constexpr int kMergeWavesB = kMergeThreads / kWave;
 constexpr int kMergeLoaders = kMergeThreads - kWave;  // threads of the entry-loading wavefronts
 constexpr int kMergePer = 8;       // sub-streams per loading thread: n_sub <= 3584
 constexpr int kSurvMax = kMergeThreads;
-constexpr uint32_t kBatchMaxDim = 288;
 
 __global__ __launch_bounds__(kMergeThreads) void mla_batch_merge_kernel(
     const uint32_t* __restrict__ planes, uint32_t n_sub, int QP, uint32_t n_tiles32, int ibits,
@@ -408,28 +462,9 @@ __global__ __launch_bounds__(kMergeThreads) void mla_batch_merge_kernel(
     }
   }
   if (wave == kMergeWavesB - 1) {
-    // the last wavefront stages the query; its lane 0 forms the law's
-    // qnorm (d ascending; zero past dim adds exact zeros)
-    const unsigned char* qbase = static_cast<const unsigned char*>(query) +
-                                 static_cast<size_t>(qi) * qstride * (q_dtype == kBF16 ? 2 : 4);
-    for (uint32_t d = lane; d < kBatchMaxDim; d += kWave) {
-      double x = 0.0;
-      if (d < dim) {
-        x = q_dtype == kBF16
-                ? static_cast<double>(bf16_to_f32(reinterpret_cast<const uint16_t*>(qbase)[d]))
-                : static_cast<double>(reinterpret_cast<const float*>(qbase)[d]);
-      }
-      s_q[d] = x;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane == 0) {
-      double acc = 0.0;
-#pragma unroll
-      for (uint32_t d = 0; d < kBatchMaxDim; ++d) acc = fma(s_q[d], s_q[d], acc);
-      s_qn = sqrt(acc);
-    }
+    // the last wavefront stages the query and forms the law's qnorm
+    const double qn = stage_query_norm(s_q, query, q_dtype, qstride, qi, dim, lane);
+    if (lane == 0) s_qn = qn;
   }
   if (tid == 0) s_count = 0u;
   // largest finite kept s~ of the thread; a +inf s~ voids the certificate
@@ -451,12 +486,7 @@ __global__ __launch_bounds__(kMergeThreads) void mla_batch_merge_kernel(
   const double qn = s_qn;
   const double nmin = static_cast<double>(__uint_as_float(norm_range[0]));
   const double nmax = static_cast<double>(__uint_as_float(norm_range[1]));
-  const double bound0 = (gamma + delta) * (1.0 + 0x1p-20) + 8.0 * 0x1p-24 +
-                        1.01e-8 / (qn * nmin) +
-                        sqrt(static_cast<double>(dim)) * 0x1p-125 * (1.0 / qn + 1.0 / nmin) +
-                        dim * 0x1p-125 / (qn * nmin);
-  const double bound = bound0 + ldexp(1.0 + bound0, ibits - 23) * (1.0 + 0x1p-20) +
-                       ldexp(1.0, ibits - 148) / qn;
+  const double bound = batch_screen_bound(gamma, delta, qn, nmin, dim, ibits);
   float L = -INFINITY, nk_all = -INFINITY;
 #pragma unroll
   for (int w = 0; w < kMergeWavesB - 1; ++w) {
@@ -578,6 +608,33 @@ __global__ __launch_bounds__(kMergeThreads) void mla_batch_merge_kernel(
     const bool ok = pre && n_fin >= k &&
                     static_cast<double>(s_ek) >= static_cast<double>(vk) - bound;
     status[qi] = ok ? 1u : 0u;
+  }
+}
+
+// Tests of the screen bound: the screened scores s~ = u * (1/||q||) of a
+// probe screen (planes[q*cap + slot], coded u bits) for slots [0, n),
+// out_values[qi*n + slot], and the query's bound B, out_bounds[qi] (+inf
+// where qn * nmax >= 2^125: B is not established there).  grid = queries
+// of the pass, one wavefront each.
+__global__ __launch_bounds__(kWave) void mla_batch_probe_finish_kernel(
+    const uint32_t* __restrict__ planes, uint64_t cap, uint32_t n, const float* __restrict__ inv_qn,
+    const void* __restrict__ query, int q_dtype, size_t qstride, uint32_t dim, double gamma,
+    double delta, const unsigned* __restrict__ norm_range, int ibits, float* __restrict__ out_values,
+    double* __restrict__ out_bounds) {
+  __shared__ double s_q[kBatchMaxDim];
+  const int qi = blockIdx.x;
+  const int lane = threadIdx.x;
+  const double qn = stage_query_norm(s_q, query, q_dtype, qstride, qi, dim, lane);
+  if (lane == 0) {
+    const double nmin = static_cast<double>(__uint_as_float(norm_range[0]));
+    const double nmax = static_cast<double>(__uint_as_float(norm_range[1]));
+    out_bounds[qi] = qn * nmax < 0x1p125 ? batch_screen_bound(gamma, delta, qn, nmin, dim, ibits)
+                                         : static_cast<double>(INFINITY);
+  }
+  const float iq = inv_qn[qi];
+  for (uint32_t s = lane; s < n; s += kWave) {
+    out_values[static_cast<size_t>(qi) * n + s] =
+        __uint_as_float(planes[static_cast<size_t>(qi) * cap + s]) * iq;
   }
 }
 

@@ -35,6 +35,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <limits>
 #include <mutex>
 #include <set>
 #include <unordered_map>
@@ -789,19 +790,51 @@ bool batch_plan(const MlaDeviceArena* a, int q_timed, BatchPlan* p) {
   return true;
 }
 
-template <int KS, int CT>
-int launch_screen(MlaDeviceArena* a, uint32_t n_tiles32, int stride, int ibits, size_t lds) {
-  auto kern = grm::mla::mla_batch_screen_kernel<KS, CT>;
+template <int KS, int CT, bool kProbe = false>
+int launch_screen(MlaDeviceArena* a, uint32_t n_tiles32, int stride, int ibits, size_t lds,
+                  uint32_t* planes) {
+  auto kern = grm::mla::mla_batch_screen_kernel<KS, CT, kProbe>;
   if (lds > 65536) {
     GRM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(lds)));
   }
   kern<<<a->cus, grm::mla::kBatchWaves * grm::kWave, lds, a->stream>>>(
-      a->d_tiles, a->d_norms, a->capacity, a->chunks, n_tiles32, a->d_qpad, stride, ibits,
-      a->d_entries);
+      a->d_tiles, a->d_norms, a->capacity, a->chunks, n_tiles32, a->d_qpad, stride, ibits, planes);
   GRM_HIP_CHECK(hipGetLastError());
   return 0;
+}
+
+template <bool kProbe>
+int dispatch_screen(MlaDeviceArena* a, const BatchPlan& p, int ct, uint32_t n_tiles32, size_t lds,
+                    uint32_t* planes) {
+  const int ibits = p.ibits;
+#define GRM_SCREEN_CT(KS)                                                                        \
+  switch (ct) {                                                                                  \
+    case 1: return launch_screen<KS, 1, kProbe>(a, n_tiles32, p.stride, ibits, lds, planes);     \
+    case 2: return launch_screen<KS, 2, kProbe>(a, n_tiles32, p.stride, ibits, lds, planes);     \
+    case 4: return launch_screen<KS, 4, kProbe>(a, n_tiles32, p.stride, ibits, lds, planes);     \
+    default: return launch_screen<KS, 8, kProbe>(a, n_tiles32, p.stride, ibits, lds, planes);    \
+  }
+  switch (p.ks) {
+    case 8: GRM_SCREEN_CT(8);
+    case 16: GRM_SCREEN_CT(16);
+    default: GRM_SCREEN_CT(18);
+  }
+#undef GRM_SCREEN_CT
+}
+
+// Screen-bound constants: gamma bounds the fp32 accumulation of 16*ks
+// products in 32x32x16 steps (with the MFMA's internal order unknown),
+// delta the rounding of an fp32 query to bf16.
+double batch_gamma(const BatchPlan& p) { return 2.0 * (16.0 * p.ks + 2.0 * p.ks) * ldexp(1.0, -24); }
+double batch_delta(int q_dtype) { return q_dtype == kF32 ? ldexp(1.0, -8) : 0.0; }
+
+// LDS of a screen pass of qp queries: the staged queries, later the
+// block's result rows.
+size_t batch_lds(const BatchPlan& p, int qp) {
+  return std::max(static_cast<size_t>(qp) * p.stride * 2,
+                  static_cast<size_t>(grm::mla::kEntryPlanes) * qp * grm::mla::kBatchWaves * 4);
 }
 
 // One pass: queries [0, qc) at q (device, dim values each) through the
@@ -818,26 +851,12 @@ int enqueue_batch_pass(MlaDeviceArena* a, const BatchPlan& p, const unsigned cha
   const uint32_t n_tiles32 = static_cast<uint32_t>((a->high_water + 31) / 32);
   const uint32_t n_waves = static_cast<uint32_t>(a->cus) * grm::mla::kBatchWaves;
   const int ibits = p.ibits;
-  // LDS: the staged queries, later the block's result rows
-  const size_t lds = std::max(static_cast<size_t>(qp) * p.stride * 2,
-                              static_cast<size_t>(grm::mla::kEntryPlanes) * qp * grm::mla::kBatchWaves * 4);
+  const size_t lds = batch_lds(p, qp);
   if (ev) GRM_HIP_CHECK(hipEventRecord(ev[0], a->stream));
-#define GRM_SCREEN_CT(KS)                                                   \
-  switch (ct) {                                                             \
-    case 1: GRM_CHECK_RC((launch_screen<KS, 1>(a, n_tiles32, p.stride, ibits, lds))); break; \
-    case 2: GRM_CHECK_RC((launch_screen<KS, 2>(a, n_tiles32, p.stride, ibits, lds))); break; \
-    case 4: GRM_CHECK_RC((launch_screen<KS, 4>(a, n_tiles32, p.stride, ibits, lds))); break; \
-    default: GRM_CHECK_RC((launch_screen<KS, 8>(a, n_tiles32, p.stride, ibits, lds))); break; \
-  }
-  switch (p.ks) {
-    case 8: GRM_SCREEN_CT(8); break;
-    case 16: GRM_SCREEN_CT(16); break;
-    default: GRM_SCREEN_CT(18); break;
-  }
-#undef GRM_SCREEN_CT
+  GRM_CHECK_RC(dispatch_screen<false>(a, p, ct, n_tiles32, lds, a->d_entries));
   if (ev) GRM_HIP_CHECK(hipEventRecord(ev[1], a->stream));
-  const double gamma = 2.0 * (16.0 * p.ks + 2.0 * p.ks) * ldexp(1.0, -24);
-  const double delta = q_dtype == kF32 ? ldexp(1.0, -8) : 0.0;
+  const double gamma = batch_gamma(p);
+  const double delta = batch_delta(q_dtype);
   grm::mla::mla_batch_merge_kernel<<<qc, grm::mla::kMergeThreads, 0, a->stream>>>(
       a->d_entries, n_waves, qp, n_tiles32, ibits, a->d_inv_qn, a->d_tiles, a->d_norms, a->d_ids,
       a->capacity, a->dim, q, q_dtype, a->dim, gamma, delta, a->d_min_norm, topk, out, status);
@@ -1694,5 +1713,71 @@ extern "C" int grm_mla_hip_route_stats(MlaDeviceArena* a, uint64_t* out4) {
 extern "C" int grm_mla_hip_screen_ms(MlaDeviceArena* a, float* ms) {
   if (!a || !ms) return grm::fail(-1, "null argument");
   *ms = a->screen_ms;
+  return 0;
+}
+
+// ------------------------------------------------------- screen-bound probe
+//
+// Test entry: runs the batched route's screen (the same kernel, in its
+// probe form) over every slot of a small bf16 bank and returns each
+// screened score s~ with its query's bound B, so a test can hold
+// |s~ - law score| <= B for every (query, node) pair.  Not on any route
+// path; allocates its own buffers.
+extern "C" int grm_mla_hip_probe_screen(MlaDeviceArena* a, const void* queries_host,
+                                        int query_dtype, int query_count, float* out_values_host,
+                                        double* out_bounds_host, uint64_t* out_slot_ids_host) {
+  if (!a || !queries_host || !out_values_host || !out_bounds_host) {
+    return grm::fail(-1, "null argument");
+  }
+  if (query_dtype != kF32 && query_dtype != kBF16) return grm::fail(-1, "query dtype must be F32 or BF16");
+  BatchPlan p;
+  if (!batch_plan(a, std::numeric_limits<int>::max(), &p)) {
+    return grm::fail(-1, "bank has no batched screen (bf16 rows, dim <= 288)");
+  }
+  if (query_count <= 0 || query_count > p.qp_max) return grm::fail(-1, "query_count out of range");
+  const int ct = query_count <= 32 ? 1 : (query_count <= 64 ? 2 : (query_count <= 128 ? 4 : 8));
+  const int qp = 32 * ct;
+  const uint64_t n = a->high_water;
+  if (n == 0) return grm::fail(-1, "empty bank");
+  if (a->capacity * static_cast<uint64_t>(qp) > (1ull << 26)) {
+    return grm::fail(-1, "probe is for banks of at most 2^26 / 256 slots");
+  }
+  GRM_HIP_CHECK(hipSetDevice(a->device));
+  struct Buf {
+    void* p = nullptr;
+    ~Buf() {
+      if (p) (void)hipFree(p);
+    }
+  } d_q, d_planes, d_vals, d_bounds;
+  const size_t qbytes = static_cast<size_t>(query_count) * a->dim * elem_size(query_dtype);
+  GRM_HIP_CHECK(hipMalloc(&d_q.p, qbytes));
+  GRM_HIP_CHECK(hipMalloc(&d_planes.p, static_cast<size_t>(qp) * a->capacity * sizeof(uint32_t)));
+  GRM_HIP_CHECK(hipMalloc(&d_vals.p, static_cast<size_t>(query_count) * n * sizeof(float)));
+  GRM_HIP_CHECK(hipMalloc(&d_bounds.p, static_cast<size_t>(query_count) * sizeof(double)));
+  GRM_CHECK_RC(reserve_device(&a->d_qpad, &a->d_qpad_count, static_cast<size_t>(p.qp_max) * p.stride));
+  GRM_CHECK_RC(reserve_device(&a->d_inv_qn, &a->d_inv_qn_count, static_cast<size_t>(p.qp_max)));
+  if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
+  GRM_HIP_CHECK(hipMemcpyAsync(d_q.p, queries_host, qbytes, hipMemcpyHostToDevice, a->stream));
+  grm::mla::mla_batch_qprep_kernel<<<qp, grm::kWave, 0, a->stream>>>(
+      d_q.p, query_dtype, query_count, a->dim, p.stride, a->d_qpad, a->d_inv_qn);
+  GRM_HIP_CHECK(hipGetLastError());
+  const uint32_t n_tiles32 = static_cast<uint32_t>((n + 31) / 32);
+  GRM_CHECK_RC(dispatch_screen<true>(a, p, ct, n_tiles32, batch_lds(p, qp),
+                                     static_cast<uint32_t*>(d_planes.p)));
+  grm::mla::mla_batch_probe_finish_kernel<<<query_count, grm::kWave, 0, a->stream>>>(
+      static_cast<const uint32_t*>(d_planes.p), a->capacity, static_cast<uint32_t>(n), a->d_inv_qn,
+      d_q.p, query_dtype, a->dim, a->dim, batch_gamma(p), batch_delta(query_dtype), a->d_min_norm,
+      p.ibits, static_cast<float*>(d_vals.p), static_cast<double*>(d_bounds.p));
+  GRM_HIP_CHECK(hipGetLastError());
+  GRM_HIP_CHECK(hipMemcpyAsync(out_values_host, d_vals.p, static_cast<size_t>(query_count) * n * sizeof(float),
+                               hipMemcpyDeviceToHost, a->stream));
+  GRM_HIP_CHECK(hipMemcpyAsync(out_bounds_host, d_bounds.p, static_cast<size_t>(query_count) * sizeof(double),
+                               hipMemcpyDeviceToHost, a->stream));
+  if (out_slot_ids_host) {
+    GRM_HIP_CHECK(hipMemcpyAsync(out_slot_ids_host, a->d_ids, n * sizeof(uint64_t),
+                                 hipMemcpyDeviceToHost, a->stream));
+  }
+  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
+  grm::clear_error();
   return 0;
 }

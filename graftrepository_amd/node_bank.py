@@ -199,6 +199,26 @@ class MlaNodeBank(_Bank):
         _lib.check(rc, "MLA route")
         return RouteResult(ids, scores, float(ms.value) if timed else float("nan"), wall)
 
+    def probe_screen(self, queries, *, query_dtype: str = "bf16"):
+        """Test entry: the batched route's screened score of every (query,
+        slot) pair of a small bf16 bank and each query's screen bound B.
+        Returns (values [Q, slots] f32, bounds [Q] f64, slot node ids)."""
+        self._need_open()
+        qd = _dtype_code(query_dtype)
+        q = np.asarray(queries)
+        if qd == DTYPE_BF16 and q.dtype != np.uint16:
+            q = as_bf16_bits(q)
+        q = np.ascontiguousarray(q, dtype=np.float32 if qd == DTYPE_F32 else np.uint16)
+        if q.ndim != 2 or q.shape[1] != self.dim:
+            raise ValueError("queries must have shape (Q, dim)")
+        n = int(self.info()["slots_in_use"])
+        vals = np.empty((q.shape[0], n), dtype=np.float32)
+        bounds = np.empty(q.shape[0], dtype=np.float64)
+        ids = np.empty(n, dtype=np.uint64)
+        _lib.check(self._lib.grm_mla_hip_probe_screen(self._h, _ptr(q), qd, q.shape[0], _ptr(vals),
+                                                      _ptr(bounds), _ptr(ids)), "MLA probe screen")
+        return vals, bounds, ids
+
     def latent_query(self, latent, tokens: int, *, dtype: str = "f16",
                      row_stride: int = 0, normalize: bool = True, out=None) -> int:
         """Write the route key of a device latent block [tokens][dim]
@@ -385,6 +405,31 @@ class GqaNodeBank(_Bank):
         del keep
         _lib.check(rc, "GQA route")
         return RouteResult(ids, scores, float(ms.value) if timed else float("nan"), wall)
+
+    def probe_screen(self, query, *, query_dtype: str = "bf16"):
+        """Test entry: the bound-and-verify screen of one query [H, Qt, hd].
+        Returns (maxima [slots, kv, R*Qt] f32 in the screen's scaled units,
+        colinfo [kv, R*Qt, 4] = (coef, eabs, scale, kcap), K [slots] f64,
+        slot node ids)."""
+        self._need_open()
+        qd = _dtype_code(query_dtype)
+        q = np.asarray(query)
+        if qd == DTYPE_BF16 and q.dtype != np.uint16:
+            q = as_bf16_bits(q)
+        q = np.ascontiguousarray(q, dtype=np.float32 if qd == DTYPE_F32 else np.uint16)
+        if q.ndim != 3 or q.shape[2] != self.head_dim:
+            raise ValueError("query must have shape (H, Qt, head_dim)")
+        H, Qt, _ = q.shape
+        cols = H // self.kv_heads * Qt
+        n = int(self.info()["capacity_nodes"])
+        maxima = np.empty((n, self.kv_heads, cols), dtype=np.float32)
+        colinfo = np.empty((self.kv_heads, cols, 4), dtype=np.float32)
+        knorm = np.empty(n, dtype=np.float64)
+        ids = np.empty(n, dtype=np.uint64)
+        _lib.check(self._lib.grm_gqa_hip_probe_screen(self._h, _ptr(q), qd, H, Qt, _ptr(maxima),
+                                                      _ptr(colinfo), _ptr(knorm), _ptr(ids)),
+                   "GQA probe screen")
+        return maxima, colinfo, knorm, ids
 
     def append(self, keys, tok_counts, node_ids, scales=None) -> int:
         self._need_open()

@@ -201,6 +201,20 @@ int grm_mla_hip_route_stats(MlaDeviceArena* arena, uint64_t* out4);
  * the last route was not batched.  No counterpart. */
 int grm_mla_hip_screen_ms(MlaDeviceArena* arena, float* ms);
 
+/* Test entry, no counterpart and on no route path: runs the batched
+ * route's matrix-core screen over every slot of a small bf16 bank
+ * (capacity x 256 <= 2^26) for query_count queries (at most one screen
+ * pass, <= 256) and writes each screened score s~ of (query q, slot s) to
+ * out_values[q * high_water + s], the query's screen bound B to
+ * out_bounds[q] (+inf where it is not established), and the slots' node
+ * ids to out_slot_ids (optional; high_water entries).  The certificate of
+ * the batched route rests on |s~ - law score| <= B for every pair.
+ * Allocates its own buffers. */
+int grm_mla_hip_probe_screen(MlaDeviceArena* arena, const void* queries_host,
+                             int query_dtype, int query_count,
+                             float* out_values_host, double* out_bounds_host,
+                             uint64_t* out_slot_ids_host);
+
 /* MLA route key from a device-resident latent block [tokens][dim] (row
  * stride row_stride elements, 0 = dim; latent_dtype F32, BF16 or F16): the
  * unit-norm token mean of core/kv_graft.py:131-142 (latent_centroid), written
@@ -297,6 +311,24 @@ int grm_gqa_hip_sync(GqaDeviceArena* arena);
 /* Bank description: [live nodes, node capacity, tokens in use, token
  * capacity, epoch, kv_heads, head_dim, key dtype].  No counterpart. */
 int grm_gqa_hip_bank_info(GqaDeviceArena* arena, uint64_t* out8);
+
+/* Test entry, no counterpart and on no route path: the screen of the
+ * bound-and-verify path for one query [query_heads][query_tokens][head_dim]
+ * (R * query_tokens <= 64 columns per kv head, R = heads / kv_heads) over
+ * every node with key tokens.  Writes, for every slot of the node
+ * capacity, the largest screened value per (slot, kv head g, column
+ * cg = r * query_tokens + t) in the screen's scaled units to
+ * out_maxima[(slot * kv + g) * R * query_tokens + cg]; the bound
+ * parameters {coef, eabs, scale, kcap} of each column to
+ * out_colinfo[(g * R * query_tokens + cg) * 4 ..]; the key norm bound K of
+ * each slot to out_knorm; the slots' node ids to out_slot_ids (optional).
+ * For a node with K < kcap, |maximum - scale * max_t |q . k_t|| <=
+ * coef * K + eabs (the screen bound both screen paths rest on).
+ * Allocates its own query buffer. */
+int grm_gqa_hip_probe_screen(GqaDeviceArena* arena, const void* query_host,
+                             int query_dtype, int query_heads, int query_tokens,
+                             float* out_maxima_host, float* out_colinfo_host,
+                             double* out_knorm_host, uint64_t* out_slot_ids_host);
 
 /* ---- GQA store route on the device (cpp/grm_runtime.cpp:6898-6961) ----
  * Per-node route filter bits, as grm_mla_hip_set_filter_bits (a slot taken
