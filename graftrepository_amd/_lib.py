@@ -84,6 +84,7 @@ SIGNATURES = {
     "grm_gqa_hip_compact": (i32, [vp]),
     "grm_gqa_hip_sync": (i32, [vp]),
     "grm_gqa_hip_bank_info": (i32, [vp, vp]),
+    "grm_gqa_hip_route_stats": (i32, [vp, vp]),
     "grm_gqa_hip_probe_screen": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp]),
     "grm_gqa_hip_set_filter_bits": (i32, [vp, vp, vp, u64]),
     "grm_gqa_hip_route_filtered": (i32, [vp, vp, i32, i32, i32, i32, i32, u64, ctypes.c_uint32,

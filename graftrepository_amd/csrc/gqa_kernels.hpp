@@ -534,6 +534,14 @@ constexpr int kMaxCols = 64;  // query columns (Qb * R * Qt) per screen pass
 //    product (0 elsewhere), sigma_q a scaled query value flushed or rounded
 //    near zero, sigma_k a key value flushed near zero, sigma_p a product
 //    lost to underflow, and 2^-40 the law's own fp64 rounding;
+// With a rounded key plane (fp32 banks screened through an fp16 copy of
+// their keys, k~ = k rounded with |k - k~| <= eps_rel |k| + eps_abs per
+// value) the bound above holds for k~, whose norm is at most
+// (1 + eps_rel) K + eps_abs sqrt(hd), and |q.(k - k~)| adds at most
+// ||q|| (eps_rel K + eps_abs sqrt(hd)), so (before scaling)
+//      coef' = coef (1 + eps_rel) + eps_rel ||q||
+//      eabs' = eabs + (coef + ||q||) eps_abs sqrt(hd)
+// (eps_rel = eps_abs = 0 for banks screened in their own values);
 // into s_ec[cg] = {coef, eabs, scale, kcap} and s_bad[cg] = 1 when the
 // column holds a non-finite value.  kcap = 2^127 / (scale * ||q|| *
 // (1 + 2^-6)), rounded down: for a node whose key norm bound K stays below
@@ -547,7 +555,8 @@ __device__ inline void stage_columns(float* __restrict__ s_q, float4* __restrict
                                      unsigned* __restrict__ s_bad, const void* __restrict__ query,
                                      int q_dtype, size_t q_elems, int cols, int R, int Qt, int Rc,
                                      int Qc, int g, int emax, double gamma, double delta,
-                                     double rho, double sigma_q, double sigma_k, double sigma_p) {
+                                     double rho, double sigma_q, double sigma_k, double sigma_p,
+                                     double eps_rel, double eps_abs) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nwaves = blockDim.x / kWave;
@@ -590,6 +599,8 @@ __device__ inline void stage_columns(float* __restrict__ s_q, float4* __restrict
       double c = (gamma + delta + gamma * delta + rho) * norm + sigma_q * (1.0 + gamma) * sq / scale +
                  0x1p-40 * norm;
       double ea = sigma_k * sq * norm + sigma_p * HD / scale;
+      ea += (c + norm) * eps_abs * sq;
+      c = c * (1.0 + eps_rel) + eps_rel * norm;
       const double up = 1.0 + 0x1p-20;
       c *= up * scale * up;
       ea *= up * scale * up;
@@ -657,12 +668,12 @@ __device__ inline void query_frags(u32x4 (&bq)[NT][KS], const float* __restrict_
 
 // Exact |dot| of one lane's (key token, query column) pair in the law's
 // order: the token's pieces come from the planes (piece c at
-// kp + (c/4)*L*4 + c%4, kp the token's piece 0; chunks of S = 4 pieces),
+// kp + (c/S)*L*S + c%S, kp the token's piece 0; chunks of S = 2^SS pieces),
 // 64 values' worth in flight at once, the column's
 // values from qrow (LDS, fp32, exact).  Only lanes with `active` set read
 // memory (the others return 0): the candidates are a few lanes of the
 // wave, and their rows are all that is read again.
-template <int KDT, int HD>
+template <int KDT, int HD, int SS = 2>
 __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restrict__ kp,
                                              uint64_t L, const unsigned char* __restrict__ sp,
                                              int scale_dtype, int cpg, const float* qrow) {
@@ -676,7 +687,7 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
     float sc[kB];
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
-      v[b] = kp[(static_cast<uint64_t>((c0 + b) >> 2) * L << 2) + ((c0 + b) & 3)];
+      v[b] = kp[(static_cast<uint64_t>((c0 + b) >> SS) * L << SS) + ((c0 + b) & ((1 << SS) - 1))];
       sc[b] = 0.0f;
       if constexpr (KDT == kI8) {
         sc[b] = load_scale(sp, scale_dtype, static_cast<uint64_t>((c0 + b) / cpg) * L);
@@ -718,14 +729,19 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
 // threshold is recomputed.  The per-column exact maxima, divided by
 // sqrt(hd) (monotone), fold into hmax[qb*hstride + (g*R + rr)*cap + slot]
 // (double bits, atomicMax).
-template <int KDT, int KS, int NT>
+//
+// XF32: the keys are an fp32 bank's fp16 copy (same rows, chunks of 4
+// pieces); the exact recomputation reads the fp32 rows from xkeys (chunks
+// of 1 piece), and eps_rel / eps_abs carry the copy's rounding into the
+// bound (stage_columns).
+template <int KDT, int KS, int NT, bool XF32 = false>
 __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
-    const unsigned char* __restrict__ keys,
+    const unsigned char* __restrict__ keys, const unsigned char* __restrict__ xkeys,
     const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
     const Item* __restrict__ items, uint32_t n_items, int kv, int R, int Qt, int Rc, int Qc,
     const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
     double gamma, double delta, double sigma_q, double sigma_k, double sigma_p,
-    unsigned* __restrict__ qflags, int flags_or, const float* __restrict__ kmax, double denom,
+    double eps_rel, double eps_abs, unsigned* __restrict__ qflags, int flags_or, const float* __restrict__ kmax, double denom,
     unsigned long long* __restrict__ hmax, size_t hstride, size_t cap, int g_fast) {
   using KT = KeyTraits<KDT>;
   constexpr int MT = ScreenTraits<KDT>::kMfma;
@@ -797,7 +813,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     load_tile(x3, 3);
   }
   stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, Rc, Qc, g, emax,
-                    gamma, delta, 0.0, sigma_q, sigma_k, sigma_p);
+                    gamma, delta, 0.0, sigma_q, sigma_k, sigma_p, eps_rel, eps_abs);
   __syncthreads();
   if (item_block == 0 && threadIdx.x < static_cast<unsigned>(Qb)) {
     unsigned bad = 0u;
@@ -917,9 +933,15 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
 
   auto pair = [&](bool active, uint32_t t, int cg) -> double {
     const uint32_t tt = min(it.t0 + t, last);
-    return exact_pair<KDT, HD>(active, kplane + static_cast<uint64_t>(tt) * 4, L,
-                           KDT == kI8 ? splane + static_cast<size_t>(tt) * ses : nullptr,
-                           scale_dtype, cpg, s_q + min(cg, cols - 1) * HD);
+    if constexpr (XF32) {
+      const u32x4* xplane = reinterpret_cast<const u32x4*>(xkeys) + row0 * (HD / 4);
+      return exact_pair<kF32, HD, 0>(active, xplane + tt, L, nullptr, scale_dtype, 1,
+                                     s_q + min(cg, cols - 1) * HD);
+    } else {
+      return exact_pair<KDT, HD>(active, kplane + static_cast<uint64_t>(tt) * 4, L,
+                                 KDT == kI8 ? splane + static_cast<size_t>(tt) * ses : nullptr,
+                                 scale_dtype, cpg, s_q + min(cg, cols - 1) * HD);
+    }
   };
   double best[NT];
 #pragma unroll
@@ -1034,7 +1056,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     int scale_dtype, int group_size, const Item* __restrict__ items, uint32_t n_items, int kv,
     int R, int Qt, const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
     double gamma, double delta, double rho, double sigma_q, double sigma_k, double sigma_p,
-    float4* __restrict__ colinfo, unsigned* __restrict__ hmaxf, int colstride) {
+    double eps_rel, double eps_abs, float4* __restrict__ colinfo, unsigned* __restrict__ hmaxf,
+    int colstride) {
   using KT = KeyTraits<KDT>;
   constexpr int MT = ScreenTraits<KDT>::kMfma;
   constexpr bool PERM = KDT == kI8;
@@ -1151,7 +1174,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     load_next(x3);
   }
   stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, R, Qt, g, emax,
-                    gamma, delta, rho, sigma_q, sigma_k, sigma_p);
+                    gamma, delta, rho, sigma_q, sigma_k, sigma_p, eps_rel, eps_abs);
   if (blockIdx.x == 0) {
     for (int cg = threadIdx.x; cg < cols; cg += blockDim.x) colinfo[g * cols + cg] = s_ec[cg];
   }
@@ -1510,13 +1533,21 @@ __global__ __launch_bounds__(kCandWaves * kWave) void gqa_cands_kernel(
 // and tokens of ||k||_2, rounded up (float bits, atomicMax).  Items carry
 // the destination base; the staged row of (item, g, t) is
 // base - src_base + g*len + t.  grid (ceil(items / 4), kv).
+//
+// With `skeys` (fp32 banks only) each row is also written, rounded to
+// fp16 (nearest even), to the bank's fp16 copy: the same rows as chunk
+// planes of 4 pieces, which the matrix-core screens read.  A slot with a
+// finite value whose fp16 rounding is not finite (|value| >= 65520) gets
+// kmax = +inf: its screen bound is then infinite and every one of its
+// tokens is recomputed exactly.
 template <int KDT>
 __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_place_kernel(
     const u32x4* __restrict__ src_keys, const unsigned char* __restrict__ src_scales,
     uint64_t src_base, unsigned char* __restrict__ keys,
     unsigned char* __restrict__ scales, int scale_dtype, int group_size,
     const Item* __restrict__ items, uint32_t n_items, int hd, int sS,
-    uint32_t* __restrict__ nonfinite, unsigned* __restrict__ kmax) {
+    uint32_t* __restrict__ nonfinite, unsigned* __restrict__ kmax,
+    unsigned char* __restrict__ skeys) {
   using T = KeyTraits<KDT>;
   const int lane = threadIdx.x & (kWave - 1);
   const uint32_t item_i = blockIdx.x * kUnitWaves + threadIdx.x / kWave;
@@ -1531,7 +1562,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_place_kernel(
   const uint64_t srow0 = row0 - src_base;
   u32x4* dst = reinterpret_cast<u32x4*>(keys) + row0 * C;
   const int S = 1 << sS;
-  bool bad = false;
+  bool bad = false, sbad = false;
   double mx = 0.0;
   for (uint32_t t = it.t0 + lane; t < it.t0 + it.count; t += kWave) {
     const u32x4* src = src_keys + (srow0 + t) * C;
@@ -1539,6 +1570,27 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_place_kernel(
     for (int c = 0; c < C; ++c) {
       const u32x4 v = src[c];
       dst[(static_cast<uint64_t>(c >> sS) * it.len << sS) + (static_cast<uint64_t>(t) << sS) + (c & (S - 1))] = v;
+      if constexpr (KDT == kF32) {
+        if (skeys) {
+          // fp16 piece c/2 of the copy (8 values), half c%2 of it
+          const float f[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
+                              __uint_as_float(v.w)};
+          _Float16 h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            h[e] = static_cast<_Float16>(f[e]);
+            sbad = sbad || (isfinite(f[e]) && !isfinite(static_cast<float>(h[e])));
+          }
+          const int p = c >> 1;
+          u32x4* sdst = reinterpret_cast<u32x4*>(skeys) + row0 * (C / 2) +
+                        (static_cast<uint64_t>(p >> 2) * it.len << 2) + (static_cast<uint64_t>(t) << 2) + (p & 3);
+          typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+          u32x2 w;
+          w.x = pack_f16x2(h[0], h[1]);
+          w.y = pack_f16x2(h[2], h[3]);
+          reinterpret_cast<u32x2*>(sdst)[c & 1] = w;
+        }
+      }
       float sc = 0.0f;
       if constexpr (KDT == kI8) {
         const int j = c / cpg;
@@ -1566,6 +1618,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_place_kernel(
   if (__ballot(bad) != 0ull && lane == 0) atomicOr(nonfinite + it.slot, 1u);
   float nrm = static_cast<float>(sqrt(mx) * (1.0 + 1e-6));
   if (!isfinite(nrm)) nrm = 3.0e38f;
+  if (sbad) nrm = INFINITY;
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) nrm = fmaxf(nrm, __shfl_xor(nrm, off));
   if (lane == 0) atomicMax(kmax + it.slot, __float_as_uint(nrm));

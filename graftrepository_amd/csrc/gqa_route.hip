@@ -18,7 +18,10 @@
 //   shortlist's exact scores.  A query whose shortlist is not certified, or
 //   whose values are non-finite or leave the fp16 range, is routed again
 //   on the exact path, so every result follows the law.
-// Route (fp32 banks and other shapes): exact path over every node.
+// fp32 banks (head_dim 64, 128 or 256) keep an fp16 copy of their keys
+// beside the fp32 rows: the screens read the copy, with its rounding in
+// their bound, and every exact recomputation reads the fp32 rows.
+// Route (other shapes): exact path over every node.
 #include "gqa_kernels.hpp"
 #include "grm_hip_router.h"
 
@@ -60,6 +63,8 @@ struct GqaDeviceArena {
   uint64_t epoch = 0;
   unsigned char* d_keys = nullptr;
   unsigned char* d_scales = nullptr;
+  // fp32 banks: fp16 copy of the keys (chunks of 4 pieces) for the screens
+  unsigned char* d_skeys = nullptr;
   uint64_t* d_tok_off = nullptr;
   uint32_t* d_len = nullptr;
   uint64_t* d_ids = nullptr;
@@ -134,6 +139,8 @@ struct GqaDeviceArena {
   Item* d_citems = nullptr;      // exact work items of the candidates
   size_t d_citems_count = 0;
   uint64_t bv_routes = 0;        // passes routed by bound and verify
+  uint64_t sr_routes = 0;        // passes routed by screen and refine
+  uint64_t exact_routes = 0;     // queries routed by the exact path
   std::map<std::pair<const void*, size_t>, int> resident;  // blocks per CU by (kernel, LDS bytes)
   uint64_t routes = 0;          // route calls
   std::vector<Cand> merged;
@@ -210,7 +217,7 @@ void destroy_arena(GqaDeviceArena* a) {
   (void)hipSetDevice(a->device);
   if (a->stream) (void)hipStreamSynchronize(a->stream);
   if (a->side) (void)hipStreamSynchronize(a->side);
-  void* dev[] = {a->d_keys,   a->d_scales,  a->d_tok_off, a->d_len,    a->d_ids,
+  void* dev[] = {a->d_keys,   a->d_scales,  a->d_tok_off, a->d_len,    a->d_ids,   a->d_skeys,
                  a->d_flags,  a->d_nonfinite, a->d_kmax,  a->d_items,  a->d_hmax,
                  a->d_qbad,   a->d_queries, a->d_stage,   a->d_q64,    a->d_hmaxf,
                  a->d_colinfo, a->d_lbub,   a->d_blists,  a->d_cslots, a->d_ccount,
@@ -267,13 +274,17 @@ int stage_buffers(GqaDeviceArena* a, size_t bytes, unsigned char** h, unsigned c
 
 // Place `count` nodes whose keys (and scales) are packed back to back in
 // host memory ([kv][len][hd] per node) at the bump pointer; `slots` are
-// already assigned on the host.  The staging copy takes the padded row
+// already assigned on the host.  With src_rows > 0 the host keys are a
+// dense bank instead: node i's block is [kv][src_rows][hd] at
+// i * kv * src_rows * hd values, of which the first len rows per kv head
+// are placed.  The staging copy takes the padded row
 // layout of the bank, so a staged row and its bank row share an index.
 // Everything runs on `st`; the staging buffer stays busy until `st` passes
 // the recorded mutation event.
 int place_nodes(GqaDeviceArena* a, const std::vector<uint64_t>& slots,
                 const std::vector<uint64_t>& ids, const uint64_t* tok_counts,
-                const void* keys_host, const void* scales_host, hipStream_t st) {
+                const void* keys_host, const void* scales_host, hipStream_t st,
+                uint64_t src_rows = 0) {
   const uint64_t count = slots.size();
   uint64_t tokens = 0;  // padded token rows
   for (uint64_t i = 0; i < count; ++i) tokens += padded_len(tok_counts[i]);
@@ -318,15 +329,16 @@ int place_nodes(GqaDeviceArena* a, const std::vector<uint64_t>& slots,
     for (uint64_t i = 0; i < count; ++i) {
       const uint64_t L = tok_counts[i], Lp = padded_len(L);
       const uint64_t row = (offs[i] - first_tok) * a->kv;
+      const uint64_t Ls = src_rows ? src_rows : L;  // source rows per kv head
       for (uint32_t g = 0; g < a->kv; ++g) {
         if (L == 0) break;
-        memcpy(h + o_keys + (row + g * Lp) * rk, ksrc, L * rk);
-        ksrc += L * rk;
+        memcpy(h + o_keys + (row + g * Lp) * rk, ksrc + g * Ls * rk, L * rk);
         if (rs) {
           memcpy(h + o_scales + (row + g * Lp) * rs, ssrc, L * rs);
           ssrc += L * rs;
         }
       }
+      ksrc += (src_rows || L ? a->kv : 0) * Ls * rk;
     }
   }
   GRM_HIP_CHECK(hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, st));
@@ -346,7 +358,7 @@ int place_nodes(GqaDeviceArena* a, const std::vector<uint64_t>& slots,
       reinterpret_cast<const u32x4*>(d + o_keys), d + o_scales, first_tok * a->kv, a->d_keys,    \
       a->d_scales, a->scale_dtype, a->group_size, reinterpret_cast<const Item*>(d + o_items),    \
       static_cast<uint32_t>(items.size()), static_cast<int>(a->hd), a->piece_shift,           \
-      a->d_nonfinite, a->d_kmax)
+      a->d_nonfinite, a->d_kmax, a->d_skeys)
     switch (a->key_dtype) {
       case kF32: GRM_PLACE(kF32); break;
       case kBF16: GRM_PLACE(kBF16); break;
@@ -371,10 +383,14 @@ int place_nodes(GqaDeviceArena* a, const std::vector<uint64_t>& slots,
   return 0;
 }
 
+// A bank from CSR host keys (tok_offsets: node i's [kv][len][hd] block at
+// value tok_offsets[i] * kv * hd), or with dense_rows > 0 from a dense
+// host bank of dense_rows rows per (node, kv head) of which node i keeps
+// the first tok_offsets[i + 1] - tok_offsets[i] (place_nodes).
 int create_arena(const void* keys, int key_dtype, const void* scales, int scale_dtype,
                  int group_size, const uint64_t* tok_offsets, uint64_t nodes, int kv_heads,
                  int head_dim, const uint64_t* node_ids, uint64_t cap_nodes, uint64_t cap_tokens,
-                 GqaDeviceArena** out) {
+                 GqaDeviceArena** out, uint64_t dense_rows = 0) {
   if (!out) return grm::fail(-1, "null output arena pointer");
   *out = nullptr;
   if (kv_heads <= 0 || head_dim <= 0 || static_cast<uint32_t>(head_dim) > grm::gqa::kMaxHeadDim) {
@@ -461,6 +477,13 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   BAIL_HIP(hipEventCreate(&a->ev_stop));
   BAIL_HIP(hipEventCreateWithFlags(&a->ev_mut, hipEventDisableTiming));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_keys), std::max<size_t>(16, cap_tokens * token_key_bytes(a))));
+  {
+    // the fp16 copy of an fp32 bank's keys (GRM_HIP_GQA_SHADOW=0: none)
+    const char* env = getenv("GRM_HIP_GQA_SHADOW");
+    const bool shadow = key_dtype == kF32 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
+                        !(env && env[0] == '0');
+    if (shadow) BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_skeys), cap_tokens * row_values(a) * 2));
+  }
   if (key_dtype == kI8) {
     BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_scales), std::max<size_t>(16, cap_tokens * token_scale_bytes(a))));
   }
@@ -494,9 +517,10 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
     }
     std::vector<uint64_t> bslots(slots.begin() + i0, slots.begin() + i1);
     std::vector<uint64_t> bids(ids.begin() + i0, ids.begin() + i1);
-    const unsigned char* kptr = static_cast<const unsigned char*>(keys) + tok_offsets[i0] * kb;
+    const unsigned char* kptr = static_cast<const unsigned char*>(keys) +
+                                (dense_rows ? i0 * dense_rows : tok_offsets[i0]) * kb;
     const unsigned char* sptr = scales ? static_cast<const unsigned char*>(scales) + tok_offsets[i0] * sb : nullptr;
-    int rc = place_nodes(a, bslots, bids, counts.data() + i0, kptr, sptr, a->stream);
+    int rc = place_nodes(a, bslots, bids, counts.data() + i0, kptr, sptr, a->stream, dense_rows);
     if (rc) return bail(rc);
     if (hipStreamSynchronize(a->stream) != hipSuccess) return bail(grm::fail(-1, "create upload failed"));
     i0 = i1;
@@ -704,10 +728,15 @@ struct SrPlan {
 // alone needs more, passes take one query).
 constexpr size_t kMaxHmaxBytes = 2ull << 30;
 
+// The plane the screens read and its element type: the keys themselves,
+// or an fp32 bank's fp16 copy.
+const unsigned char* screen_keys(const GqaDeviceArena* a) { return a->d_skeys ? a->d_skeys : a->d_keys; }
+int screen_dtype(const GqaDeviceArena* a) { return a->d_skeys ? kF16 : a->key_dtype; }
+
 bool sr_plan(const GqaDeviceArena* a, int H, int Qt, SrPlan* p) {
-  if (a->screen_mode == 0 || a->key_dtype == kF32) return false;
+  if (a->screen_mode == 0 || screen_dtype(a) == kF32) return false;
   if (a->hd != 64 && a->hd != 128 && a->hd != 256) return false;
-  if (a->piece_shift != 2) return false;  // the screen reads 64-byte chunks
+  if (!a->d_skeys && a->piece_shift != 2) return false;  // the screen reads 64-byte chunks
   const int R = H / static_cast<int>(a->kv);
   p->R = R;
   p->Qt = Qt;
@@ -721,7 +750,7 @@ bool sr_plan(const GqaDeviceArena* a, int H, int Qt, SrPlan* p) {
                   ? std::max(1, std::min(grm::gqa::kMaxCols / cols1,
                                          static_cast<int>(std::max<size_t>(1, kMaxHmaxBytes / per_q))))
                   : 1;
-  p->mfma = a->key_dtype == kBF16 ? kBF16 : kF16;
+  p->mfma = screen_dtype(a) == kBF16 ? kBF16 : kF16;
   return true;
 }
 
@@ -738,8 +767,12 @@ int prepare_sr(GqaDeviceArena* a, const SrPlan& p) {
 //   sigma_q, sigma_k  a query / key value near zero flushed or rounded
 //   sigma_p  a product lost to fp32 underflow
 //   emax   the exponent under which scaled query values stay
+//   eps_rel, eps_abs  an fp32 bank's fp16 key copy: rounding to nearest
+//          even moves a value by at most 2^-11 of it, or 2^-25 below the
+//          fp16 normal range
 struct ScreenBound {
   double gamma = 0, delta = 0, sigma_q = 0, sigma_k = 0, sigma_p = 0;
+  double eps_rel = 0, eps_abs = 0;
   int emax = 0;
 };
 
@@ -755,6 +788,10 @@ ScreenBound screen_bound(const GqaDeviceArena* a, const SrPlan& p, int q_dtype) 
     b.sigma_q = b.sigma_k = ldexp(1.0, -14);
     b.sigma_p = 0.0;
     b.emax = 15;
+  }
+  if (a->d_skeys) {
+    b.eps_rel = ldexp(1.0, -11);
+    b.eps_abs = ldexp(1.0, -25);
   }
   return b;
 }
@@ -787,29 +824,33 @@ int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
   const size_t hstride = a->cap_nodes * static_cast<size_t>(p.H);
   const double denom = sqrt(static_cast<double>(a->hd));
   const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);  // <= 64 KiB
-#define GRM_SR(KDT, KS, NTT)                                                                    \
-  grm::gqa::gqa_sr_kernel<KDT, KS, NTT><<<grid, threads, lds, a->stream>>>(                     \
-      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,                        \
+#define GRM_SR(KDT, KS, NTT, XF)                                                                \
+  grm::gqa::gqa_sr_kernel<KDT, KS, NTT, XF><<<grid, threads, lds, a->stream>>>(                 \
+      screen_keys(a), a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,        \
       static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, ps.rc, ps.qc, qpass, q_dtype, q_elems,  \
-      qb, eb.emax, eb.gamma, eb.delta, eb.sigma_q, eb.sigma_k, eb.sigma_p, a->d_qbad,           \
-      pi > 0 ? 1 : 0, reinterpret_cast<const float*>(a->d_kmax), denom, hpass, hstride,          \
-      a->cap_nodes, g_fast)
-#define GRM_SR_NT(KDT, KS)                 \
-  switch (NT) {                            \
-    case 1: GRM_SR(KDT, KS, 1); break;     \
-    case 2: GRM_SR(KDT, KS, 2); break;     \
-    default: GRM_SR(KDT, KS, 4); break;    \
+      qb, eb.emax, eb.gamma, eb.delta, eb.sigma_q, eb.sigma_k, eb.sigma_p, eb.eps_rel,          \
+      eb.eps_abs, a->d_qbad, pi > 0 ? 1 : 0, reinterpret_cast<const float*>(a->d_kmax), denom,   \
+      hpass, hstride, a->cap_nodes, g_fast)
+#define GRM_SR_NT(KDT, KS, XF)                 \
+  switch (NT) {                                \
+    case 1: GRM_SR(KDT, KS, 1, XF); break;     \
+    case 2: GRM_SR(KDT, KS, 2, XF); break;     \
+    default: GRM_SR(KDT, KS, 4, XF); break;    \
   }
-#define GRM_SR_KS(KDT)                     \
-  switch (p.KS) {                          \
-    case 2: GRM_SR_NT(KDT, 2); break;      \
-    case 4: GRM_SR_NT(KDT, 4); break;      \
-    default: GRM_SR_NT(KDT, 8); break;     \
+#define GRM_SR_KS(KDT, XF)                     \
+  switch (p.KS) {                              \
+    case 2: GRM_SR_NT(KDT, 2, XF); break;      \
+    case 4: GRM_SR_NT(KDT, 4, XF); break;      \
+    default: GRM_SR_NT(KDT, 8, XF); break;     \
   }
-  switch (a->key_dtype) {
-    case kBF16: GRM_SR_KS(kBF16); break;
-    case kF16: GRM_SR_KS(kF16); break;
-    default: GRM_SR_KS(kI8); break;
+  if (a->d_skeys) {
+    GRM_SR_KS(kF16, true);
+  } else {
+    switch (a->key_dtype) {
+      case kBF16: GRM_SR_KS(kBF16, false); break;
+      case kF16: GRM_SR_KS(kF16, false); break;
+      default: GRM_SR_KS(kI8, false); break;
+    }
   }
 #undef GRM_SR_KS
 #undef GRM_SR_NT
@@ -918,9 +959,10 @@ int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, i
     dim3 grid;                                                                                    \
     GRM_CHECK_RC(persistent_grid(a, reinterpret_cast<const void*>(fn), threads, lds, &grid));     \
     fn<<<grid, threads, lds, a->stream>>>(                                                        \
-        a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_units,                        \
+        screen_keys(a), a->d_scales, a->scale_dtype, a->group_size, a->d_units,                   \
         static_cast<uint32_t>(a->n_units), kv, p.R, p.Qt, qptr, q_dtype, q_elems, qb, emax,       \
-        gamma, delta, rho, sigma_q, sigma_k, sigma_p, a->d_colinfo, a->d_hmaxf, colstride);       \
+        gamma, delta, rho, sigma_q, sigma_k, sigma_p, eb.eps_rel, eb.eps_abs, a->d_colinfo,        \
+        a->d_hmaxf, colstride);                                                                   \
   } while (0)
 #define GRM_SMAX_NT(KDT, KS, FACT, SF16)               \
   switch (NT) {                                        \
@@ -935,7 +977,7 @@ int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, i
     default: GRM_SMAX_NT(KDT, 8, FACT, SF16); break;   \
   }
     const bool sf16 = a->scale_dtype == kF16;
-    switch (a->key_dtype) {
+    switch (screen_dtype(a)) {
       case kBF16: GRM_SMAX_KS(kBF16, false, false); break;
       case kF16: GRM_SMAX_KS(kF16, false, false); break;
       default:
@@ -1078,12 +1120,14 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
           GRM_CHECK_RC(enqueue_sr(a, plan, qbase + static_cast<size_t>(q0) * qstride, q_dtype, qb, topk,
                                   fin_blocks, a->blocks_out.dev + static_cast<size_t>(q0) * per_q,
                                   d_done ? d_done + static_cast<size_t>(q0) * fin_blocks : nullptr));
+          a->sr_routes += 1;
         }
       }
     } else {
       for (int qi = seg[0]; qi < seg[1]; ++qi) {
         GRM_CHECK_RC(enqueue_exact(a, qbase + static_cast<size_t>(qi) * qstride, q_dtype, H, Qt, topk,
                                    fin_blocks, a->blocks_out.dev + static_cast<size_t>(qi) * per_q));
+        a->exact_routes += 1;
       }
     }
   }
@@ -1114,11 +1158,36 @@ extern "C" int grm_gqa_cuda_arena_create(const float* keys_host, int nodes, int 
       head_dim <= 0) {
     return grm::fail(-1, "invalid GQA arena arguments");
   }
-  std::vector<uint64_t> offs(static_cast<size_t>(nodes) + 1);
-  for (int i = 0; i <= nodes; ++i) offs[i] = static_cast<uint64_t>(i) * key_tokens;
+  // The dense bank is zero-padded to key_tokens rows per (node, kv head).
+  // A key row of zeros adds |q.0| = 0 to a maximum that starts at 0, so
+  // the trailing tokens whose rows are zero in every kv head leave the
+  // law's score unchanged and are not placed; one token always stays
+  // (a node with no tokens scores 0.0 even against a non-finite query,
+  // which the law scores NaN over a zero key row).
+  const uint64_t rowv = static_cast<uint64_t>(kv_heads) * head_dim;  // values per token, all kv heads
+  const uint64_t block = static_cast<uint64_t>(key_tokens) * rowv;
+  std::vector<uint64_t> offs(static_cast<size_t>(nodes) + 1, 0);
+  for (int i = 0; i < nodes; ++i) {
+    const uint32_t* node = reinterpret_cast<const uint32_t*>(keys_host) + static_cast<uint64_t>(i) * block;
+    uint64_t len = static_cast<uint64_t>(key_tokens);
+    for (; len > 1; --len) {
+      bool zero = true;
+      for (int g = 0; g < kv_heads && zero; ++g) {
+        const uint32_t* row = node + (static_cast<uint64_t>(g) * key_tokens + len - 1) * head_dim;
+        for (int d = 0; d < head_dim; ++d) {
+          if (row[d] & 0x7fffffffu) {
+            zero = false;
+            break;
+          }
+        }
+      }
+      if (!zero) break;
+    }
+    offs[i + 1] = offs[i] + len;
+  }
   return create_arena(keys_host, kF32, nullptr, kF32, 0, offs.data(), static_cast<uint64_t>(nodes),
                       kv_heads, head_dim, nullptr, static_cast<uint64_t>(nodes), offs.back(),
-                      out_arena);
+                      out_arena, static_cast<uint64_t>(key_tokens));
 }
 
 extern "C" int grm_gqa_cuda_arena_route(GqaDeviceArena* arena, const float* queries_host,
@@ -1316,6 +1385,7 @@ extern "C" int grm_gqa_hip_compact(GqaDeviceArena* a) {
   std::sort(order.begin(), order.end(),
             [&](uint64_t x, uint64_t y) { return a->tok_off[x] < a->tok_off[y]; });
   const size_t kb = token_key_bytes(a), sb = token_scale_bytes(a);
+  const size_t hb = a->d_skeys ? row_values(a) * 2 : 0;  // fp16 copy bytes per token
   uint64_t dst = 0;
   std::vector<uint64_t> new_off(order.size());
   for (size_t i = 0; i < order.size(); ++i) {
@@ -1330,6 +1400,10 @@ extern "C" int grm_gqa_hip_compact(GqaDeviceArena* a) {
           GRM_HIP_CHECK(hipMemcpyAsync(a->d_scales + dst * sb, a->d_scales + src * sb, n * sb,
                                        hipMemcpyDeviceToDevice, a->stream));
         }
+        if (hb) {
+          GRM_HIP_CHECK(hipMemcpyAsync(a->d_skeys + dst * hb, a->d_skeys + src * hb, n * hb,
+                                       hipMemcpyDeviceToDevice, a->stream));
+        }
       } else {
         // Overlapping move: copy token by token in ascending order.
         for (uint64_t t = 0; t < n; ++t) {
@@ -1338,6 +1412,10 @@ extern "C" int grm_gqa_hip_compact(GqaDeviceArena* a) {
           if (sb) {
             GRM_HIP_CHECK(hipMemcpyAsync(a->d_scales + (dst + t) * sb, a->d_scales + (src + t) * sb,
                                          sb, hipMemcpyDeviceToDevice, a->stream));
+          }
+          if (hb) {
+            GRM_HIP_CHECK(hipMemcpyAsync(a->d_skeys + (dst + t) * hb, a->d_skeys + (src + t) * hb,
+                                         hb, hipMemcpyDeviceToDevice, a->stream));
           }
         }
       }
@@ -1495,6 +1573,15 @@ extern "C" int grm_gqa_hip_score_nodes(GqaDeviceArena* a, const void* query_host
   GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
   for (uint64_t i = 0; i < count; ++i) out_scores_host[i] = out[where[i]];
   grm::clear_error();
+  return 0;
+}
+
+extern "C" int grm_gqa_hip_route_stats(GqaDeviceArena* a, uint64_t* out4) {
+  if (!a || !out4) return grm::fail(-1, "null argument");
+  out4[0] = a->routes;
+  out4[1] = a->sr_routes;
+  out4[2] = a->bv_routes;
+  out4[3] = a->exact_routes;
   return 0;
 }
 

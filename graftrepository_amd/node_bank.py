@@ -472,6 +472,15 @@ class GqaNodeBank(_Bank):
                 "epoch", "kv_heads", "head_dim", "dtype")
         return {k: int(v) for k, v in zip(keys, out)}
 
+    def route_stats(self) -> dict:
+        """Counters since create: route calls, query passes screened and
+        refined, passes bound and verified, queries routed exactly."""
+        self._need_open()
+        out = np.zeros(4, dtype=np.uint64)
+        _lib.check(self._lib.grm_gqa_hip_route_stats(self._h, _ptr(out)), "GQA route stats")
+        keys = ("routes", "screen_refine", "bound_verify", "exact")
+        return {k: int(v) for k, v in zip(keys, out)}
+
 
 __all__ = ["MlaNodeBank", "GqaNodeBank", "RouteResult", "as_bf16_bits",
            "bf16_bits_to_f32", "DTYPE_F32", "DTYPE_BF16", "DTYPE_F16",

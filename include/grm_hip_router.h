@@ -312,6 +312,12 @@ int grm_gqa_hip_sync(GqaDeviceArena* arena);
  * capacity, epoch, kv_heads, head_dim, key dtype].  No counterpart. */
 int grm_gqa_hip_bank_info(GqaDeviceArena* arena, uint64_t* out8);
 
+/* Route counters since create: [route calls, query passes routed by
+ * screen and refine, passes routed by bound and verify, queries routed by
+ * the exact path].  An fp32 bank's passes are screened through its fp16
+ * key copy.  No counterpart. */
+int grm_gqa_hip_route_stats(GqaDeviceArena* arena, uint64_t* out4);
+
 /* Test entry, no counterpart and on no route path: the screen of the
  * bound-and-verify path for one query [query_heads][query_tokens][head_dim]
  * (R * query_tokens <= 64 columns per kv head, R = heads / kv_heads) over

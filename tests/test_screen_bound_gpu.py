@@ -5,7 +5,8 @@ the law's value:
 
 * batched MLA (bf16 MFMA 32x32x16): |s~ - score| <= B per query, the
   certificate's margin (law: cpp/grm_runtime.cpp:3518-3545);
-* GQA (bf16/f16 MFMA 16x16x32, INT8 dequantised or factored):
+* GQA (bf16/f16 MFMA 16x16x32, INT8 dequantised or factored, fp32 banks
+  through their fp16 key copy, whose rounding the bound carries):
   |m - scale * max_t |q . k_t|| <= E = coef * K + eabs per (node, kv head,
   query column) (law: cpp/grm_runtime.cpp:2980-3029), with E = +inf where
   the fp32 accumulation could overflow (K >= kcap).
@@ -121,9 +122,11 @@ def gqa_bank(rng, kind, n, kv, hd):
     offs[1:] = np.cumsum(lens)
     fam = np.arange(n) % 6
     blocks = []
-    wide = (-60, 60) if kind == "bf16" else (-12, 12)
-    tiny = (-133, -120) if kind == "bf16" else (-24, -14)
-    huge = (100, 118) if kind == "bf16" else (10, 14)
+    # fp32 banks are screened through an fp16 copy: their wide, tiny and
+    # huge families straddle its normal range, subnormals and maximum
+    wide = {"bf16": (-60, 60), "f32": (-20, 20)}.get(kind, (-12, 12))
+    tiny = {"bf16": (-133, -120), "f32": (-30, -16)}.get(kind, (-24, -14))
+    huge = {"bf16": (100, 118), "f32": (14, 18)}.get(kind, (10, 14))
     for i in range(n):
         shape = (kv, int(lens[i]), hd)
         f = fam[i]
@@ -148,6 +151,8 @@ def gqa_bank(rng, kind, n, kv, hd):
     if kind == "f16":
         h = vals.astype(np.float16)
         return dict(keys=h.view(np.uint16), law=h.astype(np.float32), code=oracle.F16), offs
+    if kind == "f32":
+        return dict(keys=vals, law=vals, code=oracle.F32), offs
     codes, scales = oracle.quantize_int8(vals.reshape(-1, hd), hd, "f16")
     law = oracle.dequantize_int8(codes, scales, hd, "f16").reshape(-1)
     return dict(keys=codes, scales=scales, law=law, code=oracle.I8), offs
@@ -177,13 +182,15 @@ def open_bank(bank, offs, kv, hd):
     if bank["code"] == oracle.I8:
         return GqaNodeBank(bank["keys"], offs, dtype="i8", scales=bank["scales"],
                            scale_dtype="f16", group_size=hd, **kw)
+    if bank["code"] == oracle.F32:
+        return GqaNodeBank(bank["keys"], offs, **kw)
     return GqaNodeBank(bank["keys"], offs, dtype="bf16" if bank["code"] == oracle.BF16 else "f16",
                        **kw)
 
 
-@pytest.mark.parametrize("kind", ["bf16", "f16", "i8"])
+@pytest.mark.parametrize("kind", ["bf16", "f16", "i8", "f32"])
 def test_gqa_screen_obeys_its_bound(hip_lib, kind):
-    rng = np.random.default_rng({"bf16": 5, "f16": 6, "i8": 7}[kind])
+    rng = np.random.default_rng({"bf16": 5, "f16": 6, "i8": 7, "f32": 8}[kind])
     n, kv, hd, H, Qt = 360, 2, 128, 8, 3
     R = H // kv
     bank, offs = gqa_bank(rng, kind, n, kv, hd)
@@ -210,17 +217,17 @@ def test_gqa_screen_obeys_its_bound(hip_lib, kind):
             if ok.any():
                 worst = max(worst, float(np.max(d[ok] / e[ok])))
     assert checked > n * kv * R * Qt // 2
-    if kind == "bf16":
-        assert capped > 0  # the overflow cap is exercised
+    if kind in ("bf16", "f32"):
+        assert capped > 0  # the overflow cap (fp32: the fp16 copy's range) is exercised
     assert worst <= 1.0
 
 
-@pytest.mark.parametrize("kind", ["bf16", "f16", "i8"])
+@pytest.mark.parametrize("kind", ["bf16", "f16", "i8", "f32"])
 @pytest.mark.parametrize("mode", ["sr", "bv", "exact"])
 def test_gqa_stress_banks_route_like_the_law(hip_lib, monkeypatch, kind, mode):
     monkeypatch.setenv("GRM_HIP_GQA_SCREEN", "0" if mode == "exact" else "1")
     monkeypatch.setenv("GRM_HIP_GQA_BOUND", "1" if mode == "bv" else "0")
-    rng = np.random.default_rng({"bf16": 5, "f16": 6, "i8": 7}[kind])
+    rng = np.random.default_rng({"bf16": 5, "f16": 6, "i8": 7, "f32": 8}[kind])
     n, kv, hd, H, Qt = 360, 2, 128, 8, 3
     bank, offs = gqa_bank(rng, kind, n, kv, hd)
     qs = np.stack([gqa_query(rng, H, Qt, hd, kind) for _ in range(3)])
