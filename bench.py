@@ -538,6 +538,73 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
                 sum_l=sum_l, cfg=cfg, kv=kv, H=H, qt64=qt64)
 
 
+def bench_gqa_f32_dropin(steps: int, warmup: int):
+    """The reference's own GQA hand-over at the 512-node ragged shape: a
+    dense, zero-padded fp32 bank [nodes, kv, 512, hd] through
+    grm_gqa_cuda_arena_create and host fp32 queries through
+    grm_gqa_cuda_arena_route (core/grm_cuda_router.py:183-231), timed as
+    that caller sees it (query upload included).  The library drops the
+    padding and screens the fp16 copy of the keys; the roofline counts the
+    copy's bytes over the actual tokens."""
+    import oracle
+    from graftrepository_amd import workloads as wl
+    from graftrepository_amd.grm_hip_router import CudaGQARouteSidecar
+
+    cfg = wl.GQA_RAGGED
+    kv = cfg["layers"] * cfg["kv_heads"]
+    H = cfg["layers"] * cfg["heads"]
+    hd = cfg["head_dim"]
+    n = cfg["nodes"]
+    lens = wl.gqa_lengths(n, cfg["seed"], lo=cfg["lo"], hi=cfg["hi"])
+    keys, offs = wl.gqa_bank(lens, kv, hd, cfg["seed"], dtype="f32")
+    T = int(cfg["hi"])
+    dense = np.zeros((n, kv, T, hd), dtype=np.float32)
+    for i in range(n):
+        L = int(lens[i])
+        dense[i, :, :L, :] = keys[int(offs[i]) * kv * hd:int(offs[i + 1]) * kv * hd].reshape(kv, L, hd)
+    del keys
+    q = wl.gqa_queries(1, H, cfg["tokens"], hd, cfg["seed"], dtype="f32")
+    sidecar = CudaGQARouteSidecar.build()
+    bank = sidecar.create_bank(dense)
+    for _ in range(warmup):
+        bank.route_topk(q, topk=cfg["topk"])
+    walls, devs = [], []
+    for _ in range(steps):
+        mapped, rec = bank.route_topk(q, topk=cfg["topk"])
+        walls.append(rec.route_wall_ms)
+        devs.append(rec.device_route_ms_total)
+    setup_ms = bank.setup_wall_ms
+    bank.close()
+    # parity: the oracle's fp64 law on the dense bank (checker only)
+    want, _, _ = oracle.gqa_route(dense.reshape(-1), oracle.F32,
+                                  np.arange(n + 1, dtype=np.uint64) * T, kv, hd, q, cfg["topk"])
+    parity = bool(np.array_equal(mapped.reshape(-1), want.reshape(-1)))
+    del dense
+    sum_l = int(np.sum(lens))
+    bytes_copy = sum_l * kv * hd * 2          # the screen's fp16 stream
+    bytes_f32 = sum_l * kv * hd * 4           # the fp32 bank over actual tokens
+    bytes_dense = n * T * kv * hd * 4         # the padded bank handed over
+    mean_dev = float(np.mean(devs))
+    ach = bytes_copy / (mean_dev * 1e-3) / 1e9
+    out = {"workload": "gqa_ragged_route_f32_dropin", "nodes": n, "sum_tokens": sum_l,
+           "dense_rows": T, "kv_heads_stacked": kv, "query_heads_stacked": H,
+           "head_dim": hd, "bank_dtype": "f32 (dense, zero-padded)", "screen_copy": "f16",
+           "query": "host f32, uploaded per call", "topk": cfg["topk"], "steps": steps,
+           "p50_ms": round(pct(walls, 50), 5), "p99_ms": round(pct(walls, 99), 5),
+           "device_ms_mean": round(mean_dev, 5), "setup_wall_ms": round(setup_ms, 1),
+           "oracle_ids_match": parity,
+           "bytes": {"fp16_copy_actual_tokens": bytes_copy, "f32_actual_tokens": bytes_f32,
+                     "f32_dense_handed_over": bytes_dense},
+           "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                        "kernel": "gqa_sr_kernel<f16, 4, 1, fp32 rows>",
+                        "bytes_per_call": bytes_copy},
+           "f32_equivalent_gbs": round(bytes_f32 / (mean_dev * 1e-3) / 1e9, 1)}
+    log(f"[gqa f32 drop-in] p50 {out['p50_ms']:.4f} ms  device {mean_dev:.4f} ms  "
+        f"{ach:.0f} GB/s on the fp16 copy  parity {parity}  setup {setup_ms:.0f} ms")
+    return out
+
+
 def cpu_baseline_gqa_int8(codes, scales, offs, kv, hd, q_bits, k):
     """The 100k-node INT8 route on the host, sampled: the oracle's fp64
     law with the packed format's dequant (fp16(code * scale),
@@ -927,7 +994,8 @@ def main() -> int:
     ap.add_argument("--payload-reps", type=int, default=10)
     ap.add_argument("--store-steps", type=int, default=100)
     ap.add_argument("--small-steps", type=int, default=1000)
-    ap.add_argument("--only", choices=["all", "mla", "small", "gqa", "batched", "int8",
+    ap.add_argument("--f32-steps", type=int, default=200)
+    ap.add_argument("--only", choices=["all", "mla", "small", "gqa", "f32", "batched", "int8",
                                        "bridge", "payload", "store"], default="all")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -957,6 +1025,9 @@ def main() -> int:
         small = bench_mla_small(args.small_steps, min(args.warmup, 20), cpu_s, args.skip_cpu)
     if args.only in ("all", "gqa"):
         g = bench_gqa(args.gqa_steps, min(args.warmup, 20), cpu_s)
+    f32 = None
+    if args.only in ("all", "f32"):
+        f32 = bench_gqa_f32_dropin(args.f32_steps, min(args.warmup, 10))
     i8 = None
     if args.only in ("all", "int8"):
         i8 = bench_gqa_int8(args.int8_steps, 2, cpu_s)
@@ -1062,6 +1133,16 @@ def main() -> int:
                    "ms_per_step": b["p50_ms"], "higher_is_better": False,
                    "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
                    "data": "synthetic", "config": b}
+    if f32 is not None:
+        if out:
+            out["gqa_f32_dropin"] = f32
+        else:
+            out = {"metric": "p50 ragged GQA route latency (ms), dense fp32 bank, host query",
+                   "value": f32["p50_ms"], "unit": "ms", "n_gpus": 1,
+                   "steps": args.f32_steps, "warmup": args.warmup,
+                   "ms_per_step": f32["p50_ms"], "higher_is_better": False,
+                   "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+                   "data": "synthetic", "config": f32}
     if i8 is not None:
         if out:
             out["gqa_int8"] = i8

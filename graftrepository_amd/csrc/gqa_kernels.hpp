@@ -731,9 +731,9 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
 // (double bits, atomicMax).
 //
 // XF32: the keys are an fp32 bank's fp16 copy (same rows, chunks of 4
-// pieces); the exact recomputation reads the fp32 rows from xkeys (chunks
-// of 1 piece), and eps_rel / eps_abs carry the copy's rounding into the
-// bound (stage_columns).
+// pieces); the exact recomputation reads the fp32 rows from xkeys (also
+// chunks of 4 pieces), and eps_rel / eps_abs carry the copy's rounding
+// into the bound (stage_columns).
 template <int KDT, int KS, int NT, bool XF32 = false>
 __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     const unsigned char* __restrict__ keys, const unsigned char* __restrict__ xkeys,
@@ -935,8 +935,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
     const uint32_t tt = min(it.t0 + t, last);
     if constexpr (XF32) {
       const u32x4* xplane = reinterpret_cast<const u32x4*>(xkeys) + row0 * (HD / 4);
-      return exact_pair<kF32, HD, 0>(active, xplane + tt, L, nullptr, scale_dtype, 1,
-                                     s_q + min(cg, cols - 1) * HD);
+      return exact_pair<kF32, HD>(active, xplane + static_cast<uint64_t>(tt) * 4, L, nullptr,
+                                  scale_dtype, 1, s_q + min(cg, cols - 1) * HD);
     } else {
       return exact_pair<KDT, HD>(active, kplane + static_cast<uint64_t>(tt) * 4, L,
                                  KDT == kI8 ? splane + static_cast<size_t>(tt) * ses : nullptr,

@@ -435,9 +435,16 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   a->hd = static_cast<uint32_t>(head_dim);
   {
     const size_t row_bytes = static_cast<size_t>(head_dim) * key_esize(key_dtype);
-    // fp32 banks take the lane-per-token exact path, which streams best
-    // from 16-byte pieces; the others read whole 64-byte chunks
-    a->piece_shift = key_dtype == kF32 ? 0 : (row_bytes % 64 == 0 ? 2 : (row_bytes % 32 == 0 ? 1 : 0));
+    // fp32 banks without an fp16 copy take the lane-per-token exact path,
+    // which streams best from 16-byte pieces; the others read whole
+    // 64-byte chunks (an fp32 bank with a copy gathers single rows for
+    // its exact recomputations, one 64-byte chunk per 16 values)
+    const char* env = getenv("GRM_HIP_GQA_SHADOW");
+    const bool shadow = key_dtype == kF32 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
+                        !(env && env[0] == '0');
+    a->piece_shift = key_dtype == kF32 && !shadow
+                         ? 0
+                         : (row_bytes % 64 == 0 ? 2 : (row_bytes % 32 == 0 ? 1 : 0));
   }
   a->cap_nodes = cap_nodes;
   a->cap_tokens = cap_tokens;
@@ -477,12 +484,9 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   BAIL_HIP(hipEventCreate(&a->ev_stop));
   BAIL_HIP(hipEventCreateWithFlags(&a->ev_mut, hipEventDisableTiming));
   BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_keys), std::max<size_t>(16, cap_tokens * token_key_bytes(a))));
-  {
+  if (key_dtype == kF32 && a->piece_shift == 2) {
     // the fp16 copy of an fp32 bank's keys (GRM_HIP_GQA_SHADOW=0: none)
-    const char* env = getenv("GRM_HIP_GQA_SHADOW");
-    const bool shadow = key_dtype == kF32 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
-                        !(env && env[0] == '0');
-    if (shadow) BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_skeys), cap_tokens * row_values(a) * 2));
+    BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_skeys), cap_tokens * row_values(a) * 2));
   }
   if (key_dtype == kI8) {
     BAIL_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_scales), std::max<size_t>(16, cap_tokens * token_scale_bytes(a))));
