@@ -345,13 +345,14 @@ def test_batched_config_parity(hip_lib):
     assert stats["passes"] == 1 and stats["fallbacks"] <= 2
 
 
-def test_batched_copies_of_best_rows_far_apart(hip_lib):
+@pytest.mark.parametrize("count", [48, 256])  # 256: the full-pass screen
+def test_batched_copies_of_best_rows_far_apart(hip_lib, count):
     # Exact copies of the best rows sit in different screen sub-streams
     # (slots 50.. and 100,000..), so the merge sees tied candidates from
     # two wavefronts; NaN and zero rows share tiles with the copies.
     n, dim = 140_000, 288
     rows = wl.mla_rows(n, dim, seed=65, dtype="bf16")
-    qs = wl.mla_queries(48, dim, seed=65, dtype="bf16")
+    qs = wl.mla_queries(count, dim, seed=65, dtype="bf16")
     rows[100_000:100_004] = qs[:4]          # near-perfect matches
     rows[50:54] = qs[:4]                    # their copies, far from them
     rows[1000] = qs[5]
@@ -363,7 +364,7 @@ def test_batched_copies_of_best_rows_far_apart(hip_lib):
         stats = bank.route_stats()
     ids, sc, _ = oracle.mla_route(_f32(rows), _f32(qs), 8, node_ids=node_ids)
     assert_same(res.ids, res.scores, ids, sc)
-    assert stats["batched"] == 48
+    assert stats["batched"] == count
 
 
 @pytest.mark.parametrize("dim,dtype", [(288, "f32"), (96, "f32"), (256, "bf16")])

@@ -79,17 +79,18 @@ def mla_queries(rng, count, dim):
 
 @pytest.mark.parametrize("adversarial", [False, True])
 @pytest.mark.parametrize("query_dtype", ["bf16", "f32"])
-def test_mla_batched_screen_obeys_its_bound(hip_lib, adversarial, query_dtype):
+@pytest.mark.parametrize("count", [80, 256])  # 256: the full-pass screen (queries in registers)
+def test_mla_batched_screen_obeys_its_bound(hip_lib, adversarial, query_dtype, count):
     rng = np.random.default_rng(17 + adversarial)
     n, dim = 2048, 288
     bits = mla_rows(rng, n, dim, adversarial)
     rows = bf16_bits_to_f32(bits)
-    qf = mla_queries(rng, 80, dim)
+    qf = mla_queries(rng, count, dim)
     if query_dtype == "bf16":
         qf = bf16_bits_to_f32(as_bf16_bits(qf))  # the values the law sees
     with MlaNodeBank(bits, np.arange(n, dtype=np.uint64), dtype="bf16") as bank:
         vals, bounds, ids = bank.probe_screen(qf, query_dtype=query_dtype)
-    assert vals.shape == (80, n)
+    assert vals.shape == (count, n)
     np.testing.assert_array_equal(ids, np.arange(n, dtype=np.uint64))
     score = oracle.mla_scores(rows, qf)
     norms = oracle.mla_row_norms(rows).astype(np.float64)
