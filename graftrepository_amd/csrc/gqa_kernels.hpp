@@ -1047,14 +1047,22 @@ __device__ inline void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 // law's fp16(code * scale) keys is in the bound (rho, and a norm bound
 // that covers c * scale).  At a node's end the maxima of the 16 lanes of
 // each column combine and are stored at
-// hmaxf[(slot*kv + g)*colstride + cg] (float bits, scaled units;
-// colstride >= cols): one (node, kv head)'s columns are one contiguous
-// run, written by one coalesced store.
+// hmaxf[(slot*kv + g)*colstride + gc] (float bits, scaled units): one
+// (node, kv head)'s columns are one contiguous run, written by one
+// coalesced store.
+//
+// Query passes: the launch reads pass (r0, Rc, t0, Qc) of Qb queries
+// (query advanced to the pass's first value, see "Query passes"); its
+// column cg = qb*Rc*Qc + rr*Qc + tt is column
+// gc = qb*R*Qt + (r0 + rr)*Qt + t0 + tt of the query's full set, so passes
+// over disjoint parts of a query fill disjoint cells of the same rows, and
+// colinfo[g*colstride + gc] holds each column's bound parameters.
 template <int KDT, int KS, int NT, bool FACT, bool SF16>
 __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     const unsigned char* __restrict__ keys, const unsigned char* __restrict__ scales,
     int scale_dtype, int group_size, const Item* __restrict__ items, uint32_t n_items, int kv,
-    int R, int Qt, const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
+    int R, int Qt, int r0, int Rc, int t0, int Qc, const void* __restrict__ query, int q_dtype,
+    size_t q_elems, int Qb, int emax,
     double gamma, double delta, double rho, double sigma_q, double sigma_k, double sigma_p,
     double eps_rel, double eps_abs, float4* __restrict__ colinfo, unsigned* __restrict__ hmaxf,
     int colstride) {
@@ -1071,8 +1079,14 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
   __shared__ unsigned s_bad[kMaxCols];
   const int lane = threadIdx.x & (kWave - 1);
   const int g = blockIdx.y;
-  const int RQc = R * Qt;
+  const int RQc = Rc * Qc;
   const int cols = Qb * RQc;
+  // the query's full column index of pass column cg
+  auto full_col = [&](int cg) {
+    const int qb = cg / RQc;
+    const int rem = cg - qb * RQc;
+    return qb * R * Qt + (r0 + rem / Qc) * Qt + t0 + rem % Qc;
+  };
   const int quarter = lane >> 4;
   const int r16 = lane & 15;
   const uint32_t stride = gridDim.x * kUnitWaves;
@@ -1173,10 +1187,12 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     load_next(x2);
     load_next(x3);
   }
-  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, R, Qt, g, emax,
+  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, Rc, Qc, g, emax,
                     gamma, delta, rho, sigma_q, sigma_k, sigma_p, eps_rel, eps_abs);
   if (blockIdx.x == 0) {
-    for (int cg = threadIdx.x; cg < cols; cg += blockDim.x) colinfo[g * cols + cg] = s_ec[cg];
+    for (int cg = threadIdx.x; cg < cols; cg += blockDim.x) {
+      colinfo[static_cast<size_t>(g) * colstride + full_col(cg)] = s_ec[cg];
+    }
   }
   if (!has_item) return;
 
@@ -1254,6 +1270,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
   // written by one coalesced store
   const int my_cg = (r16 >> 2) * 16 + quarter * 4 + (r16 & 3);
   const bool my_col = (r16 >> 2) < NT && my_cg < cols;
+  const int my_gc = my_col ? full_col(my_cg) : 0;
   auto emit = [&](uint32_t slot) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -1274,7 +1291,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
         m[nt][v] = 0u;
       }
     }
-    if (my_col) hmaxf[(static_cast<size_t>(slot) * kv + g) * colstride + my_cg] = mine;
+    if (my_col) hmaxf[(static_cast<size_t>(slot) * kv + g) * colstride + my_gc] = mine;
   };
   // Groups of five steps with one exit, at the bottom: steps after the
   // stream's last tile fold reloaded tiles marked kNoSlot, which emit
@@ -1327,7 +1344,11 @@ __host__ __device__ inline double screen_key_norm(float kmax, bool fact, int hd)
 // past the float range: the law's score is +inf); the block's k best
 // lower bounds among nodes with a finite upper bound (tie law) go to
 // block_out[(qb*blocks + block)*k ..).  Also
-// zeroes *zero_counter (the candidates kernel's item count).
+// zeroes *zero_counter (the candidates kernel's item count).  cols is the
+// stride of colinfo's kv-head rows.  kStaged: the query's H*Qt column
+// parameters are staged in LDS (else read from colinfo, for queries of
+// many tokens).
+template <bool kStaged>
 __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     const unsigned* __restrict__ hmaxf, int colstride, size_t cap, int H, int Qt, int R, int cols,
     int kv, uint32_t n_slots, const uint32_t* __restrict__ lens,
@@ -1346,13 +1367,18 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
   if (sblk == 0 && qb == 0 && threadIdx.x == 0) *zero_counter = 0u;
   const double denom = sqrt(static_cast<double>(hd));
   const int HQ = H * Qt;
-  for (int i = threadIdx.x; i < HQ; i += blockDim.x) {
+  // column parameters of (h, qi), with 1/scale (the scale is a power of
+  // two: its inverse is exact)
+  auto col_params = [&](int i) {
     const int h = i / Qt;
-    float4 ci = colinfo[(h / R) * cols + (qb * R + h % R) * Qt + i % Qt];
-    ci.z = 1.0f / ci.z;  // the scale is a power of two: its inverse is exact
-    s_ci[i] = ci;
+    float4 ci = colinfo[static_cast<size_t>(h / R) * cols + (qb * R + h % R) * Qt + i % Qt];
+    ci.z = 1.0f / ci.z;
+    return ci;
+  };
+  if constexpr (kStaged) {
+    for (int i = threadIdx.x; i < HQ; i += blockDim.x) s_ci[i] = col_params(i);
+    __syncthreads();
   }
-  __syncthreads();
   bool q_bad = false;
   for (int g0 = 0; g0 < kv; g0 += kWave) {
     q_bad = q_bad || (g0 + lane < kv && qbad[qb * kv + g0 + lane] != 0u);
@@ -1390,7 +1416,7 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
       for (int j = 0; j < kAhead; ++j) {
         const int hq = j0 + j;
         if (hq < HQ) {
-          const float4 ci = s_ci[hq];
+          const float4 ci = kStaged ? s_ci[hq] : col_params(hq);
           const double e = K < static_cast<double>(ci.w)
                                ? (static_cast<double>(ci.x) * K + static_cast<double>(ci.y)) * (1.0 + 0x1p-50)
                                : static_cast<double>(INFINITY);
@@ -1428,6 +1454,96 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     // is certainly finite (ub below the float range), as only finite
     // scores are ranked
     wl_consume(Lw, k, lbf, id, slot, isfinite(lbf) && isfinite(ubf) && lbf >= Lw.th_s);
+  }
+  if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(Lw);
+  __syncthreads();
+  if (wave == 0) {
+    WaveList B;
+    block_merge<kFinWaves>(s_lists, k, B);
+    if (lane < k) block_out[(static_cast<size_t>(qb) * nsblk + sblk) * k + lane] = wl_entry(B);
+  }
+}
+
+// The same bounds for queries of many tokens (H*Qt cells per node): one
+// wavefront per node at a time, its lanes over heads -- lane l takes heads
+// l, l + 64, ..., each the max over its Qt query tokens' bounds -- and the
+// heads' sums formed by a reduction across the wavefront (a different
+// order than the sequential sum, which the 2^-40 widening covers many
+// times over: the fp64 sum of H non-negative terms is within H * 2^-53 of
+// exact).  grid (queries, blocks), kFinWaves wavefronts; wavefront w of
+// block b takes nodes (b * kFinWaves + w) + i * blocks * kFinWaves.
+// Outputs as gqa_bounds_kernel.
+__global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_wide_kernel(
+    const unsigned* __restrict__ hmaxf, int colstride, size_t cap, int H, int Qt, int R, int cols,
+    int kv, uint32_t n_slots, const uint32_t* __restrict__ lens,
+    const uint32_t* __restrict__ flags, const uint64_t* __restrict__ ids,
+    const unsigned* __restrict__ kmax, const float4* __restrict__ colinfo,
+    const unsigned* __restrict__ qbad, int fact, int hd, int k, float2* __restrict__ lbub,
+    Cand* __restrict__ block_out, uint32_t* __restrict__ zero_counter) {
+  __shared__ Cand s_lists[kFinWaves][kMaxTopK];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int qb = blockIdx.x;
+  const uint32_t sblk = blockIdx.y, nsblk = gridDim.y;
+  if (sblk == 0 && qb == 0 && threadIdx.x == 0) *zero_counter = 0u;
+  const double denom = sqrt(static_cast<double>(hd));
+  bool q_bad = false;
+  for (int g0 = 0; g0 < kv; g0 += kWave) {
+    q_bad = q_bad || (g0 + lane < kv && qbad[qb * kv + g0 + lane] != 0u);
+  }
+  q_bad = __ballot(q_bad) != 0ull;
+  WaveList Lw;
+  wl_init(Lw);
+  for (uint32_t slot = sblk * kFinWaves + wave; slot < n_slots; slot += nsblk * kFinWaves) {
+    const uint32_t f = flags[slot];
+    const uint32_t len = lens[slot];
+    const uint64_t id = ids[slot];
+    const double K = screen_key_norm(__uint_as_float(kmax[slot]), fact != 0, hd);
+    const bool screened = (f & 3u) == 3u && len != 0u && !q_bad;
+    double lo_sum = 0.0, hi_sum = 0.0;
+    if (screened) {
+      const unsigned* cells = hmaxf + static_cast<size_t>(slot) * kv * colstride;
+      for (int h = lane; h < H; h += kWave) {
+        const size_t c0 = static_cast<size_t>(h / R) * colstride + (qb * R + h % R) * Qt;
+        const size_t i0 = static_cast<size_t>(h / R) * cols + (qb * R + h % R) * Qt;
+        double lo_h = 0.0, hi_h = 0.0;
+        for (int t = 0; t < Qt; ++t) {
+          const float4 ci = colinfo[i0 + t];
+          const double e = K < static_cast<double>(ci.w)
+                               ? (static_cast<double>(ci.x) * K + static_cast<double>(ci.y)) * (1.0 + 0x1p-50)
+                               : static_cast<double>(INFINITY);
+          const double m = static_cast<double>(__uint_as_float(cells[c0 + t]));
+          const double inv = 1.0 / static_cast<double>(ci.z);  // a power of two: exact
+          const double lo = fmax(0.0, m - e) * inv;
+          const double hi = (m + e) * inv;
+          lo_h = fmax(lo_h, lo);
+          hi_h = (hi > hi_h || isnan(hi)) ? hi : hi_h;
+        }
+        lo_sum += lo_h;
+        hi_sum += hi_h;
+      }
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        lo_sum += __shfl_xor(lo_sum, off);
+        const double o = __shfl_xor(hi_sum, off);
+        hi_sum = isnan(o) ? o : hi_sum + o;
+      }
+    }
+    const double lb = lo_sum / denom / static_cast<double>(H) * (1.0 - 0x1p-40);
+    const double ub = hi_sum / denom / static_cast<double>(H) * (1.0 + 0x1p-40);
+    float lbf = __builtin_nanf(""), ubf = __builtin_nanf("");
+    if (f & 1u) {
+      if (len == 0) {
+        lbf = ubf = 0.0f;
+      } else if ((f & 2u) && !q_bad && !isinf(static_cast<float>(lb))) {
+        lbf = static_cast<float>(lb);
+        if (static_cast<double>(lbf) > lb) lbf = nextafterf(lbf, -INFINITY);
+        ubf = static_cast<float>(ub);
+        if (static_cast<double>(ubf) < ub || isnan(ub)) ubf = isnan(ub) ? INFINITY : nextafterf(ubf, INFINITY);
+      }
+    }
+    if (lane == 0) lbub[static_cast<size_t>(qb) * cap + slot] = make_float2(lbf, ubf);
+    wl_consume(Lw, k, lbf, id, slot, lane == 0 && isfinite(lbf) && isfinite(ubf) && lbf >= Lw.th_s);
   }
   if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(Lw);
   __syncthreads();

@@ -881,14 +881,27 @@ int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
 
 constexpr uint32_t kCandFinBlocks = 16;  // finalize blocks per query over candidates
 
-// Bound and verify keeps per-column maxima of one pass and verifies in one
-// exact pass: routes whose query has at most 32 columns per kv head.
+// Bound and verify keeps the screened maxima of every column of the
+// query (one screen launch per query pass of at most 64 columns per kv
+// head, all into one set of rows) and verifies the candidates in exact
+// passes of at most 32 columns.
+// By default passes of more than 24 query columns per kv head take it: on
+// the 512-node bank (R = 4) screen and refine is faster up to 5 query
+// tokens (0.355 against 0.595 ms at 5) and bound and verify from 8 (0.422
+// against 0.471 ms; 2.61 against 3.61 ms at 64 tokens).
 bool use_bound(const GqaDeviceArena* a, const SrPlan& p, int qb) {
   if (a->bound_mode == 0) return false;
-  if (p.passes.size() != 1 || p.R * p.Qt > grm::gqa::kMaxRQ) return false;
   if (a->bound_mode == 1) return true;
-  return qb * p.R * p.Qt > 16;
+  return qb * p.R * p.Qt > 24;
 }
+
+// Column parameters of a bounds block beyond this many bytes are read
+// from global memory instead of LDS.
+constexpr size_t kBoundsStageBytes = 32768;
+// Queries with at least this many (head, query token) cells per node take
+// the bounds kernel with lanes over heads, in up to kWideBlocks blocks.
+constexpr int kWideCells = 1024;
+constexpr uint32_t kWideBlocks = 1024;
 
 // Grid (P, kv) of the persistent screen kernel `fn`: as many blocks as
 // the device holds resident at once (a block that had to wait for a slot
@@ -922,10 +935,10 @@ int prepare_bv(GqaDeviceArena* a, const SrPlan& p, int topk, uint32_t fin_blocks
   GRM_CHECK_RC(reserve_device(&a->d_hmaxf, &a->d_hmaxf_count,
                               qbm * static_cast<size_t>(p.H) * p.Qt * cap));
   GRM_CHECK_RC(reserve_device(&a->d_colinfo, &a->d_colinfo_count,
-                              static_cast<size_t>(a->kv) * grm::gqa::kMaxCols));
+                              static_cast<size_t>(a->kv) * qbm * p.R * p.Qt));
   GRM_CHECK_RC(reserve_device(&a->d_lbub, &a->d_lbub_count, qbm * cap));
   GRM_CHECK_RC(reserve_device(&a->d_blists, &a->d_blists_count,
-                              qbm * fin_blocks * static_cast<size_t>(topk)));
+                              qbm * std::max(fin_blocks, kWideBlocks) * static_cast<size_t>(topk)));
   GRM_CHECK_RC(reserve_device(&a->d_cslots, &a->d_cslots_count, qbm * cap));
   GRM_CHECK_RC(reserve_device(&a->d_ccount, &a->d_ccount_count, qbm + 1));
   GRM_CHECK_RC(reserve_device(&a->d_citems, &a->d_citems_count,
@@ -940,9 +953,10 @@ int prepare_bv(GqaDeviceArena* a, const SrPlan& p, int topk, uint32_t fin_blocks
 // d_hmaxf (one run of colstride cells per (slot, kv head)), the columns'
 // bound parameters into d_colinfo.
 int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
-                int colstride) {
+                int colstride, const QPass& ps) {
   const int kv = static_cast<int>(a->kv);
-  const int cols = qb * p.R * p.Qt;
+  const int cols = qb * ps.rc * ps.qc;
+  const unsigned char* qpass = qptr + pass_query_offset(a, p.Qt, ps, q_dtype);
   const int NT = (cols + 15) / 16 <= 1 ? 1 : ((cols + 15) / 16 <= 2 ? 2 : 4);
   const bool fact = a->key_dtype == kI8 && static_cast<uint32_t>(a->group_size) == a->hd;
   // error-bound constants as in enqueue_sr; rho: the INT8 row scale
@@ -964,7 +978,8 @@ int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, i
     GRM_CHECK_RC(persistent_grid(a, reinterpret_cast<const void*>(fn), threads, lds, &grid));     \
     fn<<<grid, threads, lds, a->stream>>>(                                                        \
         screen_keys(a), a->d_scales, a->scale_dtype, a->group_size, a->d_units,                   \
-        static_cast<uint32_t>(a->n_units), kv, p.R, p.Qt, qptr, q_dtype, q_elems, qb, emax,       \
+        static_cast<uint32_t>(a->n_units), kv, p.R, p.Qt, ps.r0, ps.rc, ps.t0, ps.qc, qpass,     \
+        q_dtype, q_elems, qb, emax,                                                               \
         gamma, delta, rho, sigma_q, sigma_k, sigma_p, eb.eps_rel, eb.eps_abs, a->d_colinfo,        \
         a->d_hmaxf, colstride);                                                                   \
   } while (0)
@@ -1015,30 +1030,61 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   const bool fact = a->key_dtype == kI8 && static_cast<uint32_t>(a->group_size) == a->hd;
   // screened maxima: one run of colstride cells per (slot, kv head)
   const int colstride = p.qb_max * RQ;
-  // 1. query rows as doubles and the query flags (for the exact pass)
-  GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, p.passes[0], false));
-  // 2. screened maxima of every (column, node)
-  GRM_CHECK_RC(launch_smax(a, p, qptr, q_dtype, qb, colstride));
+  (void)cols;
+  // exact passes of at most 32 columns per kv head
+  const std::vector<QPass> xpasses = query_passes(p.R, p.Qt, grm::gqa::kMaxRQ);
+  // 1. the query flags, and the query rows as doubles for a single exact
+  // pass (with several, each loads its own rows before it runs)
+  const QPass whole{0, p.R, 0, p.Qt};
+  GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, xpasses.size() == 1 ? xpasses[0] : whole, false));
+  // 2. screened maxima of every (column, node), one launch per screen pass
+  for (const QPass& ps : p.passes) GRM_CHECK_RC(launch_smax(a, p, qptr, q_dtype, qb, colstride, ps));
   // 3. score bounds, the k best lower bounds per block (with no key tokens
   // at all the column parameters are never used: every live node has no
   // tokens and scores 0)
-  grm::gqa::gqa_bounds_kernel<<<dim3(qb, fin_blocks), grm::gqa::kFinWaves * grm::kWave,
-                                static_cast<size_t>(H) * p.Qt * sizeof(float4), a->stream>>>(
-      a->d_hmaxf, colstride, a->cap_nodes, H, p.Qt, p.R, cols, kv,
-      static_cast<uint32_t>(a->high_water), a->d_len,
-      a->route_flags ? a->route_flags : a->d_flags, a->d_ids, a->d_kmax,
-      a->d_colinfo, a->d_qbad, fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub,
-      a->d_blists, a->d_ccount + p.qb_max);
+  const size_t ci_bytes = static_cast<size_t>(H) * p.Qt * sizeof(float4);
+  const bool staged = ci_bytes <= kBoundsStageBytes;
+  const bool wide = H * p.Qt >= kWideCells;
+  const uint32_t n_slots = static_cast<uint32_t>(a->high_water);
+  // the bounds blocks, and so the candidates kernel's lists per query
+  const uint32_t bblocks =
+      wide ? std::max<uint32_t>(1, std::min<uint32_t>(kWideBlocks, (n_slots + grm::gqa::kFinWaves - 1) /
+                                                                        grm::gqa::kFinWaves))
+           : fin_blocks;
+#define GRM_BOUNDS(ST)                                                                           \
+  grm::gqa::gqa_bounds_kernel<ST><<<dim3(qb, fin_blocks), grm::gqa::kFinWaves * grm::kWave,      \
+                                    ST ? ci_bytes : 0, a->stream>>>(                             \
+      a->d_hmaxf, colstride, a->cap_nodes, H, p.Qt, p.R, colstride, kv,                          \
+      static_cast<uint32_t>(a->high_water), a->d_len,                                            \
+      a->route_flags ? a->route_flags : a->d_flags, a->d_ids, a->d_kmax,                         \
+      a->d_colinfo, a->d_qbad, fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub,           \
+      a->d_blists, a->d_ccount + p.qb_max)
+  if (wide) {
+    grm::gqa::gqa_bounds_wide_kernel<<<dim3(qb, bblocks), grm::gqa::kFinWaves * grm::kWave, 0,
+                                       a->stream>>>(
+        a->d_hmaxf, colstride, a->cap_nodes, H, p.Qt, p.R, colstride, kv, n_slots, a->d_len,
+        a->route_flags ? a->route_flags : a->d_flags, a->d_ids, a->d_kmax, a->d_colinfo, a->d_qbad,
+        fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub, a->d_blists, a->d_ccount + p.qb_max);
+  } else if (staged) {
+    GRM_BOUNDS(true);
+  } else {
+    GRM_BOUNDS(false);
+  }
+#undef GRM_BOUNDS
   GRM_HIP_CHECK(hipGetLastError());
   // 4. candidates and their exact work items
   grm::gqa::gqa_cands_kernel<<<qb, grm::gqa::kCandWaves * grm::kWave, 0, a->stream>>>(
-      a->d_blists, fin_blocks, topk, a->d_lbub, a->cap_nodes, static_cast<uint32_t>(a->high_water),
+      a->d_blists, bblocks, topk, a->d_lbub, a->cap_nodes, static_cast<uint32_t>(a->high_water),
       a->d_tok_off, a->d_len, kv, a->chunk, a->d_cslots, a->d_ccount, a->d_citems,
       a->d_ccount + p.qb_max);
   GRM_HIP_CHECK(hipGetLastError());
-  // 5. the law on the candidates, then their exact scores and top-k
-  GRM_CHECK_RC(launch_exact(a, H, p.passes[0], a->d_citems,
-                            static_cast<uint64_t>(qb) * a->n_items, a->d_ccount + p.qb_max));
+  // 5. the law on the candidates (pass by pass, into the same maxima), then
+  // their exact scores and top-k
+  for (size_t i = 0; i < xpasses.size(); ++i) {
+    if (xpasses.size() > 1) GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, xpasses[i], true));
+    GRM_CHECK_RC(launch_exact(a, H, xpasses[i], a->d_citems,
+                              static_cast<uint64_t>(qb) * a->n_items, a->d_ccount + p.qb_max));
+  }
   (void)per_q;
   return launch_finalize(a, H, qb, topk, std::min(kCandFinBlocks, fin_blocks), bout, a->d_cslots,
                          a->d_ccount);
@@ -1651,7 +1697,8 @@ extern "C" int grm_gqa_hip_probe_screen(GqaDeviceArena* a, const void* query_hos
   if (a->n_units == 0) return grm::fail(-1, "no node has key tokens");
   GRM_HIP_CHECK(hipMemcpyAsync(d_q.p, query_host, qbytes, hipMemcpyHostToDevice, a->stream));
   GRM_HIP_CHECK(hipMemsetAsync(a->d_hmaxf, 0, cells * sizeof(unsigned), a->stream));
-  GRM_CHECK_RC(launch_smax(a, p, static_cast<const unsigned char*>(d_q.p), query_dtype, 1, colstride));
+  GRM_CHECK_RC(launch_smax(a, p, static_cast<const unsigned char*>(d_q.p), query_dtype, 1, colstride,
+                           p.passes[0]));
   const size_t out_cells = static_cast<size_t>(n) * a->kv * colstride;
   GRM_HIP_CHECK(hipMemcpyAsync(out_maxima_host, a->d_hmaxf, out_cells * sizeof(float),
                                hipMemcpyDeviceToHost, a->stream));

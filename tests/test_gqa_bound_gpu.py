@@ -1,8 +1,9 @@
 """Bound-and-verify GQA route (batched queries) on the GPU against the oracle.
 
-Routes with more than 16 query columns per kv head screen every node once,
-bound each node's score, and evaluate the law exactly on the nodes whose
-bound reaches the k-th best lower bound.  GRM_HIP_GQA_BOUND=1 forces that
+Routes with more than 24 query columns per kv head (batched queries, or
+queries of many tokens, whose columns are screened in passes of 64) screen
+every node once per pass, bound each node's score, and evaluate the law
+exactly on the nodes whose bound reaches the k-th best lower bound.  GRM_HIP_GQA_BOUND=1 forces that
 path for any batch and 0 disables it; both must give the oracle's ids and
 score bits (cpp/grm_runtime.cpp:2980-3029 gqa_raw_score, ties to the lowest
 node id per cpp/grm_runtime.cpp:75-82).

@@ -41,9 +41,16 @@ def c4_bank(nodes, hi, seed):
     return keys, offs, kv, H, cfg["head_dim"]
 
 
-@pytest.fixture(params=["screen", "exact"])
+@pytest.fixture(params=["screen", "refine", "exact"])
 def path(request, monkeypatch):
+    # screen: the default choice (bound and verify for these widths, its
+    # screen in passes of 64 columns and its exact pass in passes of 32);
+    # refine: screen and refine in passes; exact: the fp64 kernel
     monkeypatch.setenv("GRM_HIP_GQA_SCREEN", "0" if request.param == "exact" else "1")
+    if request.param == "refine":
+        monkeypatch.setenv("GRM_HIP_GQA_BOUND", "0")
+    else:
+        monkeypatch.delenv("GRM_HIP_GQA_BOUND", raising=False)
     return request.param
 
 
@@ -106,9 +113,9 @@ def test_f32_bank_long_query(hip_lib):
 
 @pytest.mark.parametrize("bound", ["1", "auto"])
 def test_int8_bank_batched_long_queries(hip_lib, monkeypatch, bound):
-    # 20 tokens x R = 4: 80 columns per query; batched queries that do not
-    # fit one pass are routed one by one on the screen-and-refine path,
-    # also when bound and verify is asked for
+    # 20 tokens x R = 4: 80 columns per query; queries that do not fit one
+    # screen pass are routed one by one (through bound and verify, its
+    # screen in passes of 64 columns and its exact pass in passes of 32)
     if bound == "auto":
         monkeypatch.delenv("GRM_HIP_GQA_BOUND", raising=False)
     else:
