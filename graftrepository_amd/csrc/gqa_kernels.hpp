@@ -1554,6 +1554,120 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_wide_kernel(
   }
 }
 
+// The law on the candidates of a query of many tokens (one query, every
+// column screened by gqa_smax_kernel): per (candidate, kv head g) pair a
+// wavefront first finds, for each of g's heads r, the columns (query
+// tokens) whose screened maximum can still hold the head's maximum -- the
+// screen bounds each column's law maximum in [max(0, m - E), m + E] / scale
+// (gqa_bounds_kernel), so a column whose upper bound lies below the largest
+// lower bound of its head's columns cannot -- and evaluates the law (fp64,
+// d ascending, |dot| / sqrt(hd)) only on those columns, over all of the
+// node's tokens, folding the per-column maxima into hmax[(g*R + r)*cap +
+// slot] with the 64-bit atomicMax.  The head's maximum over its columns is
+// unchanged: the column that holds it has an upper bound at or above every
+// column's lower bound.  A NaN bound keeps its column.  q64 holds the query
+// columns as doubles, value d of column gc at q64[(g*hd + d)*rqp + gc].
+// Wavefronts walk pairs p = w, w + W, ... (p = candidate * kv + g).
+template <int KDT>
+__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_sparse_kernel(
+    const unsigned char* __restrict__ keys, const unsigned char* __restrict__ scales,
+    int scale_dtype, int group_size, int sS, const uint32_t* __restrict__ cand_slots,
+    const uint32_t* __restrict__ cand_count, int kv, int R, int Qt, int hd, int colstride,
+    const unsigned* __restrict__ hmaxf, const float4* __restrict__ colinfo,
+    const unsigned* __restrict__ kmax, int fact, const uint64_t* __restrict__ tok_off,
+    const uint32_t* __restrict__ lens, const double* __restrict__ q64, int rqp, double denom,
+    unsigned long long* __restrict__ hmax, size_t cap) {
+  using T = KeyTraits<KDT>;
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint32_t W = gridDim.x * kUnitWaves;
+  const uint32_t n_pairs = cand_count[0] * static_cast<uint32_t>(kv);
+  const int C = hd / T::kEpc;
+  const int G = KDT == kI8 ? hd / group_size : 1;
+  const int cpg = KDT == kI8 ? group_size / T::kEpc : 1;
+  const int ses = scale_dtype == kF16 ? 2 : 4;
+  for (uint32_t pr = blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+       pr < n_pairs; pr += W) {
+    const uint32_t slot = cand_slots[pr / kv];
+    const int g = static_cast<int>(pr % kv);
+    const uint32_t L = lens[slot];
+    if (L == 0u) continue;
+    const double K = screen_key_norm(__uint_as_float(kmax[slot]), fact != 0, hd);
+    const unsigned* cells = hmaxf + (static_cast<size_t>(slot) * kv + g) * colstride;
+    const float4* cinf = colinfo + static_cast<size_t>(g) * colstride;
+    const uint64_t Lp = (L + kTokAlign - 1) & ~(kTokAlign - 1);
+    const uint64_t row0 = tok_off[slot] * static_cast<uint64_t>(kv) + static_cast<uint64_t>(g) * Lp;
+    const u32x4* kb = reinterpret_cast<const u32x4*>(keys) + row0 * C;
+    // the screen's bounds of column c of head r (unscaled)
+    auto bounds = [&](int c, double& lo, double& hi) {
+      const float4 ci = cinf[c];
+      const double e = K < static_cast<double>(ci.w)
+                           ? (static_cast<double>(ci.x) * K + static_cast<double>(ci.y)) * (1.0 + 0x1p-50)
+                           : static_cast<double>(INFINITY);
+      const double m = static_cast<double>(__uint_as_float(cells[c]));
+      const double inv = 1.0 / static_cast<double>(ci.z);  // a power of two: exact
+      lo = fmax(0.0, m - e) * inv;
+      hi = (m + e) * inv;
+    };
+    for (int r = 0; r < R; ++r) {
+      double lo_max = 0.0;
+      for (int q0 = 0; q0 < Qt; q0 += kWave) {
+        if (q0 + lane < Qt) {
+          double lo, hi;
+          bounds(r * Qt + q0 + lane, lo, hi);
+          lo_max = fmax(lo_max, lo);
+        }
+      }
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) lo_max = fmax(lo_max, __shfl_xor(lo_max, off));
+      double best = 0.0;  // the head's maximum |dot| over the columns evaluated
+      for (int q0 = 0; q0 < Qt; q0 += kWave) {
+        bool keep = false;
+        if (q0 + lane < Qt) {
+          double lo, hi;
+          bounds(r * Qt + q0 + lane, lo, hi);
+          keep = !(hi < lo_max);
+        }
+        uint64_t mask = __ballot(keep);
+        while (mask != 0ull) {
+          const int bit = __ffsll(static_cast<long long>(mask)) - 1;
+          mask &= mask - 1ull;
+          const int gc = r * Qt + q0 + bit;  // wave-uniform
+          const double* qcol = q64 + static_cast<size_t>(g) * hd * rqp + gc;
+          for (uint32_t t0 = 0; t0 < L; t0 += kWave) {
+            const uint32_t t = min(t0 + static_cast<uint32_t>(lane), L - 1u);
+            double acc = 0.0;
+            for (int c = 0; c < C; ++c) {
+              const u32x4 v = piece_ptr(kb, Lp, sS, t, c)[0];
+              float sc = 0.0f;
+              if constexpr (KDT == kI8) {
+                sc = load_scale(scales + (row0 * G + t) * ses, scale_dtype,
+                                static_cast<uint64_t>(c / cpg) * Lp);
+              }
+              float f[T::kEpc];
+              decode_chunk<KDT>(v, sc, f);
+#pragma unroll
+              for (int e = 0; e < T::kEpc; ++e) {
+                acc = fma(static_cast<double>(f[e]), qcol[static_cast<size_t>(c * T::kEpc + e) * rqp], acc);
+              }
+            }
+            const double x = fabs(acc);
+            if (t0 + lane < L) best = (x > best || isnan(x)) ? x : best;
+          }
+        }
+      }
+      // max(|dot|)/denom equals the law's max(|dot|/denom) (division by a
+      // positive constant is monotone under rounding to nearest)
+      unsigned long long bits = __double_as_longlong(best / denom);
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const unsigned long long o = __shfl_xor(bits, off);
+        bits = o > bits ? o : bits;
+      }
+      if (lane == 0 && bits != 0ull) atomicMax(hmax + static_cast<size_t>(g * R + r) * cap + slot, bits);
+    }
+  }
+}
+
 // Candidates; grid (queries), kCandWaves wavefronts per block.  tau = the
 // k-th best lower bound of query qb (merged from the bounds kernel's block
 // lists; -inf when fewer than k nodes are ranked); every slot with

@@ -124,6 +124,9 @@ struct GqaDeviceArena {
   // bound-and-verify path (batched queries): -1 when a pass has more than
   // 16 query columns per kv head, 0 never, 1 whenever the screen runs
   int bound_mode = -1;
+  // bound and verify of one wide query: the exact check on the columns the
+  // screen cannot rule out only (GRM_HIP_GQA_SPARSE=0: every column)
+  bool sparse_exact = true;
   unsigned* d_hmaxf = nullptr;   // screened maxima per (query, head, q token, slot), float bits
   size_t d_hmaxf_count = 0;
   float4* d_colinfo = nullptr;   // per (kv head, column): coef, eabs, scale, bad
@@ -456,6 +459,7 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
     if (v >= 16 && v <= 4096 && v % 16 == 0) a->chunk = static_cast<uint32_t>(v);
   }
   if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
+  if (const char* env = getenv("GRM_HIP_GQA_SPARSE")) a->sparse_exact = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_GQA_BOUND")) {
     a->bound_mode = env[0] == '0' ? 0 : (env[0] == '1' ? 1 : -1);
   }
@@ -1078,12 +1082,36 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
       a->d_tok_off, a->d_len, kv, a->chunk, a->d_cslots, a->d_ccount, a->d_citems,
       a->d_ccount + p.qb_max);
   GRM_HIP_CHECK(hipGetLastError());
-  // 5. the law on the candidates (pass by pass, into the same maxima), then
-  // their exact scores and top-k
-  for (size_t i = 0; i < xpasses.size(); ++i) {
-    if (xpasses.size() > 1) GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, xpasses[i], true));
-    GRM_CHECK_RC(launch_exact(a, H, xpasses[i], a->d_citems,
-                              static_cast<uint64_t>(qb) * a->n_items, a->d_ccount + p.qb_max));
+  // 5. the law on the candidates, then their exact scores and top-k: one
+  // query wider than an exact pass takes only the columns its screen
+  // cannot rule out (the query's rows as doubles are all in q64 from step
+  // 1), others the exact kernel pass by pass
+  if (xpasses.size() > 1 && qb == 1 && a->sparse_exact) {
+    const uint64_t pairs = a->cap_nodes * a->kv;
+    const unsigned blocks = static_cast<unsigned>(
+        std::max<uint64_t>(1, std::min<uint64_t>((pairs + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves, 2048)));
+    const int rqp = rq_pad_of(p.R * p.Qt);
+    const double denom = sqrt(static_cast<double>(a->hd));
+#define GRM_SPARSE(KDT)                                                                           \
+  grm::gqa::gqa_exact_sparse_kernel<KDT><<<blocks, grm::gqa::kUnitWaves * grm::kWave, 0, a->stream>>>( \
+      a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->piece_shift, a->d_cslots,        \
+      a->d_ccount, kv, p.R, p.Qt, static_cast<int>(a->hd), colstride, a->d_hmaxf, a->d_colinfo,  \
+      a->d_kmax, fact ? 1 : 0, a->d_tok_off, a->d_len, a->d_q64, rqp, denom, a->d_hmax,          \
+      a->cap_nodes)
+    switch (a->key_dtype) {
+      case kF32: GRM_SPARSE(kF32); break;
+      case kBF16: GRM_SPARSE(kBF16); break;
+      case kF16: GRM_SPARSE(kF16); break;
+      default: GRM_SPARSE(kI8); break;
+    }
+#undef GRM_SPARSE
+    GRM_HIP_CHECK(hipGetLastError());
+  } else {
+    for (size_t i = 0; i < xpasses.size(); ++i) {
+      if (xpasses.size() > 1) GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, xpasses[i], true));
+      GRM_CHECK_RC(launch_exact(a, H, xpasses[i], a->d_citems,
+                                static_cast<uint64_t>(qb) * a->n_items, a->d_ccount + p.qb_max));
+    }
   }
   (void)per_q;
   return launch_finalize(a, H, qb, topk, std::min(kCandFinBlocks, fin_blocks), bout, a->d_cslots,

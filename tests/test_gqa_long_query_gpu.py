@@ -41,12 +41,15 @@ def c4_bank(nodes, hi, seed):
     return keys, offs, kv, H, cfg["head_dim"]
 
 
-@pytest.fixture(params=["screen", "refine", "exact"])
+@pytest.fixture(params=["screen", "screen-all-columns", "refine", "exact"])
 def path(request, monkeypatch):
-    # screen: the default choice (bound and verify for these widths, its
-    # screen in passes of 64 columns and its exact pass in passes of 32);
-    # refine: screen and refine in passes; exact: the fp64 kernel
+    # screen: the default choice (bound and verify for these widths: its
+    # screen in passes of 64 columns, then the law on the columns of each
+    # candidate that the screen cannot rule out); screen-all-columns: the
+    # same with the law on every column, in passes of 32; refine: screen
+    # and refine in passes; exact: the fp64 kernel
     monkeypatch.setenv("GRM_HIP_GQA_SCREEN", "0" if request.param == "exact" else "1")
+    monkeypatch.setenv("GRM_HIP_GQA_SPARSE", "0" if request.param == "screen-all-columns" else "1")
     if request.param == "refine":
         monkeypatch.setenv("GRM_HIP_GQA_BOUND", "0")
     else:
