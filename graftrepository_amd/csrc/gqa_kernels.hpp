@@ -157,7 +157,7 @@ __device__ inline void decode_chunk(u32x4 v, float scale, float* out) {
 // load.  qflags[qb * kv + g] = 1 when a value of query qb read by kv head g
 // is non-finite; the first pass (flags_or = 0) writes 0 otherwise, later
 // passes leave the flag as it is.  grid (kv, Qb).
-__global__ __launch_bounds__(256) void gqa_q64_kernel(
+__global__ __launch_bounds__(1024) void gqa_q64_kernel(
     const void* __restrict__ query, int q_dtype, size_t q_elems, int Qt, int Qc,
     int hd, int kv, int R, int Rc, int RQP, double* __restrict__ q64,
     unsigned* __restrict__ qflags, int flags_or) {
@@ -511,6 +511,7 @@ __device__ inline uint32_t pack_f16x2(_Float16 lo, _Float16 hi) {
 }
 
 constexpr int kMaxCols = 64;  // query columns (Qb * R * Qt) per screen pass
+constexpr int kMaxSmaxCols = 128;  // per screen-only pass (gqa_smax_kernel, NT up to 8)
 
 
 // ------------------------------------------------------- query columns
@@ -1075,8 +1076,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
   static_assert(!FACT || KDT == kI8, "row-scale factoring is for INT8 banks");
   constexpr uint32_t kEnd = 0x80000000u;
   extern __shared__ float s_q[];
-  __shared__ float4 s_ec[kMaxCols];
-  __shared__ unsigned s_bad[kMaxCols];
+  __shared__ float4 s_ec[kMaxSmaxCols];
+  __shared__ unsigned s_bad[kMaxSmaxCols];
   const int lane = threadIdx.x & (kWave - 1);
   const int g = blockIdx.y;
   const int RQc = Rc * Qc;
@@ -1265,12 +1266,18 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     }
   };
   // node end: the column maxima over the 16 lanes of each quarter; lane
-  // (quarter, r16) then stores column nt*16 + quarter*4 + v, nt = r16/4,
-  // v = r16%4: one (node, kv head)'s columns are one contiguous run,
-  // written by one coalesced store
-  const int my_cg = (r16 >> 2) * 16 + quarter * 4 + (r16 & 3);
-  const bool my_col = (r16 >> 2) < NT && my_cg < cols;
-  const int my_gc = my_col ? full_col(my_cg) : 0;
+  // (quarter, r16) then stores column nt*16 + quarter*4 + v for
+  // nt = r16/4 + 4*i, v = r16%4: one (node, kv head)'s columns are one
+  // contiguous run, written by coalesced stores
+  constexpr int kStores = (NT + 3) / 4;
+  int my_gc[kStores];
+  bool my_col[kStores];
+#pragma unroll
+  for (int i = 0; i < kStores; ++i) {
+    const int cg = ((r16 >> 2) + 4 * i) * 16 + quarter * 4 + (r16 & 3);
+    my_col[i] = (r16 >> 2) + 4 * i < NT && cg < cols;
+    my_gc[i] = my_col[i] ? full_col(cg) : 0;
+  }
   auto emit = [&](uint32_t slot) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -1282,16 +1289,21 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
         m[nt][v] = x;
       }
     }
-    uint32_t mine = 0u;
+    uint32_t mine[kStores];
+#pragma unroll
+    for (int i = 0; i < kStores; ++i) mine[i] = 0u;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        if (r16 == nt * 4 + v) mine = m[nt][v];
+        if (r16 == (nt % 4) * 4 + v) mine[nt / 4] = m[nt][v];
         m[nt][v] = 0u;
       }
     }
-    if (my_col) hmaxf[(static_cast<size_t>(slot) * kv + g) * colstride + my_gc] = mine;
+#pragma unroll
+    for (int i = 0; i < kStores; ++i) {
+      if (my_col[i]) hmaxf[(static_cast<size_t>(slot) * kv + g) * colstride + my_gc[i]] = mine[i];
+    }
   };
   // Groups of five steps with one exit, at the bottom: steps after the
   // stream's last tile fold reloaded tiles marked kNoSlot, which emit

@@ -127,6 +127,9 @@ struct GqaDeviceArena {
   // bound and verify of one wide query: the exact check on the columns the
   // screen cannot rule out only (GRM_HIP_GQA_SPARSE=0: every column)
   bool sparse_exact = true;
+  // a single query's screen-only passes take up to 128 columns each at
+  // head dims up to 128 (GRM_HIP_GQA_WIDE_SMAX=0: 64)
+  bool wide_smax = true;
   unsigned* d_hmaxf = nullptr;   // screened maxima per (query, head, q token, slot), float bits
   size_t d_hmaxf_count = 0;
   float4* d_colinfo = nullptr;   // per (kv head, column): coef, eabs, scale, bad
@@ -460,6 +463,7 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   }
   if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
   if (const char* env = getenv("GRM_HIP_GQA_SPARSE")) a->sparse_exact = env[0] != '0';
+  if (const char* env = getenv("GRM_HIP_GQA_WIDE_SMAX")) a->wide_smax = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_GQA_BOUND")) {
     a->bound_mode = env[0] == '0' ? 0 : (env[0] == '1' ? 1 : -1);
   }
@@ -641,7 +645,10 @@ int launch_q64(GqaDeviceArena* a, const void* q, int q_dtype, int qb, int H, int
   GRM_CHECK_RC(reserve_device(&a->d_q64, &a->d_q64_count,
                               static_cast<size_t>(qb) * a->kv * a->hd * rq_pad));
   GRM_CHECK_RC(reserve_device(&a->d_qbad, &a->d_qbad_count, static_cast<size_t>(qb) * a->kv));
-  grm::gqa::gqa_q64_kernel<<<dim3(a->kv, qb), 256, 0, a->stream>>>(
+  // a block per (kv head, query); wide passes (a whole query of many
+  // tokens) take 1024 threads
+  const unsigned q64_threads = rq_pad >= 64 ? 1024u : 256u;
+  grm::gqa::gqa_q64_kernel<<<dim3(a->kv, qb), q64_threads, 0, a->stream>>>(
       static_cast<const unsigned char*>(q) + pass_query_offset(a, Qt, ps, q_dtype), q_dtype,
       static_cast<size_t>(H) * Qt * a->hd, Qt, ps.qc, static_cast<int>(a->hd),
       static_cast<int>(a->kv), R, ps.rc, rq_pad, a->d_q64, a->d_qbad, flags_or ? 1 : 0);
@@ -961,7 +968,11 @@ int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, i
   const int kv = static_cast<int>(a->kv);
   const int cols = qb * ps.rc * ps.qc;
   const unsigned char* qpass = qptr + pass_query_offset(a, p.Qt, ps, q_dtype);
-  const int NT = (cols + 15) / 16 <= 1 ? 1 : ((cols + 15) / 16 <= 2 ? 2 : 4);
+  const int tiles = (cols + 15) / 16;
+  const int NT = tiles <= 1 ? 1 : (tiles <= 2 ? 2 : (tiles <= 4 ? 4 : 8));
+  if (cols > grm::gqa::kMaxSmaxCols || (NT == 8 && p.KS > 4)) {
+    return grm::fail(-1, "screen-only pass wider than its kernel");
+  }
   const bool fact = a->key_dtype == kI8 && static_cast<uint32_t>(a->group_size) == a->hd;
   // error-bound constants as in enqueue_sr; rho: the INT8 row scale
   // factored out of the dot product (fp32 product then fp16 rounding of
@@ -991,7 +1002,8 @@ int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, i
   switch (NT) {                                        \
     case 1: GRM_SMAX(KDT, KS, 1, FACT, SF16); break;   \
     case 2: GRM_SMAX(KDT, KS, 2, FACT, SF16); break;   \
-    default: GRM_SMAX(KDT, KS, 4, FACT, SF16); break;  \
+    case 4: GRM_SMAX(KDT, KS, 4, FACT, SF16); break;   \
+    default: GRM_SMAX(KDT, KS, (KS <= 4 ? 8 : 4), FACT, SF16); break; \
   }
 #define GRM_SMAX_KS(KDT, FACT, SF16)                   \
   switch (p.KS) {                                      \
@@ -1041,8 +1053,13 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   // pass (with several, each loads its own rows before it runs)
   const QPass whole{0, p.R, 0, p.Qt};
   GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, xpasses.size() == 1 ? xpasses[0] : whole, false));
-  // 2. screened maxima of every (column, node), one launch per screen pass
-  for (const QPass& ps : p.passes) GRM_CHECK_RC(launch_smax(a, p, qptr, q_dtype, qb, colstride, ps));
+  // 2. screened maxima of every (column, node), one launch per screen
+  // pass: a single query wider than one pass takes passes of up to 128
+  // columns where the query fragments fit the registers (head dim <= 128)
+  const bool wide_passes = a->wide_smax && qb == 1 && p.passes.size() > 1 && p.KS <= 4;
+  const std::vector<QPass> spasses =
+      wide_passes ? query_passes(p.R, p.Qt, grm::gqa::kMaxSmaxCols) : p.passes;
+  for (const QPass& ps : spasses) GRM_CHECK_RC(launch_smax(a, p, qptr, q_dtype, qb, colstride, ps));
   // 3. score bounds, the k best lower bounds per block (with no key tokens
   // at all the column parameters are never used: every live node has no
   // tokens and scores 0)

@@ -4,7 +4,8 @@ The reference's probe key is the layer-0 query over the whole prompt,
 [H, L, hd] (core/graft_arena.py:2876-2879, core/kv_graft.py:146-171), and
 its sidecar takes any query_tokens (scripts/grm_gqa_cuda_probe.py:376-400).
 The library routes a query wider than one pass (64 query columns per kv
-head on the screen paths, 32 on the exact path) in passes over runs of its
+head on the screen paths -- 128 on a single query's screen-only passes at
+head dims up to 128 -- and 32 on the exact path) in passes over runs of its
 tokens -- or of its heads, when one token's R heads are already too many --
 folded into the same per-(node, head) maxima.  Bar: ids and score bits
 equal to the oracle's fp64 law (cpp/grm_runtime.cpp:2980-3029).
@@ -44,12 +45,14 @@ def c4_bank(nodes, hi, seed):
 @pytest.fixture(params=["screen", "screen-all-columns", "refine", "exact"])
 def path(request, monkeypatch):
     # screen: the default choice (bound and verify for these widths: its
-    # screen in passes of 64 columns, then the law on the columns of each
+    # screen in passes of 128 columns, then the law on the columns of each
     # candidate that the screen cannot rule out); screen-all-columns: the
-    # same with the law on every column, in passes of 32; refine: screen
-    # and refine in passes; exact: the fp64 kernel
+    # screen in passes of 64, the law on every column in passes of 32;
+    # refine: screen and refine in passes; exact: the fp64 kernel
+    narrow = request.param == "screen-all-columns"
     monkeypatch.setenv("GRM_HIP_GQA_SCREEN", "0" if request.param == "exact" else "1")
-    monkeypatch.setenv("GRM_HIP_GQA_SPARSE", "0" if request.param == "screen-all-columns" else "1")
+    monkeypatch.setenv("GRM_HIP_GQA_SPARSE", "0" if narrow else "1")
+    monkeypatch.setenv("GRM_HIP_GQA_WIDE_SMAX", "0" if narrow else "1")
     if request.param == "refine":
         monkeypatch.setenv("GRM_HIP_GQA_BOUND", "0")
     else:
@@ -118,7 +121,7 @@ def test_f32_bank_long_query(hip_lib):
 def test_int8_bank_batched_long_queries(hip_lib, monkeypatch, bound):
     # 20 tokens x R = 4: 80 columns per query; queries that do not fit one
     # screen pass are routed one by one (through bound and verify, its
-    # screen in passes of 64 columns and its exact pass in passes of 32)
+    # screen in one pass of 80 columns and its exact pass in passes of 32)
     if bound == "auto":
         monkeypatch.delenv("GRM_HIP_GQA_BOUND", raising=False)
     else:
