@@ -110,14 +110,29 @@ __device__ inline _Float16 dequant_i8(int code, float scale) {
   return static_cast<_Float16>(p);
 }
 
+// The bank stores an INT8 code c as the byte c ^ 0x80 (c + 128 read as an
+// unsigned byte); gqa_place_kernel applies it on upload.  The screens'
+// conversion of codes to f16 then starts from the unsigned byte directly.
+__device__ inline int stored_code(uint32_t w, int b) {
+  return static_cast<int>((w >> (8 * b)) & 0xffu) - 128;
+}
+__device__ inline u32x4 to_stored_codes(u32x4 v) {
+  v.x ^= 0x80808080u;
+  v.y ^= 0x80808080u;
+  v.z ^= 0x80808080u;
+  v.w ^= 0x80808080u;
+  return v;
+}
+
 template <int KDT>
 struct KeyTraits {
   static constexpr int kEsize = KDT == kF32 ? 4 : (KDT == kI8 ? 1 : 2);
   static constexpr int kEpc = 16 / kEsize;  // elements per 16-byte chunk
 };
 
-// Decode one 16-byte chunk into floats (law-level values); `scale` is the
-// chunk's INT8 group scale (ignored for the other types).
+// Decode one 16-byte chunk of the bank into floats (law-level values);
+// `scale` is the chunk's INT8 group scale (ignored for the other types),
+// INT8 codes in their stored form (stored_code).
 template <int KDT>
 __device__ inline void decode_chunk(u32x4 v, float scale, float* out) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -141,8 +156,7 @@ __device__ inline void decode_chunk(u32x4 v, float scale, float* out) {
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const int code = static_cast<int>(static_cast<int8_t>((w[i] >> (8 * b)) & 0xffu));
-        out[4 * i + b] = static_cast<float>(dequant_i8(code, scale));
+        out[4 * i + b] = static_cast<float>(dequant_i8(stored_code(w[i], b), scale));
       }
     }
   }
@@ -837,10 +851,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
       uint32_t o[4];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        o[2 * i] = pack_f16x2(dequant_i8(static_cast<int8_t>(w[i] & 0xffu), sc),
-                              dequant_i8(static_cast<int8_t>((w[i] >> 8) & 0xffu), sc));
-        o[2 * i + 1] = pack_f16x2(dequant_i8(static_cast<int8_t>((w[i] >> 16) & 0xffu), sc),
-                                  dequant_i8(static_cast<int8_t>(w[i] >> 24), sc));
+        o[2 * i] = pack_f16x2(dequant_i8(stored_code(w[i], 0), sc), dequant_i8(stored_code(w[i], 1), sc));
+        o[2 * i + 1] = pack_f16x2(dequant_i8(stored_code(w[i], 2), sc), dequant_i8(stored_code(w[i], 3), sc));
       }
       u32x4 a;
       a.x = o[0];
@@ -1017,13 +1029,24 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
 // scores < tau, in float as well (lb rounded down, ub rounded up), so the
 // top-k of the candidates is the law's top-k, ties included.
 
-// Four int8 codes (one dword) as four exact f16 values (two dwords, codes
-// 0,1 then 2,3): byte b ^ 0x80 = code + 128 goes under the exponent of
-// 1024 (f16 bits 0x6400 | u = 1024 + u), then 1152 comes off.  Exact:
-// every value involved is an integer below 2048.
+// Maximum over the 16 lanes of a DPP row (lanes 16j .. 16j + 15), in every
+// lane of the row: quad_perm [1,0,3,2] and [2,3,0,1] give each lane its
+// quad's maximum, row_half_mirror (lane i of 8 reads lane 7 - i) the other
+// quad's, row_mirror (lane i of 16 reads lane 15 - i) the other half's.
+__device__ inline uint32_t row_max16(uint32_t x) {
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0xB1, 0xF, 0xF, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x4E, 0xF, 0xF, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x141, 0xF, 0xF, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x140, 0xF, 0xF, false)));
+  return x;
+}
+
+// Four stored int8 codes (one dword) as four exact f16 values (two dwords,
+// codes 0,1 then 2,3): the stored byte u = code + 128 goes under the
+// exponent of 1024 (f16 bits 0x6400 | u = 1024 + u), then 1152 comes off.
+// Exact: every value involved is an integer below 2048.
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-__device__ inline void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  const uint32_t u = w ^ 0x80808080u;
+__device__ inline void codes_to_f16(uint32_t u, uint32_t& lo, uint32_t& hi) {
   const f16x2 bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
   lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
   hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
@@ -1059,7 +1082,7 @@ __device__ inline void codes_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 // over disjoint parts of a query fill disjoint cells of the same rows, and
 // colinfo[g*colstride + gc] holds each column's bound parameters.
 template <int KDT, int KS, int NT, bool FACT, bool SF16>
-__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
+__global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || NT == 1)) ? 2 : 1) void gqa_smax_kernel(
     const unsigned char* __restrict__ keys, const unsigned char* __restrict__ scales,
     int scale_dtype, int group_size, const Item* __restrict__ items, uint32_t n_items, int kv,
     int R, int Qt, int r0, int Rc, int t0, int Qc, const void* __restrict__ query, int q_dtype,
@@ -1224,10 +1247,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
           uint32_t o[4];
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
-            o[2 * i] = pack_f16x2(dequant_i8(static_cast<int8_t>(w[i] & 0xffu), sc),
-                                  dequant_i8(static_cast<int8_t>((w[i] >> 8) & 0xffu), sc));
-            o[2 * i + 1] = pack_f16x2(dequant_i8(static_cast<int8_t>((w[i] >> 16) & 0xffu), sc),
-                                      dequant_i8(static_cast<int8_t>(w[i] >> 24), sc));
+            o[2 * i] = pack_f16x2(dequant_i8(stored_code(w[i], 0), sc), dequant_i8(stored_code(w[i], 1), sc));
+            o[2 * i + 1] = pack_f16x2(dequant_i8(stored_code(w[i], 2), sc), dequant_i8(stored_code(w[i], 3), sc));
           }
           bk[ks].x = o[0];
           bk[ks].y = o[1];
@@ -1283,10 +1304,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_smax_kernel(
     for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        uint32_t x = m[nt][v];
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) x = max(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), off)));
-        m[nt][v] = x;
+        m[nt][v] = row_max16(m[nt][v]);
       }
     }
     uint32_t mine[kStores];
@@ -1776,6 +1794,8 @@ __global__ __launch_bounds__(kCandWaves * kWave) void gqa_cands_kernel(
 // the destination base; the staged row of (item, g, t) is
 // base - src_base + g*len + t.  grid (ceil(items / 4), kv).
 //
+// INT8 codes are written in their stored form (stored_code).
+//
 // With `skeys` (fp32 banks only) each row is also written, rounded to
 // fp16 (nearest even), to the bank's fp16 copy: the same rows as chunk
 // planes of 4 pieces, which the matrix-core screens read.  A slot with a
@@ -1810,7 +1830,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_place_kernel(
     const u32x4* src = src_keys + (srow0 + t) * C;
     double acc = 0.0;
     for (int c = 0; c < C; ++c) {
-      const u32x4 v = src[c];
+      u32x4 v = src[c];
+      if constexpr (KDT == kI8) v = to_stored_codes(v);
       dst[(static_cast<uint64_t>(c >> sS) * it.len << sS) + (static_cast<uint64_t>(t) << sS) + (c & (S - 1))] = v;
       if constexpr (KDT == kF32) {
         if (skeys) {
