@@ -1095,7 +1095,12 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || N
   constexpr bool PERM = KDT == kI8;
   constexpr int HD = 32 * KS;
   constexpr int C = HD / KT::kEpc;            // 16-byte pieces per key row
-  constexpr int NL = PERM ? KS / 2 : KS;       // 16-byte key loads per lane per tile
+  constexpr int NL = PERM ? KS / 2 : KS;       // 16-byte key loads per lane per 16 tokens
+  // INT8 rows are half as wide: a tile is 32 tokens (two halves of 16, lane
+  // l holding tokens l%16 and 16 + l%16) at head dims up to 128, so a tile
+  // is 4 KiB as for 16-bit keys
+  constexpr int NH = (KDT == kI8 && KS <= 4) ? 2 : 1;
+  constexpr uint32_t TT = 16 * NH;              // tokens per tile
   static_assert(!FACT || KDT == kI8, "row-scale factoring is for INT8 banks");
   constexpr uint32_t kEnd = 0x80000000u;
   extern __shared__ float s_q[];
@@ -1135,15 +1140,15 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || N
     d.L = it.len;
     d.t0 = it.t0;
     d.last = it.t0 + it.count - 1;
-    d.ntiles = (it.count + 15) / 16;
+    d.ntiles = (it.count + TT - 1) / TT;
     d.slot = it.slot;
     return d;
   };
   // INT8 scales stay raw bits until the tile is folded: a conversion next
   // to the load would make the wave wait for every load in flight
   struct Tile {
-    u32x4 v[NL];
-    uint32_t s[KDT == kI8 ? (FACT ? 1 : NL) : 1];
+    u32x4 v[NH][NL];
+    uint32_t s[NH][KDT == kI8 ? (FACT ? 1 : NL) : 1];
     uint32_t fin;  // slot | kEnd on an item's last tile, else kNoSlot
   };
   auto scale_raw = [](const unsigned char* sp, uint64_t idx) -> uint32_t {
@@ -1166,19 +1171,23 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || N
   Item nx = items[min(lnext, n_items - 1)];
   bool ldone = false;
   auto load_tile = [&](Tile& b, uint32_t tile) {
-    const uint32_t t = min(ld.t0 + tile * 16 + r16, ld.last);
-    // piece p of token t at kp + (p/4)*L*4 + t*4 + p%4 (chunks of 4 pieces);
-    // load i reads piece i*4 + quarter: 16 tokens x 4 pieces, 1 KiB
-    const u32x4* p = ld.kp + static_cast<uint64_t>(t) * 4 + quarter;
 #pragma unroll
-    for (int i = 0; i < NL; ++i) b.v[i] = __builtin_nontemporal_load(p + i * 4 * ld.L);
-    if constexpr (KDT == kI8) {
-      if constexpr (FACT) {
-        b.s[0] = scale_raw(ld.sp, t);
-      } else {
+    for (int h = 0; h < NH; ++h) {
+      const uint32_t t = min(ld.t0 + tile * TT + h * 16 + r16, ld.last);
+      // piece p of token t at kp + (p/4)*L*4 + t*4 + p%4 (chunks of 4
+      // pieces); load i reads piece i*4 + quarter: 16 tokens x 4 pieces,
+      // 1 KiB
+      const u32x4* p = ld.kp + static_cast<uint64_t>(t) * 4 + quarter;
 #pragma unroll
-        for (int i = 0; i < NL; ++i) {
-          b.s[i] = scale_raw(ld.sp, static_cast<uint64_t>((i * 64 + quarter * 16) / group_size) * ld.L + t);
+      for (int i = 0; i < NL; ++i) b.v[h][i] = __builtin_nontemporal_load(p + i * 4 * ld.L);
+      if constexpr (KDT == kI8) {
+        if constexpr (FACT) {
+          b.s[h][0] = scale_raw(ld.sp, t);
+        } else {
+#pragma unroll
+          for (int i = 0; i < NL; ++i) {
+            b.s[h][i] = scale_raw(ld.sp, static_cast<uint64_t>((i * 64 + quarter * 16) / group_size) * ld.L + t);
+          }
         }
       }
     }
@@ -1223,14 +1232,15 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || N
   u32x4 bq[NT][KS];
   query_frags<MT, PERM, KS, NT>(bq, s_q, s_ec, cols, r16, quarter);
 
-  // key fragment ks of a tile: 8 values of the lane's token in the MFMA type
-  auto key_frags = [&](const Tile& b, u32x4 (&bk)[KS]) {
+  // key fragment ks of half h of a tile: 8 values of the lane's token in
+  // the MFMA type
+  auto key_frags = [&](const Tile& b, int h, u32x4 (&bk)[KS]) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if constexpr (KDT != kI8) {
-        bk[ks] = b.v[ks];
+        bk[ks] = b.v[h][ks];
       } else {
-        const u32x4 v = b.v[ks >> 1];
+        const u32x4 v = b.v[h][ks >> 1];
         const uint32_t w0 = (ks & 1) ? v.z : v.x;
         const uint32_t w1 = (ks & 1) ? v.w : v.y;
         if constexpr (FACT) {
@@ -1242,7 +1252,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || N
           bk[ks].z = o[2];
           bk[ks].w = o[3];
         } else {
-          const float sc = scale_of(b.s[ks >> 1]);
+          const float sc = scale_of(b.s[h][ks >> 1]);
           const uint32_t w[2] = {w0, w1};
           uint32_t o[4];
 #pragma unroll
@@ -1269,20 +1279,32 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || N
     for (int v = 0; v < 4; ++v) m[nt][v] = 0u;
   }
   auto fold = [&](const Tile& b) {
-    u32x4 bk[KS];
-    key_frags(b, bk);
-    float sc = 1.0f;
-    if constexpr (FACT) sc = scale_of(b.s[0]);
+    f32x4 c[NH][NT];
+    float sc[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      u32x4 bk[KS];
+      key_frags(b, h, bk);
+      sc[h] = 1.0f;
+      if constexpr (FACT) sc[h] = scale_of(b.s[h][0]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        c[h][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) c[h][nt] = mfma16x16x32<MT>(bq[nt][ks], bk[ks], c[h][nt]);
+      }
+    }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) c = mfma16x16x32<MT>(bq[nt][ks], bk[ks], c);
-      const float cv[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float x = FACT ? fabsf(cv[v]) * sc : fabsf(cv[v]);
-        m[nt][v] = max(m[nt][v], __float_as_uint(x));
+        const float x0 = FACT ? fabsf(c[0][nt][v]) * sc[0] : fabsf(c[0][nt][v]);
+        if constexpr (NH == 2) {
+          const float x1 = FACT ? fabsf(c[1][nt][v]) * sc[1] : fabsf(c[1][nt][v]);
+          m[nt][v] = max(max(m[nt][v], __float_as_uint(x0)), __float_as_uint(x1));  // v_max3_u32
+        } else {
+          m[nt][v] = max(m[nt][v], __float_as_uint(x0));
+        }
       }
     }
   };
@@ -1374,7 +1396,8 @@ __host__ __device__ inline double screen_key_norm(float kmax, bool fact, int hd)
 // past the float range: the law's score is +inf); the block's k best
 // lower bounds among nodes with a finite upper bound (tie law) go to
 // block_out[(qb*blocks + block)*k ..).  Also
-// zeroes *zero_counter (the candidates kernel's item count).  cols is the
+// zeroes the candidates kernel's counters: counters[qb] (query qb's
+// candidates) and counters[n_counters - 1] (work items).  cols is the
 // stride of colinfo's kv-head rows.  kStaged: the query's H*Qt column
 // parameters are staged in LDS (else read from colinfo, for queries of
 // many tokens).
@@ -1385,7 +1408,7 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     const uint32_t* __restrict__ flags, const uint64_t* __restrict__ ids,
     const unsigned* __restrict__ kmax, const float4* __restrict__ colinfo,
     const unsigned* __restrict__ qbad, int fact, int hd, int k, float2* __restrict__ lbub,
-    Cand* __restrict__ block_out, uint32_t* __restrict__ zero_counter) {
+    Cand* __restrict__ block_out, uint32_t* __restrict__ counters, int n_counters) {
   __shared__ Cand s_lists[kFinWaves][kMaxTopK];
   extern __shared__ float4 s_ci[];  // [H*Qt]: query qb's {coef, eabs, 1/scale, kcap}, (h, qi) order
   const int lane = threadIdx.x & (kWave - 1);
@@ -1394,9 +1417,14 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
   // back to back and share the cache lines of the slots' maxima
   const int qb = blockIdx.x;
   const uint32_t sblk = blockIdx.y, nsblk = gridDim.y;
-  if (sblk == 0 && qb == 0 && threadIdx.x == 0) *zero_counter = 0u;
+  if (sblk == 0 && threadIdx.x == 0) {
+    counters[qb] = 0u;
+    if (qb == 0) counters[n_counters - 1] = 0u;
+  }
   const double denom = sqrt(static_cast<double>(hd));
   const int HQ = H * Qt;
+  const int RQ = R * Qt;
+  const bool vec4 = RQ % 4 == 0 && colstride % 4 == 0;
   // column parameters of (h, qi), with 1/scale (the scale is a power of
   // two: its inverse is exact)
   auto col_params = [&](int i) {
@@ -1428,18 +1456,33 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     // only ranked nodes with key tokens have screened maxima
     const bool screened = in && (f & 3u) == 3u && len != 0u && !q_bad;
     const unsigned* cells = hmaxf + static_cast<size_t>(screened ? slot : 0u) * kv * colstride;
-    // (h, qi) in ascending order, the cells of 16 of them loaded ahead
+    // (h, qi) in ascending order, the cells of 16 of them loaded ahead.
+    // (h, qi) = (g*R + r, qi) is cell g*colstride + qb*RQ + r*Qt + qi: a
+    // query's cells of one kv head are one run of RQ, loaded 4 at a time
+    // when runs and rows are multiples of 4 cells (16-byte aligned)
     constexpr int kAhead = 16;
     double lo_sum = 0.0, hi_sum = 0.0, lo_h = 0.0, hi_h = 0.0;
     for (int j0 = 0; j0 < HQ; j0 += kAhead) {
       float mv[kAhead];
+      if (vec4) {
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j) {
-        const int hq = j0 + j;
-        mv[j] = 0.0f;
-        if (screened && hq < HQ) {
-          const int h = hq / Qt;
-          mv[j] = __uint_as_float(cells[(h / R) * colstride + (qb * R + h % R) * Qt + hq % Qt]);
+        for (int j = 0; j < kAhead; j += 4) {
+          const int hq = j0 + j;
+          uint4 w = make_uint4(0u, 0u, 0u, 0u);
+          if (screened && hq < HQ) {
+            w = *reinterpret_cast<const uint4*>(cells + (hq / RQ) * colstride + qb * RQ + hq % RQ);
+          }
+          mv[j] = __uint_as_float(w.x);
+          mv[j + 1] = __uint_as_float(w.y);
+          mv[j + 2] = __uint_as_float(w.z);
+          mv[j + 3] = __uint_as_float(w.w);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) {
+          const int hq = j0 + j;
+          mv[j] = 0.0f;
+          if (screened && hq < HQ) mv[j] = __uint_as_float(cells[(hq / RQ) * colstride + qb * RQ + hq % RQ]);
         }
       }
 #pragma unroll
@@ -1509,13 +1552,16 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_wide_kernel(
     const uint32_t* __restrict__ flags, const uint64_t* __restrict__ ids,
     const unsigned* __restrict__ kmax, const float4* __restrict__ colinfo,
     const unsigned* __restrict__ qbad, int fact, int hd, int k, float2* __restrict__ lbub,
-    Cand* __restrict__ block_out, uint32_t* __restrict__ zero_counter) {
+    Cand* __restrict__ block_out, uint32_t* __restrict__ counters, int n_counters) {
   __shared__ Cand s_lists[kFinWaves][kMaxTopK];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int qb = blockIdx.x;
   const uint32_t sblk = blockIdx.y, nsblk = gridDim.y;
-  if (sblk == 0 && qb == 0 && threadIdx.x == 0) *zero_counter = 0u;
+  if (sblk == 0 && threadIdx.x == 0) {
+    counters[qb] = 0u;
+    if (qb == 0) counters[n_counters - 1] = 0u;
+  }
   const double denom = sqrt(static_cast<double>(hd));
   bool q_bad = false;
   for (int g0 = 0; g0 < kv; g0 += kWave) {
@@ -1698,13 +1744,15 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_sparse_kernel(
   }
 }
 
-// Candidates; grid (queries), kCandWaves wavefronts per block.  tau = the
-// k-th best lower bound of query qb (merged from the bounds kernel's block
-// lists; -inf when fewer than k nodes are ranked); every slot with
-// ub >= tau is a candidate: its slot goes to cand_slots[qb*cap ..) (count
-// in cand_count[qb]) and its key tokens, in items of `chunk` tokens, to the
-// shared list citems (count in *n_citems, zeroed before the launch) with
-// q = qb, for the exact kernel.
+// Candidates; grid (queries, slot blocks), kCandWaves wavefronts per
+// block.  tau = the k-th best lower bound of query qb (merged from the
+// bounds kernel's block lists, by every block; -inf when fewer than k
+// nodes are ranked); every slot with ub >= tau is a candidate: its slot
+// goes to cand_slots[qb*cap ..) (count in cand_count[qb]) and its key
+// tokens, in items of `chunk` tokens, to the shared list citems (count in
+// *n_citems) with q = qb, for the exact kernel.  Both counts are zeroed
+// before the launch (by the bounds kernel); each wavefront with candidates
+// reserves its places with one atomicAdd on each.
 constexpr int kCandWaves = 16;
 __global__ __launch_bounds__(kCandWaves * kWave) void gqa_cands_kernel(
     const Cand* __restrict__ lists, uint32_t n_lists, int k, const float2* __restrict__ lbub,
@@ -1713,7 +1761,6 @@ __global__ __launch_bounds__(kCandWaves * kWave) void gqa_cands_kernel(
     uint32_t* __restrict__ cand_count, Item* __restrict__ citems, uint32_t* __restrict__ n_citems) {
   __shared__ Cand s_lists[kCandWaves][kMaxTopK];
   __shared__ float s_tau;
-  __shared__ uint32_t s_count;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int qb = blockIdx.x;
@@ -1722,7 +1769,6 @@ __global__ __launch_bounds__(kCandWaves * kWave) void gqa_cands_kernel(
   wl_consume_global(G, k, lists + static_cast<size_t>(qb) * n_lists * k, n_lists * k,
                     static_cast<uint32_t>(wave), kCandWaves);
   if (lane < kMaxTopK) s_lists[wave][lane] = wl_entry(G);
-  if (threadIdx.x == 0) s_count = 0u;
   __syncthreads();
   if (wave == 0) {
     WaveList B;
@@ -1733,7 +1779,8 @@ __global__ __launch_bounds__(kCandWaves * kWave) void gqa_cands_kernel(
   __syncthreads();
   const float tau = s_tau;
   const float2* lq = lbub + static_cast<size_t>(qb) * cap;
-  for (uint32_t base = wave * kWave; base < n_slots; base += kCandWaves * kWave) {
+  const uint32_t gstride = gridDim.y * kCandWaves * kWave;
+  for (uint32_t base = (blockIdx.y * kCandWaves + wave) * kWave; base < n_slots; base += gstride) {
     const uint32_t slot = base + lane;
     bool c = false;
     uint32_t len = 0u;
@@ -1756,7 +1803,7 @@ __global__ __launch_bounds__(kCandWaves * kWave) void gqa_cands_kernel(
     pre_items -= n_items;
     uint32_t cbase = 0u, ibase = 0u;
     if (lane == 0) {
-      cbase = atomicAdd(&s_count, static_cast<uint32_t>(__popcll(cm)));
+      cbase = atomicAdd(cand_count + qb, static_cast<uint32_t>(__popcll(cm)));
       if (tot_items) ibase = atomicAdd(n_citems, tot_items);
     }
     cbase = __shfl(cbase, 0);
@@ -1779,8 +1826,6 @@ __global__ __launch_bounds__(kCandWaves * kWave) void gqa_cands_kernel(
       }
     }
   }
-  __syncthreads();
-  if (threadIdx.x == 0) cand_count[qb] = s_count;
 }
 
 // ----------------------------------------------------------- bank upkeep

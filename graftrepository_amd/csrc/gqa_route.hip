@@ -1095,13 +1095,13 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
       static_cast<uint32_t>(a->high_water), a->d_len,                                            \
       a->route_flags ? a->route_flags : a->d_flags, a->d_ids, a->d_kmax,                         \
       a->d_colinfo, a->d_qbad, fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub,           \
-      a->d_blists, a->d_ccount + p.qb_max)
+      a->d_blists, a->d_ccount, p.qb_max + 1)
   if (wide) {
     grm::gqa::gqa_bounds_wide_kernel<<<dim3(qb, bblocks), grm::gqa::kFinWaves * grm::kWave, 0,
                                        a->stream>>>(
         a->d_hmaxf, colstride, a->cap_nodes, H, p.Qt, p.R, colstride, kv, n_slots, a->d_len,
         a->route_flags ? a->route_flags : a->d_flags, a->d_ids, a->d_kmax, a->d_colinfo, a->d_qbad,
-        fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub, a->d_blists, a->d_ccount + p.qb_max);
+        fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub, a->d_blists, a->d_ccount, p.qb_max + 1);
   } else if (staged) {
     GRM_BOUNDS(true);
   } else {
@@ -1109,8 +1109,12 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   }
 #undef GRM_BOUNDS
   GRM_HIP_CHECK(hipGetLastError());
-  // 4. candidates and their exact work items
-  grm::gqa::gqa_cands_kernel<<<qb, grm::gqa::kCandWaves * grm::kWave, 0, a->stream>>>(
+  // 4. candidates and their exact work items, each query's slots split
+  // over blocks of about four rounds of the block's wavefronts
+  const uint32_t cblocks = std::max<uint32_t>(
+      1, std::min<uint32_t>(64, (n_slots + 4 * grm::gqa::kCandWaves * grm::kWave - 1) /
+                                    (4 * grm::gqa::kCandWaves * grm::kWave)));
+  grm::gqa::gqa_cands_kernel<<<dim3(qb, cblocks), grm::gqa::kCandWaves * grm::kWave, 0, a->stream>>>(
       a->d_blists, bblocks, topk, a->d_lbub, a->cap_nodes, static_cast<uint32_t>(a->high_water),
       a->d_tok_off, a->d_len, kv, a->chunk, a->d_cslots, a->d_ccount, a->d_citems,
       a->d_ccount + p.qb_max);
