@@ -474,6 +474,13 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
         devs.append(r.device_ms)
         timed_walls.append(r.wall_ms)
     dq.close()
+    # the same query handed over from host memory (one H2D copy per call,
+    # as the drop-in route takes it)
+    host_walls = []
+    for _ in range(min(steps, 300)):
+        r = bank.route(q, cfg["topk"], query_dtype="bf16", timed=False)
+        assert np.array_equal(r.ids, ids0) and np.array_equal(r.scores, sc0)
+        host_walls.append(r.wall_ms)
     # the same bank with 4 query tokens per head (16 query columns per kv
     # head instead of 4)
     q4 = wl.gqa_queries(1, H, 4, hd, cfg["seed"] + 1)
@@ -526,7 +533,7 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
         f"  {qt4['achieved_gbs']:.0f} GB/s")
     log(f"[gqa] sumL {sum_l}  p50 {pct(walls, 50):.4f} ms  p99 {pct(walls, 99):.4f} ms"
         f"  device {mean_dev:.4f} ms  {achieved:.0f} GB/s"
-        f"  (timed calls p50 {pct(timed_walls, 50):.4f} ms)")
+        f"  (timed calls p50 {pct(timed_walls, 50):.4f} ms, host query p50 {pct(host_walls, 50):.4f} ms)")
     cpu = None
     if cpu_seconds > 0:
         cpu = cpu_baseline_gqa(keys, offs, kv, hd, q, cfg["topk"], ids0[0], sc0[0],
@@ -534,7 +541,7 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
     return dict(keys=keys, offs=offs, q=q, ids=r.ids[0].copy(), cpu=cpu,
                 scores=r.scores[0].copy(), walls=walls, devs=devs,
                 bytes=bytes_per_call, achieved=achieved, mean_dev=mean_dev,
-                timed_p50=pct(timed_walls, 50), qt4=qt4,
+                timed_p50=pct(timed_walls, 50), host_p50=pct(host_walls, 50), qt4=qt4,
                 sum_l=sum_l, cfg=cfg, kv=kv, H=H, qt64=qt64)
 
 
@@ -1114,6 +1121,7 @@ def main() -> int:
             "p99_ms": round(pct(g["walls"], 99), 5),
             "device_ms_mean": round(g["mean_dev"], 5),
             "timed_calls_p50_ms": round(g["timed_p50"], 5),
+            "host_query_p50_ms": round(g["host_p50"], 5),
             "query_tokens_4": g["qt4"],
             "query_tokens_64": g["qt64"],
             "cpu_baseline": g["cpu"],

@@ -750,7 +750,7 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
 // chunks of 4 pieces), and eps_rel / eps_abs carry the copy's rounding
 // into the bound (stage_columns).
 template <int KDT, int KS, int NT, bool XF32 = false>
-__global__ __launch_bounds__(kUnitWaves * kWave) void gqa_sr_kernel(
+__global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && KS <= 4 && (KDT != kI8 || KS == 4 || NT == 1)) ? 2 : 1) void gqa_sr_kernel(
     const unsigned char* __restrict__ keys, const unsigned char* __restrict__ xkeys,
     const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
     const Item* __restrict__ items, uint32_t n_items, int kv, int R, int Qt, int Rc, int Qc,

@@ -152,6 +152,10 @@ struct GqaDeviceArena {
   std::vector<Cand> merged;
   void* d_queries = nullptr;
   size_t d_queries_bytes = 0;
+  // pinned staging of host queries (the route's own; mutations stage
+  // through h_stage on the side stream)
+  unsigned char* h_qstage = nullptr;
+  size_t h_qstage_bytes = 0;
   void* h_stage = nullptr;
   size_t h_stage_bytes = 0;
   void* d_stage = nullptr;
@@ -235,6 +239,7 @@ void destroy_arena(GqaDeviceArena* a) {
   grm::release_mapped(&a->blocks_out);
   grm::release_mapped_bytes(&a->done_flags);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
+  if (a->h_qstage) (void)hipHostFree(a->h_qstage);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
   if (a->ev_mut) (void)hipEventDestroy(a->ev_mut);
@@ -1083,13 +1088,17 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   const bool staged = ci_bytes <= kBoundsStageBytes;
   const bool wide = H * p.Qt >= kWideCells;
   const uint32_t n_slots = static_cast<uint32_t>(a->high_water);
-  // the bounds blocks, and so the candidates kernel's lists per query
+  // the bounds blocks, and so the candidates kernel's lists per query: a
+  // wavefront per slot (wide), else a lane per slot and about two rounds
+  // of slots per wavefront (a block's fixed cost -- column parameters,
+  // list merge -- would dominate one round)
+  constexpr uint32_t kBoundsSlots = 2 * grm::gqa::kFinWaves * grm::kWave;
   const uint32_t bblocks =
       wide ? std::max<uint32_t>(1, std::min<uint32_t>(kWideBlocks, (n_slots + grm::gqa::kFinWaves - 1) /
                                                                         grm::gqa::kFinWaves))
-           : fin_blocks;
+           : std::max<uint32_t>(1, std::min<uint32_t>(fin_blocks, (n_slots + kBoundsSlots - 1) / kBoundsSlots));
 #define GRM_BOUNDS(ST)                                                                           \
-  grm::gqa::gqa_bounds_kernel<ST><<<dim3(qb, fin_blocks), grm::gqa::kFinWaves * grm::kWave,      \
+  grm::gqa::gqa_bounds_kernel<ST><<<dim3(qb, bblocks), grm::gqa::kFinWaves * grm::kWave,         \
                                     ST ? ci_bytes : 0, a->stream>>>(                             \
       a->d_hmaxf, colstride, a->cap_nodes, H, p.Qt, p.R, colstride, kv,                          \
       static_cast<uint32_t>(a->high_water), a->d_len,                                            \
@@ -1178,9 +1187,16 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   const size_t qstride = qvals * (q_dtype == kF32 ? 4 : 2);
   const unsigned char* qbase = static_cast<const unsigned char*>(queries);
   if (!on_device) {
-    GRM_CHECK_RC(reserve_device(reinterpret_cast<unsigned char**>(&a->d_queries), &a->d_queries_bytes,
-                                qstride * q_count));
-    GRM_HIP_CHECK(hipMemcpyAsync(a->d_queries, queries, qstride * q_count, hipMemcpyHostToDevice, a->stream));
+    // Host queries go through a pinned buffer: a copy from pageable memory
+    // stages through the runtime's own buffers, which cost about 30 us more
+    // per call for a 64 KiB query and 12 us for 32 KiB.  The buffer is free
+    // again once the previous route returned (every route waits for its
+    // stream before returning).
+    const size_t qbytes = qstride * q_count;
+    GRM_CHECK_RC(reserve_device(reinterpret_cast<unsigned char**>(&a->d_queries), &a->d_queries_bytes, qbytes));
+    GRM_CHECK_RC(reserve_pinned(&a->h_qstage, &a->h_qstage_bytes, qbytes));
+    memcpy(a->h_qstage, queries, qbytes);
+    GRM_HIP_CHECK(hipMemcpyAsync(a->d_queries, a->h_qstage, qbytes, hipMemcpyHostToDevice, a->stream));
     qbase = static_cast<const unsigned char*>(a->d_queries);
   }
   const uint32_t n_slots = static_cast<uint32_t>(a->high_water);
