@@ -34,11 +34,19 @@
 // kept only when its last score lies above the (k+1)-th's normalised raw
 // score; otherwise every entry taking part is scored exactly.
 //
-// Limits: topk <= 16 (the device route's list length); one route key per
-// entry (multi-row MLA entries and multi-key GQA entries are refused, as
-// the reference's device sidecars decline them); MLA keys of the store's
-// dim; GQA keys of whole [kv_heads][L][head_dim] blocks.  Calls on one
-// handle are serialized by its mutex.
+// Entries with several route keys (multi-row MLA, multi-key GQA;
+// set_route_multi / set_route_list with key_count != 1) score the maximum
+// of their keys' finite law scores, NaN when none is finite
+// (cpp/grm_runtime.cpp:3518-3545 exact_mla_entry_score, :3031-3051
+// max_gqa_raw_score).  Their keys live in a second bank of the same kind
+// under internal ids; every route scores all of them exactly on the device
+// (one score_nodes call) and folds each entry's maximum in beside the main
+// bank's filtered top k, so the answer is the law's whenever the main
+// bank's is.  An entry with no key never scores.
+//
+// Limits: topk <= 16 (the device route's list length); MLA keys of the
+// store's dim; GQA keys of whole [kv_heads][L][head_dim] blocks.  Calls on
+// one handle are serialized by its mutex.
 
 #include "grm_common.hpp"
 #include "grm_hip_router.h"
@@ -99,6 +107,9 @@ struct Entry {
   std::vector<std::string> lex;
   std::string meta[4];
   uint64_t bits = 0;
+  // an entry with no key or several: its keys' ids on the multi-key bank
+  bool multi = false;
+  std::vector<uint64_t> mkeys;
 };
 
 }  // namespace
@@ -110,6 +121,12 @@ struct grm_store_handle {
   uint32_t dim = 0;      // MLA key length
   uint32_t kv = 0;       // GQA kv heads
   uint32_t hd = 0;       // GQA head dim
+  uint64_t cap_nodes = 0, cap_tokens = 0;  // the main bank's, for the multi-key bank
+  // keys of entries with several keys (created on first use)
+  MlaDeviceArena* mla_multi = nullptr;
+  GqaDeviceArena* gqa_multi = nullptr;
+  uint64_t next_mkey = 0;
+  std::unordered_set<uint64_t> multi;  // node ids of entries with multi set
   std::unordered_map<uint64_t, Entry> entries;
   std::unordered_map<std::string, std::unordered_set<uint64_t>> index;  // lexical key -> nodes
   std::mutex mu;
@@ -139,8 +156,114 @@ void unindex(grm_store_handle* h, uint64_t nid, const Entry& e) {
   }
 }
 
-// Put a route key on the bank: a new entry starts from the default
-// metadata, a replaced one keeps its own (cpp/grm_runtime.cpp:2877-2902).
+// Take an entry's key(s) off its bank and its lexical keys out of the index
+// (the entry itself stays in h->entries).
+int drop_keys(grm_store_handle* h, uint64_t nid, const Entry& e) {
+  if (e.multi) {
+    if (!e.mkeys.empty()) {
+      const int rc = h->dialect == kMla
+                         ? grm_mla_hip_evict(h->mla_multi, e.mkeys.data(), e.mkeys.size(), nullptr)
+                         : grm_gqa_hip_evict(h->gqa_multi, e.mkeys.data(), e.mkeys.size(), nullptr);
+      if (rc != 0) return rc;
+    }
+    h->multi.erase(nid);
+  } else {
+    const uint64_t id = nid;
+    const int rc = h->dialect == kMla ? grm_mla_hip_evict(h->mla, &id, 1, nullptr)
+                                      : grm_gqa_hip_evict(h->gqa, &id, 1, nullptr);
+    if (rc != 0) return rc;
+  }
+  unindex(h, nid, e);
+  return 0;
+}
+
+// GQA append with one compaction and retry when the token space is short.
+int gqa_append(GqaDeviceArena* a, const float* keys, const uint64_t* tokens, uint64_t count,
+               const uint64_t* ids) {
+  int rc = grm_gqa_hip_append(a, keys, nullptr, tokens, count, ids, nullptr);
+  if (rc == -3) {
+    // token space: reclaim evicted nodes' tokens and try once more
+    const int crc = grm_gqa_hip_compact(a);
+    if (crc != 0) return crc;
+    rc = grm_gqa_hip_append(a, keys, nullptr, tokens, count, ids, nullptr);
+  }
+  return rc;
+}
+
+// Key tokens of a GQA key of len values (whole [kv][L][hd] blocks).
+int gqa_tokens(const grm_store_handle* h, uint64_t len, uint64_t* tokens) {
+  const uint64_t row = static_cast<uint64_t>(h->kv) * h->hd;
+  if (len % row != 0) return grm::fail(-1, "GQA route key is not whole [kv_heads][L][head_dim] blocks");
+  *tokens = len / row;
+  return 0;
+}
+
+// A new entry starts from the default metadata, a replaced one keeps its
+// own (cpp/grm_runtime.cpp:2877-2902).
+Entry new_entry(const grm_store_handle* h, uint64_t nid, const char* lexical) {
+  Entry e;
+  auto found = h->entries.find(nid);
+  for (int c = 0; c < 4; ++c) e.meta[c] = found != h->entries.end() ? found->second.meta[c] : kDefaultMeta[c];
+  e.lex = split_keys(lexical);
+  e.bits = entry_bits(e);
+  return e;
+}
+
+// Put an entry with `count` route keys (keys[i], lens[i] values) on the
+// multi-key bank, replacing the node's entry if it has one.
+int put_multi(grm_store_handle* h, uint64_t nid, const std::vector<const float*>& keys,
+              const std::vector<uint64_t>& lens, const char* lexical) {
+  if (nid == kNone) return grm::fail(-1, "node id UINT64_MAX is reserved");
+  const uint64_t count = keys.size();
+  std::vector<uint64_t> tokens(count);
+  uint64_t total = 0;
+  for (uint64_t i = 0; i < count; ++i) {
+    if (lens[i] > 0 && !keys[i]) return grm::fail(-1, "null route key with nonzero length");
+    if (h->dialect == kMla) {
+      if (lens[i] != h->dim) return grm::fail(-1, "route key length does not match the store dim");
+    } else {
+      GRM_CHECK_RC(gqa_tokens(h, lens[i], &tokens[i]));
+    }
+    total += lens[i];
+  }
+  if (count > 0 && !h->mla_multi && !h->gqa_multi) {
+    if (h->dialect == kMla) {
+      GRM_CHECK_RC(grm_mla_hip_bank_create(nullptr, GRM_DTYPE_F32, 0, static_cast<int>(h->dim),
+                                           nullptr, std::max<uint64_t>(h->cap_nodes, 64), &h->mla_multi));
+    } else {
+      const uint64_t zero = 0;
+      GRM_CHECK_RC(grm_gqa_hip_bank_create(nullptr, GRM_DTYPE_F32, nullptr, GRM_DTYPE_F32, 0, &zero, 0,
+                                           static_cast<int>(h->kv), static_cast<int>(h->hd), nullptr,
+                                           std::max<uint64_t>(h->cap_nodes, 1),
+                                           std::max<uint64_t>(h->cap_tokens, 8), &h->gqa_multi));
+    }
+  }
+  Entry e = new_entry(h, nid, lexical);
+  auto found = h->entries.find(nid);
+  if (found != h->entries.end()) {
+    GRM_CHECK_RC(drop_keys(h, nid, found->second));
+    h->entries.erase(found);  // its old keys are gone
+  }
+  e.multi = true;
+  if (count > 0) {
+    std::vector<float> flat;
+    flat.reserve(total);
+    for (uint64_t i = 0; i < count; ++i) flat.insert(flat.end(), keys[i], keys[i] + lens[i]);
+    e.mkeys.resize(count);
+    for (uint64_t i = 0; i < count; ++i) e.mkeys[i] = h->next_mkey++;
+    const int rc = h->dialect == kMla
+                       ? grm_mla_hip_append(h->mla_multi, flat.data(), GRM_DTYPE_F32, count,
+                                            e.mkeys.data(), nullptr)
+                       : gqa_append(h->gqa_multi, flat.data(), tokens.data(), count, e.mkeys.data());
+    if (rc != 0) return rc;
+  }
+  for (const auto& s : e.lex) h->index[s].insert(nid);
+  h->multi.insert(nid);
+  h->entries[nid] = std::move(e);
+  return 0;
+}
+
+// Put a single route key on the main bank (see new_entry for metadata).
 int put_entry(grm_store_handle* h, uint64_t nid, const float* key, uint64_t len,
               const char* lexical) {
   if (nid == kNone) return grm::fail(-1, "node id UINT64_MAX is reserved");
@@ -149,42 +272,17 @@ int put_entry(grm_store_handle* h, uint64_t nid, const float* key, uint64_t len,
   if (h->dialect == kMla) {
     if (len != h->dim) return grm::fail(-1, "route key length does not match the store dim");
   } else {
-    const uint64_t row = static_cast<uint64_t>(h->kv) * h->hd;
-    if (len % row != 0) return grm::fail(-1, "GQA route key is not whole [kv_heads][L][head_dim] blocks");
-    tokens = len / row;
+    GRM_CHECK_RC(gqa_tokens(h, len, &tokens));
   }
+  Entry e = new_entry(h, nid, lexical);
   auto found = h->entries.find(nid);
   if (found != h->entries.end()) {
-    const uint64_t id = nid;
-    const int rc = h->dialect == kMla ? grm_mla_hip_evict(h->mla, &id, 1, nullptr)
-                                      : grm_gqa_hip_evict(h->gqa, &id, 1, nullptr);
-    if (rc != 0) return rc;
-    unindex(h, nid, found->second);
+    GRM_CHECK_RC(drop_keys(h, nid, found->second));
+    h->entries.erase(found);  // its old key is gone
   }
-  int rc;
-  if (h->dialect == kMla) {
-    rc = grm_mla_hip_append(h->mla, key, GRM_DTYPE_F32, 1, &nid, nullptr);
-  } else {
-    rc = grm_gqa_hip_append(h->gqa, key, nullptr, &tokens, 1, &nid, nullptr);
-    if (rc == -3) {
-      // token space: reclaim evicted nodes' tokens and try once more
-      const int crc = grm_gqa_hip_compact(h->gqa);
-      if (crc != 0) return crc;
-      rc = grm_gqa_hip_append(h->gqa, key, nullptr, &tokens, 1, &nid, nullptr);
-    }
-  }
-  if (rc != 0) {
-    if (found != h->entries.end()) h->entries.erase(found);  // its old key is gone
-    return rc;
-  }
-  Entry e;
-  if (found != h->entries.end()) {
-    for (int c = 0; c < 4; ++c) e.meta[c] = found->second.meta[c];
-  } else {
-    for (int c = 0; c < 4; ++c) e.meta[c] = kDefaultMeta[c];
-  }
-  e.lex = split_keys(lexical);
-  e.bits = entry_bits(e);
+  const int rc = h->dialect == kMla ? grm_mla_hip_append(h->mla, key, GRM_DTYPE_F32, 1, &nid, nullptr)
+                                    : gqa_append(h->gqa, key, &tokens, 1, &nid);
+  if (rc != 0) return rc;
   for (const auto& s : e.lex) h->index[s].insert(nid);
   h->entries[nid] = e;
   return set_bits(h, {nid}, {e.bits});
@@ -231,17 +329,41 @@ bool passes(const Entry& e, const Filters& f) {
   return true;
 }
 
-// Score listed nodes exactly on the device (NaN where not finite).
+// Score listed nodes exactly on the device (NaN where not finite), on the
+// main bank or (multi) the multi-key bank.
 int score_nodes(grm_store_handle* h, const float* query, uint64_t heads, uint64_t tokens,
-                const std::vector<uint64_t>& ids, std::vector<float>* out) {
+                const std::vector<uint64_t>& ids, std::vector<float>* out, bool multi = false) {
   out->assign(ids.size(), std::nanf(""));
   if (ids.empty()) return 0;
   return h->dialect == kMla
-             ? grm_mla_hip_score_nodes(h->mla, query, GRM_DTYPE_F32, ids.data(), ids.size(),
-                                       out->data())
-             : grm_gqa_hip_score_nodes(h->gqa, query, GRM_DTYPE_F32, static_cast<int>(heads),
-                                       static_cast<int>(tokens), ids.data(), ids.size(),
-                                       out->data());
+             ? grm_mla_hip_score_nodes(multi ? h->mla_multi : h->mla, query, GRM_DTYPE_F32,
+                                       ids.data(), ids.size(), out->data())
+             : grm_gqa_hip_score_nodes(multi ? h->gqa_multi : h->gqa, query, GRM_DTYPE_F32,
+                                       static_cast<int>(heads), static_cast<int>(tokens), ids.data(),
+                                       ids.size(), out->data());
+}
+
+// Law scores of the multi-key entries taking part: the maximum of each
+// entry's finite key scores; entries with none are left out.
+int score_multi(grm_store_handle* h, const float* query, uint64_t heads, uint64_t tokens,
+                const Filters& f, std::unordered_map<uint64_t, float>* out) {
+  std::vector<uint64_t> keys, owner;
+  for (uint64_t nid : h->multi) {
+    const Entry& e = h->entries.at(nid);
+    if (!passes(e, f)) continue;
+    for (uint64_t k : e.mkeys) {
+      keys.push_back(k);
+      owner.push_back(nid);
+    }
+  }
+  std::vector<float> sc;
+  GRM_CHECK_RC(score_nodes(h, query, heads, tokens, keys, &sc, true));
+  for (size_t i = 0; i < keys.size(); ++i) {
+    if (!std::isfinite(sc[i])) continue;
+    auto ins = out->emplace(owner[i], sc[i]);
+    if (!ins.second && sc[i] > ins.first->second) ins.first->second = sc[i];
+  }
+  return 0;
 }
 
 struct Ranked {
@@ -273,6 +395,7 @@ int route(grm_store_handle* h, const float* query, uint64_t heads, uint64_t toke
     const auto& vals = f.values[c];
     const uint64_t bit = 1ull << (16 * c + kMatchBit);
     for (const auto& kvp : h->entries) {
+      if (kvp.second.multi) continue;  // not on the main bank
       if (std::find(vals.begin(), vals.end(), kvp.second.meta[c]) == vals.end()) continue;
       auto ins = temp_at.emplace(kvp.first, temp_ids.size());
       if (ins.second) {
@@ -285,16 +408,20 @@ int route(grm_store_handle* h, const float* query, uint64_t heads, uint64_t toke
     }
   }
   GRM_CHECK_RC(set_bits(h, temp_ids, temp_bits));
-  const uint64_t live = h->entries.size();
+  // entries on the main bank (one key each)
+  const uint64_t live = h->entries.size() - h->multi.size();
   const uint64_t want = gqa && !lex.empty() ? topk + 1 : topk;
   const int kf = static_cast<int>(std::min<uint64_t>({want, live, static_cast<uint64_t>(grm::kMaxTopK)}));
   std::vector<uint64_t> ids(kf, kNone);
   std::vector<float> sc(kf, std::nanf(""));
-  int rc = gqa ? grm_gqa_hip_route_filtered(h->gqa, query, GRM_DTYPE_F32, 0, static_cast<int>(heads),
-                                            static_cast<int>(tokens), kf, f.mask, f.cats, ids.data(),
-                                            sc.data(), nullptr)
-               : grm_mla_hip_route_filtered(h->mla, query, GRM_DTYPE_F32, 0, kf, f.mask, f.cats,
-                                            ids.data(), sc.data(), nullptr);
+  int rc = 0;
+  if (kf > 0) {
+    rc = gqa ? grm_gqa_hip_route_filtered(h->gqa, query, GRM_DTYPE_F32, 0, static_cast<int>(heads),
+                                          static_cast<int>(tokens), kf, f.mask, f.cats, ids.data(),
+                                          sc.data(), nullptr)
+             : grm_mla_hip_route_filtered(h->mla, query, GRM_DTYPE_F32, 0, kf, f.mask, f.cats,
+                                          ids.data(), sc.data(), nullptr);
+  }
   const int rc2 = set_bits(h, temp_ids, back_bits);
   if (rc != 0) return rc;
   if (rc2 != 0) return rc2;
@@ -306,12 +433,24 @@ int route(grm_store_handle* h, const float* query, uint64_t heads, uint64_t toke
       fetched.push_back({sc[j], ids[j]});
     }
   }
+  // every multi-key entry taking part, scored exactly
+  std::unordered_map<uint64_t, float> mbase;
+  GRM_CHECK_RC(score_multi(h, query, heads, tokens, f, &mbase));
+  float mmax = 0.0f;  // largest |raw| among them (GQA normalisation)
+  for (const auto& kvp : mbase) {
+    base.emplace(kvp.first, kvp.second);
+    mmax = std::max(mmax, std::fabs(kvp.second));
+  }
   if (lex.empty()) {
-    // no bonus: the bank's filtered order is the law's
-    const uint64_t n = std::min<uint64_t>({static_cast<uint64_t>(fetched.size()), topk, out_cap});
+    // no bonus: the main bank's filtered order is the law's; the
+    // multi-key entries join it by score
+    std::vector<Ranked> all = fetched;
+    for (const auto& kvp : mbase) all.push_back({kvp.second, kvp.first});
+    std::sort(all.begin(), all.end(), ranked_better);
+    const uint64_t n = std::min<uint64_t>({static_cast<uint64_t>(all.size()), topk, out_cap});
     for (uint64_t i = 0; i < n; ++i) {
-      out_ids[i] = fetched[i].id;
-      if (out_scores) out_scores[i] = fetched[i].score;
+      out_ids[i] = all[i].id;
+      if (out_scores) out_scores[i] = all[i].score;
     }
     *out_count = n;
     return 0;
@@ -326,7 +465,7 @@ int route(grm_store_handle* h, const float* query, uint64_t heads, uint64_t toke
   std::vector<uint64_t> need;
   for (const auto& kvp : hits) {
     const Entry& e = h->entries.at(kvp.first);
-    if (passes(e, f) && !base.count(kvp.first)) need.push_back(kvp.first);
+    if (!e.multi && passes(e, f) && !base.count(kvp.first)) need.push_back(kvp.first);
   }
   std::vector<float> extra;
   GRM_CHECK_RC(score_nodes(h, query, heads, tokens, need, &extra));
@@ -355,7 +494,7 @@ int route(grm_store_handle* h, const float* query, uint64_t heads, uint64_t toke
       std::sort(r.begin(), r.end(), ranked_better);
       return r;
     };
-    const float max_abs = fetched.empty() ? 0.0f : std::fabs(fetched.front().score);
+    const float max_abs = std::max(fetched.empty() ? 0.0f : std::fabs(fetched.front().score), mmax);
     ranked = rank_gqa(base, max_abs);
     const bool all_fetched = static_cast<int>(fetched.size()) < kf || fetched.size() >= live;
     if (!all_fetched) {
@@ -366,12 +505,12 @@ int route(grm_store_handle* h, const float* query, uint64_t heads, uint64_t toke
         // every entry taking part, scored exactly
         std::vector<uint64_t> all;
         for (const auto& kvp : h->entries) {
-          if (passes(kvp.second, f)) all.push_back(kvp.first);
+          if (!kvp.second.multi && passes(kvp.second, f)) all.push_back(kvp.first);
         }
         std::vector<float> raw;
         GRM_CHECK_RC(score_nodes(h, query, heads, tokens, all, &raw));
-        std::unordered_map<uint64_t, float> every;
-        float mx = 0.0f;
+        std::unordered_map<uint64_t, float> every(mbase);
+        float mx = mmax;
         for (size_t i = 0; i < all.size(); ++i) {
           if (!std::isfinite(raw[i])) continue;
           every.emplace(all[i], raw[i]);
@@ -412,6 +551,7 @@ extern "C" int grm_hip_store_create_mla(int dim, uint64_t capacity, int row_dtyp
   auto* h = new grm_store_handle();
   h->dialect = kMla;
   h->dim = static_cast<uint32_t>(dim);
+  h->cap_nodes = capacity;
   const int rc = grm_mla_hip_bank_create(nullptr, row_dtype, 0, dim, nullptr,
                                          std::max<uint64_t>(capacity, 64), &h->mla);
   if (rc != 0) {
@@ -429,6 +569,8 @@ extern "C" int grm_hip_store_create_gqa(int kv_heads, int head_dim, uint64_t cap
   h->dialect = kGqa;
   h->kv = static_cast<uint32_t>(kv_heads);
   h->hd = static_cast<uint32_t>(head_dim);
+  h->cap_nodes = capacity_nodes;
+  h->cap_tokens = capacity_tokens;
   const uint64_t zero = 0;
   const int rc = grm_gqa_hip_bank_create(nullptr, GRM_DTYPE_F32, nullptr, GRM_DTYPE_F32, 0, &zero, 0,
                                          kv_heads, head_dim, nullptr,
@@ -446,6 +588,8 @@ extern "C" void grm_hip_store_destroy(grm_store_handle* h) {
   if (!h) return;
   if (h->mla) grm_mla_cuda_arena_destroy(h->mla);
   if (h->gqa) grm_gqa_cuda_arena_destroy(h->gqa);
+  if (h->mla_multi) grm_mla_cuda_arena_destroy(h->mla_multi);
+  if (h->gqa_multi) grm_gqa_cuda_arena_destroy(h->gqa_multi);
   delete h;
 }
 
@@ -464,20 +608,44 @@ extern "C" int grm_store_set_route_multi(grm_store_handle* h, uint64_t node_id,
                                          const float* route_keys, uint64_t key_count,
                                          uint64_t route_len, const char* lexical_keys) {
   if (!h) return grm::fail(-1, "invalid set_route_multi arguments");
-  if (key_count != 1) return grm::fail(-1, "multi-row route entries are not served on the device");
-  return grm_store_set_route(h, node_id, route_keys, route_len, lexical_keys);
+  if (!route_keys && key_count > 0 && route_len > 0) return grm::fail(-1, "null route keys with nonzero shape");
+  if (key_count == 1) return grm_store_set_route(h, node_id, route_keys, route_len, lexical_keys);
+  std::vector<const float*> keys(key_count);
+  std::vector<uint64_t> lens(key_count, route_len);
+  for (uint64_t k = 0; k < key_count; ++k) keys[k] = route_keys ? route_keys + k * route_len : nullptr;
+  std::lock_guard<std::mutex> lock(h->mu);
+  const int rc = put_multi(h, node_id, keys, lens, lexical_keys);
+  if (rc == 0) grm::clear_error();
+  return rc;
 }
 
 extern "C" int grm_store_set_route_list(grm_store_handle* h, uint64_t node_id,
                                         const float* route_values, uint64_t value_count,
                                         const uint64_t* route_offsets, uint64_t key_count,
                                         const char* lexical_keys) {
-  if (!h || !route_offsets) return grm::fail(-1, "invalid set_route_list arguments");
-  if (key_count != 1) return grm::fail(-1, "multi-key route entries are not served on the device");
-  if (route_offsets[0] != 0 || route_offsets[1] != value_count) {
-    return grm::fail(-1, "route offsets must run from 0 to value_count");
+  // argument checks in the reference's order (cpp/grm_runtime.cpp:6691-6731)
+  if (!h) return grm::fail(-1, "invalid set_route_list arguments");
+  if (!route_values && value_count > 0) return grm::fail(-1, "null route values with nonzero length");
+  if (!route_offsets && key_count > 0) return grm::fail(-1, "null route offsets with nonzero key count");
+  if (key_count == 0 && value_count != 0) return grm::fail(-1, "route values require route offsets");
+  if (key_count > 0 && route_offsets[0] != 0) return grm::fail(-1, "route offsets must start at zero");
+  if (key_count > 0 && route_offsets[key_count] != value_count) {
+    return grm::fail(-1, "route offsets must end at value_count");
   }
-  return grm_store_set_route(h, node_id, route_values, value_count, lexical_keys);
+  std::vector<const float*> keys(key_count);
+  std::vector<uint64_t> lens(key_count);
+  for (uint64_t k = 0; k < key_count; ++k) {
+    if (route_offsets[k + 1] < route_offsets[k] || route_offsets[k + 1] > value_count) {
+      return grm::fail(-1, "invalid route key offsets");
+    }
+    keys[k] = route_values ? route_values + route_offsets[k] : nullptr;
+    lens[k] = route_offsets[k + 1] - route_offsets[k];
+  }
+  if (key_count == 1) return grm_store_set_route(h, node_id, keys[0], lens[0], lexical_keys);
+  std::lock_guard<std::mutex> lock(h->mu);
+  const int rc = put_multi(h, node_id, keys, lens, lexical_keys);
+  if (rc == 0) grm::clear_error();
+  return rc;
 }
 
 extern "C" int grm_store_clear_route(grm_store_handle* h, uint64_t node_id) {
@@ -485,10 +653,7 @@ extern "C" int grm_store_clear_route(grm_store_handle* h, uint64_t node_id) {
   std::lock_guard<std::mutex> lock(h->mu);
   auto it = h->entries.find(node_id);
   if (it == h->entries.end()) return 0;  // no route entry: nothing to clear
-  const int rc = h->dialect == kMla ? grm_mla_hip_evict(h->mla, &node_id, 1, nullptr)
-                                    : grm_gqa_hip_evict(h->gqa, &node_id, 1, nullptr);
-  if (rc != 0) return rc;
-  unindex(h, node_id, it->second);
+  GRM_CHECK_RC(drop_keys(h, node_id, it->second));
   h->entries.erase(it);
   grm::clear_error();
   return 0;
@@ -506,7 +671,8 @@ extern "C" int grm_store_set_route_metadata(grm_store_handle* h, uint64_t node_i
     if (in[c] && in[c][0]) it->second.meta[c] = in[c];
   }
   it->second.bits = entry_bits(it->second);
-  const int rc = set_bits(h, {node_id}, {it->second.bits});
+  // a multi-key entry's filters are applied on the host
+  const int rc = it->second.multi ? 0 : set_bits(h, {node_id}, {it->second.bits});
   if (rc == 0) grm::clear_error();
   return rc;
 }

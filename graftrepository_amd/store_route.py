@@ -16,8 +16,10 @@ law), are described in ``csrc/store.hip``.  ``DeviceRouteStore`` (MLA) and
 ``DeviceGqaRouteStore`` hold a handle; ``route_scored`` also returns the
 fp32 route scores the law ranks by.
 
-Multi-row MLA entries and multi-key GQA entries are not served; the
-reference's device sidecars decline them too (core/graft_arena.py:1128-1131).
+Entries with several route keys (``set_route_multi`` / ``set_route_list``)
+score their best finite key, as the reference's store does
+(cpp/grm_runtime.cpp:3518-3545, 3031-3051); the library scores their keys
+exactly on every route.
 """
 
 from __future__ import annotations
@@ -118,6 +120,28 @@ class _Store:
         key = np.ascontiguousarray(route_key, dtype=np.float32).reshape(-1)
         self._check(self._lib.grm_store_set_route(self._h, int(node_id), _ptr(key), key.size,
                                                   _blob(lexical_keys)), "set_route")
+
+    def set_route_list(self, node_id: int, route_keys, lexical_keys=()) -> None:
+        """``grm_store_set_route_list``: the entry's keys (any number, each
+        a whole route key; MLA rows of the store's dim, GQA [kv][L][hd]
+        blocks).  It scores the best of them."""
+        self._need_open()
+        flat = [np.ascontiguousarray(k, dtype=np.float32).reshape(-1) for k in route_keys]
+        values = np.concatenate(flat) if flat else np.zeros(0, np.float32)
+        offs = np.zeros(len(flat) + 1, dtype=np.uint64)
+        offs[1:] = np.cumsum([f.size for f in flat])
+        self._check(self._lib.grm_store_set_route_list(
+            self._h, int(node_id), _ptr(values), values.size, _ptr(offs), len(flat),
+            _blob(lexical_keys)), "set_route_list")
+
+    def set_route_multi(self, node_id: int, route_keys, lexical_keys=()) -> None:
+        """``grm_store_set_route_multi``: keys of one length, [keys, len]."""
+        self._need_open()
+        k = np.ascontiguousarray(route_keys, dtype=np.float32)
+        k = k.reshape(k.shape[0], -1) if k.ndim >= 1 and k.size else k.reshape(0, 0)
+        self._check(self._lib.grm_store_set_route_multi(
+            self._h, int(node_id), _ptr(k), k.shape[0], k.shape[1] if k.ndim == 2 else 0,
+            _blob(lexical_keys)), "set_route_multi")
 
     def _set_routes(self, node_ids, keys, key_lens, lexical_keys, metadata) -> None:
         self._need_open()

@@ -367,8 +367,10 @@ int grm_gqa_hip_score_nodes(GqaDeviceArena* arena, const void* query_host, int q
  * success, nonzero with grm_store_last_error() on failure; out_count
  * receives min(results, out_cap).  Nodes need no grm_store_add_node here:
  * the CPU store keeps nodes and payloads, this store their route entries.
- * Limits: topk <= 16; one key per entry (set_route_multi / set_route_list
- * take key_count 1); MLA keys of the store's dim, GQA keys of whole
+ * An entry with several keys (set_route_multi / set_route_list) scores the
+ * maximum of its keys' finite law scores (cpp/grm_runtime.cpp:3518-3545,
+ * 3031-3051); its keys are scored exactly on every route.
+ * Limits: topk <= 16; MLA keys of the store's dim, GQA keys of whole
  * [kv_heads][L][head_dim] blocks; calls on one handle are serialized. */
 typedef struct grm_store_handle grm_store_handle;
 
@@ -387,11 +389,11 @@ void grm_hip_store_destroy(grm_store_handle* handle);
 /* cpp/grm_runtime_c.h:381-385 */
 int grm_store_set_route(grm_store_handle* handle, uint64_t node_id, const float* route_key,
                         uint64_t route_len, const char* lexical_keys);
-/* cpp/grm_runtime_c.h:386-391 (key_count 1 only) */
+/* cpp/grm_runtime_c.h:386-391 */
 int grm_store_set_route_multi(grm_store_handle* handle, uint64_t node_id,
                               const float* route_keys, uint64_t key_count, uint64_t route_len,
                               const char* lexical_keys);
-/* cpp/grm_runtime_c.h:392-399 (key_count 1 only) */
+/* cpp/grm_runtime_c.h:392-399 */
 int grm_store_set_route_list(grm_store_handle* handle, uint64_t node_id,
                              const float* route_values, uint64_t value_count,
                              const uint64_t* route_offsets, uint64_t key_count,

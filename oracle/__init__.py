@@ -50,7 +50,10 @@ PINNING = {
                  "nodes are not modelled)",
     "store_route_gqa": "the reference store's grm_store_route_gqa (oracle/_ref, fp64 "
                        "law path) on random stores with lexical keys, metadata and "
-                       "filters (tests/test_store_route.py)",
+                       "filters, single- and multi-key entries (tests/test_store_route.py)",
+    "store_route": "the reference store's grm_store_route_filtered (oracle/_ref) on "
+                   "random stores with lexical keys, metadata, filters, single- and "
+                   "multi-row entries (tests/test_store_route.py)",
     "f16 conversion": "exhaustive agreement with numpy astype(float16)",
     "bf16 rounding": "agreement with torch.bfloat16 conversion",
     "int8 quantise/dequant": "round-trip invariants of "
@@ -241,10 +244,24 @@ _FILTER_KNOWN = (
 )
 
 
+def _entry_max(key_scores, owners, n_entries):
+    """Entry scores of multi-key entries: the largest finite score among an
+    entry's keys, NaN when it has none (exact_mla_entry_score,
+    cpp/grm_runtime.cpp:3518-3545; max_gqa_raw_score, :3031-3051).
+    owners[j] is the entry of key j."""
+    out = np.full(n_entries, np.nan, dtype=np.float32)
+    for j, e in enumerate(owners):
+        v = key_scores[j]
+        if np.isfinite(v) and (not np.isfinite(out[e]) or v > out[e]):
+            out[e] = v
+    return out
+
+
 def store_route(rows: np.ndarray, node_ids, lexical: list, meta: list, query: np.ndarray,
-                query_lexical=(), filters=((), (), (), ()), topk: int = 3):
+                query_lexical=(), filters=((), (), (), ()), topk: int = 3, owners=None):
     """The store's MLA route law, route_mla_arena (cpp/grm_runtime.cpp:
-    4299-4361), single-row entries.
+    4299-4361).  One row per entry, or with ``owners`` (entry index of each
+    row) entries of any number of rows, scored as their best row.
 
     * meta[i] holds the values passed to set_route_metadata after the
       route was set (:2922-2946): an empty value keeps the entry's default,
@@ -260,8 +277,13 @@ def store_route(rows: np.ndarray, node_ids, lexical: list, meta: list, query: np
       asc).
 
     Returns (node ids, route scores fp32) of the best topk."""
-    base = mla_scores(rows, np.asarray(query, np.float32)[None])[0]
     ids = np.asarray(node_ids, dtype=np.uint64)
+    if len(rows):
+        base = mla_scores(rows, np.asarray(query, np.float32)[None])[0]
+    else:
+        base = np.zeros(0, np.float32)
+    if owners is not None:
+        base = _entry_max(base, owners, ids.size)
     qlex = [s for s in query_lexical if s]
     out = []
     for i in range(base.size):
@@ -305,10 +327,12 @@ def _route_allowed(meta_i, filters) -> bool:
 
 def store_route_gqa(keys, tok_offsets, kv_heads: int, head_dim: int, node_ids, lexical: list,
                     meta: list, query, query_lexical=(), filters=((), (), (), ()),
-                    topk: int = 3):
+                    topk: int = 3, owners=None):
     """The store's GQA route law, route_gqa_raw (cpp/grm_runtime.cpp:
-    4498-4881), single-key entries over fp32 keys in CSR layout (node i's
-    [kv][L_i][hd] block at tok_offsets[i] * kv * hd).
+    4498-4881), over fp32 keys in CSR layout (key j's [kv][L_j][hd] block at
+    tok_offsets[j] * kv * hd): one key per entry, or with ``owners`` (entry
+    index of each key) entries of any number of keys, scored as their best
+    key.
 
     * raw = the fp64 GQA law (gqa_raw_score, :2980-3029) as float; entries
       that fail the route filters or whose raw score is not finite drop out;
@@ -319,8 +343,13 @@ def store_route_gqa(keys, tok_offsets, kv_heads: int, head_dim: int, node_ids, l
 
     Returns (node ids, route scores fp32) of the best topk."""
     q = np.ascontiguousarray(query, dtype=np.float32)
-    raw = gqa_scores(keys, F32, tok_offsets, kv_heads, head_dim, q[None])[0]
     ids = np.asarray(node_ids, dtype=np.uint64)
+    if len(tok_offsets) > 1:
+        raw = gqa_scores(keys, F32, tok_offsets, kv_heads, head_dim, q[None])[0]
+    else:
+        raw = np.zeros(0, np.float32)
+    if owners is not None:
+        raw = _entry_max(raw, owners, ids.size)
     qlex = [s for s in query_lexical if s]
     have = [i for i in range(raw.size)
             if _route_allowed(meta[i], filters) and np.isfinite(raw[i])]

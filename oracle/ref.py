@@ -107,7 +107,7 @@ class _Store:
         self._check(lib().grm_store_set_route(self.h, node_id, k.ctypes.data,
                                               k.size, b""))
 
-    def set_route_list(self, node_id: int, keys: list[np.ndarray]):
+    def set_route_list(self, node_id: int, keys: list[np.ndarray], lexical: bytes = b""):
         flat = [np.ascontiguousarray(k, dtype=np.float32).reshape(-1)
                 for k in keys]
         values = (np.concatenate(flat) if flat
@@ -116,31 +116,46 @@ class _Store:
         offs[1:] = np.cumsum([f.size for f in flat])
         self._check(lib().grm_store_set_route_list(
             self.h, node_id, values.ctypes.data, values.size,
-            offs.ctypes.data, len(flat), b""))
+            offs.ctypes.data, len(flat), lexical))
+
+
+def _keys_of(entry, row_len: int | None = None) -> list:
+    """An entry's route keys: one array, or a list / 2-D stack of them."""
+    if isinstance(entry, (list, tuple)):
+        return [np.asarray(k, dtype=np.float32) for k in entry]
+    a = np.asarray(entry, dtype=np.float32)
+    if row_len is not None and a.ndim == 2:
+        return [a[i] for i in range(a.shape[0])]
+    return [a]
 
 
 def _blob(items) -> bytes:
     return "\n".join(items).encode("utf-8")
 
 
-def store_route(rows: np.ndarray, lexical: list, meta: list, query: np.ndarray,
+def store_route(rows, lexical: list, meta: list, query: np.ndarray,
                 query_lexical=(), filters=((), (), (), ()), topk: int = 3) -> list[int]:
     """Route order from the reference ``grm_store_route_filtered``
     (cpp/grm_runtime.cpp:6840-6897 -> route_mla_arena): node i has route
-    key rows[i], lexical keys lexical[i] and route metadata meta[i] =
-    (kind, scope, durability, mutability).  filters = (kinds, scopes,
-    durabilities, mutabilities), each a list of values."""
-    r = np.ascontiguousarray(rows, dtype=np.float32)
+    key rows[i] (one row; a 2-D stack or a list of rows makes a multi-row
+    entry, set through grm_store_set_route_list), lexical keys lexical[i]
+    and route metadata meta[i] = (kind, scope, durability, mutability).
+    filters = (kinds, scopes, durabilities, mutabilities), each a list of
+    values."""
     q = np.ascontiguousarray(query, dtype=np.float32).reshape(-1)
-    d = r.shape[1]
+    d = q.size
     h = lib().grm_store_create_mla(b"MiniCPM3_TC", 62, 2560, d, 0, d, 0)
     with _Store(h) as st:
-        for i in range(r.shape[0]):
+        for i in range(len(rows)):
             nid = st.add_node()
             assert nid == i
-            k = np.ascontiguousarray(r[i])
-            st._check(lib().grm_store_set_route(st.h, nid, k.ctypes.data, k.size,
-                                                _blob(lexical[i])))
+            keys = _keys_of(rows[i], d)
+            if len(keys) == 1:
+                k = np.ascontiguousarray(keys[0]).reshape(-1)
+                st._check(lib().grm_store_set_route(st.h, nid, k.ctypes.data, k.size,
+                                                    _blob(lexical[i])))
+            else:
+                st.set_route_list(nid, keys, _blob(lexical[i]))
             st._check(lib().grm_store_set_route_metadata(
                 st.h, nid, *[str(v).encode("utf-8") for v in meta[i]]))
         out = np.empty(max(1, topk), dtype=np.uint64)
@@ -206,10 +221,11 @@ def gqa_route(node_keys: list, query: np.ndarray, kv_heads: int, topk: int,
 def store_route_gqa(blocks: list, lexical: list, meta: list, query: np.ndarray, kv_heads: int,
                     query_lexical=(), filters=((), (), (), ()), topk: int = 3) -> list[int]:
     """Route order from the reference ``grm_store_route_gqa`` with lexical
-    keys and route filters: node i (id i) has key blocks[i] [kv, L, hd],
-    lexical keys lexical[i] and metadata meta[i].  A sentinel node with a
-    one-value key keeps the store on its fp64 law path (see gqa_route) and
-    is dropped from the order."""
+    keys and route filters: node i (id i) has key blocks[i] [kv, L, hd] (a
+    list of such blocks makes a multi-key entry), lexical keys lexical[i]
+    and metadata meta[i].  A sentinel node with a one-value key keeps the
+    store on its fp64 law path (see gqa_route) and is dropped from the
+    order."""
     q = np.ascontiguousarray(query, dtype=np.float32)
     H, Qt, hd = q.shape
     h = lib().grm_store_create_gqa(b"Qwen3_TC", 36, 2560, 2 * kv_heads * hd, 0, kv_heads, hd)
@@ -217,10 +233,7 @@ def store_route_gqa(blocks: list, lexical: list, meta: list, query: np.ndarray, 
         for i, key in enumerate(blocks):
             nid = st.add_node()
             assert nid == i
-            k = np.ascontiguousarray(key, dtype=np.float32).reshape(-1)
-            offs = np.asarray([0, k.size], dtype=np.uint64)
-            st._check(lib().grm_store_set_route_list(st.h, nid, k.ctypes.data, k.size,
-                                                     offs.ctypes.data, 1, _blob(lexical[i])))
+            st.set_route_list(nid, _keys_of(key), _blob(lexical[i]))
             st._check(lib().grm_store_set_route_metadata(
                 st.h, nid, *[str(v).encode("utf-8") for v in meta[i]]))
         sentinel = st.add_node()

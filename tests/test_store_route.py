@@ -113,3 +113,64 @@ def test_oracle_gqa_store_law_matches_the_reference_store():
         got, _ = oracle.store_route_gqa(keys, offs, kv, hd, np.arange(n), lexical, meta, q,
                                         qlex, filters, k)
         assert got == want, (case, qlex, filters, k)
+
+
+def multi_entries(rng, n, make_key, max_keys=3):
+    """Entries of 0..max_keys keys; a few keys not finite."""
+    entries, owners, flat = [], [], []
+    for i in range(n):
+        k = int(rng.integers(0, max_keys + 1)) if i % 4 == 0 else 1
+        keys = [make_key() for _ in range(k)]
+        if k > 1 and i % 8 == 0 and keys[0].size:
+            keys[0] = keys[0].copy()
+            keys[0].reshape(-1)[0] = np.nan                 # one key not finite
+        entries.append(keys)
+        for key in keys:
+            owners.append(i)
+            flat.append(key)
+    return entries, owners, flat
+
+
+def test_oracle_multi_row_mla_law_matches_the_reference_store():
+    # multi-row entries score their best finite row (exact_mla_entry_score,
+    # cpp/grm_runtime.cpp:3518-3545); an entry with no finite row drops out
+    rng = np.random.default_rng(44)
+    n, dim = 90, 10
+    entries, owners, flat = multi_entries(rng, n, lambda: rng.standard_normal(dim).astype(np.float32))
+    entries[7] = [entries[3][0].copy()] if entries[3] else entries[7]   # a tie across entries
+    owners = [i for i, e in enumerate(entries) for _ in e]
+    flat = [k for e in entries for k in e]
+    rows = np.stack(flat)
+    _, lexical, meta = random_store(rng, n, dim)
+    for case in range(40):
+        q, qlex, filters = random_query(rng, rows, dim)
+        k = int(rng.integers(1, 17))
+        want = ref.store_route(entries, lexical, meta, q, qlex, filters, k)
+        got, _ = oracle.store_route(rows, np.arange(n), lexical, meta, q, qlex, filters, k,
+                                    owners=owners)
+        assert got == want, (case, qlex, filters, k)
+
+
+def test_oracle_multi_key_gqa_law_matches_the_reference_store():
+    # multi-key entries score their best finite key (max_gqa_raw_score,
+    # cpp/grm_runtime.cpp:3031-3051)
+    rng = np.random.default_rng(45)
+    n, kv, hd, H = 60, 2, 8, 4
+    entries, owners, flat = multi_entries(
+        rng, n, lambda: rng.standard_normal((kv, int(rng.integers(0, 12)), hd)).astype(np.float32))
+    lens = np.asarray([b.shape[1] for b in flat], dtype=np.uint64)
+    offs = np.zeros(len(flat) + 1, dtype=np.uint64)
+    offs[1:] = np.cumsum(lens)
+    keys = np.concatenate([b.reshape(-1) for b in flat])
+    _, lexical, meta = random_gqa_store(rng, n, kv, hd)
+    for case in range(40):
+        Qt = int(rng.integers(1, 3))
+        q = rng.standard_normal((H, Qt, hd)).astype(np.float32)
+        qlex = list(rng.choice(VOCAB, size=rng.integers(0, 5), replace=True))
+        filters = tuple([v for v in (list(rng.choice(m, size=rng.integers(0, 3), replace=False))
+                                     if rng.random() < 0.5 else []) if v] for m in META)
+        k = int(rng.integers(1, 17))
+        want = ref.store_route_gqa(entries, lexical, meta, q, kv, qlex, filters, k)
+        got, _ = oracle.store_route_gqa(keys, offs, kv, hd, np.arange(n), lexical, meta, q,
+                                        qlex, filters, k, owners=owners)
+        assert got == want, (case, qlex, filters, k)

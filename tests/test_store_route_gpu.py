@@ -9,7 +9,9 @@ Covered:
   string-match bit);
 * metadata updates that keep unset fields (cpp/grm_runtime.cpp:2922-2946);
 * route replacement (set_route on a live node) and clear_route;
-* score ties from duplicate rows.
+* score ties from duplicate rows;
+* entries of several route keys (none, one with a non-finite value, ties
+  across entries), replaced by single keys and back, cleared.
 """
 
 import numpy as np
@@ -149,9 +151,12 @@ def test_device_store_refuses_what_it_does_not_serve(hip_lib):
     with DeviceRouteStore(8, capacity=64) as st:
         with pytest.raises(RuntimeError):
             st.set_route(1, np.zeros(7, np.float32))          # wrong length
-        keys = np.zeros((2, 8), np.float32)
-        rc = lib.grm_store_set_route_multi(st._h, 3, keys.ctypes.data, 2, 8, b"")
-        assert rc != 0 and b"multi-row" in lib.grm_store_last_error(st._h)
+        keys = np.zeros((2, 7), np.float32)
+        rc = lib.grm_store_set_route_multi(st._h, 3, keys.ctypes.data, 2, 7, b"")
+        assert rc != 0 and b"dim" in lib.grm_store_last_error(st._h)   # rows of another length
+        offs = np.asarray([0, 8, 4], np.uint64)
+        rc = lib.grm_store_set_route_list(st._h, 3, keys.ctypes.data, 4, offs.ctypes.data, 2, b"")
+        assert rc != 0                                          # offsets out of order
         st.set_route(1, np.ones(8, np.float32), "a")
         with pytest.raises(RuntimeError):
             st.route_scored(np.ones(8, np.float32), topk=17)   # above the device list
@@ -163,3 +168,88 @@ def test_device_store_refuses_what_it_does_not_serve(hip_lib):
         q = np.zeros((3, 1, 8), np.float32)
         with pytest.raises(RuntimeError):
             st.route_gqa(q, topk=2)                             # heads not a multiple of kv
+
+
+def _multi_case(rng, make_key):
+    k = int(rng.integers(0, 4))
+    keys = [make_key() for _ in range(k)]
+    if k > 1 and rng.random() < 0.3 and keys[0].size:
+        keys[0] = keys[0].copy()
+        keys[0].reshape(-1)[0] = np.nan
+    return keys
+
+
+@pytest.mark.parametrize("dialect", ["mla", "gqa"])
+def test_device_store_multi_key_entries_match_the_law(hip_lib, dialect):
+    # entries of several keys score their best finite key
+    # (exact_mla_entry_score cpp/grm_runtime.cpp:3518-3545; max_gqa_raw_score
+    # :3031-3051); law pinned against the reference store in
+    # test_store_route.py
+    from graftrepository_amd.store_route import DeviceGqaRouteStore
+
+    rng = np.random.default_rng(57 if dialect == "mla" else 58)
+    if dialect == "mla":
+        n, dim = 1500, 48
+        make = lambda: rng.standard_normal(dim).astype(np.float32)
+        st = DeviceRouteStore(dim, capacity=2048)
+    else:
+        n, kv, hd, H = 300, 2, 64, 8
+        make = lambda: rng.standard_normal((kv, int(rng.integers(0, 30)), hd)).astype(np.float32)
+        st = DeviceGqaRouteStore(kv, hd, capacity_nodes=512, capacity_tokens=30_000)
+    entries, lex, meta = {}, {}, {}
+
+    def put(nid, keys):
+        entries[nid] = keys
+        lex[nid] = list(rng.choice(VOCAB, size=rng.integers(0, 4), replace=False))
+        if len(keys) == 1 and rng.random() < 0.5:
+            st.set_route(nid, keys[0], lex[nid])
+        elif dialect == "mla" and len(keys) > 0 and rng.random() < 0.5:
+            st.set_route_multi(nid, np.stack(keys), lex[nid])
+        else:
+            st.set_route_list(nid, keys, lex[nid])
+        meta.setdefault(nid, DEFAULT)
+
+    with st:
+        for i in range(n):
+            put(2000 + i, _multi_case(rng, make) if i % 3 == 0 else [make()])
+        entries[2009] = [entries[2003][0].copy()] if entries[2003] else [make()]
+        st.set_route(2009, entries[2009][0], lex[2009])          # a tie across entries
+        for step in range(24):
+            if step % 4 == 3:
+                for nid in rng.choice(sorted(entries), size=12, replace=False):
+                    nid = int(nid)
+                    op = rng.integers(0, 3)
+                    if op == 0:
+                        put(nid, _multi_case(rng, make) if rng.random() < 0.5 else [make()])
+                    elif op == 1:
+                        vals = tuple(str(rng.choice(m)) for m in META)
+                        st.set_route_metadata(nid, *vals)
+                        meta[nid] = tuple(v if v else o for v, o in zip(vals, meta[nid]))
+                    else:
+                        st.clear_route(nid)
+                        del entries[nid], lex[nid], meta[nid]
+            ids = sorted(entries)
+            owners = [j for j, nid in enumerate(ids) for _ in entries[nid]]
+            flat = [key for nid in ids for key in entries[nid]]
+            qlex = list(rng.choice(VOCAB, size=rng.integers(0, 5), replace=True))
+            filters = tuple([str(v) for v in rng.choice(m, size=rng.integers(0, 3), replace=False)
+                             if v] if rng.random() < 0.5 else [] for m in META)
+            k = int(rng.integers(1, 17))
+            lexs, metas = [lex[i] for i in ids], [meta[i] for i in ids]
+            if dialect == "mla":
+                q = rng.standard_normal(dim).astype(np.float32)
+                want_ids, want_sc = oracle.store_route(np.stack(flat), ids, lexs, metas, q, qlex,
+                                                       filters, k, owners=owners)
+            else:
+                lens = np.asarray([b.shape[1] for b in flat], dtype=np.uint64)
+                offs = np.zeros(len(flat) + 1, dtype=np.uint64)
+                offs[1:] = np.cumsum(lens)
+                keys = np.concatenate([b.reshape(-1) for b in flat])
+                q = rng.standard_normal((H, int(rng.integers(1, 4)), hd)).astype(np.float32)
+                want_ids, want_sc = oracle.store_route_gqa(keys, offs, kv, hd, ids, lexs, metas,
+                                                           q, qlex, filters, k, owners=owners)
+            got_ids, got_sc = st.route_scored(q, qlex, k, kinds=filters[0], scopes=filters[1],
+                                              durabilities=filters[2], mutabilities=filters[3])
+            assert got_ids == want_ids, (step, qlex, filters, k)
+            np.testing.assert_array_equal(np.asarray(got_sc, np.float32).view(np.uint32),
+                                          want_sc.view(np.uint32))
