@@ -1052,6 +1052,12 @@ __device__ inline void codes_to_f16(uint32_t u, uint32_t& lo, uint32_t& hi) {
   hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
 }
 
+// Query passes of one screen-only launch (see gqa_smax_kernel): pass p is
+// heads r0[p] .. + rc[p] of each kv head, tokens t0[p] .. + qc[p].
+struct SmaxPasses {
+  int r0[4], rc[4], t0[4], qc[4];
+};
+
 // Screen-only pass; grid (P, kv heads), persistent: wave w of block b walks
 // the work items b*4 + w, b*4 + w + 4P, ... -- one item per live node with
 // key tokens, all of its tokens, so each (node, kv head) has one writer --
@@ -1081,11 +1087,19 @@ __device__ inline void codes_to_f16(uint32_t u, uint32_t& lo, uint32_t& hi) {
 // gc = qb*R*Qt + (r0 + rr)*Qt + t0 + tt of the query's full set, so passes
 // over disjoint parts of a query fill disjoint cells of the same rows, and
 // colinfo[g*colstride + gc] holds each column's bound parameters.
-template <int KDT, int KS, int NT, bool FACT, bool SF16>
-__global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || NT == 1)) ? 2 : 1) void gqa_smax_kernel(
+//
+// NP > 1 (a single wide query): a block is 8 wavefronts, wavefront w
+// screening pass w % NP for walker blockIdx.x * (8/NP) + w / NP, so the NP
+// wavefronts of a walker read the same tiles at about the same time and
+// the bank is streamed from HBM once for NP passes (the tiles come again
+// from L2; the loads are not marked nontemporal).  Each pass's columns are
+// staged in their own LDS region.
+template <int KDT, int KS, int NT, bool FACT, bool SF16, int NP = 1>
+__global__ __launch_bounds__((NP == 1 ? kUnitWaves : 8) * kWave,
+                              (NT * KS <= 16 && (KS <= 4 || NT == 1)) ? 2 : 1) void gqa_smax_kernel(
     const unsigned char* __restrict__ keys, const unsigned char* __restrict__ scales,
     int scale_dtype, int group_size, const Item* __restrict__ items, uint32_t n_items, int kv,
-    int R, int Qt, int r0, int Rc, int t0, int Qc, const void* __restrict__ query, int q_dtype,
+    int R, int Qt, SmaxPasses ps, const void* __restrict__ query, int q_dtype,
     size_t q_elems, int Qb, int emax,
     double gamma, double delta, double rho, double sigma_q, double sigma_k, double sigma_p,
     double eps_rel, double eps_abs, float4* __restrict__ colinfo, unsigned* __restrict__ hmaxf,
@@ -1103,23 +1117,30 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || N
   constexpr uint32_t TT = 16 * NH;              // tokens per tile
   static_assert(!FACT || KDT == kI8, "row-scale factoring is for INT8 banks");
   constexpr uint32_t kEnd = 0x80000000u;
-  extern __shared__ float s_q[];
-  __shared__ float4 s_ec[kMaxSmaxCols];
-  __shared__ unsigned s_bad[kMaxSmaxCols];
+  static_assert(NP == 1 || NP == 2 || NP == 4, "1, 2 or 4 passes per launch");
+  static_assert(NP == 1 || NT <= 4, "split passes hold at most 64 columns each");
+  constexpr int WPB = NP == 1 ? kUnitWaves : 8 / NP;  // walkers per block
+  constexpr int kPassCols = NP == 1 ? kMaxSmaxCols : kMaxCols;
+  extern __shared__ float s_q[];                    // [NP][NT*16][HD]
+  __shared__ float4 s_ec[NP * kPassCols];
+  __shared__ unsigned s_bad[NP * kPassCols];
   const int lane = threadIdx.x & (kWave - 1);
   const int g = blockIdx.y;
-  const int RQc = Rc * Qc;
-  const int cols = Qb * RQc;
-  // the query's full column index of pass column cg
-  auto full_col = [&](int cg) {
-    const int qb = cg / RQc;
-    const int rem = cg - qb * RQc;
-    return qb * R * Qt + (r0 + rem / Qc) * Qt + t0 + rem % Qc;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int pi = NP == 1 ? 0 : wave % NP;           // this wavefront's pass
+  // the query's full column index of column cg of pass p
+  auto full_col_of = [&](int p, int cg) {
+    const int RQp = ps.rc[p] * ps.qc[p];
+    const int qb = cg / RQp;
+    const int rem = cg - qb * RQp;
+    return qb * R * Qt + (ps.r0[p] + rem / ps.qc[p]) * Qt + ps.t0[p] + rem % ps.qc[p];
   };
+  const int cols = Qb * ps.rc[pi] * ps.qc[pi];
+  auto full_col = [&](int cg) { return full_col_of(pi, cg); };
   const int quarter = lane >> 4;
   const int r16 = lane & 15;
-  const uint32_t stride = gridDim.x * kUnitWaves;
-  uint32_t li = blockIdx.x * kUnitWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t stride = gridDim.x * WPB;
+  uint32_t li = blockIdx.x * WPB + (NP == 1 ? wave : wave / NP);
   const bool has_item = li < n_items;
   const int G = KDT == kI8 ? HD / group_size : 1;
   const int ses = scale_dtype == kF16 ? 2 : 4;
@@ -1179,7 +1200,13 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || N
       // 1 KiB
       const u32x4* p = ld.kp + static_cast<uint64_t>(t) * 4 + quarter;
 #pragma unroll
-      for (int i = 0; i < NL; ++i) b.v[h][i] = __builtin_nontemporal_load(p + i * 4 * ld.L);
+      for (int i = 0; i < NL; ++i) {
+        if constexpr (NP == 1) {
+          b.v[h][i] = __builtin_nontemporal_load(p + i * 4 * ld.L);
+        } else {
+          b.v[h][i] = p[i * 4 * ld.L];
+        }
+      }
       if constexpr (KDT == kI8) {
         if constexpr (FACT) {
           b.s[h][0] = scale_raw(ld.sp, t);
@@ -1220,17 +1247,29 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && (KS <= 4 || N
     load_next(x2);
     load_next(x3);
   }
-  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, Rc, Qc, g, emax,
-                    gamma, delta, rho, sigma_q, sigma_k, sigma_p, eps_rel, eps_abs);
-  if (blockIdx.x == 0) {
-    for (int cg = threadIdx.x; cg < cols; cg += blockDim.x) {
-      colinfo[static_cast<size_t>(g) * colstride + full_col(cg)] = s_ec[cg];
+  // every pass's columns, each in its own LDS region (the query advanced
+  // to the pass's first value, see "Query passes")
+  const size_t esz = q_dtype == kBF16 ? 2 : 4;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const unsigned char* qp = static_cast<const unsigned char*>(query) +
+                              static_cast<size_t>(ps.r0[p] * Qt + ps.t0[p]) * HD * esz;
+    const int cols_p = Qb * ps.rc[p] * ps.qc[p];
+    stage_columns<HD>(s_q + static_cast<size_t>(p) * NT * 16 * HD, s_ec + p * kPassCols,
+                      s_bad + p * kPassCols, qp, q_dtype, q_elems, cols_p, R, Qt, ps.rc[p],
+                      ps.qc[p], g, emax, gamma, delta, rho, sigma_q, sigma_k, sigma_p, eps_rel,
+                      eps_abs);
+    if (blockIdx.x == 0) {
+      for (int cg = threadIdx.x; cg < cols_p; cg += blockDim.x) {
+        colinfo[static_cast<size_t>(g) * colstride + full_col_of(p, cg)] = s_ec[p * kPassCols + cg];
+      }
     }
   }
   if (!has_item) return;
 
   u32x4 bq[NT][KS];
-  query_frags<MT, PERM, KS, NT>(bq, s_q, s_ec, cols, r16, quarter);
+  query_frags<MT, PERM, KS, NT>(bq, s_q + static_cast<size_t>(pi) * NT * 16 * HD,
+                                s_ec + pi * kPassCols, cols, r16, quarter);
 
   // key fragment ks of half h of a tile: 8 values of the lane's token in
   // the MFMA type

@@ -130,6 +130,12 @@ struct GqaDeviceArena {
   // a single query's screen-only passes take up to 128 columns each at
   // head dims up to 128 (GRM_HIP_GQA_WIDE_SMAX=0: 64)
   bool wide_smax = true;
+  // ... or, with at least smax_split (2 or 4) passes of 64 columns, that
+  // many passes to a launch, which streams the bank once for all of them
+  // (GRM_HIP_GQA_SMAX_SPLIT=0: one launch per pass).  A 64-token query
+  // (R = 4, 4 passes) measured 0.776 ms in passes of 128 and 0.726 ms split
+  // 4 ways; 2 passes split 2 ways were slower than one pass of 128.
+  int smax_split = 4;
   unsigned* d_hmaxf = nullptr;   // screened maxima per (query, head, q token, slot), float bits
   size_t d_hmaxf_count = 0;
   float4* d_colinfo = nullptr;   // per (kv head, column): coef, eabs, scale, bad
@@ -469,6 +475,10 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
   if (const char* env = getenv("GRM_HIP_GQA_SPARSE")) a->sparse_exact = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_GQA_WIDE_SMAX")) a->wide_smax = env[0] != '0';
+  if (const char* env = getenv("GRM_HIP_GQA_SMAX_SPLIT")) {
+    const long v = strtol(env, nullptr, 10);
+    a->smax_split = (v == 2 || v == 4) ? static_cast<int>(v) : 0;
+  }
   if (const char* env = getenv("GRM_HIP_GQA_BOUND")) {
     a->bound_mode = env[0] == '0' ? 0 : (env[0] == '1' ? 1 : -1);
   }
@@ -939,7 +949,8 @@ constexpr uint32_t kWideBlocks = 1024;
 // the device holds resident at once (a block that had to wait for a slot
 // would start its whole share of the items when the others finish), and
 // no more than there are items to give every wave one.
-int persistent_grid(GqaDeviceArena* a, const void* fn, unsigned threads, size_t lds, dim3* grid) {
+int persistent_grid(GqaDeviceArena* a, const void* fn, unsigned threads, size_t lds, dim3* grid,
+                    uint32_t walkers_per_block = grm::gqa::kUnitWaves) {
   const std::pair<const void*, size_t> key(fn, lds);
   auto it = a->resident.find(key);
   int per_cu = 0;
@@ -954,7 +965,7 @@ int persistent_grid(GqaDeviceArena* a, const void* fn, unsigned threads, size_t 
   GRM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, a->device));
   const uint64_t resident = static_cast<uint64_t>(std::max(1, cus)) * static_cast<uint64_t>(per_cu);
   const uint64_t px = std::max<uint64_t>(
-      1, std::min<uint64_t>((a->n_units + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves,
+      1, std::min<uint64_t>((a->n_units + walkers_per_block - 1) / walkers_per_block,
                             std::max<uint64_t>(1, resident / a->kv)));
   *grid = dim3(static_cast<unsigned>(px), a->kv);
   return 0;
@@ -985,13 +996,21 @@ int prepare_bv(GqaDeviceArena* a, const SrPlan& p, int topk, uint32_t fin_blocks
 // d_hmaxf (one run of colstride cells per (slot, kv head)), the columns'
 // bound parameters into d_colinfo.
 int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
-                int colstride, const QPass& ps) {
+                int colstride, const QPass* passes, int np) {
   const int kv = static_cast<int>(a->kv);
-  const int cols = qb * ps.rc * ps.qc;
-  const unsigned char* qpass = qptr + pass_query_offset(a, p.Qt, ps, q_dtype);
+  if (np != 1 && np != 2 && np != 4) return grm::fail(-1, "1, 2 or 4 screen passes per launch");
+  grm::gqa::SmaxPasses sp{};
+  int cols = 0;
+  for (int i = 0; i < np; ++i) {
+    sp.r0[i] = passes[i].r0;
+    sp.rc[i] = passes[i].rc;
+    sp.t0[i] = passes[i].t0;
+    sp.qc[i] = passes[i].qc;
+    cols = std::max(cols, qb * passes[i].rc * passes[i].qc);
+  }
   const int tiles = (cols + 15) / 16;
   const int NT = tiles <= 1 ? 1 : (tiles <= 2 ? 2 : (tiles <= 4 ? 4 : 8));
-  if (cols > grm::gqa::kMaxSmaxCols || (NT == 8 && p.KS > 4)) {
+  if (cols > grm::gqa::kMaxSmaxCols || (NT == 8 && p.KS > 4) || (np > 1 && (NT > 4 || p.KS > 4))) {
     return grm::fail(-1, "screen-only pass wider than its kernel");
   }
   const bool fact = a->key_dtype == kI8 && static_cast<uint32_t>(a->group_size) == a->hd;
@@ -1004,27 +1023,40 @@ int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, i
   const int emax = eb.emax;
   const double rho = fact ? ldexp(1.0, -11) + ldexp(1.0, -21) : 0.0;
   const size_t q_elems = static_cast<size_t>(p.H) * p.Qt * a->hd;
-  const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
+  const unsigned threads = (np == 1 ? grm::gqa::kUnitWaves : 8) * grm::kWave;
   if (a->n_units > 0) {
-    const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);
-#define GRM_SMAX(KDT, KS, NTT, FACT, SF16)                                                        \
+    // one LDS region of NT*16 columns per pass when passes are split
+    const size_t lds = np == 1 ? static_cast<size_t>(cols) * a->hd * sizeof(float)
+                               : static_cast<size_t>(np) * NT * 16 * a->hd * sizeof(float);
+#define GRM_SMAX_NP(KDT, KS, NTT, FACT, SF16, NPP)                                                \
   do {                                                                                            \
-    auto fn = grm::gqa::gqa_smax_kernel<KDT, KS, NTT, FACT, SF16>;                                \
+    auto fn = grm::gqa::gqa_smax_kernel<KDT, KS, NTT, FACT, SF16, NPP>;                           \
     dim3 grid;                                                                                    \
-    GRM_CHECK_RC(persistent_grid(a, reinterpret_cast<const void*>(fn), threads, lds, &grid));     \
+    GRM_CHECK_RC(persistent_grid(a, reinterpret_cast<const void*>(fn), threads, lds, &grid,       \
+                                 NPP == 1 ? grm::gqa::kUnitWaves : 8 / NPP));                     \
     fn<<<grid, threads, lds, a->stream>>>(                                                        \
         screen_keys(a), a->d_scales, a->scale_dtype, a->group_size, a->d_units,                   \
-        static_cast<uint32_t>(a->n_units), kv, p.R, p.Qt, ps.r0, ps.rc, ps.t0, ps.qc, qpass,     \
+        static_cast<uint32_t>(a->n_units), kv, p.R, p.Qt, sp, qptr,                               \
         q_dtype, q_elems, qb, emax,                                                               \
         gamma, delta, rho, sigma_q, sigma_k, sigma_p, eb.eps_rel, eb.eps_abs, a->d_colinfo,        \
         a->d_hmaxf, colstride);                                                                   \
+  } while (0)
+#define GRM_SMAX(KDT, KS, NTT, FACT, SF16)                                        \
+  do {                                                                            \
+    if (np == 1) {                                                                \
+      GRM_SMAX_NP(KDT, KS, NTT, FACT, SF16, 1);                                   \
+    } else if (np == 2) {                                                         \
+      GRM_SMAX_NP(KDT, KS, (NTT <= 4 ? NTT : 4), FACT, SF16, (KS <= 4 ? 2 : 1));  \
+    } else {                                                                      \
+      GRM_SMAX_NP(KDT, KS, (NTT <= 4 ? NTT : 4), FACT, SF16, (KS <= 4 ? 4 : 1));  \
+    }                                                                             \
   } while (0)
 #define GRM_SMAX_NT(KDT, KS, FACT, SF16)               \
   switch (NT) {                                        \
     case 1: GRM_SMAX(KDT, KS, 1, FACT, SF16); break;   \
     case 2: GRM_SMAX(KDT, KS, 2, FACT, SF16); break;   \
     case 4: GRM_SMAX(KDT, KS, 4, FACT, SF16); break;   \
-    default: GRM_SMAX(KDT, KS, (KS <= 4 ? 8 : 4), FACT, SF16); break; \
+    default: GRM_SMAX_NP(KDT, KS, (KS <= 4 ? 8 : 4), FACT, SF16, 1); break; \
   }
 #define GRM_SMAX_KS(KDT, FACT, SF16)                   \
   switch (p.KS) {                                      \
@@ -1051,6 +1083,7 @@ int launch_smax(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, i
 #undef GRM_SMAX_KS
 #undef GRM_SMAX_NT
 #undef GRM_SMAX
+#undef GRM_SMAX_NP
     GRM_HIP_CHECK(hipGetLastError());
   }
   return 0;
@@ -1077,10 +1110,22 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   // 2. screened maxima of every (column, node), one launch per screen
   // pass: a single query wider than one pass takes passes of up to 128
   // columns where the query fragments fit the registers (head dim <= 128)
-  const bool wide_passes = a->wide_smax && qb == 1 && p.passes.size() > 1 && p.KS <= 4;
-  const std::vector<QPass> spasses =
-      wide_passes ? query_passes(p.R, p.Qt, grm::gqa::kMaxSmaxCols) : p.passes;
-  for (const QPass& ps : spasses) GRM_CHECK_RC(launch_smax(a, p, qptr, q_dtype, qb, colstride, ps));
+  const bool single_wide = qb == 1 && p.passes.size() > 1 && p.KS <= 4;
+  if (single_wide && a->smax_split > 1 && p.passes.size() >= static_cast<size_t>(a->smax_split)) {
+    // passes of 64 columns, up to smax_split of them per launch
+    const std::vector<QPass>& sp = p.passes;
+    for (size_t i = 0; i < sp.size();) {
+      const size_t left = sp.size() - i;
+      const int np = left >= static_cast<size_t>(a->smax_split) ? a->smax_split : (left >= 2 ? 2 : 1);
+      GRM_CHECK_RC(launch_smax(a, p, qptr, q_dtype, qb, colstride, &sp[i], np));
+      i += static_cast<size_t>(np);
+    }
+  } else {
+    const bool wide_passes = a->wide_smax && single_wide;
+    const std::vector<QPass> spasses =
+        wide_passes ? query_passes(p.R, p.Qt, grm::gqa::kMaxSmaxCols) : p.passes;
+    for (const QPass& ps : spasses) GRM_CHECK_RC(launch_smax(a, p, qptr, q_dtype, qb, colstride, &ps, 1));
+  }
   // 3. score bounds, the k best lower bounds per block (with no key tokens
   // at all the column parameters are never used: every live node has no
   // tokens and scores 0)
@@ -1779,7 +1824,7 @@ extern "C" int grm_gqa_hip_probe_screen(GqaDeviceArena* a, const void* query_hos
   GRM_HIP_CHECK(hipMemcpyAsync(d_q.p, query_host, qbytes, hipMemcpyHostToDevice, a->stream));
   GRM_HIP_CHECK(hipMemsetAsync(a->d_hmaxf, 0, cells * sizeof(unsigned), a->stream));
   GRM_CHECK_RC(launch_smax(a, p, static_cast<const unsigned char*>(d_q.p), query_dtype, 1, colstride,
-                           p.passes[0]));
+                           &p.passes[0], 1));
   const size_t out_cells = static_cast<size_t>(n) * a->kv * colstride;
   GRM_HIP_CHECK(hipMemcpyAsync(out_maxima_host, a->d_hmaxf, out_cells * sizeof(float),
                                hipMemcpyDeviceToHost, a->stream));

@@ -45,14 +45,18 @@ def c4_bank(nodes, hi, seed):
 @pytest.fixture(params=["screen", "screen-all-columns", "refine", "exact"])
 def path(request, monkeypatch):
     # screen: the default choice (bound and verify for these widths: its
-    # screen in passes of 128 columns, then the law on the columns of each
-    # candidate that the screen cannot rule out); screen-all-columns: the
-    # screen in passes of 64, the law on every column in passes of 32;
+    # screen in passes of 128 columns, or 4 passes of 64 to a launch, then
+    # the law on the columns of each candidate that the screen cannot rule
+    # out); screen-all-columns: the screen in passes of 64, two to a
+    # launch, the law on every column in passes of 32;
     # refine: screen and refine in passes; exact: the fp64 kernel
     narrow = request.param == "screen-all-columns"
     monkeypatch.setenv("GRM_HIP_GQA_SCREEN", "0" if request.param == "exact" else "1")
     monkeypatch.setenv("GRM_HIP_GQA_SPARSE", "0" if narrow else "1")
     monkeypatch.setenv("GRM_HIP_GQA_WIDE_SMAX", "0" if narrow else "1")
+    # narrow: split launches of 2 passes; otherwise the default (4 passes
+    # of 64 columns to a launch from 4 passes on, else passes of 128)
+    monkeypatch.setenv("GRM_HIP_GQA_SMAX_SPLIT", "2" if narrow else "4")
     if request.param == "refine":
         monkeypatch.setenv("GRM_HIP_GQA_BOUND", "0")
     else:
