@@ -1447,15 +1447,20 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_kernel(
     const uint32_t* __restrict__ flags, const uint64_t* __restrict__ ids,
     const unsigned* __restrict__ kmax, const float4* __restrict__ colinfo,
     const unsigned* __restrict__ qbad, int fact, int hd, int k, float2* __restrict__ lbub,
-    Cand* __restrict__ block_out, uint32_t* __restrict__ counters, int n_counters) {
+    Cand* __restrict__ block_out, uint32_t* __restrict__ counters, int n_counters, int nq) {
   __shared__ Cand s_lists[kFinWaves][kMaxTopK];
   extern __shared__ float4 s_ci[];  // [H*Qt]: query qb's {coef, eabs, 1/scale, kcap}, (h, qi) order
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  // grid (queries, slot blocks): the queries of one group of slots run
-  // back to back and share the cache lines of the slots' maxima
-  const int qb = blockIdx.x;
-  const uint32_t sblk = blockIdx.y, nsblk = gridDim.y;
+  // 1-D grid of nq * nsblk blocks (nsblk a multiple of 8).  Blocks go to
+  // the 8 XCDs in turn (block b to XCD b % 8), each with its own L2, and a
+  // slot's maxima for all queries share cache lines: block b takes slot
+  // block ((b/8) / nq) * 8 + b % 8 of query (b/8) % nq, so the nq blocks
+  // of one slot block run on one XCD, one after another in dispatch order.
+  const uint32_t nsblk = gridDim.x / static_cast<uint32_t>(nq);
+  const uint32_t bj = blockIdx.x / 8u;
+  const int qb = static_cast<int>(bj % static_cast<uint32_t>(nq));
+  const uint32_t sblk = (bj / static_cast<uint32_t>(nq)) * 8u + blockIdx.x % 8u;
   if (sblk == 0 && threadIdx.x == 0) {
     counters[qb] = 0u;
     if (qb == 0) counters[n_counters - 1] = 0u;

@@ -1141,15 +1141,16 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   const uint32_t bblocks =
       wide ? std::max<uint32_t>(1, std::min<uint32_t>(kWideBlocks, (n_slots + grm::gqa::kFinWaves - 1) /
                                                                         grm::gqa::kFinWaves))
-           : std::max<uint32_t>(1, std::min<uint32_t>(fin_blocks, (n_slots + kBoundsSlots - 1) / kBoundsSlots));
+           : (std::max<uint32_t>(1, std::min<uint32_t>(fin_blocks, (n_slots + kBoundsSlots - 1) / kBoundsSlots)) +
+              7u) / 8u * 8u;  // a multiple of 8 (the kernel's XCD mapping)
 #define GRM_BOUNDS(ST)                                                                           \
-  grm::gqa::gqa_bounds_kernel<ST><<<dim3(qb, bblocks), grm::gqa::kFinWaves * grm::kWave,         \
+  grm::gqa::gqa_bounds_kernel<ST><<<dim3(qb * bblocks), grm::gqa::kFinWaves * grm::kWave,         \
                                     ST ? ci_bytes : 0, a->stream>>>(                             \
       a->d_hmaxf, colstride, a->cap_nodes, H, p.Qt, p.R, colstride, kv,                          \
       static_cast<uint32_t>(a->high_water), a->d_len,                                            \
       a->route_flags ? a->route_flags : a->d_flags, a->d_ids, a->d_kmax,                         \
       a->d_colinfo, a->d_qbad, fact ? 1 : 0, static_cast<int>(a->hd), topk, a->d_lbub,           \
-      a->d_blists, a->d_ccount, p.qb_max + 1)
+      a->d_blists, a->d_ccount, p.qb_max + 1, qb)
   if (wide) {
     grm::gqa::gqa_bounds_wide_kernel<<<dim3(qb, bblocks), grm::gqa::kFinWaves * grm::kWave, 0,
                                        a->stream>>>(
