@@ -177,3 +177,17 @@ def test_reference_surface_prompt_length_query(hip_lib):
     want, _, _ = oracle.gqa_route(dense.reshape(-1), oracle.F32, offs, kv, hd, qs, 4)
     np.testing.assert_array_equal(mapped, want + 7)
     bank.close()
+
+
+def test_query_wider_than_the_staged_rows(hip_lib, path):
+    # 4 heads per kv head x 1024 query tokens: 4096 columns per kv head,
+    # past the query-row staging of the exact step's double rows (they go
+    # straight to device memory), and 64 screen passes
+    lens = wl.gqa_lengths(24, seed=91, lo=1, hi=40)
+    keys, offs = wl.gqa_bank(lens, 4, 64, seed=91, dtype="bf16")
+    qs = wl.gqa_queries(1, 16, 1024, 64, seed=92, dtype="bf16")
+    with GqaNodeBank(keys, offs, kv_heads=4, head_dim=64, dtype="bf16") as bank:
+        res = bank.route(qs, 3, query_dtype="bf16")
+    ids, sc, _ = oracle.gqa_route(keys, oracle.BF16, offs, 4, 64,
+                                  bf16_bits_to_f32(qs).reshape(qs.shape), 3)
+    assert_same(res, ids, sc)
