@@ -1728,6 +1728,7 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_bounds_wide_kernel(
 // column's lower bound.  A NaN bound keeps its column.  q64 holds the query
 // columns as doubles, value d of column gc at q64[(g*hd + d)*rqp + gc].
 // Wavefronts walk pairs p = w, w + W, ... (p = candidate * kv + g).
+constexpr int kSparseCols = 4;  // columns evaluated per read of a pair's key rows
 template <int KDT>
 __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_sparse_kernel(
     const unsigned char* __restrict__ keys, const unsigned char* __restrict__ scales,
@@ -1738,7 +1739,9 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_sparse_kernel(
     const uint32_t* __restrict__ lens, const double* __restrict__ q64, int rqp, double denom,
     unsigned long long* __restrict__ hmax, size_t cap) {
   using T = KeyTraits<KDT>;
+  extern __shared__ double s_qv[];  // [kUnitWaves][kSparseCols][hd]
   const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
   const uint32_t W = gridDim.x * kUnitWaves;
   const uint32_t n_pairs = cand_count[0] * static_cast<uint32_t>(kv);
   const int C = hd / T::kEpc;
@@ -1768,62 +1771,120 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_sparse_kernel(
       lo = fmax(0.0, m - e) * inv;
       hi = (m + e) * inv;
     };
-    for (int r = 0; r < R; ++r) {
-      double lo_max = 0.0;
-      for (int q0 = 0; q0 < Qt; q0 += kWave) {
-        if (q0 + lane < Qt) {
-          double lo, hi;
-          bounds(r * Qt + q0 + lane, lo, hi);
-          lo_max = fmax(lo_max, lo);
-        }
-      }
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) lo_max = fmax(lo_max, __shfl_xor(lo_max, off));
-      double best = 0.0;  // the head's maximum |dot| over the columns evaluated
-      for (int q0 = 0; q0 < Qt; q0 += kWave) {
-        bool keep = false;
-        if (q0 + lane < Qt) {
-          double lo, hi;
-          bounds(r * Qt + q0 + lane, lo, hi);
-          keep = !(hi < lo_max);
-        }
-        uint64_t mask = __ballot(keep);
-        while (mask != 0ull) {
-          const int bit = __ffsll(static_cast<long long>(mask)) - 1;
-          mask &= mask - 1ull;
-          const int gc = r * Qt + q0 + bit;  // wave-uniform
-          const double* qcol = q64 + static_cast<size_t>(g) * hd * rqp + gc;
-          for (uint32_t t0 = 0; t0 < L; t0 += kWave) {
-            const uint32_t t = min(t0 + static_cast<uint32_t>(lane), L - 1u);
-            double acc = 0.0;
-            for (int c = 0; c < C; ++c) {
-              const u32x4 v = piece_ptr(kb, Lp, sS, t, c)[0];
-              float sc = 0.0f;
-              if constexpr (KDT == kI8) {
-                sc = load_scale(scales + (row0 * G + t) * ses, scale_dtype,
-                                static_cast<uint64_t>(c / cpg) * Lp);
-              }
-              float f[T::kEpc];
-              decode_chunk<KDT>(v, sc, f);
-#pragma unroll
-              for (int e = 0; e < T::kEpc; ++e) {
-                acc = fma(static_cast<double>(f[e]), qcol[static_cast<size_t>(c * T::kEpc + e) * rqp], acc);
+    // kept columns in (head, token) order, kSparseCols at a time: their
+    // query rows go to this wavefront's LDS rows, and each lane reads its
+    // token's key row once per group, one fp64 sum per column
+    double* qv = s_qv + static_cast<size_t>(wave) * kSparseCols * hd;
+    int r = 0, q0 = 0;
+    uint64_t mask = 0ull;
+    bool run_loaded = false;
+    double lo_max = 0.0;
+    auto next_col = [&]() -> int {
+      while (r < R) {
+        if (!run_loaded) {
+          if (q0 == 0) {
+            double m = 0.0;
+            for (int x0 = 0; x0 < Qt; x0 += kWave) {
+              if (x0 + lane < Qt) {
+                double lo, hi;
+                bounds(r * Qt + x0 + lane, lo, hi);
+                m = fmax(m, lo);
               }
             }
-            const double x = fabs(acc);
-            if (t0 + lane < L) best = (x > best || isnan(x)) ? x : best;
+#pragma unroll
+            for (int off = 1; off < kWave; off <<= 1) m = fmax(m, __shfl_xor(m, off));
+            lo_max = m;
+          }
+          bool keep = false;
+          if (q0 + lane < Qt) {
+            double lo, hi;
+            bounds(r * Qt + q0 + lane, lo, hi);
+            keep = !(hi < lo_max);
+          }
+          mask = __ballot(keep);
+          run_loaded = true;
+        }
+        if (mask != 0ull) {
+          const int bit = __ffsll(static_cast<long long>(mask)) - 1;
+          mask &= mask - 1ull;
+          return r * Qt + q0 + bit;
+        }
+        run_loaded = false;
+        q0 += kWave;
+        if (q0 >= Qt) {
+          q0 = 0;
+          ++r;
+        }
+      }
+      return -1;
+    };
+    const double* qb0 = q64 + static_cast<size_t>(g) * hd * rqp;
+    for (;;) {
+      int gcs[kSparseCols];
+      int n = 0;
+      for (int j = 0; j < kSparseCols; ++j) {
+        gcs[j] = n == j ? next_col() : -1;
+        if (gcs[j] >= 0) ++n;
+      }
+      if (n == 0) break;
+      // stage the group's query rows (unused rows zero)
+      for (int idx = lane; idx < kSparseCols * hd; idx += kWave) {
+        const int j = idx / hd;
+        const int d = idx - j * hd;
+        qv[idx] = j < n ? qb0[static_cast<size_t>(d) * rqp + gcs[j]] : 0.0;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      double best[kSparseCols];
+#pragma unroll
+      for (int j = 0; j < kSparseCols; ++j) best[j] = 0.0;
+      for (uint32_t t0 = 0; t0 < L; t0 += kWave) {
+        const uint32_t t = min(t0 + static_cast<uint32_t>(lane), L - 1u);
+        double acc[kSparseCols];
+#pragma unroll
+        for (int j = 0; j < kSparseCols; ++j) acc[j] = 0.0;
+        for (int c = 0; c < C; ++c) {
+          const u32x4 v = piece_ptr(kb, Lp, sS, t, c)[0];
+          float sc = 0.0f;
+          if constexpr (KDT == kI8) {
+            sc = load_scale(scales + (row0 * G + t) * ses, scale_dtype,
+                            static_cast<uint64_t>(c / cpg) * Lp);
+          }
+          float f[T::kEpc];
+          decode_chunk<KDT>(v, sc, f);
+#pragma unroll
+          for (int e = 0; e < T::kEpc; ++e) {
+            const double fe = static_cast<double>(f[e]);
+            const int d = c * T::kEpc + e;
+#pragma unroll
+            for (int j = 0; j < kSparseCols; ++j) acc[j] = fma(fe, qv[j * hd + d], acc[j]);
+          }
+        }
+        if (t0 + lane < L) {
+#pragma unroll
+          for (int j = 0; j < kSparseCols; ++j) {
+            const double x = fabs(acc[j]);
+            best[j] = (x > best[j] || isnan(x)) ? x : best[j];
           }
         }
       }
+      // the group's LDS rows are read before the next group writes them
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       // max(|dot|)/denom equals the law's max(|dot|/denom) (division by a
       // positive constant is monotone under rounding to nearest)
-      unsigned long long bits = __double_as_longlong(best / denom);
+      for (int j = 0; j < n; ++j) {
+        unsigned long long bits = __double_as_longlong(best[j] / denom);
 #pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const unsigned long long o = __shfl_xor(bits, off);
-        bits = o > bits ? o : bits;
+        for (int off = 1; off < kWave; off <<= 1) {
+          const unsigned long long o = __shfl_xor(bits, off);
+          bits = o > bits ? o : bits;
+        }
+        const int hr = gcs[j] / Qt;
+        if (lane == 0 && bits != 0ull) atomicMax(hmax + static_cast<size_t>(g * R + hr) * cap + slot, bits);
       }
-      if (lane == 0 && bits != 0ull) atomicMax(hmax + static_cast<size_t>(g * R + r) * cap + slot, bits);
     }
   }
 }

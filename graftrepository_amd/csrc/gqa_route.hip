@@ -1185,7 +1185,10 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
     const int rqp = rq_pad_of(p.R * p.Qt);
     const double denom = sqrt(static_cast<double>(a->hd));
 #define GRM_SPARSE(KDT)                                                                           \
-  grm::gqa::gqa_exact_sparse_kernel<KDT><<<blocks, grm::gqa::kUnitWaves * grm::kWave, 0, a->stream>>>( \
+  grm::gqa::gqa_exact_sparse_kernel<KDT><<<blocks, grm::gqa::kUnitWaves * grm::kWave,           \
+                                           grm::gqa::kUnitWaves * grm::gqa::kSparseCols *       \
+                                               a->hd * sizeof(double),                           \
+                                           a->stream>>>(                                         \
       a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->piece_shift, a->d_cslots,        \
       a->d_ccount, kv, p.R, p.Qt, static_cast<int>(a->hd), colstride, a->d_hmaxf, a->d_colinfo,  \
       a->d_kmax, fact ? 1 : 0, a->d_tok_off, a->d_len, a->d_q64, rqp, denom, a->d_hmax,          \
