@@ -1178,7 +1178,7 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
   // query wider than an exact pass takes only the columns its screen
   // cannot rule out (the query's rows as doubles are all in q64 from step
   // 1), others the exact kernel pass by pass
-  if (xpasses.size() > 1 && qb == 1 && a->sparse_exact) {
+  if (qb == 1 && a->sparse_exact) {
     const uint64_t pairs = a->cap_nodes * a->kv;
     const unsigned blocks = static_cast<unsigned>(
         std::max<uint64_t>(1, std::min<uint64_t>((pairs + grm::gqa::kUnitWaves - 1) / grm::gqa::kUnitWaves, 2048)));
