@@ -170,55 +170,29 @@ __device__ inline void decode_chunk(u32x4 v, float scale, float* out) {
 // lets a wave read the RQP values of one d as one wave-uniform (scalar)
 // load.  qflags[qb * kv + g] = 1 when a value of query qb read by kv head g
 // is non-finite; the first pass (flags_or = 0) writes 0 otherwise, later
-// passes leave the flag as it is.  grid (kv, Qb).  The values go through
-// LDS DC dims at a time (DC * (RQP + 1) <= 4096), read along d (the
-// query's contiguous axis) and written along j; rows wider than the stage
-// (RQP >= 4096) go straight from the query to q64.
-constexpr int kQ64Stage = 4096;  // doubles staged per round
+// passes leave the flag as it is.  grid (kv, Qb).
 __global__ __launch_bounds__(1024) void gqa_q64_kernel(
     const void* __restrict__ query, int q_dtype, size_t q_elems, int Qt, int Qc,
     int hd, int kv, int R, int Rc, int RQP, double* __restrict__ q64,
     unsigned* __restrict__ qflags, int flags_or) {
-  __shared__ double s_t[kQ64Stage + 64];  // [DC][RQP + 1]
   const int g = blockIdx.x;
   const int qb = blockIdx.y;
   const int rq = Rc * Qc;
-  double* out = q64 + static_cast<size_t>(qb * kv + g) * hd * RQP;
   bool bad = false;
-  auto value = [&](int j, int d) -> double {
-    if (j >= rq) return 0.0;
-    const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
-                         (static_cast<uint64_t>(g * R + j / Qc) * Qt + j % Qc) * hd + d;
-    const float f = q_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
-                                     : static_cast<const float*>(query)[src];
-    bad = bad || !isfinite(f);
-    return static_cast<double>(f);
-  };
-  if (RQP + 1 > kQ64Stage) {
-    for (int idx = threadIdx.x; idx < RQP * hd; idx += blockDim.x) {
-      const int d = idx / RQP;
-      const int j = idx - d * RQP;
-      out[static_cast<size_t>(d) * RQP + j] = value(j, d);
+  for (int idx = threadIdx.x; idx < RQP * hd; idx += blockDim.x) {
+    const int d = idx / RQP;
+    const int j = idx - d * RQP;
+    double v = 0.0;
+    if (j < rq) {
+      const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
+                           (static_cast<uint64_t>(g * R + j / Qc) * Qt + j % Qc) * hd + d;
+      const float f = q_dtype == kBF16
+                          ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
+                          : static_cast<const float*>(query)[src];
+      bad = bad || !isfinite(f);
+      v = static_cast<double>(f);
     }
-    bad = __syncthreads_or(bad);
-    if (threadIdx.x == 0 && (bad || !flags_or)) qflags[qb * kv + g] = bad ? 1u : 0u;
-    return;
-  }
-  const int DC = max(1, min(hd, kQ64Stage / (RQP + 1)));
-  for (int d0 = 0; d0 < hd; d0 += DC) {
-    const int dc = min(DC, hd - d0);
-    for (int idx = threadIdx.x; idx < dc * RQP; idx += blockDim.x) {
-      const int j = idx / dc;
-      const int dd = idx - j * dc;
-      s_t[dd * (RQP + 1) + j] = value(j, d0 + dd);
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < dc * RQP; idx += blockDim.x) {
-      const int dd = idx / RQP;
-      const int j = idx - dd * RQP;
-      out[static_cast<size_t>(d0 + dd) * RQP + j] = s_t[dd * (RQP + 1) + j];
-    }
-    __syncthreads();
+    q64[(static_cast<size_t>(qb * kv + g) * hd + d) * RQP + idx % RQP] = v;
   }
   bad = __syncthreads_or(bad);
   if (threadIdx.x == 0 && (bad || !flags_or)) qflags[qb * kv + g] = bad ? 1u : 0u;
