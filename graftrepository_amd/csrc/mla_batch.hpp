@@ -136,20 +136,22 @@ __global__ __launch_bounds__(kBatchWaves * kWave) void mla_batch_screen_kernel(
     med3_i32_into(b1[ct], b2[ct], v);
     b1[ct] = max(b1[ct], v);
   };
-  // Matrix-core chains: one dependent accumulation chain per wavefront
-  // issues a 32x32x16 MFMA only about every fourth slot of the matrix
-  // core (a result feeds the next step's accumulator after several times
-  // the issue interval), so the column tiles advance in groups of kG
-  // independent chains -- step ks issues the kG MFMAs of a[ks] with the
-  // group's kG query fragments -- and the group's 16*kG results are
-  // reduced once its chains end.  Query fragments stream from LDS kPre
-  // fragments ahead, across step and group boundaries.  In the tile's last
+  // Matrix-core chains: the column tiles advance in groups of kG
+  // independent accumulation chains -- step ks issues the kG MFMAs of a[ks]
+  // with the group's kG query fragments -- and the group's 16*kG results
+  // are reduced once its chains end.  With two wavefronts per SIMD, two
+  // chains keep the matrix core as busy as four (the other wavefront
+  // fills the gaps) and halve the stretch of MFMAs between reductions,
+  // which the other wavefront's reductions then overlap more evenly: 1M x
+  // 288 x 256 queries screened in 152 us with kG = 2 against 161 us with
+  // kG = 4.  Query fragments stream from LDS kPre fragments ahead, across
+  // step and group boundaries.  In the tile's last
   // group each a[ks] is reloaded with the next tile's fragment as soon as
   // its last MFMA has issued, so the next tile's loads are in flight
   // during the rest of the group and the reductions (no second tile
   // buffer is needed).  The reload is unconditional: after a wavefront's
   // last tile it reads that tile again (cached, and never folded).
-  constexpr int kG = CT < 4 ? CT : 4;
+  constexpr int kG = CT < 2 ? CT : 2;
   constexpr int kGroups = CT / kG;
   constexpr int kPre = 4;
   constexpr int kSteps = CT * KS;  // fragment stream: (group, ks, chain)
