@@ -605,8 +605,7 @@ def bench_gqa_f32_dropin(steps: int, warmup: int):
            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                         "kernel": "gqa_sr_kernel<f16, 4, 1, fp32 rows>",
-                        "bytes_per_call": bytes_copy},
-           "f32_equivalent_gbs": round(bytes_f32 / (mean_dev * 1e-3) / 1e9, 1)}
+                        "bytes_per_call": bytes_copy}}
     log(f"[gqa f32 drop-in] p50 {out['p50_ms']:.4f} ms  device {mean_dev:.4f} ms  "
         f"{ach:.0f} GB/s on the fp16 copy  parity {parity}  setup {setup_ms:.0f} ms")
     return out
@@ -1012,6 +1011,124 @@ def cpu_baseline_mla(m, seconds: float):
                 host=host_cpu())
 
 
+def reference_router_mla(rows, q, k, gpu_ids, seconds: float):
+    """The reference's own CPU router on the full 1M x 288 bank:
+    grm_store_route of its C++ store (cpp/grm_runtime.cpp:6767-6825 ->
+    route_mla_arena, :4299-4361), compiled from its sources into
+    oracle/_ref.  At 1M entries it scores with OpenMP over entries
+    (:4318-4322) on the process's OpenMP threads.  The store's first route
+    builds its snapshot and arena; that is reported apart and not timed."""
+    import ctypes
+
+    import oracle
+    import oracle.ref as oref
+
+    if not oracle.REF_LIB_PATH.exists():
+        return None
+    n, d = rows.shape
+    L = oref.lib()
+    t0 = time.perf_counter()
+    st = oref._Store(L.grm_store_create_mla(b"MiniCPM3_TC", 62, 2560, d, 0, d, 0))
+    try:
+        nid = ctypes.c_uint64()
+        for i in range(n):
+            st._check(L.grm_store_add_node(st.h, b"n", 1, None, 0, ctypes.byref(nid)))
+            st._check(L.grm_store_set_route(st.h, nid.value, rows[i].ctypes.data, d, b""))
+            if (i + 1) % 250_000 == 0:
+                log(f"[ref mla] {i + 1} entries stored ({time.perf_counter() - t0:.0f}s)")
+        load_s = time.perf_counter() - t0
+        out = np.empty(k, dtype=np.uint64)
+        cnt = ctypes.c_uint64()
+        q1 = np.ascontiguousarray(q[0], dtype=np.float32)
+
+        def route():
+            st._check(L.grm_store_route(st.h, q1.ctypes.data, d, b"", k, out.ctypes.data, k,
+                                        ctypes.byref(cnt)))
+
+        t0 = time.perf_counter()
+        route()
+        first_ms = (time.perf_counter() - t0) * 1e3
+        times = time_cpu(route, seconds, warmup=1, min_calls=3, max_calls=20)
+        match = bool(np.array_equal(out[:cnt.value], gpu_ids))
+    finally:
+        st.close()
+    r = dict(cpu_figure(times, cpu_threads_all()), kind="reference",
+             what="grm_store_route of the reference's C++ store, compiled from "
+                  "cpp/grm_runtime.cpp into oracle/_ref; OpenMP over the 1,000,000 entries "
+                  "(cpp/grm_runtime.cpp:4318-4322)",
+             sample="the full workload", ids_match_gpu=match,
+             store_load_s=round(load_s, 1), first_route_ms=round(first_ms, 1))
+    log(f"[ref mla] grm_store_route p50 {r['p50_ms']:.1f} ms on {r['threads']} threads "
+        f"(load {load_s:.0f}s, first route {first_ms:.0f} ms), ids match GPU: {match}")
+    return r
+
+
+def reference_router_gqa(keys_bits, offs, kv, hd, q_bits, k, seconds: float,
+                         sample_nodes: int = 128):
+    """The reference's own CPU router on the ragged bank, sampled:
+    grm_store_route_gqa (cpp/grm_runtime.cpp:6898-6961 -> route_gqa_raw,
+    :4498-4881) over one fp32 key [kv, L_i, hd] per node (the bf16 keys,
+    widened), which takes its default fp32 arena path
+    (gqa_arena_key_score, :3588-3671).  Its route time is linear in the
+    bank's tokens, but its arena build (the first route after a change)
+    reserves each key's rows exactly (:3350), so it copies the arena once
+    per key and grows with the square of the node count: over two minutes
+    at 512 nodes.  The store therefore holds the first `sample_nodes`
+    nodes, the route is timed on them and scaled to the whole bank's
+    tokens, and its ids are checked against the oracle's fp64 law on the
+    same sample."""
+    import ctypes
+
+    import oracle
+    import oracle.ref as oref
+    from graftrepository_amd.node_bank import bf16_bits_to_f32
+
+    if not oracle.REF_LIB_PATH.exists():
+        return None
+    L = oref.lib()
+    H, Qt = q_bits.shape[1], q_bits.shape[2]
+    qf = np.ascontiguousarray(bf16_bits_to_f32(q_bits).reshape(H, Qt, hd))
+    m = min(sample_nodes, offs.size - 1)
+    st = oref._Store(L.grm_store_create_gqa(b"Qwen3_TC", 36, 2560, 2 * kv * hd, 0, kv, hd))
+    try:
+        for i in range(m):
+            a, b = int(offs[i]), int(offs[i + 1])
+            blk = bf16_bits_to_f32(keys_bits[a * kv * hd:b * kv * hd]).reshape(kv, b - a, hd)
+            st.set_route_list(st.add_node(), [blk])
+        out = np.empty(k, dtype=np.uint64)
+        cnt = ctypes.c_uint64()
+
+        def route():
+            st._check(L.grm_store_route_gqa(st.h, qf.ctypes.data, H, Qt, hd, b"", b"", b"", b"",
+                                            b"", k, out.ctypes.data, k, ctypes.byref(cnt)))
+
+        t0 = time.perf_counter()
+        route()
+        first_ms = (time.perf_counter() - t0) * 1e3
+        times = time_cpu(route, seconds, warmup=1, min_calls=3, max_calls=50)
+        got = out[:cnt.value].copy()
+    finally:
+        st.close()
+    tok_s, tok = int(offs[m]), int(offs[-1])
+    law_ids, _, _ = oracle.gqa_route(keys_bits[:tok_s * kv * hd], oracle.BF16, offs[:m + 1],
+                                     kv, hd, qf[None], k)
+    match = bool(np.array_equal(got, law_ids[0]))
+    scale = tok / tok_s
+    r = {"value": round(pct(times, 50) * scale, 3), "unit": "ms", "threads": cpu_threads_all(),
+         "kind": "reference",
+         "what": "grm_store_route_gqa of the reference's C++ store, compiled from "
+                 "cpp/grm_runtime.cpp into oracle/_ref; its default fp32 arena path "
+                 "(cpp/grm_runtime.cpp:3588-3671, 4498-4881)",
+         "sample": f"the first {m} of {offs.size - 1} nodes ({tok_s} of {tok} tokens), "
+                   f"p50 over {len(times)} routes scaled by the token ratio {scale:.3f}",
+         "sample_p50_ms": round(pct(times, 50), 3), "sample_p95_ms": round(pct(times, 95), 3),
+         "ids_match_oracle_on_sample": match, "first_route_ms": round(first_ms, 1)}
+    log(f"[ref gqa] grm_store_route_gqa {r['sample_p50_ms']:.2f} ms on {m} nodes -> "
+        f"{r['value']:.1f} ms for the bank on {r['threads']} threads (first route "
+        f"{first_ms:.0f} ms), ids match the fp64 law on the sample: {match}")
+    return r
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1077,6 +1194,15 @@ def main() -> int:
     cpu = None
     if m is not None and not args.skip_cpu:
         cpu = cpu_baseline_mla(m, args.cpu_seconds)
+    if not args.skip_cpu:
+        # the reference's own CPU router, after every GPU leg
+        if g is not None and g["cpu"] is not None:
+            g["cpu"]["reference_router"] = reference_router_gqa(
+                g["keys"], g["offs"], g["kv"], g["cfg"]["head_dim"], g["q"],
+                g["cfg"]["topk"], args.cpu_seconds * 0.3)
+        if cpu is not None:
+            cpu["reference_router"] = reference_router_mla(
+                m["rows"], m["q"], m["cfg"]["topk"], m["ids"], args.cpu_seconds * 0.5)
 
     if m is not None:
         cfg = m["cfg"]

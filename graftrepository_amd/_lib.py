@@ -116,6 +116,7 @@ SIGNATURES = {
     "grm_hip_device_free": (i32, [vp]),
     "grm_hip_copy_to_host": (i32, [vp, vp, u64]),
     "grm_hip_copy_to_device": (i32, [vp, vp, u64]),
+    "grm_hip_synth_int8_rows": (i32, [u64, u64, u64, i32, vp, i32, vp, vp]),
 }
 
 _libs: dict[str, ctypes.CDLL] = {}

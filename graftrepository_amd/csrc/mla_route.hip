@@ -1216,8 +1216,11 @@ int enqueue_latent_query(MlaDeviceArena* a, const void* d_latent, int dtype, uin
 // the array from load to process end, and host code reaches it only through
 // the address hipGetSymbolAddress returns for the current device (the
 // array's name in host code is a host-side stand-in, not a device address).
-// Every call on one GPU shares that GPU's array: calls that overlap on a
-// GPU race.  Queries run one after another on the bank's stream, so one
+// Every call on one GPU shares that GPU's array, so calls on one GPU are
+// serialised by a per-device mutex held from the first launch until the
+// bank's stream has drained (on the error path too): two host threads
+// routing different banks on one GPU take turns and each gets its own
+// answer.  Queries run one after another on the bank's stream, so one
 // query's lists fit the array: up to kScratchCands entries (grid blocks x
 // topk; 1024 blocks x 16 at most with the default grid cap).  Each block
 // writes all k of its entries before the merge reads them, so nothing in
@@ -1226,6 +1229,8 @@ constexpr int kScratchDevices = 64;
 
 std::mutex g_scratch_mu;
 Cand* g_scratch_ptr[kScratchDevices] = {};
+// Held by a call from its first launch until its stream has drained.
+std::mutex g_noalloc_mu[kScratchDevices];
 
 // Device address of this device's scratch (the device must be current).
 int scratch_for(int device, Cand** out) {
@@ -1282,18 +1287,28 @@ int route_noalloc(MlaDeviceArena* a, const void* d_queries, int q_dtype, int q_c
   GRM_HIP_CHECK(hipSetDevice(a->device));
   Cand* lists = nullptr;
   GRM_CHECK_RC(scratch_for(a->device, &lists));
-  if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
+  std::lock_guard<std::mutex> hold(g_noalloc_mu[a->device]);
   const size_t qstride = static_cast<size_t>(a->dim) * elem_size(q_dtype);
   const unsigned char* qbase = static_cast<const unsigned char*>(d_queries);
-  for (int qi = 0; qi < q_count; ++qi) {
-    GRM_CHECK_RC(launch_single(a, g, qbase + qi * qstride, q_dtype, topk, lists));
-    mla_merge_out_kernel<<<1, grm::kMergeWaves * grm::kWave, 0, a->stream>>>(
-        lists, static_cast<uint32_t>(per_q), topk, d_out_ids + static_cast<size_t>(qi) * topk,
-        d_out_scores ? d_out_scores + static_cast<size_t>(qi) * topk : nullptr);
-    GRM_HIP_CHECK(hipGetLastError());
-  }
+  auto launch_all = [&]() -> int {
+    if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
+    for (int qi = 0; qi < q_count; ++qi) {
+      GRM_CHECK_RC(launch_single(a, g, qbase + qi * qstride, q_dtype, topk, lists));
+      mla_merge_out_kernel<<<1, grm::kMergeWaves * grm::kWave, 0, a->stream>>>(
+          lists, static_cast<uint32_t>(per_q), topk,
+          d_out_ids + static_cast<size_t>(qi) * topk,
+          d_out_scores ? d_out_scores + static_cast<size_t>(qi) * topk : nullptr);
+      GRM_HIP_CHECK(hipGetLastError());
+    }
+    return 0;
+  };
+  const int rc = launch_all();
+  // Drain before the lock is released, also when a launch failed part way:
+  // kernels already queued still write this GPU's scratch.
+  const hipError_t sync = hipStreamSynchronize(a->stream);
+  if (rc != 0) return rc;
+  GRM_HIP_CHECK(sync);
   a->single_queries += static_cast<uint64_t>(q_count);
-  GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
   grm::clear_error();
   return 0;
 }

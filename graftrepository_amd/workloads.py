@@ -10,6 +10,8 @@ generators produce the same shapes and distributions without a model:
   (bf16 by default), lengths uniform or lognormal; queries [H, Qt, hd].
   Stacked routing layers fold into the head axes: kv head g of layer y is
   bank head y*KV+g, query head h of layer y is y*H+h (so kv head = h'/R).
+* INT8 ragged banks: N(0, 1) keys quantised per (kv head, token) row by the
+  packed graft format's law with an fp16 scale (gqa_int8_bank).
 
 Every generator is a pure function of its arguments and seed.
 """
@@ -100,68 +102,74 @@ def gqa_bank(lengths: np.ndarray, kv_heads: int, head_dim: int, seed: int,
     return out, offs
 
 
-_SM1 = np.uint64(0x9E3779B97F4A7C15)
-_SM2 = np.uint64(0xBF58476D1CE4E5B9)
-_SM3 = np.uint64(0x94D049BB133111EB)
+def quantize_rows_i8(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The packed graft format's symmetric INT8 quantiser
+    (core/graft_quant.py:93-131, bits = 8) with one group per row and the
+    scale stored as fp16: scale = max|row| / 127 in fp32 (0 -> 1), rounded
+    to fp16 (0 -> 1), codes = clip(round_half_even(row / scale), -128, 127)
+    against the stored scale.  x: float32 [rows, d].  Returns (codes int8
+    [rows, d], scales as fp16 bits [rows])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    scale = np.abs(x).max(axis=1) / np.float32(127.0)
+    scale[scale == 0] = np.float32(1.0)
+    s16 = scale.astype(np.float16)
+    s16[s16 == 0] = np.float16(1.0)
+    y = x / s16.astype(np.float32)[:, None]
+    np.rint(y, out=y)
+    np.clip(y, -128.0, 127.0, out=y)
+    return y.astype(np.int8), s16.view(np.uint16)
 
 
-def _splitmix_fill(out: np.ndarray, start: int, seed: int) -> None:
-    """out[i] = splitmix64 finaliser of ((start + i) * golden + seed): a
-    counter-based stream, so any slice can be filled independently."""
-    blk = 1 << 18
-    tmp = np.empty(min(blk, out.size), dtype=np.uint64)
-    key = np.uint64(seed & 0xFFFFFFFFFFFFFFFF)
-    for i in range(0, out.size, blk):
-        n = min(blk, out.size - i)
-        z = out[i:i + n]
-        t = tmp[:n]
-        z[:] = np.arange(start + i, start + i + n, dtype=np.uint64)
-        z *= _SM1
-        z += key
-        np.right_shift(z, np.uint64(30), out=t)
-        z ^= t
-        z *= _SM2
-        np.right_shift(z, np.uint64(27), out=t)
-        z ^= t
-        z *= _SM3
-        np.right_shift(z, np.uint64(31), out=t)
-        z ^= t
+_NORMAL_TABLE: np.ndarray | None = None
+
+
+def _normal_table() -> np.ndarray:
+    """The 65,536 quantiles Phi^-1((i + 0.5) / 65536) of N(0, 1) as
+    float32: a uniform 16-bit index looked up here is a standard normal
+    draw discretised to 2^16 equiprobable levels (tails to about 4.3)."""
+    global _NORMAL_TABLE
+    if _NORMAL_TABLE is None:
+        from statistics import NormalDist
+
+        inv = NormalDist().inv_cdf
+        _NORMAL_TABLE = np.asarray([inv((i + 0.5) / 65536.0) for i in range(65536)],
+                                   dtype=np.float32)
+    return _NORMAL_TABLE
+
+
+def int8_stream_key(seed: int) -> int:
+    """The 64-bit key of the synthetic INT8 key stream for `seed`."""
+    return (int(seed) * 0xD1B54A32D192ED03 + 0x2545F4914F6CDD1D) & 0xFFFFFFFFFFFFFFFF
 
 
 def gqa_int8_bank(lengths: np.ndarray, kv_heads: int, head_dim: int, seed: int,
                   workers: int = 16) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
-    """INT8 CSR bank in the packed graft format: codes (node blocks
-    [kv, L_i, hd] back to back, int8), one fp16 scale per (kv head, token)
-    row (group size = head_dim; fp16 bits) and tok_offsets [N+1].
+    """INT8 CSR bank in the packed graft format: N(0, 1) keys quantised row
+    by row (the law of quantize_rows_i8: one fp16 scale per (kv head,
+    token) row, group size = head_dim).  Returns codes (node blocks
+    [kv, L_i, hd] back to back, int8), scales (fp16 bits, one per row, in
+    row order) and tok_offsets [N+1].
 
-    Codes are uniform in [-127, 127] (the bytes of a splitmix64 counter
-    stream, -128 folded to -127) and scales uniform in [2, 4] / 127 (the
-    symmetric code range of rows whose absolute maximum lies in [2, 4]).
-    `workers` threads fill fixed 32 MiB chunks of the counter stream, so
-    banks of tens of GB build in seconds on the host and the result
-    depends only on (lengths, kv_heads, head_dim, seed)."""
-    from concurrent.futures import ThreadPoolExecutor
+    Row r's keys are normal quantiles (_normal_table) of the 16-bit words
+    of a splitmix64 counter stream at word indices r * hd/4 ... (key
+    int8_stream_key(seed)); the library's host generator
+    (grm_hip_synth_int8_rows) draws and quantises them on `workers`
+    threads, so the bank is a pure function of (lengths, kv_heads,
+    head_dim, seed) and banks of tens of GB build in seconds."""
+    from . import _lib
 
+    if head_dim % 4:
+        raise ValueError("head_dim must be a multiple of 4")
     lengths = np.asarray(lengths, dtype=np.uint64)
     offs = np.zeros(lengths.size + 1, dtype=np.uint64)
     offs[1:] = np.cumsum(lengths)
     rows = int(offs[-1]) * kv_heads
-    n_codes = rows * head_dim
-    words = np.empty((n_codes + 7) // 8, dtype=np.uint64)
-    step = 1 << 22
-    key = (int(seed) * 0xD1B54A32D192ED03 + 0x2545F4914F6CDD1D) & 0xFFFFFFFFFFFFFFFF
-
-    def fill(i):
-        seg = words[i:i + step]
-        _splitmix_fill(seg, i, key)
-        b = seg.view(np.int8)
-        np.maximum(b, -127, out=b)
-
-    with ThreadPoolExecutor(max_workers=max(1, workers)) as ex:
-        list(ex.map(fill, range(0, words.size, step)))
-    codes = words.view(np.int8)[:n_codes]
-    rng = _rng(seed + 0x5CA1E)
-    scales = (rng.uniform(2.0, 4.0, size=rows) / 127.0).astype(np.float16).view(np.uint16)
+    codes = np.empty(rows * head_dim, dtype=np.int8)
+    scales = np.empty(rows, dtype=np.uint16)
+    table = _normal_table()
+    _lib.check(_lib.load().grm_hip_synth_int8_rows(
+        int8_stream_key(seed), 0, rows, head_dim, table.ctypes.data, max(1, workers),
+        codes.ctypes.data, scales.ctypes.data), "synthetic INT8 rows")
     return codes, scales, offs
 
 

@@ -153,8 +153,8 @@ int grm_mla_hip_route(MlaDeviceArena* arena, const void* queries,
                       float* out_scores_host, float* elapsed_ms_host);
 
 /* Allocation-free variant of grm_mla_hip_route for callers that cannot
- * allocate device or host memory (code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * allocate device or host memory (tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the
  * reference.  Queries are device memory [query_count][dim] (F32 or BF16
  * bits); results go to device memory: d_out_ids [query_count][topk] and
  * d_out_scores (may be NULL), unfilled slots UINT64_MAX / NaN.  Every query
@@ -162,8 +162,11 @@ int grm_mla_hip_route(MlaDeviceArena* arena, const void* queries,
  * The per-block lists live in a fixed 256 KiB device array inside the
  * library (one per GPU, held until the process ends); a route whose grid
  * blocks x topk exceed its 16384 entries is refused with -1.  The call
- * allocates nothing and returns once the outputs are written.  Calls that
- * overlap on one GPU share that array and race. */
+ * allocates nothing and returns once the outputs are written.  Calls on
+ * one GPU share that array, so they are serialised: a per-device lock is
+ * held from the first launch until the bank's stream has drained.  The
+ * work runs on the bank's own stream and the call synchronizes it, so it
+ * cannot be recorded into a caller's HIP graph. */
 int grm_mla_hip_route_noalloc(MlaDeviceArena* arena, const void* d_queries,
                               int query_dtype, int query_count, int dim,
                               int topk, uint64_t* d_out_ids,
@@ -476,6 +479,20 @@ int grm_hip_device_alloc(uint64_t bytes, void** out_ptr);
 int grm_hip_device_free(void* ptr);
 int grm_hip_copy_to_host(void* host, const void* device, uint64_t bytes);
 int grm_hip_copy_to_device(void* device, const void* host, uint64_t bytes);
+
+/* ---- Synthetic workload keys (host only) --------------------------------
+ * Rows [row0, row0 + rows) of the synthetic INT8 key stream: each row's dim
+ * values are normal quantiles (normal_table[65536], the caller's table of
+ * Phi^-1((u + 0.5) / 65536)) indexed by 16-bit words of a splitmix64
+ * counter stream keyed by `key`, quantised by the packed graft format's
+ * law (core/graft_quant.py:93-131) with one group per row and the scale
+ * stored as fp16.  Writes codes [rows][dim] int8 and scales_f16 [rows]
+ * (fp16 bits) on `threads` host threads.  No counterpart in the reference;
+ * it builds benchmark and test banks and is on no route path.  dim must be
+ * a multiple of 4. */
+int grm_hip_synth_int8_rows(uint64_t key, uint64_t row0, uint64_t rows, int dim,
+                            const float* normal_table, int threads, int8_t* codes,
+                            uint16_t* scales_f16);
 
 #ifdef __cplusplus
 }

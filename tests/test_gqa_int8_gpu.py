@@ -1,19 +1,23 @@
 """Large ragged GQA route over INT8 graft storage on the GPU.
 
 Workload: node lengths lognormal (median 256, sigma 0.5, capped at 4096),
-8 kv heads x head_dim 128 stored as INT8 codes with one fp16 scale per
-(kv head, token) row (the packed graft format, core/graft_quant.py:136-144
-dequantises fp16(code * scale)), 32 query heads in bf16, 16 queries
-batched, top-5, with 1% of the nodes evicted and as many appended between
-routes.
+8 kv heads x head_dim 128: N(0, 1) keys quantised to INT8 codes with one
+fp16 scale per (kv head, token) row (the packed graft format's quantiser,
+core/graft_quant.py:93-131, group = head_dim; dequantised as
+fp16(code * scale), :136-144), 32 query heads in bf16, 16 queries batched,
+top-5, with 1% of the nodes evicted and as many appended between routes.
 
 * At a size the oracle finishes in seconds: node ids and scores bit-exact
   against the oracle's route over the live nodes after every churn round.
-* At the full 100,000-node size (about 30 GB of codes): the certified
-  screen-and-refine path against the exact fp64 path of the same library
-  (ids and score bits), the returned nodes and a random sample of 2,000
-  nodes through the oracle (its top-5 over that subset must be the GPU's
-  global top-5, scores bit-exact), before and after a 1% churn round.
+* At the full 100,000-node size (about 30 GB of codes), before and after a
+  1% churn round:
+  - the certified screen path against the exact fp64 path of the same
+    library (ids and score bits, all 16 queries);
+  - 2 of the 16 queries through the oracle over every live node (ids and
+    score bits);
+  - the other queries: the returned nodes plus a random sample of 2,000
+    nodes through the oracle (its top-5 over that subset must be the GPU's
+    global top-5, scores bit-exact).
 """
 
 import os
@@ -107,7 +111,7 @@ def test_int8_lognormal_churn_matches_oracle(hip_lib):
         assert_same(res, ids, sc)
 
 
-@pytest.mark.timeout(900)
+@pytest.mark.timeout(1100)
 def test_int8_config_size_screen_vs_exact_and_oracle(hip_lib):
     cfg = wl.GQA_INT8
     n, k = cfg["nodes"], cfg["topk"]
@@ -140,8 +144,22 @@ def test_int8_config_size_screen_vs_exact_and_oracle(hip_lib):
                                     rng.choice(live, size=2000, replace=False))
                 ids, sc, _ = mirror.route(qf, k, ids=sample)
                 assert_same(r1, ids, sc)
-                print(f"[int8 config] round {rnd}: screen path == exact path == oracle "
-                      f"on {sample.size} nodes", flush=True)
+                # two whole queries through the oracle over every live node
+                # (the first round routes the generated arrays as they are)
+                full = [0, 1 + 7 * rnd]
+                if rnd == 0:
+                    ids, sc, _ = oracle.gqa_route(
+                        codes, oracle.I8, offs, KV, HD, qf[full], k, scales=scales,
+                        scale_dtype="f16", group_size=HD, node_ids=ids0,
+                        threads=min(16, os.cpu_count() or 1))
+                else:
+                    ids, sc, _ = mirror.route(qf[full], k)
+                np.testing.assert_array_equal(r1.ids[full], ids)
+                np.testing.assert_array_equal(r1.scores[full].view(np.uint32),
+                                              sc.view(np.uint32))
+                print(f"[int8 config] round {rnd}: screen path == exact path; oracle "
+                      f"on {sample.size} nodes, and queries {full} on all {live.size} "
+                      f"nodes", flush=True)
                 ev = rng.choice(live, size=n // 100, replace=False)
                 fast.evict(ev)
                 exact.evict(ev)

@@ -5,7 +5,11 @@ Bar: ids and score bits equal on every query, on two calls in a row, the
 second on a smaller bank with fewer grid blocks and a smaller topk, so a
 stale list the first call left in the shared scratch array would show.
 The outputs also match the oracle (the allocating route's own bar).
+A two-thread case routes two banks on one GPU at the same time, many
+times over, and every answer must equal the oracle's.
 """
+
+import threading
 
 import numpy as np
 import pytest
@@ -84,3 +88,54 @@ def test_noalloc_rejects_bad_arguments(hip_lib):
                                              None) == -1
         assert lib.grm_mla_hip_route_noalloc(bank._h, dq.ptr, F32, 1, 32, 3, None, None) == -1
         assert b"null" in lib.grm_hip_last_error()
+
+def test_noalloc_two_threads_two_banks(hip_lib):
+    """Two host threads, each routing its own bank on the same GPU through
+    the allocation-free entry, start together and call it repeatedly (ctypes
+    releases the GIL, so the calls overlap on the host).  Every result must
+    equal the oracle's ids and score bits."""
+    lib = hip_lib
+    rows_a = wl.mla_rows(200_000, 288, seed=81)
+    qs_a = wl.mla_queries(2, 288, seed=81)
+    rows_b = wl.mla_rows(120_000, 128, seed=82)
+    qs_b = wl.mla_queries(3, 128, seed=82)
+    want_a = oracle.mla_route(rows_a, qs_a, 8)[:2]
+    want_b = oracle.mla_route(rows_b, qs_b, 5)[:2]
+    reps = 40
+    start = threading.Barrier(2)
+    errors: list = []
+    results: dict = {}
+
+    def worker(name, bank, qs, topk):
+        try:
+            q_count = qs.shape[0]
+            outs = []
+            with DeviceArray.from_host(qs) as dq, \
+                    DeviceArray((q_count, topk), np.uint64) as d_ids, \
+                    DeviceArray((q_count, topk), np.float32) as d_sc:
+                start.wait(timeout=60)
+                for _ in range(reps):
+                    rc = lib.grm_mla_hip_route_noalloc(bank._h, dq.ptr, F32, q_count, bank.dim,
+                                                       topk, d_ids.ptr, d_sc.ptr)
+                    if rc != 0:
+                        raise RuntimeError(f"rc {rc}: {lib.grm_hip_last_error()}")
+                    outs.append((d_ids.to_host(), d_sc.to_host()))
+            results[name] = outs
+        except BaseException as exc:  # reported by the main thread
+            errors.append((name, exc))
+            start.abort()
+
+    with MlaNodeBank(rows_a) as bank_a, MlaNodeBank(rows_b) as bank_b:
+        threads = [threading.Thread(target=worker, args=("a", bank_a, qs_a, 8)),
+                   threading.Thread(target=worker, args=("b", bank_b, qs_b, 5))]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=120)
+        assert not any(t.is_alive() for t in threads), "a routing thread did not finish"
+    assert not errors, errors
+    assert len(results["a"]) == reps and len(results["b"]) == reps
+    for got in results["a"]:
+        assert_same(got, want_a)
+    for got in results["b"]:
+        assert_same(got, want_b)
