@@ -31,6 +31,22 @@ and the bytes uploaded.
 A route result depends only on the set of (node id, row) pairs, not on the
 slots that hold them: ties go to the lower node id.  So a bank updated this
 way answers exactly as a bank built from scratch over the same rows.
+
+Two cases send the reference's arena to its CPU path; the bridges serve
+both on the device:
+
+* Digest nodes (grafts with ``child_cents``) score the best of their own
+  key and their children's (core/graft_arena.py:803-811), the law of a
+  store entry with several keys (cpp/grm_runtime.cpp:3518-3545, 3031-3051).
+  The reference's CUDA walk declines any arena holding one (:1141-1142,
+  2951).  Here their keys sit in a second device bank of the same kind,
+  scored exactly on every route, and each digest node's best finite key
+  score joins the main bank's top k.
+* ``length_debias`` (:839-874): the route ranks raw / sqrt(log2(K + 1))
+  (raw * that factor for a negative raw score), K the node's route key
+  length (:813-837).  The reference leaves its native and CUDA routes for
+  its Python path when it is on (:686-687).  Here every eligible node is
+  scored exactly on the device and the ranking applies the factor.
 """
 
 from __future__ import annotations
@@ -63,12 +79,73 @@ class RowSet(NamedTuple):
                 and np.array_equal(self.extents, other.extents))
 
 
-def _walk_mla(grafts):
+class Digest(NamedTuple):
+    """Digest nodes of a walk: node ``node_ids[i]`` (graft ``gidx[i]``) has
+    the keys ``keys[offs[i]:offs[i + 1]]``, its own centroid first and then
+    its ``child_cents`` (core/graft_arena.py:803-811).  ``sig`` holds each
+    node's id with the ids and extents of its key objects: an unchanged
+    ``sig`` keeps the side bank."""
+    node_ids: np.ndarray
+    offs: np.ndarray
+    keys: list
+    gidx: list
+    sig: tuple
+    pinned: list
+
+
+def route_key_length(g) -> int:
+    """The reference's route key length K of a graft
+    (core/graft_arena.py:813-837): the token axis of a key with two or
+    more dims, else the graft's ``ntok``; 1 when missing or malformed."""
+    cent = g.get("cent")
+    if cent is not None:
+        shape = np.asarray(cent).shape
+        if len(shape) >= 2:
+            try:
+                return max(1, int(shape[-2]))
+            except (TypeError, ValueError, OverflowError):
+                pass
+    try:
+        return max(1, int(g.get("ntok", 1)))
+    except (TypeError, ValueError, OverflowError):
+        return 1
+
+
+def length_debias_factor(key_length) -> np.ndarray:
+    """sqrt(log2(K + 1)) in float64 (core/graft_arena.py:839-846), K >= 1."""
+    k = np.maximum(np.asarray(key_length, dtype=np.float64), 1.0)
+    return np.sqrt(np.log2(k + 1.0))
+
+
+def apply_length_debias(scores, key_length) -> np.ndarray:
+    """raw / sqrt(log2(K + 1)) for raw >= 0, raw * sqrt(log2(K + 1)) below
+    zero, in float64 (core/graft_arena.py:848-874)."""
+    raw = np.asarray(scores, dtype=np.float32).astype(np.float64)
+    n = length_debias_factor(key_length)
+    return np.where(raw >= 0.0, raw / n, raw * n)
+
+
+def _digest(nids, keysets, gidx):
+    offs = np.zeros(len(keysets) + 1, dtype=np.int64)
+    offs[1:] = np.cumsum([len(k) for k in keysets])
+    keys = [k for ks in keysets for k, _ in ks]
+    pinned = [o for ks in keysets for _, o in ks]
+    sig = tuple((int(n), tuple(id(o) for _, o in ks), tuple(k.shape for k, _ in ks))
+                for n, ks in zip(nids, keysets))
+    return Digest(np.asarray(nids, dtype=np.uint64), offs, keys, list(gidx), sig, pinned)
+
+
+def _walk_mla(grafts, digests: bool = False, lengths: bool = False):
     """The MLA walk (core/graft_arena.py:1124-1162): rows are the grafts
     that are neither retired nor recall entries (:1139-1140).  Returns
-    ``(RowSet, rows, graft_indices, cents)`` or None."""
+    ``(RowSet, rows, graft_indices, cents, Digest or None, key lengths or
+    None)`` or None.  A graft with ``child_cents`` makes the walk decline,
+    as the reference's does, unless ``digests``: its keys then go to the
+    Digest part.  ``lengths``: each row's and digest node's K."""
     rows, nids, cids, gidx = [], [], [], []
     add_row, add_nid, add_cid, add_g = rows.append, nids.append, cids.append, gidx.append
+    d_nids, d_keys, d_gidx = [], [], []
+    klen, d_klen = [], []
     dim = None
     f32 = np.dtype(np.float32)
     ndarray = np.ndarray
@@ -76,7 +153,8 @@ def _walk_mla(grafts):
         get = g.get
         if get("retired") or get("kind", "turn") == "recall":
             continue
-        if get("child_cents"):
+        children = get("child_cents")
+        if children and not digests:
             return None
         node_id = get("native_node_id")
         cent = get("cent")
@@ -91,59 +169,104 @@ def _walk_mla(grafts):
             if dim is not None:
                 return None
             dim = n
+        nid = node_id if type(node_id) is int else int(node_id)
+        if children:
+            ks = [(key, cent)]
+            for ch in children:
+                k = np.asarray(ch, dtype=np.float32).reshape(-1)
+                if k.shape[0] != dim:
+                    return None
+                ks.append((k, ch))
+            d_nids.append(nid)
+            d_keys.append(ks)
+            d_gidx.append(i)
+            if lengths:
+                d_klen.append(route_key_length(g))
+            continue
         add_row(key)
-        add_nid(node_id if type(node_id) is int else int(node_id))
+        add_nid(nid)
         add_cid(id(cent))
         add_g(i)
-    if not rows:
+        if lengths:
+            klen.append(route_key_length(g))
+    if not rows and not d_nids:
         return None
     rs = RowSet(np.asarray(nids, dtype=np.uint64), np.asarray(cids, dtype=np.int64),
                 np.full(len(rows), dim, dtype=np.int64))
     cents = [g["cent"] for g in (grafts[i] for i in gidx)]
-    return rs, rows, gidx, cents
+    dg = _digest(d_nids, d_keys, d_gidx) if d_nids else None
+    kl = (np.asarray(klen, dtype=np.int64), np.asarray(d_klen, dtype=np.int64)) if lengths else None
+    return rs, rows, gidx, cents, dg, kl
 
 
-def _walk_gqa(grafts):
+def _gqa_key(cent):
+    key = np.asarray(cent, dtype=np.float32)
+    if key.ndim != 3 or any(int(d) <= 0 for d in key.shape):
+        return None
+    if not np.isfinite(key).all():
+        return None
+    return key
+
+
+def _walk_gqa(grafts, digests: bool = False, lengths: bool = False):
     """The GQA walk (core/graft_arena.py:2933-2977): keys are
     ``[kv_heads, tokens, head_dim]``, may differ only in their token
     extent, and must be finite.  Returns ``(RowSet, rows, graft_indices,
-    cents)`` or None."""
+    cents, Digest or None, key lengths or None)`` or None; ``digests`` and
+    ``lengths`` as in the MLA walk."""
     rows, nids, cids, lens, gidx, cents = [], [], [], [], [], []
+    d_nids, d_keys, d_gidx = [], [], []
+    klen, d_klen = [], []
     geometry = None
     for i, g in enumerate(grafts):
         if g.get("retired") or g.get("kind", "turn") == "recall":
             continue
         node_id = g.get("native_node_id")
-        if node_id is None or g.get("child_cents") or "cent" not in g:
+        children = g.get("child_cents")
+        if node_id is None or (children and not digests) or "cent" not in g:
             return None
         cent = g["cent"]
-        key = np.asarray(cent, dtype=np.float32)
-        if key.ndim != 3 or any(int(d) <= 0 for d in key.shape):
-            return None
-        if not np.isfinite(key).all():
-            return None
-        geo = (int(key.shape[0]), int(key.shape[2]))
-        if geometry is None:
-            geometry = geo
-        elif geo != geometry:
-            return None
+        ks = [(cent, cent)] + [(ch, ch) for ch in (children or ())]
+        checked = []
+        for raw, obj in ks:
+            key = _gqa_key(raw)
+            if key is None:
+                return None
+            geo = (int(key.shape[0]), int(key.shape[2]))
+            if geometry is None:
+                geometry = geo
+            elif geo != geometry:
+                return None
+            checked.append((key, obj))
+        if children:
+            d_nids.append(int(node_id))
+            d_keys.append(checked)
+            d_gidx.append(i)
+            if lengths:
+                d_klen.append(route_key_length(g))
+            continue
+        key = checked[0][0]
         rows.append(key)
         nids.append(int(node_id))
         cids.append(id(cent))
         lens.append(int(key.shape[1]))
         gidx.append(i)
         cents.append(cent)
-    if not rows:
+        if lengths:
+            klen.append(route_key_length(g))
+    if not rows and not d_nids:
         return None
     rs = RowSet(np.asarray(nids, dtype=np.uint64), np.asarray(cids, dtype=np.int64),
                 np.asarray(lens, dtype=np.int64))
-    return rs, rows, gidx, cents
+    dg = _digest(d_nids, d_keys, d_gidx) if d_nids else None
+    kl = (np.asarray(klen, dtype=np.int64), np.asarray(d_klen, dtype=np.int64)) if lengths else None
+    return rs, rows, gidx, cents, dg, kl
 
 
 def _reference_form(walk, shape_of):
-    if walk is None:
+    if walk is None or not walk[0].node_ids.size:
         return None
-    rs, rows, _, _ = walk
+    rs, rows = walk[0], walk[1]
     sig = tuple((int(n), shape_of(r), r.dtype.str, int(c))
                 for n, r, c in zip(rs.node_ids, rows, rs.cent_ids))
     return rs.node_ids, sig, rows
@@ -196,16 +319,23 @@ class _Bridge:
 
     _full_walk = None
 
-    def __init__(self, *, dtype: str = "f32", headroom: float = 1.25):
+    def __init__(self, *, dtype: str = "f32", headroom: float = 1.25,
+                 length_debias: bool = False):
         if headroom < 1.0:
             raise ValueError("headroom must be >= 1")
         self.dtype = dtype
         self.headroom = float(headroom)
-        self.bank = None
+        self.length_debias = bool(length_debias)
+        self.bank = None               # single-key nodes
+        self.side = None               # digest nodes' keys, ids 0..keys-1
         self._epoch = None
         self._eligible_bank = False
         self._resident = None          # RowSet on the device
         self._pinned: list = []
+        self._digest = None            # Digest held by the side bank
+        self._side_owner = np.empty(0, dtype=np.int64)   # digest node of each side key
+        self._klen_main = np.empty(0, dtype=np.int64)
+        self._klen_digest = np.empty(0, dtype=np.int64)
         self._sorted_nid = np.empty(0, dtype=np.uint64)
         self._sorted_gidx = np.empty(0, dtype=np.int64)
         self._in_bank = np.zeros(0, dtype=bool)
@@ -215,9 +345,12 @@ class _Bridge:
 
     # --------------------------------------------------------- lifecycle
     def close(self) -> None:
-        if self.bank is not None:
-            self.bank.close()
-            self.bank = None
+        for b in (self.bank, self.side):
+            if b is not None:
+                b.close()
+        self.bank = None
+        self.side = None
+        self._digest = None
         self._resident = None
         self._pinned = []
         self._epoch = None
@@ -237,9 +370,11 @@ class _Bridge:
 
     @property
     def bank_size(self) -> int:
+        """Nodes the bridge routes: single-key rows plus digest nodes."""
         if not self._eligible_bank or self._resident is None:
             return 0
-        return int(self._resident.node_ids.size)
+        d = 0 if self._digest is None else int(self._digest.node_ids.size)
+        return int(self._resident.node_ids.size) + d
 
     def refresh(self, grafts, epoch: int) -> dict:
         """Bring the device bank in step with ``grafts`` at ``epoch``.
@@ -248,8 +383,9 @@ class _Bridge:
         ``ineligible_reused``).  Otherwise the walk runs; unchanged rows
         keep the bank (``signature_reused``); changed ones are applied as
         evictions and appends (``updated``; ``rebuilt`` when the bank had
-        to grow), or as a first upload (``created``).  Returns the event
-        (also ``last_event``).
+        to grow), or as a first upload (``created``).  Digest nodes' keys
+        go to the side bank, which is built again when they change.
+        Returns the event (also ``last_event``).
         """
         t0 = time.perf_counter()
         if self._epoch is not None and epoch == self._epoch:
@@ -257,7 +393,7 @@ class _Bridge:
                 "status": "reused" if self._eligible_bank else "ineligible_reused",
                 "epoch": int(epoch), "signature_walk": False}
             return self.last_event
-        walk = type(self)._full_walk(grafts)
+        walk = type(self)._full_walk(grafts, True, self.length_debias)
         if walk is None:
             self._epoch = epoch
             # The device bank stays allocated: a later epoch may make the
@@ -266,12 +402,14 @@ class _Bridge:
             self.last_event = {"status": "ineligible", "epoch": int(epoch),
                                "signature_walk": True}
             return self.last_event
-        rs, rows, gidx, cents = walk
+        rs, rows, gidx, cents, dg, klen = walk
         # Reverse map, native node id -> graft index: row i is the i-th
         # eligible graft (core/graft_arena.py:1200-1245, 3205-3262).  A
         # repeated id fails closed.
-        order = np.argsort(rs.node_ids, kind="stable")
-        snid = rs.node_ids[order]
+        all_nid = rs.node_ids if dg is None else np.concatenate([rs.node_ids, dg.node_ids])
+        g = np.asarray(gidx + ([] if dg is None else dg.gidx), dtype=np.int64)
+        order = np.argsort(all_nid, kind="stable")
+        snid = all_nid[order]
         if snid.size > 1 and np.any(snid[1:] == snid[:-1]):
             self._epoch = epoch
             self._eligible_bank = False
@@ -279,17 +417,26 @@ class _Bridge:
                                "signature_walk": True,
                                "reason": "duplicate native id"}
             return self.last_event
-        g = np.asarray(gidx, dtype=np.int64)
         self._sorted_nid, self._sorted_gidx = snid, g[order]
         self._in_bank = np.zeros(len(grafts), dtype=bool)
         self._in_bank[g] = True
-        if self.bank is not None and rs.same(self._resident):
+        if klen is not None:
+            self._klen_main, self._klen_digest = klen
+        n_digest = 0 if dg is None else int(dg.node_ids.size)
+        side_same = (dg is None and self._digest is None) or (
+            dg is not None and self._digest is not None and dg.sig == self._digest.sig
+            and np.array_equal(dg.node_ids, self._digest.node_ids))
+        main_same = (self._resident is not None and rs.same(self._resident)
+                     and (self.bank is not None or not rs.node_ids.size))
+        if main_same and side_same:
             self._epoch = epoch
             self._eligible_bank = True
             self._pinned = cents
+            if dg is not None:
+                self._digest = dg
             self.last_event = {"status": "signature_reused", "epoch": int(epoch),
                                "signature_walk": True,
-                               "node_count": int(rs.node_ids.size)}
+                               "node_count": int(rs.node_ids.size) + n_digest}
             return self.last_event
         # Fail closed (core/graft_arena.py:1270-1281): until the device bank
         # holds exactly this row set the route is unavailable, and an error
@@ -297,17 +444,32 @@ class _Bridge:
         # take as current; the bank, in an unknown state, is dropped.
         self._eligible_bank = False
         self._epoch = None
+        moved = 0
+        status, evicted, appended = "updated", 0, 0
         try:
-            if self.bank is None:
-                moved = self._create(rs.node_ids, rows)
-                status, evicted, appended = "created", 0, int(rs.node_ids.size)
-            else:
-                evict_ids, append_pos = plan_delta(self._resident, rs)
-                moved, rebuilt = self._apply(evict_ids, append_pos, rs.node_ids, rows)
-                status = "rebuilt" if rebuilt else "updated"
-                evicted, appended = int(evict_ids.size), int(append_pos.size)
-                if rebuilt:
-                    self.totals["rebuilt"] += 1
+            if not main_same:
+                if self.bank is None:
+                    if rs.node_ids.size:
+                        moved += self._create(rs.node_ids, rows)
+                    status, appended = "created", int(rs.node_ids.size)
+                else:
+                    evict_ids, append_pos = plan_delta(self._resident, rs)
+                    m, rebuilt = self._apply(evict_ids, append_pos, rs.node_ids, rows)
+                    moved += m
+                    status = "rebuilt" if rebuilt else "updated"
+                    evicted, appended = int(evict_ids.size), int(append_pos.size)
+                    if rebuilt:
+                        self.totals["rebuilt"] += 1
+            if not side_same:
+                if self.side is not None:
+                    self.side.close()
+                    self.side = None
+                self._digest = None
+                if dg is not None:
+                    moved += self._create_side(dg.keys)
+                    self._side_owner = np.repeat(np.arange(n_digest, dtype=np.int64),
+                                                 np.diff(dg.offs))
+                    self._digest = dg
         except BaseException:
             self.close()
             raise
@@ -316,6 +478,7 @@ class _Bridge:
         # The row set holds id(cent); keeping the resident centroid objects
         # alive means no later object can take one of those ids while its
         # row is on the device (a recycled id would read as "unchanged").
+        # The Digest keeps the digest keys' objects.
         self._pinned = cents
         self._eligible_bank = True
         self.totals["appended"] += appended
@@ -323,14 +486,72 @@ class _Bridge:
         self.totals["bytes_uploaded"] += moved
         self.last_event = {
             "status": status, "epoch": int(epoch), "signature_walk": True,
-            "node_count": int(rs.node_ids.size), "appended": appended,
+            "node_count": int(rs.node_ids.size) + n_digest, "appended": appended,
             "evicted": evicted, "bytes_uploaded": int(moved),
+            "digest_nodes": n_digest,
+            "digest_keys": 0 if dg is None else len(dg.keys),
             "seconds": time.perf_counter() - t0}
         return self.last_event
 
     # ------------------------------------------------------------- route
-    def _route_ids(self, query, topk: int):
+    def _route_main(self, query, topk: int):
         raise NotImplementedError
+
+    def _score_main(self, query, node_ids):
+        raise NotImplementedError
+
+    def _score_side(self, query):
+        raise NotImplementedError
+
+    def _digest_scores(self, query) -> np.ndarray:
+        """Each digest node's best finite key score, NaN when none is
+        finite (cpp/grm_runtime.cpp:3518-3545, 3031-3051)."""
+        dg = self._digest
+        ks = self._score_side(query)
+        out = np.full(dg.node_ids.size, -np.inf, dtype=np.float32)
+        fin = np.isfinite(ks)
+        np.maximum.at(out, self._side_owner[fin], ks[fin])
+        out[out == -np.inf] = np.nan
+        return out
+
+    def route_scored(self, query, topk: int):
+        """The best ``topk`` nodes for one query: (node ids uint64[topk],
+        scores float64[topk]), unfilled UINT64_MAX / NaN, ranked by score
+        (descending) then node id.  Scores are the law's (float32 values);
+        with ``length_debias`` they are the debiased float64 scores the
+        ranking uses."""
+        ids_out = np.full(topk, np.iinfo(np.uint64).max, dtype=np.uint64)
+        sc_out = np.full(topk, np.nan, dtype=np.float64)
+        if not self._eligible_bank or topk <= 0:
+            return ids_out, sc_out
+        main_n = int(self._resident.node_ids.size)
+        if self.length_debias:
+            ids = self._resident.node_ids
+            sc = (self._score_main(query, ids) if main_n
+                  else np.empty(0, dtype=np.float32))
+            kl = self._klen_main
+            if self._digest is not None:
+                ids = np.concatenate([ids, self._digest.node_ids])
+                sc = np.concatenate([sc, self._digest_scores(query)])
+                kl = np.concatenate([kl, self._klen_digest])
+            score = apply_length_debias(sc, kl)
+        else:
+            ids = np.empty(0, dtype=np.uint64)
+            sc = np.empty(0, dtype=np.float32)
+            if main_n:
+                ids, sc = self._route_main(query, min(topk, main_n, MAX_TOPK))
+                keep = ids != np.iinfo(np.uint64).max
+                ids, sc = ids[keep], sc[keep]
+            if self._digest is not None:
+                ids = np.concatenate([ids, self._digest.node_ids])
+                sc = np.concatenate([sc, self._digest_scores(query)])
+            score = sc.astype(np.float64)
+        fin = np.isfinite(score)
+        ids, score = ids[fin], score[fin]
+        order = np.lexsort((ids, -score))[:topk]
+        ids_out[:order.size] = ids[order]
+        sc_out[:order.size] = score[order]
+        return ids_out, sc_out
 
     def _graft_index(self, nid) -> int | None:
         i = int(np.searchsorted(self._sorted_nid, np.uint64(nid)))
@@ -339,7 +560,7 @@ class _Bridge:
         return None
 
     def route_order(self, query, limit: int, exclude=(), cand_count=None):
-        """Graft indices of the best ``limit`` rows, excluded indices
+        """Graft indices of the best ``limit`` nodes, excluded indices
         dropped.  Follows core/graft_arena.py:1282-1364:
 
         * ask the bank for ``min(16, bank_size, want + excludes in bank)``;
@@ -352,7 +573,7 @@ class _Bridge:
         excludes in the bank, else None (the reference's fail-closed
         candidate check).
         """
-        if limit is None or not self._eligible_bank or self.bank is None:
+        if limit is None or not self._eligible_bank:
             return None
         size = self.bank_size
         exclude_set = set(exclude) if exclude else None
@@ -368,7 +589,7 @@ class _Bridge:
         if topk < want:
             return None
         out = []
-        for nid in self._route_ids(query, topk):
+        for nid in self.route_scored(query, topk)[0]:
             if nid == np.iinfo(np.uint64).max:
                 continue
             gi = self._graft_index(nid)
@@ -422,9 +643,24 @@ class MlaRouteBankBridge(_Bridge):
             bank.append(add, node_ids[append_pos])
         return self._bytes(append_pos.size, dim), False
 
-    def _route_ids(self, query, topk):
+    def _create_side(self, keys):
+        stacked = np.ascontiguousarray(np.stack(keys), dtype=np.float32)
+        self.side = MlaNodeBank(stacked, np.arange(len(keys), dtype=np.uint64),
+                                dtype=self.dtype)
+        return self._bytes(stacked.shape[0], stacked.shape[1])
+
+    def _route_main(self, query, topk):
         q = np.ascontiguousarray(query, dtype=np.float32).reshape(1, -1)
-        return self.bank.route(q, topk).ids[0]
+        r = self.bank.route(q, topk)
+        return r.ids[0], r.scores[0]
+
+    def _score_main(self, query, node_ids):
+        return self.bank.score_nodes(np.asarray(query, dtype=np.float32).reshape(-1), node_ids)
+
+    def _score_side(self, query):
+        n = len(self._digest.keys)
+        return self.side.score_nodes(np.asarray(query, dtype=np.float32).reshape(-1),
+                                     np.arange(n, dtype=np.uint64))
 
 
 class GqaRouteBankBridge(_Bridge):
@@ -460,6 +696,11 @@ class GqaRouteBankBridge(_Bridge):
 
     def _apply(self, evict_ids, append_pos, node_ids, rows):
         bank = self.bank
+        if not rows:
+            # every single-key node left (digest nodes may remain)
+            if evict_ids.size:
+                bank.evict(evict_ids)
+            return 0, False
         kv, _, hd = rows[0].shape
         if (kv, hd) != (bank.kv_heads, bank.head_dim):
             self.bank.close()
@@ -489,12 +730,33 @@ class GqaRouteBankBridge(_Bridge):
             return int(counts.sum()) * int(kv) * int(hd) * self._elem(), False
         return 0, False
 
-    def _route_ids(self, query, topk):
+    def _create_side(self, keys):
+        kv, _, hd = keys[0].shape
+        counts = np.asarray([k.shape[1] for k in keys], dtype=np.uint64)
+        offs = np.zeros(len(keys) + 1, dtype=np.uint64)
+        offs[1:] = np.cumsum(counts)
+        self.side = GqaNodeBank(self._flat(keys), offs, kv_heads=int(kv), head_dim=int(hd),
+                                node_ids=np.arange(len(keys), dtype=np.uint64),
+                                dtype=self.dtype)
+        return int(offs[-1]) * int(kv) * int(hd) * self._elem()
+
+    @staticmethod
+    def _query3(query):
         q = np.ascontiguousarray(query, dtype=np.float32)
-        if q.ndim == 3:
-            q = q[None]
-        return self.bank.route(q, topk, query_dtype="f32").ids[0]
+        return q[0] if q.ndim == 4 else q
+
+    def _route_main(self, query, topk):
+        r = self.bank.route(self._query3(query)[None], topk, query_dtype="f32")
+        return r.ids[0], r.scores[0]
+
+    def _score_main(self, query, node_ids):
+        return self.bank.score_nodes(self._query3(query), node_ids)
+
+    def _score_side(self, query):
+        n = len(self._digest.keys)
+        return self.side.score_nodes(self._query3(query), np.arange(n, dtype=np.uint64))
 
 
-__all__ = ["MlaRouteBankBridge", "GqaRouteBankBridge", "RowSet", "mla_bank_walk",
-           "gqa_bank_walk", "plan_delta"]
+__all__ = ["MlaRouteBankBridge", "GqaRouteBankBridge", "RowSet", "Digest", "mla_bank_walk",
+           "gqa_bank_walk", "plan_delta", "route_key_length", "length_debias_factor",
+           "apply_length_debias"]

@@ -1551,6 +1551,31 @@ extern "C" int grm_gqa_hip_evict(GqaDeviceArena* a, const uint64_t* node_ids, ui
   return 0;
 }
 
+namespace grm {
+// Whether appending nodes of tok_counts[0, count) fits once the live ids
+// drop[0, n_drop) are evicted, compacting the token arena if it must (the
+// device store checks this before it replaces an entry's keys, so a
+// replace that cannot fit leaves the old entry in place).
+bool gqa_append_fits(const GqaDeviceArena* a, const uint64_t* drop, uint64_t n_drop,
+                     const uint64_t* tok_counts, uint64_t count) {
+  uint64_t dropped = 0, drop_pad = 0;
+  for (uint64_t i = 0; i < n_drop; ++i) {
+    auto it = a->slot_of.find(drop[i]);
+    if (it == a->slot_of.end()) continue;
+    dropped += 1;
+    drop_pad += padded_len(a->len[it->second]);
+  }
+  const uint64_t room = a->free_slots.size() + (a->cap_nodes - a->high_water) + dropped;
+  if (count > room) return false;
+  uint64_t need = 0;
+  for (uint64_t i = 0; i < count; ++i) need += padded_len(tok_counts[i]);
+  if (need <= a->cap_tokens - a->used_tokens) return true;
+  uint64_t live_pad = 0;  // what a compaction keeps
+  for (const auto& kv : a->slot_of) live_pad += padded_len(a->len[kv.second]);
+  return live_pad - drop_pad + need <= a->cap_tokens;
+}
+}  // namespace grm
+
 extern "C" int grm_gqa_hip_compact(GqaDeviceArena* a) {
   if (!a) return grm::fail(-1, "null arena");
   GRM_HIP_CHECK(hipSetDevice(a->device));

@@ -1527,6 +1527,15 @@ extern "C" int grm_mla_hip_route_filtered(MlaDeviceArena* a, const void* query, 
   return rc;
 }
 
+namespace grm {
+// Whether `count` appends fit once `n_drop` live rows are evicted (the
+// device store checks this before it replaces an entry's keys).
+bool mla_append_fits(const MlaDeviceArena* a, uint64_t n_drop, uint64_t count) {
+  const uint64_t live = a->live >= n_drop ? a->live - n_drop : 0;
+  return count <= a->capacity - live;
+}
+}  // namespace grm
+
 extern "C" int grm_mla_hip_score_nodes(MlaDeviceArena* a, const void* query_host,
                                        int query_dtype, const uint64_t* node_ids, uint64_t count,
                                        float* out_scores_host) {

@@ -60,6 +60,15 @@
 #include <unordered_set>
 #include <vector>
 
+namespace grm {
+// Room checks of the bank files: a replace runs only when the new keys fit
+// once the entry's old keys are gone, so a put that cannot fit leaves the
+// old entry in place.
+bool mla_append_fits(const MlaDeviceArena* a, uint64_t n_drop, uint64_t count);
+bool gqa_append_fits(const GqaDeviceArena* a, const uint64_t* drop, uint64_t n_drop,
+                     const uint64_t* tok_counts, uint64_t count);
+}  // namespace grm
+
 namespace {
 
 constexpr int kMla = 0;
@@ -240,6 +249,17 @@ int put_multi(grm_store_handle* h, uint64_t nid, const std::vector<const float*>
   }
   Entry e = new_entry(h, nid, lexical);
   auto found = h->entries.find(nid);
+  if (count > 0) {
+    // the old keys leave the multi-key bank only when the entry had several
+    const std::vector<uint64_t> none;
+    const std::vector<uint64_t>& old_keys =
+        found != h->entries.end() && found->second.multi ? found->second.mkeys : none;
+    const bool fits = h->dialect == kMla
+                          ? grm::mla_append_fits(h->mla_multi, old_keys.size(), count)
+                          : grm::gqa_append_fits(h->gqa_multi, old_keys.data(), old_keys.size(),
+                                                 tokens.data(), count);
+    if (!fits) return grm::fail(-3, "multi-key bank capacity exceeded; the entry is unchanged");
+  }
   if (found != h->entries.end()) {
     GRM_CHECK_RC(drop_keys(h, nid, found->second));
     h->entries.erase(found);  // its old keys are gone
@@ -276,6 +296,12 @@ int put_entry(grm_store_handle* h, uint64_t nid, const float* key, uint64_t len,
   }
   Entry e = new_entry(h, nid, lexical);
   auto found = h->entries.find(nid);
+  // the old key leaves this bank only when it is a single key
+  const bool drops_here = found != h->entries.end() && !found->second.multi;
+  const bool fits = h->dialect == kMla
+                        ? grm::mla_append_fits(h->mla, drops_here ? 1 : 0, 1)
+                        : grm::gqa_append_fits(h->gqa, &nid, drops_here ? 1 : 0, &tokens, 1);
+  if (!fits) return grm::fail(-3, "route bank capacity exceeded; the entry is unchanged");
   if (found != h->entries.end()) {
     GRM_CHECK_RC(drop_keys(h, nid, found->second));
     h->entries.erase(found);  // its old key is gone
@@ -499,7 +525,19 @@ int route(grm_store_handle* h, const float* query, uint64_t heads, uint64_t toke
     const bool all_fetched = static_cast<int>(fetched.size()) < kf || fetched.size() >= live;
     if (!all_fetched) {
       const float norm = max_abs + 1.0e-8f;
-      const float guard = fetched.back().score / norm;
+      const float r_last = fetched.back().score;
+      // An entry the bank did not return (and without lexical hits) has
+      // raw <= r_last.  With k + 1 fetched, it normalises to at most
+      // guard = fl(r_last / norm), so the top k is certain when the k-th
+      // ranked score lies above guard.  When the fetch stopped at the
+      // kernels' cap (k = 16, so only k fetched), the last fetched entry
+      // is itself one of the k: an unfetched entry with raw == r_last has
+      // a higher node id (the bank's tie law) and ranks after it, and one
+      // with raw < r_last normalises to at most fl(pred(r_last) / norm), so
+      // the top k is certain when the k-th ranked score lies above that.
+      const float guard = kf > static_cast<int>(topk)
+                              ? r_last / norm
+                              : std::nextafter(r_last, -INFINITY) / norm;
       const bool sure = ranked.size() >= topk && ranked[topk - 1].score > guard;
       if (!sure) {
         // every entry taking part, scored exactly

@@ -247,6 +247,23 @@ class MlaNodeBank(_Bank):
         _lib.check(rc, "MLA latent route")
         return RouteResult(ids, scores, float(ms.value) if timed else float("nan"), wall)
 
+    def score_nodes(self, query, node_ids, *, query_dtype: str = "f32") -> np.ndarray:
+        """Exact law scores (float32, NaN where not finite) of the listed
+        live node ids for one host query [dim]."""
+        self._need_open()
+        qd = _dtype_code(query_dtype)
+        q = np.asarray(query)
+        if qd == DTYPE_BF16 and q.dtype != np.uint16:
+            q = as_bf16_bits(q)
+        q = np.ascontiguousarray(q, dtype=np.float32 if qd == DTYPE_F32 else np.uint16).reshape(-1)
+        if q.size != self.dim:
+            raise ValueError("query must have dim values")
+        ids = np.ascontiguousarray(node_ids, dtype=np.uint64).reshape(-1)
+        out = np.empty(ids.size, dtype=np.float32)
+        _lib.check(self._lib.grm_mla_hip_score_nodes(self._h, _ptr(q), qd, _ptr(ids), ids.size,
+                                                     _ptr(out)), "MLA score nodes")
+        return out
+
     def append(self, rows, node_ids) -> int:
         self._need_open()
         r = self._rows(rows, self.dim)
@@ -430,6 +447,24 @@ class GqaNodeBank(_Bank):
                                                       _ptr(colinfo), _ptr(knorm), _ptr(ids)),
                    "GQA probe screen")
         return maxima, colinfo, knorm, ids
+
+    def score_nodes(self, query, node_ids, *, query_dtype: str = "f32") -> np.ndarray:
+        """Exact raw law scores (float32, NaN where not finite) of the
+        listed live node ids for one host query [H, Qt, hd]."""
+        self._need_open()
+        qd = _dtype_code(query_dtype)
+        q = np.asarray(query)
+        if qd == DTYPE_BF16 and q.dtype != np.uint16:
+            q = as_bf16_bits(q)
+        q = np.ascontiguousarray(q, dtype=np.float32 if qd == DTYPE_F32 else np.uint16)
+        if q.ndim != 3 or q.shape[2] != self.head_dim:
+            raise ValueError("query must have shape (H, Qt, head_dim)")
+        ids = np.ascontiguousarray(node_ids, dtype=np.uint64).reshape(-1)
+        out = np.empty(ids.size, dtype=np.float32)
+        _lib.check(self._lib.grm_gqa_hip_score_nodes(self._h, _ptr(q), qd, q.shape[0], q.shape[1],
+                                                     _ptr(ids), ids.size, _ptr(out)),
+                   "GQA score nodes")
+        return out
 
     def append(self, keys, tok_counts, node_ids, scales=None) -> int:
         self._need_open()

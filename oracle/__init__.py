@@ -257,6 +257,40 @@ def _entry_max(key_scores, owners, n_entries):
     return out
 
 
+def length_debias(scores, key_lengths) -> np.ndarray:
+    """The reference's length-debiased latent score
+    (core/graft_arena.py:839-874), one node at a time: K = max(1, key
+    length), n = sqrt(log2(K + 1)) (numpy float64, :839-846), and the score
+    s (a float32 law score, widened) becomes s / n when s >= 0 and s * n
+    below zero (:866-873).  Returns float64."""
+    out = np.empty(len(scores), dtype=np.float64)
+    for i, (sc, kl) in enumerate(zip(scores, key_lengths)):
+        try:
+            k = max(1, int(kl))
+        except (TypeError, ValueError, OverflowError):
+            k = 1
+        n = float(np.sqrt(np.log2(k + 1.0)))
+        v = float(np.float32(sc))
+        out[i] = v / n if v >= 0.0 else v * n
+    return out
+
+
+def rank_entries(scores, node_ids, topk: int):
+    """(ids uint64[topk], scores float64[topk]) of the best finite scores,
+    score descending then node id ascending; unfilled UINT64_MAX / NaN
+    (the tie law score_node_better, cpp/grm_runtime.cpp:75-82)."""
+    sc = np.asarray(scores, dtype=np.float64)
+    ids = np.asarray(node_ids, dtype=np.uint64)
+    keep = np.isfinite(sc)
+    pairs = sorted(zip((-sc[keep]).tolist(), ids[keep].tolist()))[:topk]
+    out_ids = np.full(topk, np.iinfo(np.uint64).max, dtype=np.uint64)
+    out_sc = np.full(topk, np.nan, dtype=np.float64)
+    for j, (ns, nid) in enumerate(pairs):
+        out_ids[j] = nid
+        out_sc[j] = -ns
+    return out_ids, out_sc
+
+
 def store_route(rows: np.ndarray, node_ids, lexical: list, meta: list, query: np.ndarray,
                 query_lexical=(), filters=((), (), (), ()), topk: int = 3, owners=None):
     """The store's MLA route law, route_mla_arena (cpp/grm_runtime.cpp:

@@ -44,12 +44,24 @@ class CpuMlaBridge(bb._Bridge):
         self.bank.ops.append(("delta", len(evict_ids), len(append_pos)))
         return len(append_pos), False
 
-    def _route_ids(self, query, topk):
+    def _create_side(self, keys):
+        self.side = _RowStore(range(len(keys)), keys)
+        return len(keys)
+
+    def _route_main(self, query, topk):
         ids = np.asarray(sorted(self.bank.rows), dtype=np.uint64)
         rows = np.stack([self.bank.rows[int(i)] for i in ids])
-        got, _, _ = oracle.mla_route(rows, np.asarray(query, np.float32)[None],
-                                     topk, node_ids=ids)
-        return got[0]
+        got, sc, _ = oracle.mla_route(rows, np.asarray(query, np.float32)[None],
+                                      topk, node_ids=ids)
+        return got[0], sc[0]
+
+    def _score_main(self, query, node_ids):
+        rows = np.stack([self.bank.rows[int(i)] for i in node_ids])
+        return oracle.mla_scores(rows, np.asarray(query, np.float32)[None])[0]
+
+    def _score_side(self, query):
+        rows = np.stack([self.side.rows[i] for i in range(len(self.side.rows))])
+        return oracle.mla_scores(rows, np.asarray(query, np.float32)[None])[0]
 
 
 def graft(nid, cent, **kw):
@@ -130,12 +142,23 @@ def test_epoch_gate_and_events():
     gs[7]["cent"] = rng.standard_normal(6).astype(np.float32)
     ev = br.refresh(gs, 3)
     assert ev["status"] == "updated" and ev["evicted"] == 2 and ev["appended"] == 2
+    # a digest node: served beside the bank (its keys in the side store)
     gs.append(graft(600, gs[0]["cent"], child_cents=[gs[1]["cent"]]))
-    assert br.refresh(gs, 4)["status"] == "ineligible"
-    assert br.refresh(NoWalk(gs), 4)["status"] == "ineligible_reused"
+    ev = br.refresh(gs, 4)
+    assert ev["status"] == "updated" and ev["digest_nodes"] == 1 and ev["digest_keys"] == 2
+    assert br.refresh(NoWalk(gs), 4)["status"] == "reused"
+    assert br.route_order(gs[0]["cent"], 3) is not None
+    gs[-1]["note"] = "metadata only"
+    assert br.refresh(gs, 5)["status"] == "signature_reused"
+    gs.pop()
+    ev = br.refresh(gs, 6)
+    assert ev["status"] == "updated" and ev["digest_nodes"] == 0 and br.side is None
+    gs.append(graft(700, np.full(7, 1.0, np.float32)))  # a dim the bank cannot hold
+    assert br.refresh(gs, 7)["status"] == "ineligible"
+    assert br.refresh(NoWalk(gs), 7)["status"] == "ineligible_reused"
     assert br.route_order(gs[0]["cent"], 3) is None
     gs.pop()
-    ev = br.refresh(gs, 5)
+    ev = br.refresh(gs, 8)
     assert ev["status"] == "signature_reused"
     assert sorted(br.bank.rows) == sorted(int(g["native_node_id"]) for g in gs
                                           if not g.get("retired"))
@@ -228,3 +251,113 @@ def test_failed_update_fails_closed_and_retries_from_scratch():
     want = sorted(int(g["native_node_id"]) for g in gs if not g.get("retired"))
     assert sorted(br.bank.rows) == want
     assert br.route_order(q, 3) is not None
+
+
+def expected_order(gs, q, topk, *, debias=False):
+    """The law's order over an arena with digest nodes, from the oracle:
+    each node's best finite key score (own centroid, then child_cents;
+    cpp/grm_runtime.cpp:3518-3545), optionally length-debiased
+    (core/graft_arena.py:839-874), ranked score desc then node id."""
+    keys, owners, nids, klen = [], [], [], []
+    for g in gs:
+        if g.get("retired") or g.get("kind", "turn") == "recall":
+            continue
+        e = len(nids)
+        nids.append(int(g["native_node_id"]))
+        klen.append(bb.route_key_length(g))
+        for k in [g["cent"], *g.get("child_cents", ())]:
+            keys.append(np.asarray(k, np.float32).reshape(-1))
+            owners.append(e)
+    ks = oracle.mla_scores(np.stack(keys), np.asarray(q, np.float32)[None])[0]
+    sc = oracle._entry_max(ks, owners, len(nids))
+    if debias:
+        sc = oracle.length_debias(sc, klen)
+    return oracle.rank_entries(sc, nids, topk)
+
+
+def digest_arena(rng, n, dim, n_digest):
+    gs = [graft(3 * n - 2 * i, rng.standard_normal(dim).astype(np.float32),
+                ntok=int(rng.integers(1, 600))) for i in range(n)]
+    for j in range(n_digest):
+        src = [g for g in gs if not g.get("retired") and "child_cents" not in g][:3]
+        child = []
+        for g in src:
+            child.append(g["cent"])
+            child.extend(g.get("child_cents", ()))
+            g["retired"] = True
+        gs.append(graft(10_000 + j, rng.standard_normal(dim).astype(np.float32),
+                        child_cents=child, kind="digest", ntok=int(rng.integers(1, 600))))
+    return gs
+
+
+def test_digest_walk_law():
+    rng = np.random.default_rng(7)
+    gs = digest_arena(rng, 12, 5, 2)
+    assert bb.mla_bank_walk(gs) is None          # the reference's walk declines
+    rs, rows, gidx, cents, dg, kl = bb._walk_mla(gs, True, True)
+    live = [i for i, g in enumerate(gs) if not g.get("retired")]
+    plain = [i for i in live if "child_cents" not in gs[i]]
+    assert list(gidx) == plain and list(dg.gidx) == [i for i in live if i not in plain]
+    for j, gi in enumerate(dg.gidx):
+        g = gs[gi]
+        want = [g["cent"], *g["child_cents"]]
+        got = dg.keys[dg.offs[j]:dg.offs[j + 1]]
+        assert len(got) == len(want)
+        assert all(np.array_equal(a, b) for a, b in zip(got, want))
+    # the second digest holds the first one's leaf keys too (generations flatten)
+    assert dg.offs[2] - dg.offs[1] >= 4
+    assert list(kl[0]) == [gs[i]["ntok"] for i in plain]
+    assert list(kl[1]) == [gs[i]["ntok"] for i in dg.gidx]
+
+
+def test_length_debias_law_closed_forms():
+    # K = 1: sqrt(log2 2) = 1, the identity; K = 3: sqrt(2); K = 15: 2;
+    # K <= 0 or malformed counts as 1; negative scores are multiplied
+    sc = [0.5, 0.5, 0.5, -0.5, 0.5, -0.25, 0.0, 0.75]
+    kl = [1, 3, 15, 15, 0, 3, 40, "x"]
+    want = [0.5, 0.5 / np.sqrt(2.0), 0.25, -1.0, 0.5, -0.25 * np.sqrt(2.0), 0.0, 0.75]
+    got = oracle.length_debias(sc, kl)
+    np.testing.assert_array_equal(got, np.asarray(want))
+    # the bridge's vectorised form equals the oracle's on random scores
+    rng = np.random.default_rng(9)
+    s = rng.standard_normal(2000).astype(np.float32)
+    k = rng.integers(-2, 5000, size=2000)
+    np.testing.assert_array_equal(bb.apply_length_debias(s, k), oracle.length_debias(s, k))
+    # monotone in the score for a fixed K, and a longer key never gains
+    d = oracle.length_debias(np.sort(s), np.full(2000, 37))
+    assert np.all(np.diff(d) >= 0)
+    pos = np.abs(s)
+    assert np.all(oracle.length_debias(pos, k + 10) <= oracle.length_debias(pos, k))
+
+
+def test_route_key_length_law():
+    assert bb.route_key_length({"cent": np.zeros((2, 9, 4))}) == 9
+    assert bb.route_key_length({"cent": np.zeros((2, 0, 4))}) == 1
+    assert bb.route_key_length({"cent": np.zeros(8), "ntok": 33}) == 33
+    assert bb.route_key_length({"cent": np.zeros(8)}) == 1
+    assert bb.route_key_length({"cent": np.zeros(8), "ntok": "?"}) == 1
+    assert bb.route_key_length({"cent": np.zeros(8), "ntok": -4}) == 1
+
+
+@pytest.mark.parametrize("debias", [False, True])
+def test_digest_and_debias_routes_follow_the_law(debias):
+    rng = np.random.default_rng(8 + debias)
+    dim = 6
+    gs = digest_arena(rng, 40, dim, 3)
+    br = CpuMlaBridge(length_debias=debias)
+    for epoch in range(6):
+        if epoch:
+            live = [g for g in gs if not g.get("retired")]
+            live[int(rng.integers(len(live)))]["retired"] = True
+            gs.append(graft(20_000 + epoch, rng.standard_normal(dim).astype(np.float32),
+                            ntok=int(rng.integers(1, 600))))
+            if epoch % 2:
+                d = [g for g in gs if "child_cents" in g and not g.get("retired")][0]
+                d["child_cents"] = d["child_cents"] + [rng.standard_normal(dim).astype(np.float32)]
+        br.refresh(gs, epoch)
+        for _ in range(3):
+            q = rng.standard_normal(dim).astype(np.float32)
+            ids, sc = br.route_scored(q, 9)
+            w_ids, w_sc = expected_order(gs, q, 9, debias=debias)
+            np.testing.assert_array_equal(ids, w_ids)
+            np.testing.assert_array_equal(sc, w_sc)

@@ -6,6 +6,11 @@ sequences retire, add, replace and touch (metadata only) grafts between
 epochs, as the arena's mutation sites do (core/graft_arena.py:278-291).
 The bridges start with no headroom, so their capacity-growth path runs;
 the GQA bank also compacts its token arena.
+
+Arenas with digest nodes (child_cents: the best of the node's own key and
+its children's, core/graft_arena.py:803-811) and the length-debiased score
+(:839-874) are routed through the bridge and checked per epoch against the
+oracle's multi-key law, debias law and tie order.
 """
 
 import numpy as np
@@ -13,6 +18,7 @@ import pytest
 
 import oracle
 from graftrepository_amd import GqaRouteBankBridge, MlaRouteBankBridge
+from graftrepository_amd import bank_bridge as bb
 
 pytestmark = pytest.mark.gpu
 NO_ID = np.iinfo(np.uint64).max
@@ -114,3 +120,102 @@ def test_gqa_bridge_follows_the_arena(hip_lib):
             assert_same(res, want_ids, want_sc)
             assert br.bank.info()["live"] == len(live)
     assert {"created", "updated"} <= statuses, statuses
+
+
+def law_order(gs, score_keys, q, topk, debias):
+    """Oracle order over the arena's live nodes: best finite key score per
+    node (own key, then child_cents), optionally length-debiased, ranked
+    score desc then node id."""
+    keys, owners, nids, klen = [], [], [], []
+    for g in gs:
+        if g.get("retired") or g.get("kind", "turn") == "recall":
+            continue
+        e = len(nids)
+        nids.append(int(g["native_node_id"]))
+        klen.append(bb.route_key_length(g))
+        for k in [g["cent"], *g.get("child_cents", ())]:
+            keys.append(k)
+            owners.append(e)
+    sc = oracle._entry_max(score_keys(keys, q), owners, len(nids))
+    if debias:
+        sc = oracle.length_debias(sc, klen)
+    return oracle.rank_entries(sc, nids, topk)
+
+
+def consolidate(rng, gs, nxt, make, ntok):
+    """Retire up to three live grafts into a new digest node that carries
+    their keys (core/graft_arena.py:1665-1690)."""
+    src = [g for g in gs if not g.get("retired")][:3]
+    child = []
+    for g in src:
+        child.append(g["cent"])
+        child.extend(g.get("child_cents", ()))
+        g["retired"] = True
+    gs.append({"native_node_id": nxt, "cent": make(), "child_cents": child,
+               "kind": "digest", "ntok": ntok()})
+    return nxt + 1
+
+
+@pytest.mark.parametrize("debias", [False, True])
+def test_mla_bridge_digests_and_debias(hip_lib, debias):
+    rng = np.random.default_rng(31 + debias)
+    dim = 80
+    make = lambda: rng.standard_normal(dim).astype(np.float32)
+    ntok = lambda: int(rng.integers(1, 2000))
+    gs = [{"native_node_id": 4000 - i, "cent": make(), "ntok": ntok()} for i in range(2000)]
+    nxt = 9000
+
+    def score_keys(keys, q):
+        return oracle.mla_scores(np.stack([np.asarray(k, np.float32) for k in keys]), q[None])[0]
+
+    with MlaRouteBankBridge(headroom=1.0, length_debias=debias) as br:
+        for epoch in range(12):
+            if epoch:
+                nxt = mutate(rng, gs, make, nxt, int(rng.integers(0, 30)))
+                for g in gs[-3:]:
+                    g.setdefault("ntok", ntok())
+            if epoch % 3 == 1:
+                nxt = consolidate(rng, gs, nxt, make, ntok)
+            ev = br.refresh(gs, epoch)
+            assert ev["status"] != "ineligible", ev
+            for _ in range(3):
+                q = make()
+                if epoch % 2:
+                    d = [g for g in gs if "child_cents" in g and not g.get("retired")]
+                    if d:
+                        q = d[-1]["child_cents"][0].copy()   # a digest's child key
+                ids, sc = br.route_scored(q, 10)
+                w_ids, w_sc = law_order(gs, score_keys, q, 10, debias)
+                np.testing.assert_array_equal(ids, w_ids)
+                np.testing.assert_array_equal(sc, w_sc)
+
+
+@pytest.mark.parametrize("debias", [False, True])
+def test_gqa_bridge_digests_and_debias(hip_lib, debias):
+    rng = np.random.default_rng(41 + debias)
+    kv, hd = 2, 64
+    make = lambda: rng.standard_normal((kv, int(rng.integers(1, 40)), hd)).astype(np.float32)
+    gs = [{"native_node_id": 700 - i, "cent": make()} for i in range(120)]
+    nxt = 3000
+
+    def score_keys(keys, q):
+        lens = np.asarray([k.shape[1] for k in keys], np.uint64)
+        offs = np.zeros(len(keys) + 1, np.uint64)
+        offs[1:] = np.cumsum(lens)
+        flat = np.concatenate([np.asarray(k, np.float32).reshape(-1) for k in keys])
+        return oracle.gqa_scores(flat, oracle.F32, offs, kv, hd, q)[0]
+
+    with GqaRouteBankBridge(headroom=1.0, length_debias=debias) as br:
+        for epoch in range(10):
+            if epoch:
+                nxt = mutate(rng, gs, make, nxt, int(rng.integers(0, 12)))
+            if epoch % 3 == 1:
+                nxt = consolidate(rng, gs, nxt, make, lambda: 1)
+            ev = br.refresh(gs, epoch)
+            assert ev["status"] != "ineligible", ev
+            for _ in range(2):
+                q = rng.standard_normal((4 * kv, 2, hd)).astype(np.float32)
+                ids, sc = br.route_scored(q, 6)
+                w_ids, w_sc = law_order(gs, score_keys, q, 6, debias)
+                np.testing.assert_array_equal(ids, w_ids)
+                np.testing.assert_array_equal(sc, w_sc)

@@ -253,3 +253,83 @@ def test_device_store_multi_key_entries_match_the_law(hip_lib, dialect):
             assert got_ids == want_ids, (step, qlex, filters, k)
             np.testing.assert_array_equal(np.asarray(got_sc, np.float32).view(np.uint32),
                                           want_sc.view(np.uint32))
+
+
+def test_device_gqa_store_topk16_with_lexical_keys(hip_lib):
+    # k = 16 is the bank's list cap, so a lexical route fetches 16, not
+    # k + 1; the guard then rests on fl(pred(r_16) / norm) (csrc/store.hip).
+    # Raw ties (duplicate blocks) straddle the 16th place.  Ids and scores
+    # must equal the law.
+    from graftrepository_amd.store_route import DeviceGqaRouteStore
+
+    rng = np.random.default_rng(57)
+    n, kv, hd, H = 300, 2, 32, 8
+    blocks = {700 + i: rng.standard_normal((kv, int(rng.integers(1, 30)), hd)).astype(np.float32)
+              for i in range(n)}
+    for a in range(700, 760, 3):
+        blocks[a + 1] = blocks[a].copy()
+    lex = {nid: (list(rng.choice(VOCAB, size=2, replace=False)) if rng.random() < 0.1 else [])
+           for nid in blocks}
+    meta = {nid: DEFAULT for nid in blocks}
+    ids = sorted(blocks)
+    lens = np.asarray([blocks[i].shape[1] for i in ids], dtype=np.uint64)
+    offs = np.zeros(len(ids) + 1, dtype=np.uint64)
+    offs[1:] = np.cumsum(lens)
+    keys = np.concatenate([blocks[i].reshape(-1) for i in ids])
+    with DeviceGqaRouteStore(kv, hd, capacity_nodes=400, capacity_tokens=20_000) as st:
+        st.set_routes(ids, [blocks[i] for i in ids], [lex[i] for i in ids],
+                      [meta[i] for i in ids])
+        for step in range(25):
+            q = rng.standard_normal((H, int(rng.integers(1, 3)), hd)).astype(np.float32)
+            qlex = list(rng.choice(VOCAB, size=int(rng.integers(1, 4)), replace=True))
+            want_ids, want_sc = oracle.store_route_gqa(
+                keys, offs, kv, hd, ids, [lex[i] for i in ids], [meta[i] for i in ids], q, qlex,
+                ((), (), (), ()), 16)
+            got_ids, got_sc = st.route_scored(q, qlex, 16)
+            assert got_ids == want_ids, step
+            np.testing.assert_array_equal(np.asarray(got_sc, np.float32).view(np.uint32),
+                                          want_sc.view(np.uint32))
+
+
+def test_device_store_put_that_cannot_fit_keeps_the_old_entry(hip_lib):
+    # A set_route / set_route_multi whose new keys cannot fit once the old
+    # ones are gone fails before touching the entry: it stays routable with
+    # its old key.
+    from graftrepository_amd.store_route import DeviceGqaRouteStore
+
+    rng = np.random.default_rng(59)
+    # GQA: 4 nodes of 8 tokens in a bank of 4 nodes and 32 tokens (the bank
+    # adds 7 tokens of alignment room per node: 60 in all)
+    kv, hd, H = 2, 16, 4
+    with DeviceGqaRouteStore(kv, hd, capacity_nodes=4, capacity_tokens=32) as st:
+        blocks = {i: rng.standard_normal((kv, 8, hd)).astype(np.float32) for i in range(4)}
+        for i, b in blocks.items():
+            st.set_route(i, b)
+        q = blocks[0][:, :1, :].repeat(2, axis=0).copy()   # matches node 0 best
+        before = st.route_scored(q, (), 4)
+        assert before[0][0] == 0
+        with pytest.raises(RuntimeError, match="unchanged"):
+            st.set_route(0, rng.standard_normal((kv, 40, hd)).astype(np.float32))
+        assert st.route_scored(q, (), 4) == before
+        with pytest.raises(RuntimeError):
+            st.set_route(9, blocks[1])                         # a fifth node
+        assert st.route_scored(q, (), 4) == before and len(st) == 4
+        st.set_route(0, rng.standard_normal((kv, 32, hd)).astype(np.float32))  # fits
+        assert len(st) == 4 and st.route_scored(q, (), 4) != before
+    # MLA: 64 slots full; a new entry fails, a replacement fits; a multi-key
+    # entry with more keys than its bank holds fails and keeps the old key
+    dim = 12
+    with DeviceRouteStore(dim, capacity=64) as st:
+        rows = {i: rng.standard_normal(dim).astype(np.float32) for i in range(64)}
+        for i, r in rows.items():
+            st.set_route(i, r)
+        q = rows[5].copy()
+        before = st.route_scored(q, (), 3)
+        with pytest.raises(RuntimeError, match="unchanged"):
+            st.set_route(100, rows[1])
+        assert st.route_scored(q, (), 3) == before and len(st) == 64
+        with pytest.raises(RuntimeError, match="unchanged"):
+            st.set_route_multi(5, rng.standard_normal((65, dim)).astype(np.float32))
+        assert st.route_scored(q, (), 3) == before
+        st.set_route(5, -rows[5])                              # a replacement fits
+        assert st.route_scored(q, (), 3)[0][0] != 5
