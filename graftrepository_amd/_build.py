@@ -48,9 +48,17 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+# Per-source flags.  mla_route.hip: MFMA accumulators in VGPRs (the ring
+# screen keeps its query fragments in AGPRs and reduces the accumulators
+# with VALU instructions, which then need no AGPR-to-VGPR copies).
+SOURCE_FLAGS = {
+    "mla_route.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")

@@ -272,6 +272,278 @@ __global__ __launch_bounds__(kBatchWaves * kWave) void mla_batch_screen_kernel(
   }
 }
 
+// ------------------------------------------------------------ ring screen
+//
+// The same screen for a full pass of 256 queries, with the roles of LDS
+// and registers swapped: each wavefront holds 64 queries' B fragments in
+// registers for the whole bank, and the bank's 32-slot tiles stream into
+// LDS, so every A fragment read from LDS feeds two MFMAs (the query
+// fragments of mla_batch_screen_kernel cost one 1 KiB LDS read per MFMA).
+//
+//  * One block of four wavefronts per CU; wavefront w holds queries
+//    [64 w, 64 w + 64) and has SIMD w to itself, so its 512 registers hold
+//    the queries, two sets of accumulators and A fragments four K-steps
+//    ahead.  The MFMAs of tile s and the reductions of tile s - 1 form one
+//    straight-line region, interleaved (sched_group_barrier): the matrix
+//    core and the VALU work side by side within the wavefront.
+//  * Block b is sub-stream b of W = blocks and walks tiles
+//    [b * n_tiles32 / W, (b + 1) * n_tiles32 / W), one per step, so the
+//    merge decodes its slot codes as for the wavefront sub-streams of
+//    mla_batch_screen_kernel.
+//  * A ring of kRing tiles in LDS (2 KS chunk planes of 512 bytes each,
+//    chunk c of the tile at c * 512) with their 32 slot weights.  Direct
+//    loads (global_load_lds_dwordx4) fill it without registers.  A step is
+//    KS tile loads of 1 KiB (two chunk planes each) and one weight load,
+//    spread so that every wavefront issues the same number
+//    (kLoadsPerWave); wavefronts without a tile load left for their last
+//    issue all bring the weights (8 lanes carry the 128 bytes, the rest
+//    repeat them into the pad of a 1 KiB weight area).  kRing - 1 tiles are
+//    in flight while one is screened.
+//  * Step s: each wavefront waits for its own loads of tile s (vmcnt) and
+//    its LDS reads of tile s - 1 (lgkmcnt); the block barrier then makes
+//    the whole tile visible and says every wavefront is done with tile
+//    s - 1, whose slot the loads of tile s + kRing - 1 then refill.  Loads
+//    past the block's last tile re-read that tile (never screened), so
+//    every step has the same load count.
+//  * The slot weights 1/norm_f come from mla_batch_weights_kernel, the
+//    values mla_batch_screen_kernel forms per tile (same reciprocal).
+template <int KS>
+struct RingShape {
+  static constexpr int kRing = 8;                         // tiles in LDS
+  static constexpr int kTileU4 = 2 * KS * 32;             // u32x4 per tile
+  static constexpr int kTileLoads = KS;                   // 1 KiB loads per tile
+  static constexpr int kLoadsPerWave = kTileLoads / 4 + 1;  // every wavefront, every step
+  static constexpr size_t kWeightOffset = static_cast<size_t>(kRing) * kTileU4 * 16;
+  static constexpr size_t kWeightArea = 1024;             // bytes per tile (128 used)
+  static constexpr size_t kLds = kWeightOffset + static_cast<size_t>(kRing) * kWeightArea;
+};
+
+constexpr int kRingWaves = 4;      // wavefronts per block, one block per CU
+constexpr int kRingQueries = 256;  // queries per ring pass
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding; expcnt left alone): the
+// wavefront's loads but the last n are done, and so are its LDS reads.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lds() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
+}
+
+// The slot weights the screens multiply by: 1/norm_f (v_rcp_f32), 0 for
+// an all-zero row, -0 for a slot that never ranks (NaN norm: tombstone,
+// unused slot, non-finite row) and for a norm that overflowed.
+__global__ void mla_batch_weights_kernel(const float* __restrict__ norms, uint64_t n,
+                                         float* __restrict__ winv) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float nf = norms[i];
+  winv[i] = nf == 0.0f ? 0.0f : (nf < INFINITY ? __builtin_amdgcn_rcpf(nf) : -0.0f);
+}
+
+template <int KS, bool kProbe = false>
+__global__ __launch_bounds__(kRingWaves * kWave, 1) void mla_batch_ring_kernel(
+    const u32x4* __restrict__ tiles, const float* __restrict__ winv, uint64_t cap,
+    uint32_t n_tiles32, const uint16_t* __restrict__ qpad, int ibits, uint32_t* __restrict__ planes) {
+  using RS = RingShape<KS>;
+  constexpr int stride = 16 * KS + 8;  // qpad row stride (bf16 elements)
+  constexpr int QP = kRingQueries;
+  constexpr int kPre = 4;              // A fragments in flight ahead of their MFMAs
+  extern __shared__ u32x4 s_ring[];   // [kRing][2 KS][32 slots], then the weights
+  unsigned char* s_w = reinterpret_cast<unsigned char*>(s_ring) + RS::kWeightOffset;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int half = lane >> 5;
+  const int col = lane & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // query group
+  const uint32_t W = gridDim.x;
+  const uint32_t t_begin = static_cast<uint32_t>(static_cast<uint64_t>(blockIdx.x) * n_tiles32 / W);
+  const uint32_t t_end = static_cast<uint32_t>(static_cast<uint64_t>(blockIdx.x + 1) * n_tiles32 / W);
+  const uint32_t steps = t_end - t_begin;
+
+  // B fragments of the wavefront's 64 queries: column tile c, K-step ks:
+  // query 64 wv + 32 c + col at dims 16 ks + 8 half .. +8
+  u32x4 bq[2][KS];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const uint16_t* row = qpad + static_cast<size_t>(64 * wv + 32 * c + col) * stride + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) bq[c][ks] = *reinterpret_cast<const u32x4*>(row + 16 * ks);
+  }
+  // The fragments are in registers before the ring's loads start, so the
+  // only loads a step waits for are the ring's own (the empty asm uses
+  // each value, which keeps its load ahead of the ring's).  They live in
+  // AGPRs (the MFMAs read their B operand there), which leaves the VGPRs
+  // to the accumulators, so the reductions read them without copies
+  // (mla_route.hip is built with the MFMA VGPR-accumulator form).
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+a"(bq[c][ks]));
+  }
+  asm volatile("" ::: "memory");
+
+  // The wavefront's loads of a step: tile loads m = wv + 4 j while
+  // m < KS (load m: chunk planes 2 m and 2 m + 1), and for its last
+  // issue, when no tile load is left, the step's weights.  Branch-free:
+  // every issue is one 16-byte direct load whose addresses are selected.
+  constexpr int kPer = RS::kLoadsPerWave;
+  const u32x4* w16 = reinterpret_cast<const u32x4*>(winv);
+  auto issue_step = [&](uint32_t s) {
+    const int slot = static_cast<int>(s % RS::kRing);
+    const uint32_t t = min(t_begin + s, t_end - 1);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int m = wv + kRingWaves * j;
+      const bool tile_load = m < RS::kTileLoads;
+      const u32x4* src_t = tiles + static_cast<uint64_t>(2 * m + half) * cap +
+                           static_cast<uint64_t>(t) * 32 + col;
+      const u32x4* src_w = w16 + static_cast<uint64_t>(t) * 8 + (lane & 7);
+      u32x4* dst_t = s_ring + slot * RS::kTileU4 + m * 64;
+      u32x4* dst_w = reinterpret_cast<u32x4*>(s_w + slot * RS::kWeightArea);
+      __builtin_amdgcn_global_load_lds(tile_load ? src_t : src_w,
+                                       (__attribute__((address_space(3))) void*)(tile_load ? dst_t : dst_w),
+                                       16, 0, 0);
+    }
+  };
+  // Wait for tile s, pass the barrier, refill the slot of tile s - 1.
+  auto enter_step = [&](uint32_t s) {
+    asm volatile("" ::: "memory");
+    wait_vmcnt_lds<(RS::kRing - 2) * kPer>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue_step(s + RS::kRing - 1);
+  };
+
+  // per column tile: the three largest coded u as signed-integer bits
+  int b1[2], b2[2], b3[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) b1[c] = b2[c] = b3[c] = INT32_MIN;
+  const uint32_t keep_mask = ~((1u << ibits) - 1u);
+
+  // One tile's screen results: accumulators, the weights of the lane's
+  // result rows 8 (r / 4) + 4 half + r % 4, and the tile.
+  struct Res {
+    f32x16 acc[2];
+    float w[16];
+    uint32_t t;
+    uint32_t tcode;
+  };
+  // Reduction of value v = 16 c + r of a finished tile.
+  auto reduce_one = [&](const Res& R, int v) {
+    const int c = v >> 4;
+    const int r = v & 15;
+    const uint32_t code = R.tcode | static_cast<uint32_t>(r);
+    if constexpr (kProbe) {
+      const uint32_t slot_id = R.t * 32u + 8u * (r / 4) + 4u * half + (r % 4);
+      const uint32_t q = 64u * wv + 32u * c + col;
+      planes[static_cast<size_t>(q) * cap + slot_id] =
+          and_or_b32(__float_as_uint(R.acc[c][r] * R.w[r]), keep_mask, code);
+    } else {
+      const int u = static_cast<int>(and_or_b32(__float_as_uint(R.acc[c][r] * R.w[r]),
+                                                keep_mask, code));
+      med3_i32_into(b2[c], b3[c], u);
+      med3_i32_into(b1[c], b2[c], u);
+      b1[c] = max(b1[c], u);
+    }
+  };
+  // Tile s into R: its reads and MFMAs, with the 32 reductions of the
+  // previous tile P (when there is one) spread over its MFMAs, each MFMA
+  // and its share fenced (sched_barrier) so that the share runs on the
+  // VALU while its MFMA executes.  The weights are read as integers: the compiler then
+  // does not order them after the ring's pending loads.
+  auto step_tile = [&](uint32_t s, Res& R, const Res& P, auto has_prev) {
+    const int slot = static_cast<int>(s % RS::kRing);
+    const u32x4* tile = s_ring + slot * RS::kTileU4;
+    const uint32_t* wt = reinterpret_cast<const uint32_t*>(s_w + slot * RS::kWeightArea);
+    u32x4 af[kPre];
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) af[j] = tile[(2 * j + half) * 32 + col];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 w4 = *reinterpret_cast<const u32x4*>(wt + 8 * i + 4 * half);
+      R.w[4 * i] = __uint_as_float(w4.x);
+      R.w[4 * i + 1] = __uint_as_float(w4.y);
+      R.w[4 * i + 2] = __uint_as_float(w4.z);
+      R.w[4 * i + 3] = __uint_as_float(w4.w);
+    }
+    R.t = t_begin + s;
+    R.tcode = (static_cast<uint32_t>(half) << (ibits - 1)) | (s << 4);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4 a = af[ks % kPre];
+      if (ks + kPre < KS) af[ks % kPre] = tile[(2 * (ks + kPre) + half) * 32 + col];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        R.acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, bq[c][ks]),
+            ks == 0 ? f32x16{} : R.acc[c], 0, 0, 0);
+        // the 32 reductions spread over the tile's 2 KS MFMAs (one each,
+        // about 6 VALU issues, at KS = 16 or 18; two at KS = 8): they
+        // issue while the MFMA runs, before the next MFMA (issue is in order)
+        if constexpr (decltype(has_prev)::value) {
+          constexpr int kM = 2 * KS;
+          const int m = 2 * ks + c;
+#pragma unroll
+          for (int v = m * 32 / kM; v < (m + 1) * 32 / kM; ++v) reduce_one(P, v);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  auto reduce_tile = [&](const Res& R) {
+#pragma unroll
+    for (int v = 0; v < 32; ++v) reduce_one(R, v);
+  };
+
+  Res RA, RB;
+  if (steps > 0) {
+#pragma unroll
+    for (int s = 0; s < RS::kRing - 1; ++s) issue_step(static_cast<uint32_t>(s));
+    enter_step(0);
+    step_tile(0, RA, RB, std::false_type{});
+  }
+  uint32_t s = 1;
+  for (; s + 1 < steps; s += 2) {
+    enter_step(s);
+    step_tile(s, RB, RA, std::true_type{});
+    enter_step(s + 1);
+    step_tile(s + 1, RA, RB, std::true_type{});
+  }
+  if (s < steps) {
+    enter_step(s);
+    step_tile(s, RB, RA, std::true_type{});
+    reduce_tile(RB);
+  } else if (steps > 0) {
+    reduce_tile(RA);
+  }
+  // no load may still be writing LDS when the block ends
+  asm volatile("" ::: "memory");
+  wait_vmcnt_lds<0>();
+  if constexpr (kProbe) return;
+  // merge the two lane halves (disjoint slots of one query), then one
+  // value per (plane, query, sub-stream)
+  const size_t n_sub = W;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int o1 = __shfl_xor(b1[c], 32);
+    const int o2 = __shfl_xor(b2[c], 32);
+    const int o3 = __shfl_xor(b3[c], 32);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int v = j == 0 ? o1 : (j == 1 ? o2 : o3);
+      med3_i32_into(b2[c], b3[c], v);
+      med3_i32_into(b1[c], b2[c], v);
+      b1[c] = max(b1[c], v);
+    }
+    if (half == 0) {
+      const size_t q = static_cast<size_t>(64 * wv + 32 * c + col);
+      planes[(0 * QP + q) * n_sub + blockIdx.x] = static_cast<uint32_t>(b1[c]);
+      planes[(1 * QP + q) * n_sub + blockIdx.x] = static_cast<uint32_t>(b2[c]);
+      planes[(2 * QP + q) * n_sub + blockIdx.x] = static_cast<uint32_t>(b3[c]);
+    }
+  }
+}
+
 // Query rows of one pass for the screen: qpad[j][0, stride) = query j's
 // values rounded to bf16 (nearest even; bf16 queries are copied), zero past
 // dim; inv_qn[j] = 1 / ||q_j|| rounded to fp32.  Rows j >= qc are zero with

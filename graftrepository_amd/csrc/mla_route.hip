@@ -428,6 +428,10 @@ struct MlaDeviceArena {
   grm::MappedCands batch_out;
   grm::MappedBuf batch_status;
   int batch_min = 4;         // timed queries per call from which the batched path runs
+  bool ring = true;          // full 256-query passes on the ring screen (GRM_HIP_BATCH_RING=0: off)
+  float* d_winv = nullptr;   // slot weights of the ring screen (capacity), for bank epoch winv_epoch
+  size_t d_winv_count = 0;
+  uint64_t winv_epoch = ~0ull;
   size_t lds_max = 65536;    // dynamic LDS one block may use
   uint64_t batch_queries = 0;    // queries screened on the matrix cores
   uint64_t batch_fallbacks = 0;  // of those, routed again on the single-query path
@@ -465,6 +469,7 @@ void destroy_arena(MlaDeviceArena* a) {
   if (a->d_qpad) (void)hipFree(a->d_qpad);
   if (a->d_inv_qn) (void)hipFree(a->d_inv_qn);
   if (a->d_entries) (void)hipFree(a->d_entries);
+  if (a->d_winv) (void)hipFree(a->d_winv);
   grm::release_mapped(&a->batch_out);
   grm::release_mapped_bytes(&a->batch_status);
   grm::release_mapped(&a->blocks_out);
@@ -588,6 +593,7 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
     if (v >= 1 && v <= 65536) a->max_blocks = static_cast<uint32_t>(v);
   }
   if (const char* env = getenv("GRM_HIP_MLA_PIPELINE")) a->pipeline = env[0] != '0';
+  if (const char* env = getenv("GRM_HIP_BATCH_RING")) a->ring = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_MLA_BATCH_MIN")) {
     const long v = strtol(env, nullptr, 10);
     if (v >= 1) a->batch_min = static_cast<int>(std::min<long>(v, 1l << 30));
@@ -751,6 +757,8 @@ struct BatchPlan {
   int stride = 0;    // bf16 elements per staged query row
   int qp_max = 0;    // queries per pass (multiple of 32, <= 256)
   int ibits = 0;     // width of the slot code the screen writes into its values
+  bool ring = false;   // full passes run mla_batch_ring_kernel
+  int ibits_ring = 0;  // its slot code width (one sub-stream per block)
 };
 
 // Slot code width of the batched screen: 4 bits of result register, the
@@ -780,14 +788,55 @@ bool batch_plan(const MlaDeviceArena* a, int q_timed, BatchPlan* p) {
   }
   if (a->dim > grm::mla::kBatchMaxDim) return false;
   const uint32_t n_tiles32 = static_cast<uint32_t>((a->high_water + 31) / 32);
-  const uint32_t n_waves = static_cast<uint32_t>(a->cus) * grm::mla::kBatchWaves;
-  const uint32_t max_run = (n_tiles32 + n_waves - 1) / n_waves;
-  int ibits = 5;
-  while ((1u << (ibits - 5)) < max_run) ++ibits;
+  auto code_bits = [&](uint32_t n_sub) {
+    const uint32_t max_run = (n_tiles32 + n_sub - 1) / n_sub;
+    int ibits = 5;
+    while ((1u << (ibits - 5)) < max_run) ++ibits;
+    return ibits;
+  };
+  const int ibits = code_bits(static_cast<uint32_t>(a->cus) * grm::mla::kBatchWaves);
   if (ibits > kMaxSlotCodeBits) return false;
   p->ibits = ibits;
   p->qp_max = qp;
+  p->ibits_ring = code_bits(static_cast<uint32_t>(a->cus));
+  p->ring = a->ring && qp == grm::mla::kRingQueries && p->ibits_ring <= kMaxSlotCodeBits &&
+            grm::mla::RingShape<18>::kLds <= a->lds_max;
   return true;
+}
+
+// A pass of ct column tiles runs on the ring screen when the plan allows
+// it and the pass is full (more than 128 queries, padded to 256).
+bool ring_pass(const BatchPlan& p, int ct) { return p.ring && ct == 8; }
+uint32_t pass_subs(const MlaDeviceArena* a, const BatchPlan& p, int ct) {
+  return static_cast<uint32_t>(a->cus) * (ring_pass(p, ct) ? 1u : static_cast<uint32_t>(grm::mla::kBatchWaves));
+}
+int pass_ibits(const BatchPlan& p, int ct) { return ring_pass(p, ct) ? p.ibits_ring : p.ibits; }
+
+// The ring screen's slot weights, formed again when the bank changed.
+int ensure_weights(MlaDeviceArena* a) {
+  GRM_CHECK_RC(reserve_device(&a->d_winv, &a->d_winv_count, static_cast<size_t>(a->capacity)));
+  if (a->winv_epoch != a->epoch) {
+    const unsigned blocks = static_cast<unsigned>((a->capacity + 255) / 256);
+    grm::mla::mla_batch_weights_kernel<<<blocks, 256, 0, a->stream>>>(a->d_norms, a->capacity,
+                                                                     a->d_winv);
+    GRM_HIP_CHECK(hipGetLastError());
+    a->winv_epoch = a->epoch;
+  }
+  return 0;
+}
+
+template <int KS, bool kProbe = false>
+int launch_ring(MlaDeviceArena* a, uint32_t n_tiles32, int ibits, uint32_t* planes) {
+  using RS = grm::mla::RingShape<KS>;
+  auto kern = grm::mla::mla_batch_ring_kernel<KS, kProbe>;
+  GRM_CHECK_RC(ensure_weights(a));
+  GRM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(RS::kLds)));
+  kern<<<a->cus, grm::mla::kRingWaves * grm::kWave, RS::kLds, a->stream>>>(
+      a->d_tiles, a->d_winv, a->capacity, n_tiles32, a->d_qpad, ibits, planes);
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
 }
 
 template <int KS, int CT, bool kProbe = false>
@@ -808,6 +857,13 @@ int launch_screen(MlaDeviceArena* a, uint32_t n_tiles32, int stride, int ibits, 
 template <bool kProbe>
 int dispatch_screen(MlaDeviceArena* a, const BatchPlan& p, int ct, uint32_t n_tiles32, size_t lds,
                     uint32_t* planes) {
+  if (ring_pass(p, ct)) {
+    switch (p.ks) {
+      case 8: return launch_ring<8, kProbe>(a, n_tiles32, p.ibits_ring, planes);
+      case 16: return launch_ring<16, kProbe>(a, n_tiles32, p.ibits_ring, planes);
+      default: return launch_ring<18, kProbe>(a, n_tiles32, p.ibits_ring, planes);
+    }
+  }
   const int ibits = p.ibits;
 #define GRM_SCREEN_CT(KS)                                                                        \
   switch (ct) {                                                                                  \
@@ -849,8 +905,8 @@ int enqueue_batch_pass(MlaDeviceArena* a, const BatchPlan& p, const unsigned cha
       q, q_dtype, qc, a->dim, p.stride, a->d_qpad, a->d_inv_qn);
   GRM_HIP_CHECK(hipGetLastError());
   const uint32_t n_tiles32 = static_cast<uint32_t>((a->high_water + 31) / 32);
-  const uint32_t n_waves = static_cast<uint32_t>(a->cus) * grm::mla::kBatchWaves;
-  const int ibits = p.ibits;
+  const uint32_t n_waves = pass_subs(a, p, ct);
+  const int ibits = pass_ibits(p, ct);
   const size_t lds = batch_lds(p, qp);
   if (ev) GRM_HIP_CHECK(hipEventRecord(ev[0], a->stream));
   GRM_CHECK_RC(dispatch_screen<false>(a, p, ct, n_tiles32, lds, a->d_entries));
@@ -1791,7 +1847,7 @@ extern "C" int grm_mla_hip_probe_screen(MlaDeviceArena* a, const void* queries_h
   grm::mla::mla_batch_probe_finish_kernel<<<query_count, grm::kWave, 0, a->stream>>>(
       static_cast<const uint32_t*>(d_planes.p), a->capacity, static_cast<uint32_t>(n), a->d_inv_qn,
       d_q.p, query_dtype, a->dim, a->dim, batch_gamma(p), batch_delta(query_dtype), a->d_min_norm,
-      p.ibits, static_cast<float*>(d_vals.p), static_cast<double*>(d_bounds.p));
+      pass_ibits(p, ct), static_cast<float*>(d_vals.p), static_cast<double*>(d_bounds.p));
   GRM_HIP_CHECK(hipGetLastError());
   GRM_HIP_CHECK(hipMemcpyAsync(out_values_host, d_vals.p, static_cast<size_t>(query_count) * n * sizeof(float),
                                hipMemcpyDeviceToHost, a->stream));

@@ -345,6 +345,36 @@ def test_batched_config_parity(hip_lib):
     assert stats["passes"] == 1 and stats["fallbacks"] <= 2
 
 
+@pytest.mark.parametrize("dim", [100, 256, 288])  # K-steps 8, 16 and 18
+def test_batched_ring_screen_dims_and_churn(hip_lib, dim):
+    # Passes of more than 128 queries run the ring screen (queries in
+    # registers, the bank streamed through LDS); its slot weights follow
+    # the bank through evictions and appends.  Ids and score bits against
+    # the oracle, before and after each churn round.
+    rng = np.random.default_rng(dim + 70)
+    rows = wl.mla_rows(30_000, dim, seed=dim + 7, dtype="bf16")
+    ids0 = np.arange(30_000, dtype=np.uint64) * 3 + 5
+    qs = wl.mla_queries(200, dim, seed=dim + 7, dtype="bf16")
+    live = {int(i): rows[j] for j, i in enumerate(ids0)}
+    with MlaNodeBank(rows, ids0, dtype="bf16", capacity=32_000) as bank:
+        for step in range(3):
+            res = bank.route(qs, 8)
+            keys = np.asarray(sorted(live), dtype=np.uint64)
+            mat = np.stack([live[int(k)] for k in keys])
+            want, wsc, _ = oracle.mla_route(_f32(mat), _f32(qs), 8, node_ids=keys)
+            assert_same(res.ids, res.scores, want, wsc)
+            ev = rng.choice(keys, size=900, replace=False)
+            bank.evict(ev)
+            for i in ev.tolist():
+                del live[i]
+            new = wl.mla_rows(800, dim, seed=dim * 10 + step, dtype="bf16")
+            nid = np.arange(800, dtype=np.uint64) + 1_000_000 + 10_000 * step
+            bank.append(new, nid)
+            live.update({int(i): r for i, r in zip(nid.tolist(), new)})
+        stats = bank.route_stats()
+    assert stats["batched"] == 600 and stats["fallbacks"] <= 6
+
+
 @pytest.mark.parametrize("count", [48, 256])  # 256: the full-pass screen
 def test_batched_copies_of_best_rows_far_apart(hip_lib, count):
     # Exact copies of the best rows sit in different screen sub-streams
