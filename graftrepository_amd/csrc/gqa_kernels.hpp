@@ -535,8 +535,9 @@ constexpr int kMaxSmaxCols = 128;  // per screen-only pass (gqa_smax_kernel, NT 
 // the pass (strides R and Qt, see "Query passes"), q_elems values after
 // query qb-1's.
 
-// Block-wide: stage the columns in s_q[cg][HD] as fp32 (exact: queries are
-// fp32 or bf16) and derive each column's screen parameters
+// Block-wide: stage the columns in s_q[cg][QS] (values at [0, HD), rows
+// QS >= HD floats apart) as fp32 (exact: queries are fp32 or bf16) and
+// derive each column's screen parameters
 //  * scale(cg) = 2^-e, the power of two that brings max|q| of the column
 //    under 2^emax (the MFMA type's safe range), 1 for ordinary values;
 //  * the column's bound per unit of key norm, and its absolute part, in the
@@ -565,7 +566,7 @@ constexpr int kMaxSmaxCols = 128;  // per screen-only pass (gqa_smax_kernel, NT 
 // of query, key and sums), so no screened value overflows; for K >= kcap
 // the bound is not established and the screen's users take E = +inf.
 // Ends with a barrier.
-template <int HD>
+template <int HD, int QS = HD>
 __device__ inline void stage_columns(float* __restrict__ s_q, float4* __restrict__ s_ec,
                                      unsigned* __restrict__ s_bad, const void* __restrict__ query,
                                      int q_dtype, size_t q_elems, int cols, int R, int Qt, int Rc,
@@ -576,33 +577,45 @@ __device__ inline void stage_columns(float* __restrict__ s_q, float4* __restrict
   const int wave = threadIdx.x / kWave;
   const int nwaves = blockDim.x / kWave;
   const int RQc = Rc * Qc;
-  for (int i = threadIdx.x; i < cols * HD; i += blockDim.x) {
-    const int cg = i / HD;
-    const int qb = cg / RQc;
-    const int r = (cg % RQc) / Qc;
-    const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
-                         (static_cast<uint64_t>(g * R + r) * Qt + cg % Qc) * HD + (i - cg * HD);
-    s_q[i] = q_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
-                              : static_cast<const float*>(query)[src];
+  {
+    // thread t stages value t % HD of columns t / HD, t / HD + per, ...
+    const int per = static_cast<int>(blockDim.x) / HD;
+    const int d = static_cast<int>(threadIdx.x) % HD;
+    const int first = static_cast<int>(threadIdx.x) / HD;
+    for (int cg = first; cg < cols && first < per; cg += per) {
+      const int qb = cg / RQc;
+      const int r = (cg % RQc) / Qc;
+      const uint64_t src = static_cast<uint64_t>(qb) * q_elems +
+                           (static_cast<uint64_t>(g * R + r) * Qt + cg % Qc) * HD + d;
+      s_q[cg * QS + d] = q_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(query)[src])
+                                          : static_cast<const float*>(query)[src];
+    }
   }
   __syncthreads();
-  for (int cg = wave; cg < cols; cg += nwaves) {
+  // 16 lanes per column, four columns per wave at a time; the first lane
+  // of each column derives its parameters
+  const int sub = lane >> 4;
+  const int sl = lane & 15;
+  for (int c0 = wave * 4; c0 < cols; c0 += nwaves * 4) {
+    const int cg = c0 + sub;
     double ss = 0.0;
     float mx = 0.0f;
-    bool bad = false;
-    for (int d = lane; d < HD; d += kWave) {
-      const float f = s_q[cg * HD + d];
-      bad = bad || !isfinite(f);
-      mx = fmaxf(mx, fabsf(f));
-      ss = fma(static_cast<double>(f), static_cast<double>(f), ss);
+    unsigned bad = 0u;
+    if (cg < cols) {
+      for (int d = sl; d < HD; d += 16) {
+        const float f = s_q[cg * QS + d];
+        bad |= isfinite(f) ? 0u : 1u;
+        mx = fmaxf(mx, fabsf(f));
+        ss = fma(static_cast<double>(f), static_cast<double>(f), ss);
+      }
     }
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
+    for (int off = 1; off < 16; off <<= 1) {
       ss += __shfl_xor(ss, off);
       mx = fmaxf(mx, __shfl_xor(mx, off));
+      bad |= __shfl_xor(bad, off);
     }
-    bad = __ballot(bad) != 0ull;
-    if (lane == 0) {
+    if (sl == 0 && cg < cols) {
       int e = 0;
       if (isfinite(mx) && mx > 0.0f) {
         const int ex = ilogbf(mx);  // mx in [2^ex, 2^(ex+1))
@@ -623,7 +636,7 @@ __device__ inline void stage_columns(float* __restrict__ s_q, float4* __restrict
       s_ec[cg] = make_float4(isfinite(c) ? static_cast<float>(c) * 1.000001f : INFINITY,
                              isfinite(ea) ? static_cast<float>(ea) * 1.000001f : INFINITY, scale,
                              kcap < 0x1p127 ? static_cast<float>(kcap) : INFINITY);
-      s_bad[cg] = bad ? 1u : 0u;
+      s_bad[cg] = bad;
     }
   }
   __syncthreads();
@@ -645,7 +658,7 @@ __device__ inline int frag_dim(int ks, int quarter, int j) {
 // Query fragments of the staged columns: fragment (nt, ks) of lane l holds
 // column nt*16 + l%16 at dims frag_dim(ks, l/16, j), j < 8, of q * scale
 // rounded to nearest even in the MFMA type (columns >= cols are zero).
-template <int MT, bool PERM, int KS, int NT>
+template <int MT, bool PERM, int KS, int NT, int QS = 32 * KS>
 __device__ inline void query_frags(u32x4 (&bq)[NT][KS], const float* __restrict__ s_q,
                                    const float4* __restrict__ s_ec, int cols, int r16,
                                    int quarter) {
@@ -654,7 +667,7 @@ __device__ inline void query_frags(u32x4 (&bq)[NT][KS], const float* __restrict_
   for (int nt = 0; nt < NT; ++nt) {
     const int cg = nt * 16 + r16;
     const float sc = cg < cols ? s_ec[cg].z : 0.0f;
-    const float* qc = s_q + min(cg, cols - 1) * HD;
+    const float* qc = s_q + min(cg, cols - 1) * QS;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       uint32_t w[4];
@@ -684,17 +697,18 @@ __device__ inline void query_frags(u32x4 (&bq)[NT][KS], const float* __restrict_
 // Exact |dot| of one lane's (key token, query column) pair in the law's
 // order: the token's pieces come from the planes (piece c at
 // kp + (c/S)*L*S + c%S, kp the token's piece 0; chunks of S = 2^SS pieces),
-// 64 values' worth in flight at once, the column's
-// values from qrow (LDS, fp32, exact).  Only lanes with `active` set read
-// memory (the others return 0): the candidates are a few lanes of the
-// wave, and their rows are all that is read again.
+// up to 8 pieces in flight at once, the column's values from qrow (LDS,
+// fp32, exact, 16-byte aligned, read 4 values at a time).  Only lanes with
+// `active` set read memory (the others return 0): the candidates are a few
+// lanes of the wave, and their rows are all that is read again.
 template <int KDT, int HD, int SS = 2>
 __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restrict__ kp,
                                              uint64_t L, const unsigned char* __restrict__ sp,
                                              int scale_dtype, int cpg, const float* qrow) {
   using T = KeyTraits<KDT>;
   constexpr int C = HD / T::kEpc;
-  constexpr int kB = C < 64 / T::kEpc ? C : 64 / T::kEpc;  // 64 values per batch
+  // pieces (16 bytes) per batch: 8, or 64 values when fewer
+  constexpr int kB = C < 64 / T::kEpc ? C : (64 / T::kEpc < 8 ? 64 / T::kEpc : 8);
   double acc = 0.0;
   if (!active) return 0.0;
   for (int c0 = 0; c0 < C; c0 += kB) {
@@ -712,10 +726,14 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
     for (int b = 0; b < kB; ++b) {
       float f[T::kEpc];
       decode_chunk<KDT>(v[b], sc[b], f);
-      const float* q = qrow + (c0 + b) * T::kEpc;
+      const float4* q4 = reinterpret_cast<const float4*>(qrow + (c0 + b) * T::kEpc);
 #pragma unroll
-      for (int e = 0; e < T::kEpc; ++e) {
-        acc = fma(static_cast<double>(f[e]), static_cast<double>(q[e]), acc);
+      for (int i = 0; i < T::kEpc / 4; ++i) {
+        const float4 q = q4[i];
+        acc = fma(static_cast<double>(f[4 * i]), static_cast<double>(q.x), acc);
+        acc = fma(static_cast<double>(f[4 * i + 1]), static_cast<double>(q.y), acc);
+        acc = fma(static_cast<double>(f[4 * i + 2]), static_cast<double>(q.z), acc);
+        acc = fma(static_cast<double>(f[4 * i + 3]), static_cast<double>(q.w), acc);
       }
     }
   }
@@ -749,8 +767,18 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
 // pieces); the exact recomputation reads the fp32 rows from xkeys (also
 // chunks of 4 pieces), and eps_rel / eps_abs carry the copy's rounding
 // into the bound (stage_columns).
+//
+// Waves per SIMD asked of the compiler: 4 (at most 128 VGPRs) for the fp32
+// bank's single column block at head_dim 128, which otherwise takes a few
+// registers more for its exact recomputation and loses a wave of the
+// stream; 2 or 1 elsewhere.
+template <int KDT, int KS, int NT, bool XF32>
+constexpr int sr_waves_per_simd() {
+  return XF32 && NT == 1 && KS == 4 ? 4 : ((NT * KS <= 16 && KS <= 4 && (KDT != kI8 || KS == 4 || NT == 1)) ? 2 : 1);
+}
+
 template <int KDT, int KS, int NT, bool XF32 = false>
-__global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && KS <= 4 && (KDT != kI8 || KS == 4 || NT == 1)) ? 2 : 1) void gqa_sr_kernel(
+__global__ __launch_bounds__(kUnitWaves * kWave, (sr_waves_per_simd<KDT, KS, NT, XF32>())) void gqa_sr_kernel(
     const unsigned char* __restrict__ keys, const unsigned char* __restrict__ xkeys,
     const unsigned char* __restrict__ scales, int scale_dtype, int group_size,
     const Item* __restrict__ items, uint32_t n_items, int kv, int R, int Qt, int Rc, int Qc,
@@ -762,7 +790,11 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && KS <= 4 && (K
   constexpr int MT = ScreenTraits<KDT>::kMfma;
   constexpr int HD = 32 * KS;
   constexpr int C = HD / KT::kEpc;  // chunks per key row
-  extern __shared__ float s_q[];  // [cols][HD]: the block's query columns
+  // [cols][QS]: the block's query columns; rows padded by 4 floats, so the
+  // exact recomputations of 16 columns (one lane each, 16-byte reads at
+  // the same offset) fall in distinct banks
+  constexpr int QS = HD + 4;
+  extern __shared__ __align__(16) float s_q[];
   __shared__ float4 s_ec[kMaxCols];  // {coef, eabs, scale, kcap} per column
   __shared__ unsigned s_bad[kMaxCols];
   const int lane = threadIdx.x & (kWave - 1);
@@ -827,8 +859,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && KS <= 4 && (K
     load_tile(x2, 2);
     load_tile(x3, 3);
   }
-  stage_columns<HD>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, Rc, Qc, g, emax,
-                    gamma, delta, 0.0, sigma_q, sigma_k, sigma_p, eps_rel, eps_abs);
+  stage_columns<HD, QS>(s_q, s_ec, s_bad, query, q_dtype, q_elems, cols, R, Qt, Rc, Qc, g, emax,
+                        gamma, delta, 0.0, sigma_q, sigma_k, sigma_p, eps_rel, eps_abs);
   __syncthreads();
   if (item_block == 0 && threadIdx.x < static_cast<unsigned>(Qb)) {
     unsigned bad = 0u;
@@ -840,7 +872,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && KS <= 4 && (K
   // B fragments from the staged columns: fragment (nt, ks) lane l holds
   // column nt*16 + l%16 at dims ks*32 + (l/16)*8 + j, j < 8.
   u32x4 bq[NT][KS];
-  query_frags<MT, false, KS, NT>(bq, s_q, s_ec, cols, r16, quarter);
+  query_frags<MT, false, KS, NT, QS>(bq, s_q, s_ec, cols, r16, quarter);
 
   auto frag = [&](const Tile& b, int ks) -> u32x4 {
     if constexpr (KDT != kI8) {
@@ -949,11 +981,11 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (NT * KS <= 16 && KS <= 4 && (K
     if constexpr (XF32) {
       const u32x4* xplane = reinterpret_cast<const u32x4*>(xkeys) + row0 * (HD / 4);
       return exact_pair<kF32, HD>(active, xplane + static_cast<uint64_t>(tt) * 4, L, nullptr,
-                                  scale_dtype, 1, s_q + min(cg, cols - 1) * HD);
+                                  scale_dtype, 1, s_q + min(cg, cols - 1) * QS);
     } else {
       return exact_pair<KDT, HD>(active, kplane + static_cast<uint64_t>(tt) * 4, L,
                                  KDT == kI8 ? splane + static_cast<size_t>(tt) * ses : nullptr,
-                                 scale_dtype, cpg, s_q + min(cg, cols - 1) * HD);
+                                 scale_dtype, cpg, s_q + min(cg, cols - 1) * QS);
     }
   };
   double best[NT];

@@ -869,8 +869,14 @@ int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
   const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
   const size_t hstride = a->cap_nodes * static_cast<size_t>(p.H);
   const double denom = sqrt(static_cast<double>(a->hd));
-  const size_t lds = static_cast<size_t>(cols) * a->hd * sizeof(float);  // <= 64 KiB
+  // query columns in rows of hd + 4 floats: <= 66,560 bytes
+  const size_t lds = static_cast<size_t>(cols) * (a->hd + 4) * sizeof(float);
 #define GRM_SR(KDT, KS, NTT, XF)                                                                \
+  if (lds > 65536) {                                                                            \
+    GRM_HIP_CHECK(hipFuncSetAttribute(                                                          \
+        reinterpret_cast<const void*>(grm::gqa::gqa_sr_kernel<KDT, KS, NTT, XF>),               \
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));                    \
+  }                                                                                             \
   grm::gqa::gqa_sr_kernel<KDT, KS, NTT, XF><<<grid, threads, lds, a->stream>>>(                 \
       screen_keys(a), a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,        \
       static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, ps.rc, ps.qc, qpass, q_dtype, q_elems,  \
