@@ -98,6 +98,10 @@ struct GqaDeviceArena {
   uint32_t chunk = 256;  // key tokens per work item
   Item* d_items = nullptr;
   size_t d_items_count = 0;
+  // the same items by decreasing token count in 64-token classes, address
+  // order within a class (screen-and-refine passes with a heavy refine)
+  Item* d_items_sized = nullptr;
+  size_t d_items_sized_count = 0;
   uint64_t n_items = 0;
   // one item per live node with key tokens (all of them), for the
   // screen-only pass of the bound-and-verify path
@@ -121,6 +125,9 @@ struct GqaDeviceArena {
   size_t d_q64_count = 0;
   // screen-and-refine path
   int screen_mode = -1;  // -1 whenever the shape allows, 0 never
+  // item order of screen-and-refine passes: -1 by the pass's shape, 0
+  // address (slot) order, 1 by decreasing size
+  int sr_order = -1;
   // bound-and-verify path (batched queries): -1 when a pass has more than
   // 16 query columns per kv head, 0 never, 1 whenever the screen runs
   int bound_mode = -1;
@@ -234,7 +241,7 @@ void destroy_arena(GqaDeviceArena* a) {
   if (a->stream) (void)hipStreamSynchronize(a->stream);
   if (a->side) (void)hipStreamSynchronize(a->side);
   void* dev[] = {a->d_keys,   a->d_scales,  a->d_tok_off, a->d_len,    a->d_ids,   a->d_skeys,
-                 a->d_flags,  a->d_nonfinite, a->d_kmax,  a->d_items,  a->d_hmax,
+                 a->d_flags,  a->d_nonfinite, a->d_kmax,  a->d_items,  a->d_items_sized, a->d_hmax,
                  a->d_qbad,   a->d_queries, a->d_stage,   a->d_q64,    a->d_hmaxf,
                  a->d_colinfo, a->d_lbub,   a->d_blists,  a->d_cslots, a->d_ccount,
                  a->d_citems, a->d_units,   a->d_fbits,   a->d_fflags,  a->d_sitems,
@@ -473,6 +480,9 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
     if (v >= 16 && v <= 4096 && v % 16 == 0) a->chunk = static_cast<uint32_t>(v);
   }
   if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
+  if (const char* env = getenv("GRM_HIP_GQA_SR_ORDER")) {
+    a->sr_order = strcmp(env, "slot") == 0 ? 0 : (strcmp(env, "size") == 0 ? 1 : -1);
+  }
   if (const char* env = getenv("GRM_HIP_GQA_SPARSE")) a->sparse_exact = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_GQA_WIDE_SMAX")) a->wide_smax = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_GQA_SMAX_SPLIT")) {
@@ -589,10 +599,17 @@ int ensure_items(GqaDeviceArena* a) {
     for (const Item& u : units) sorted[start[key(u)]++] = u;
     units.swap(sorted);
   }
+  std::vector<Item> sized(items);
+  std::stable_sort(sized.begin(), sized.end(), [](const Item& x, const Item& y) {
+    return (x.count + 63) / 64 > (y.count + 63) / 64;
+  });
   GRM_CHECK_RC(reserve_device(&a->d_items, &a->d_items_count, items.size()));
+  GRM_CHECK_RC(reserve_device(&a->d_items_sized, &a->d_items_sized_count, items.size()));
   GRM_CHECK_RC(reserve_device(&a->d_units, &a->d_units_count, units.size()));
   if (!items.empty()) {
     GRM_HIP_CHECK(hipMemcpyAsync(a->d_items, items.data(), items.size() * sizeof(Item),
+                                 hipMemcpyHostToDevice, a->stream));
+    GRM_HIP_CHECK(hipMemcpyAsync(a->d_items_sized, sized.data(), sized.size() * sizeof(Item),
                                  hipMemcpyHostToDevice, a->stream));
     GRM_HIP_CHECK(hipMemcpyAsync(a->d_units, units.data(), units.size() * sizeof(Item),
                                  hipMemcpyHostToDevice, a->stream));
@@ -869,6 +886,15 @@ int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
   const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
   const size_t hstride = a->cap_nodes * static_cast<size_t>(p.H);
   const double denom = sqrt(static_cast<double>(a->hd));
+  // Item order: with a light refine (at most 4 query columns per kv head,
+  // keys exact in the screen) address order streams best (C4 shape, one
+  // query token: 192 us against 198 us by size); with a heavier refine
+  // (more columns, or an fp32 bank's rows read again in fp32) the waves of
+  // short items at the launch's end even out the refines' cost (4 tokens:
+  // 221 us against 252 us; fp32 bank: 215 us against 227 us).
+  // GRM_HIP_GQA_SR_ORDER=slot / size fixes either.
+  const bool by_size = a->sr_order >= 0 ? a->sr_order == 1 : (cols > 4 || a->d_skeys != nullptr);
+  const Item* sr_items = by_size ? a->d_items_sized : a->d_items;
   // query columns in rows of hd + 4 floats: <= 66,560 bytes
   const size_t lds = static_cast<size_t>(cols) * (a->hd + 4) * sizeof(float);
 #define GRM_SR(KDT, KS, NTT, XF)                                                                \
@@ -878,7 +904,7 @@ int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));                    \
   }                                                                                             \
   grm::gqa::gqa_sr_kernel<KDT, KS, NTT, XF><<<grid, threads, lds, a->stream>>>(                 \
-      screen_keys(a), a->d_keys, a->d_scales, a->scale_dtype, a->group_size, a->d_items,        \
+      screen_keys(a), a->d_keys, a->d_scales, a->scale_dtype, a->group_size, sr_items,          \
       static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, ps.rc, ps.qc, qpass, q_dtype, q_elems,  \
       qb, eb.emax, eb.gamma, eb.delta, eb.sigma_q, eb.sigma_k, eb.sigma_p, eb.eps_rel,          \
       eb.eps_abs, a->d_qbad, pi > 0 ? 1 : 0, reinterpret_cast<const float*>(a->d_kmax), denom,   \
