@@ -740,6 +740,92 @@ __device__ __forceinline__ double exact_pair(bool active, const u32x4* __restric
   return fabs(acc);
 }
 
+// Exact |dot| of the wavefront's candidate pairs (the lanes with `active`
+// set: key token tok of the wavefront's plane, plane + tok*S + (c/S)*L*S +
+// c%S holding its piece c, chunks of S = 2^SS pieces; query column values
+// at qrow, LDS, fp32, 16-byte aligned),
+// each in the law's order as in exact_pair, with the candidates' rows read
+// once for the whole wavefront: in rounds of up to kRows candidates (about
+// 4 KiB of rows) every lane loads 4 of the round's 16-byte pieces -- one
+// memory round trip per round instead of a dependent batch per 64 values
+// of one lane's row -- the pieces go to the wavefront's LDS rows s_rows
+// (rows C + 1 pieces apart, so the candidates' reads of one piece spread
+// over the banks), and each candidate lane runs its dot product from
+// there.  s_tok holds the round's tokens.  Called by the whole
+// wavefront (plane and L wave-uniform); inactive lanes return 0.
+template <int RKDT, int HD>
+struct GatherShape {
+  static constexpr int kC = HD / KeyTraits<RKDT>::kEpc;  // pieces per row
+  static constexpr int kRows = 4096 / (kC * 16) < 1 ? 1 : (4096 / (kC * 16) > 64 ? 64 : 4096 / (kC * 16));
+  static constexpr int kStride = kC + 1;  // LDS row stride in pieces
+  static constexpr int kPieces = kRows * kStride;
+};
+
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int RKDT, int HD, int SS = 2>
+__device__ __forceinline__ double exact_gathered(bool active, const u32x4* __restrict__ plane,
+                                                 uint32_t tok, uint64_t L, const float* qrow,
+                                                 u32x4* s_rows, uint32_t* s_tok) {
+  using T = KeyTraits<RKDT>;
+  using GS = GatherShape<RKDT, HD>;
+  constexpr int C = GS::kC;
+  constexpr int kPer = (GS::kRows * C + kWave - 1) / kWave;  // pieces per lane per round
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint64_t m = __ballot(active);
+  const int n = __popcll(m);
+  const int rank = __popcll(m & ((1ull << lane) - 1ull));
+  double out = 0.0;
+  for (int r0 = 0; r0 < n; r0 += GS::kRows) {
+    const int nr = min(GS::kRows, n - r0);
+    const bool mine = active && rank >= r0 && rank < r0 + nr;
+    if (mine) s_tok[rank - r0] = tok;
+    wave_lds_sync();
+    u32x4 v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int pc = lane + kWave * i;
+      if (pc < nr * C) {
+        const int j = pc % C;
+        v[i] = plane[(static_cast<uint64_t>(s_tok[pc / C]) << SS) +
+                     (static_cast<uint64_t>(j >> SS) * L << SS) + (j & ((1 << SS) - 1))];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int pc = lane + kWave * i;
+      if (pc < nr * C) s_rows[(pc / C) * GS::kStride + pc % C] = v[i];
+    }
+    wave_lds_sync();
+    if (mine) {
+      const u32x4* row = s_rows + (rank - r0) * GS::kStride;
+      double acc = 0.0;
+#pragma unroll
+      for (int j = 0; j < C; ++j) {
+        float f[T::kEpc];
+        decode_chunk<RKDT>(row[j], 0.0f, f);
+        const float4* q4 = reinterpret_cast<const float4*>(qrow + j * T::kEpc);
+#pragma unroll
+        for (int i = 0; i < T::kEpc / 4; ++i) {
+          const float4 q = q4[i];
+          acc = fma(static_cast<double>(f[4 * i]), static_cast<double>(q.x), acc);
+          acc = fma(static_cast<double>(f[4 * i + 1]), static_cast<double>(q.y), acc);
+          acc = fma(static_cast<double>(f[4 * i + 2]), static_cast<double>(q.z), acc);
+          acc = fma(static_cast<double>(f[4 * i + 3]), static_cast<double>(q.w), acc);
+        }
+      }
+      out = fabs(acc);
+    }
+    // the next round writes the same rows and addresses
+    wave_lds_sync();
+  }
+  return out;
+}
+
 // Screen and refine; grid (kv heads, ceil(items / 4)) -- or, past the
 // grid's y limit, (ceil(items / 4), kv heads) -- one wavefront per
 // (item, kv head g).
@@ -797,6 +883,15 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (sr_waves_per_simd<KDT, KS, NT,
   extern __shared__ __align__(16) float s_q[];
   __shared__ float4 s_ec[kMaxCols];  // {coef, eabs, scale, kcap} per column
   __shared__ unsigned s_bad[kMaxCols];
+  // each wavefront's gathered candidate rows: an fp32 bank's exact
+  // recomputations read fp32 rows, 512 bytes at head_dim 128, which a
+  // lane alone would fetch in four dependent batches (exact_gathered: one
+  // round trip for the wave); rows of the screened keys themselves take
+  // one or two batches and are recomputed lane by lane (exact_pair), which
+  // measured faster for them
+  using GS = GatherShape<kF32, HD>;
+  __shared__ u32x4 s_rows[kUnitWaves][XF32 ? GS::kPieces : 1];
+  __shared__ uint32_t s_tok[kUnitWaves][XF32 ? GS::kRows : 1];
   const int lane = threadIdx.x & (kWave - 1);
   // g_fast: grid (kv, item blocks), so consecutive blocks read one node's
   // neighbouring kv-head blocks; else grid (item blocks, kv)
@@ -976,12 +1071,13 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (sr_waves_per_simd<KDT, KS, NT,
   }
   const bool enumerate = __ballot(amb) != 0ull;
 
+  const int wv = threadIdx.x / kWave;
   auto pair = [&](bool active, uint32_t t, int cg) -> double {
     const uint32_t tt = min(it.t0 + t, last);
     if constexpr (XF32) {
       const u32x4* xplane = reinterpret_cast<const u32x4*>(xkeys) + row0 * (HD / 4);
-      return exact_pair<kF32, HD>(active, xplane + static_cast<uint64_t>(tt) * 4, L, nullptr,
-                                  scale_dtype, 1, s_q + min(cg, cols - 1) * QS);
+      return exact_gathered<kF32, HD>(active, xplane, tt, L, s_q + min(cg, cols - 1) * QS,
+                                      s_rows[wv], s_tok[wv]);
     } else {
       return exact_pair<KDT, HD>(active, kplane + static_cast<uint64_t>(tt) * 4, L,
                                  KDT == kI8 ? splane + static_cast<size_t>(tt) * ses : nullptr,
