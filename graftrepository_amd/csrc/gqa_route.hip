@@ -167,8 +167,8 @@ struct GqaDeviceArena {
   size_t d_queries_bytes = 0;
   // pinned staging of host queries (the route's own; mutations stage
   // through h_stage on the side stream)
-  unsigned char* h_qstage = nullptr;
-  size_t h_qstage_bytes = 0;
+  grm::MappedBuf q_map;
+  bool query_dma = false;  // GRM_HIP_QUERY_COPY=dma: copy engine instead of fetch_async
   void* h_stage = nullptr;
   size_t h_stage_bytes = 0;
   void* d_stage = nullptr;
@@ -252,7 +252,7 @@ void destroy_arena(GqaDeviceArena* a) {
   grm::release_mapped(&a->blocks_out);
   grm::release_mapped_bytes(&a->done_flags);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
-  if (a->h_qstage) (void)hipHostFree(a->h_qstage);
+  grm::release_mapped_bytes(&a->q_map);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
   if (a->ev_mut) (void)hipEventDestroy(a->ev_mut);
@@ -480,6 +480,7 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
     if (v >= 16 && v <= 4096 && v % 16 == 0) a->chunk = static_cast<uint32_t>(v);
   }
   if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
+  if (const char* env = getenv("GRM_HIP_QUERY_COPY")) a->query_dma = strcmp(env, "dma") == 0;
   if (const char* env = getenv("GRM_HIP_GQA_SR_ORDER")) {
     a->sr_order = strcmp(env, "slot") == 0 ? 0 : (strcmp(env, "size") == 0 ? 1 : -1);
   }
@@ -1268,16 +1269,22 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   const size_t qstride = qvals * (q_dtype == kF32 ? 4 : 2);
   const unsigned char* qbase = static_cast<const unsigned char*>(queries);
   if (!on_device) {
-    // Host queries go through a pinned buffer: a copy from pageable memory
-    // stages through the runtime's own buffers, which cost about 30 us more
-    // per call for a 64 KiB query and 12 us for 32 KiB.  The buffer is free
-    // again once the previous route returned (every route waits for its
-    // stream before returning).
+    // Host queries go through a pinned, device-mapped buffer, which a copy
+    // kernel on the route's stream reads (fetch_async): a copy from
+    // pageable memory stages through the runtime's own buffers (about 30 us
+    // more per call for a 64 KiB query, 12 us for 32 KiB), and a copy
+    // engine's transfer is handed over to the route's queue.  The buffer is
+    // free again once the previous route returned (every route waits for
+    // its stream before returning).
     const size_t qbytes = qstride * q_count;
     GRM_CHECK_RC(reserve_device(reinterpret_cast<unsigned char**>(&a->d_queries), &a->d_queries_bytes, qbytes));
-    GRM_CHECK_RC(reserve_pinned(&a->h_qstage, &a->h_qstage_bytes, qbytes));
-    memcpy(a->h_qstage, queries, qbytes);
-    GRM_HIP_CHECK(hipMemcpyAsync(a->d_queries, a->h_qstage, qbytes, hipMemcpyHostToDevice, a->stream));
+    GRM_CHECK_RC(grm::reserve_mapped_bytes(&a->q_map, qbytes));
+    memcpy(a->q_map.host, queries, qbytes);
+    if (a->query_dma) {
+      GRM_HIP_CHECK(hipMemcpyAsync(a->d_queries, a->q_map.host, qbytes, hipMemcpyHostToDevice, a->stream));
+    } else {
+      GRM_CHECK_RC(grm::fetch_async(a->d_queries, a->q_map.dev, qbytes, a->stream));
+    }
     qbase = static_cast<const unsigned char*>(a->d_queries);
   }
   const uint32_t n_slots = static_cast<uint32_t>(a->high_water);

@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 
 namespace grm {
@@ -169,6 +170,30 @@ __global__ __launch_bounds__(kMergeWaves * kWave) void topk_merge_kernel(
     if (lane < k) out[static_cast<size_t>(blockIdx.x) * k + lane] = wl_entry(B);
     if (lane == 0 && flags) flags[blockIdx.x] = 0u;
   }
+}
+
+// dst[i] = src[i] for the 16-byte words [0, n16) and the tail bytes
+// [16 * n16, bytes), grid-stride.
+__global__ __launch_bounds__(256) void fetch_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src,
+                                                    size_t n16, size_t bytes) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride) {
+    dst[i] = src[i];
+  }
+  if (blockIdx.x == 0 && threadIdx.x < bytes - n16 * 16) {
+    reinterpret_cast<unsigned char*>(dst)[n16 * 16 + threadIdx.x] =
+        reinterpret_cast<const unsigned char*>(src)[n16 * 16 + threadIdx.x];
+  }
+}
+
+int fetch_async(void* dst, const void* src_mapped, size_t bytes, hipStream_t stream) {
+  if (bytes == 0) return 0;
+  const size_t n16 = bytes / 16;
+  const unsigned blocks = static_cast<unsigned>(std::max<size_t>(1, std::min<size_t>((n16 + 255) / 256, 1024)));
+  fetch_kernel<<<blocks, 256, 0, stream>>>(static_cast<uint4*>(dst), static_cast<const uint4*>(src_mapped), n16,
+                                           bytes);
+  GRM_HIP_CHECK(hipGetLastError());
+  return 0;
 }
 
 }  // namespace grm

@@ -296,6 +296,13 @@ struct MappedCands {
 int reserve_mapped(MappedCands* m, size_t count);
 void release_mapped(MappedCands* m);
 
+// Copy `bytes` from host-mapped pinned memory (src: its device address) to
+// device memory dst on `stream` with a copy kernel.  For a route's small
+// per-call upload (a query) the kernel runs on the route's own queue right
+// before the route's kernels; a copy engine's transfer would first be
+// handed over between queues, which costs more than the transfer itself.
+int fetch_async(void* dst, const void* src_mapped, size_t bytes, hipStream_t stream);
+
 // Merge `count` candidates per query (query q reads in + q*in_stride) into
 // out + q*k; one block of kMergeWaves waves per query.  Clears flags[q] when
 // flags is given.  Defined in grm_common.hip.
