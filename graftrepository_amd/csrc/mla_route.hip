@@ -427,6 +427,10 @@ struct MlaDeviceArena {
   size_t d_entries_count = 0;
   grm::MappedCands batch_out;
   grm::MappedBuf batch_status;
+  // host queries staged for fetch_async (GRM_HIP_QUERY_COPY=dma: the copy
+  // engine instead)
+  grm::MappedBuf q_map;
+  bool query_dma = false;
   int batch_min = 4;         // timed queries per call from which the batched path runs
   bool ring = true;          // full 256-query passes on the ring screen (GRM_HIP_BATCH_RING=0: off)
   float* d_winv = nullptr;   // slot weights of the ring screen (capacity), for bank epoch winv_epoch
@@ -472,6 +476,7 @@ void destroy_arena(MlaDeviceArena* a) {
   if (a->d_winv) (void)hipFree(a->d_winv);
   grm::release_mapped(&a->batch_out);
   grm::release_mapped_bytes(&a->batch_status);
+  grm::release_mapped_bytes(&a->q_map);
   grm::release_mapped(&a->blocks_out);
   grm::release_mapped_bytes(&a->done_flags);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
@@ -594,6 +599,7 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
   }
   if (const char* env = getenv("GRM_HIP_MLA_PIPELINE")) a->pipeline = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_BATCH_RING")) a->ring = env[0] != '0';
+  if (const char* env = getenv("GRM_HIP_QUERY_COPY")) a->query_dma = strcmp(env, "dma") == 0;
   if (const char* env = getenv("GRM_HIP_MLA_BATCH_MIN")) {
     const long v = strtol(env, nullptr, 10);
     if (v >= 1) a->batch_min = static_cast<int>(std::min<long>(v, 1l << 30));
@@ -941,10 +947,17 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
   const size_t per_q = static_cast<size_t>(g.blocks) * topk;
   const unsigned char* qbase = static_cast<const unsigned char*>(queries);
   if (!on_device) {
+    // through a pinned, device-mapped buffer and a copy kernel on the
+    // route's stream (fetch_async), as the GQA routes take theirs
     GRM_CHECK_RC(reserve_device(reinterpret_cast<unsigned char**>(&a->d_queries),
                                 &a->d_queries_bytes, qbytes));
-    GRM_HIP_CHECK(hipMemcpyAsync(a->d_queries, queries, qbytes,
-                                 hipMemcpyHostToDevice, a->stream));
+    GRM_CHECK_RC(grm::reserve_mapped_bytes(&a->q_map, qbytes));
+    memcpy(a->q_map.host, queries, qbytes);
+    if (a->query_dma) {
+      GRM_HIP_CHECK(hipMemcpyAsync(a->d_queries, a->q_map.host, qbytes, hipMemcpyHostToDevice, a->stream));
+    } else {
+      GRM_CHECK_RC(grm::fetch_async(a->d_queries, a->q_map.dev, qbytes, a->stream));
+    }
     qbase = static_cast<const unsigned char*>(a->d_queries);
   }
   if (a->mut_pending) GRM_HIP_CHECK(hipStreamWaitEvent(a->stream, a->ev_mut, 0));
