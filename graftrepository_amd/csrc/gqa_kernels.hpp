@@ -658,29 +658,48 @@ __device__ inline int frag_dim(int ks, int quarter, int j) {
 // Query fragments of the staged columns: fragment (nt, ks) of lane l holds
 // column nt*16 + l%16 at dims frag_dim(ks, l/16, j), j < 8, of q * scale
 // rounded to nearest even in the MFMA type (columns >= cols are zero).
+// split (one column block, cols <= 8): column slots [cols, 2 cols) hold
+// the remainders of columns [0, cols), q * scale minus its rounding,
+// themselves rounded to the MFMA type, so that a column's screened value
+// is the sum of its slot and the slot cols lanes up: the query's rounding
+// error drops from u |q| to u^2 |q| per value (u the type's unit
+// roundoff); the remainder is exact in fp32 (Sterbenz: within u of q).
 template <int MT, bool PERM, int KS, int NT, int QS = 32 * KS>
 __device__ inline void query_frags(u32x4 (&bq)[NT][KS], const float* __restrict__ s_q,
                                    const float4* __restrict__ s_ec, int cols, int r16,
-                                   int quarter) {
-  constexpr int HD = 32 * KS;
+                                   int quarter, bool split = false) {
+  auto rne = [](float f) -> uint32_t {  // bf16 bits, round to nearest even (finite inputs)
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  };
+  auto rounded = [&](float f) -> float {  // f in the MFMA type, as fp32
+    if constexpr (MT == kBF16) {
+      return __uint_as_float(rne(f) << 16);
+    } else {
+      return static_cast<float>(static_cast<_Float16>(f));
+    }
+  };
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int cg = nt * 16 + r16;
-    const float sc = cg < cols ? s_ec[cg].z : 0.0f;
-    const float* qc = s_q + min(cg, cols - 1) * QS;
+    const bool lo = split && cg >= cols && cg < 2 * cols;
+    const int src = lo ? cg - cols : cg;
+    const bool has = src < cols;
+    const float sc = has ? s_ec[src].z : 0.0f;
+    const float* qc = s_q + min(src, cols - 1) * QS;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       uint32_t w[4];
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
         const int d = frag_dim<PERM>(ks, quarter, j);
-        const float f0 = cg < cols ? qc[d] * sc : 0.0f;
-        const float f1 = cg < cols ? qc[d + 1] * sc : 0.0f;
+        float f0 = has ? qc[d] * sc : 0.0f;
+        float f1 = has ? qc[d + 1] * sc : 0.0f;
+        if (lo) {
+          f0 -= rounded(f0);
+          f1 -= rounded(f1);
+        }
         if constexpr (MT == kBF16) {
-          auto rne = [](float f) {  // round to nearest even (finite inputs)
-            const uint32_t u = __float_as_uint(f);
-            return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-          };
           w[j / 2] = rne(f0) | (rne(f1) << 16);
         } else {
           w[j / 2] = pack_f16x2(static_cast<_Float16>(f0), static_cast<_Float16>(f1));
@@ -871,7 +890,7 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (sr_waves_per_simd<KDT, KS, NT,
     const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
     double gamma, double delta, double sigma_q, double sigma_k, double sigma_p,
     double eps_rel, double eps_abs, unsigned* __restrict__ qflags, int flags_or, const float* __restrict__ kmax, double denom,
-    unsigned long long* __restrict__ hmax, size_t hstride, size_t cap, int g_fast) {
+    unsigned long long* __restrict__ hmax, size_t hstride, size_t cap, int g_fast, int split) {
   using KT = KeyTraits<KDT>;
   constexpr int MT = ScreenTraits<KDT>::kMfma;
   constexpr int HD = 32 * KS;
@@ -967,7 +986,9 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (sr_waves_per_simd<KDT, KS, NT,
   // B fragments from the staged columns: fragment (nt, ks) lane l holds
   // column nt*16 + l%16 at dims ks*32 + (l/16)*8 + j, j < 8.
   u32x4 bq[NT][KS];
-  query_frags<MT, false, KS, NT, QS>(bq, s_q, s_ec, cols, r16, quarter);
+  // split (fp32 queries, at most 8 columns): remainders in the idle slots
+  const bool sp = NT == 1 && split != 0;
+  query_frags<MT, false, KS, NT, QS>(bq, s_q, s_ec, cols, r16, quarter, sp);
 
   auto frag = [&](const Tile& b, int ks) -> u32x4 {
     if constexpr (KDT != kI8) {
@@ -996,7 +1017,13 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (sr_waves_per_simd<KDT, KS, NT,
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) c = mfma16x16x32<MT>(frag(b, ks), bq[nt][ks], c);
     const uint32_t tb = static_cast<uint32_t>(tile) * 16 + quarter * 4;  // item-relative
-    const float cv[4] = {c.x, c.y, c.z, c.w};
+    float cv[4] = {c.x, c.y, c.z, c.w};
+    if (sp) {
+      // the remainder slot of column r16 (< cols) is cols lanes up, in
+      // the same quarter; lanes of other slots are not live
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cv[i] += __shfl(cv[i], lane + cols);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = tb + i < it.count ? fabsf(cv[i]) : -INFINITY;
   };

@@ -169,6 +169,7 @@ struct GqaDeviceArena {
   // through h_stage on the side stream)
   grm::MappedBuf q_map;
   bool query_dma = false;  // GRM_HIP_QUERY_COPY=dma: copy engine instead of fetch_async
+  bool query_split = true;  // fp32 queries split into two MFMA-type parts (launch_sr_pass)
   void* h_stage = nullptr;
   size_t h_stage_bytes = 0;
   void* d_stage = nullptr;
@@ -481,6 +482,7 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   }
   if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
   if (const char* env = getenv("GRM_HIP_QUERY_COPY")) a->query_dma = strcmp(env, "dma") == 0;
+  if (const char* env = getenv("GRM_HIP_GQA_SPLIT")) a->query_split = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_GQA_SR_ORDER")) {
     a->sr_order = strcmp(env, "slot") == 0 ? 0 : (strcmp(env, "size") == 0 ? 1 : -1);
   }
@@ -895,6 +897,22 @@ int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
   // 221 us against 252 us; fp32 bank: 215 us against 227 us).
   // GRM_HIP_GQA_SR_ORDER=slot / size fixes either.
   const bool by_size = a->sr_order >= 0 ? a->sr_order == 1 : (cols > 4 || a->d_skeys != nullptr);
+  // fp32 queries over at most 8 columns: each column's remainder after its
+  // rounding to the MFMA type rides in an idle column slot (gqa_sr_kernel,
+  // query_frags), so the query's rounding leaves the bound: per value
+  // |q - hi - lo| <= u^2 |q| + (1 + u) sigma_q (u the type's unit
+  // roundoff), and the two fp32 accumulations plus their sum stay within
+  // (gamma (1 + 3u) + 2^-24) ||q|| ||k||, so gamma' = gamma (1 + 2^-6) +
+  // 2^-23, delta' = u^2 and sigma_q' = 2 sigma_q bound it
+  // (GRM_HIP_GQA_SPLIT=0: no split).
+  const int split = a->query_split && q_dtype == kF32 && NT == 1 && cols <= 8 ? 1 : 0;
+  ScreenBound sb = eb;
+  if (split) {
+    const double u = p.mfma == kBF16 ? ldexp(1.0, -8) : ldexp(1.0, -11);
+    sb.delta = u * u;
+    sb.gamma = eb.gamma * (1.0 + ldexp(1.0, -6)) + ldexp(1.0, -23);
+    sb.sigma_q = 2.0 * eb.sigma_q;
+  }
   const Item* sr_items = by_size ? a->d_items_sized : a->d_items;
   // query columns in rows of hd + 4 floats: <= 66,560 bytes
   const size_t lds = static_cast<size_t>(cols) * (a->hd + 4) * sizeof(float);
@@ -907,9 +925,9 @@ int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
   grm::gqa::gqa_sr_kernel<KDT, KS, NTT, XF><<<grid, threads, lds, a->stream>>>(                 \
       screen_keys(a), a->d_keys, a->d_scales, a->scale_dtype, a->group_size, sr_items,          \
       static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, ps.rc, ps.qc, qpass, q_dtype, q_elems,  \
-      qb, eb.emax, eb.gamma, eb.delta, eb.sigma_q, eb.sigma_k, eb.sigma_p, eb.eps_rel,          \
-      eb.eps_abs, a->d_qbad, pi > 0 ? 1 : 0, reinterpret_cast<const float*>(a->d_kmax), denom,   \
-      hpass, hstride, a->cap_nodes, g_fast)
+      qb, sb.emax, sb.gamma, sb.delta, sb.sigma_q, sb.sigma_k, sb.sigma_p, sb.eps_rel,          \
+      sb.eps_abs, a->d_qbad, pi > 0 ? 1 : 0, reinterpret_cast<const float*>(a->d_kmax), denom,   \
+      hpass, hstride, a->cap_nodes, g_fast, split)
 #define GRM_SR_NT(KDT, KS, XF)                 \
   switch (NT) {                                \
     case 1: GRM_SR(KDT, KS, 1, XF); break;     \

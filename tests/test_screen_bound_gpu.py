@@ -241,3 +241,47 @@ def test_gqa_stress_banks_route_like_the_law(hip_lib, monkeypatch, kind, mode):
     np.testing.assert_array_equal(res.ids, want)
     filled = want != NO_ID
     np.testing.assert_array_equal(res.scores[filled].view(np.uint32), sc[filled].view(np.uint32))
+
+
+def fp32_query(rng, H, Qt, hd):
+    """Queries in fp32 proper (not bf16-representable): Gaussian, wide,
+    paired and tiny families, so both parts of a split query matter."""
+    fam = np.arange(H) % 4
+    q = np.empty((H, Qt, hd))
+    for h in range(H):
+        f = fam[h]
+        if f == 0:
+            q[h] = rng.standard_normal((Qt, hd))
+        elif f == 1:
+            q[h] = spread(rng, (Qt, hd), -12, 12)
+        elif f == 2:
+            q[h] = paired(rng, (Qt, hd)) * (1.0 + 2.0 ** -9 * rng.standard_normal((Qt, hd)))
+        else:
+            q[h] = spread(rng, (Qt, hd), -40, -20)
+    return q.astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("Qt", [1, 2])
+@pytest.mark.parametrize("split", ["1", "0"])
+def test_gqa_fp32_query_split_routes_like_the_law(hip_lib, monkeypatch, kind, Qt, split):
+    """One fp32 query over at most 8 columns per kv head takes the screen
+    with each column's remainder in an idle column slot (split) or rounded
+    once (GRM_HIP_GQA_SPLIT=0); both must route like the law."""
+    monkeypatch.setenv("GRM_HIP_GQA_SCREEN", "1")
+    monkeypatch.setenv("GRM_HIP_GQA_BOUND", "0")
+    monkeypatch.setenv("GRM_HIP_GQA_SPLIT", split)
+    rng = np.random.default_rng({"bf16": 15, "f16": 16, "f32": 18}[kind] + 3 * Qt)
+    n, kv, hd, H = 360, 2, 128, 8
+    bank, offs = gqa_bank(rng, kind, n, kv, hd)
+    qs = [fp32_query(rng, H, Qt, hd)[None] for _ in range(3)]
+    with open_bank(bank, offs, kv, hd) as b:
+        got = [b.route(q, 8) for q in qs]
+        stats = b.route_stats()
+    assert stats["screen_refine"] >= 3
+    for q, res in zip(qs, got):
+        want, sc, _ = oracle.gqa_route(bank["keys"], bank["code"], offs, kv, hd, q, 8)
+        np.testing.assert_array_equal(res.ids, want)
+        filled = want != NO_ID
+        np.testing.assert_array_equal(res.scores[filled].view(np.uint32),
+                                      sc[filled].view(np.uint32))
