@@ -383,7 +383,10 @@ def bench_mla_batched(steps: int, warmup: int, cpu_queries: int, traffic: dict |
                "parity_with_gpu": match, "host": host_cpu()}
     flops = 2.0 * nq * n * d
     bytes_screen = n * d * 2 + n * 4
-    prof = (traffic or {}).get("mla_batch_screen", {})
+    # the screen kernel bench.py's bank takes: the LDS-ring screen unless
+    # GRM_HIP_BATCH_RING=0 selects the previous one (not profiled)
+    ring = os.environ.get("GRM_HIP_BATCH_RING", "1") != "0"
+    prof = (traffic or {}).get("mla_batch_ring", {}) if ring else {}
     scr = float(np.mean(screens))
     tflops = flops / (scr * 1e-3) / 1e12
     gbs = bytes_screen / (scr * 1e-3) / 1e9
@@ -402,7 +405,7 @@ def bench_mla_batched(steps: int, warmup: int, cpu_queries: int, traffic: dict |
                      "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
                      "traffic": prof.get("fetch_bytes"),
                      "mfma_util_counters": prof.get("mfma_util"),
-                     "kernel": "mla_batch_screen_kernel<18, 8>",
+                     "kernel": "mla_batch_ring_kernel<18>" if ring else "mla_batch_screen_kernel<18, 8>",
                      "flops_per_launch": flops, "kernel_ms_mean": round(scr, 5)},
         "roofline_hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -545,7 +548,7 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
                 sum_l=sum_l, cfg=cfg, kv=kv, H=H, qt64=qt64)
 
 
-def bench_gqa_f32_dropin(steps: int, warmup: int):
+def bench_gqa_f32_dropin(steps: int, warmup: int, traffic: dict | None = None):
     """The reference's own GQA hand-over at the 512-node ragged shape: a
     dense, zero-padded fp32 bank [nodes, kv, 512, hd] through
     grm_gqa_cuda_arena_create and host fp32 queries through
@@ -605,6 +608,7 @@ def bench_gqa_f32_dropin(steps: int, warmup: int):
            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                         "kernel": "gqa_sr_kernel<f16, 4, 1, fp32 rows>",
+                        "traffic": (traffic or {}).get("gqa_sr_f32", {}).get("bytes_per_launch"),
                         "bytes_per_call": bytes_copy}}
     log(f"[gqa f32 drop-in] p50 {out['p50_ms']:.4f} ms  device {mean_dev:.4f} ms  "
         f"{ach:.0f} GB/s on the fp16 copy  parity {parity}  setup {setup_ms:.0f} ms")
@@ -650,7 +654,7 @@ def cpu_baseline_gqa_int8(codes, scales, offs, kv, hd, q_bits, k):
             "host": host_cpu()}
 
 
-def bench_gqa_int8(steps: int, warmup: int, cpu_seconds: float = 0.0):
+def bench_gqa_int8(steps: int, warmup: int, cpu_seconds: float = 0.0, traffic: dict | None = None):
     """100,000 lognormal-length nodes (median 256, sigma 0.5, cap 4096),
     8 kv heads x 128 stored INT8 with one fp16 scale per row, 32 bf16 query
     heads, 16 queries per call, top-5; 1% of the nodes are evicted and as
@@ -744,6 +748,8 @@ def bench_gqa_int8(steps: int, warmup: int, cpu_seconds: float = 0.0):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "bytes_per_call": round(bytes_per_call),
+                     "screen_kernel": "gqa_smax_kernel<i8, 4, 4, fact, f16>",
+                     "screen_traffic": (traffic or {}).get("gqa_int8_smax", {}).get("bytes_per_launch"),
                      "note": "whole route (6 kernels), each call right after a churn step"},
         "steady": {"calls": len(steady_devs), "p50_ms": round(pct(steady_walls, 50), 5),
                    "device_ms_mean": round(steady_dev, 5), "live_tokens": int(steady_tokens),
@@ -1174,10 +1180,10 @@ def main() -> int:
         g = bench_gqa(args.gqa_steps, min(args.warmup, 20), cpu_s)
     f32 = None
     if args.only in ("all", "f32"):
-        f32 = bench_gqa_f32_dropin(args.f32_steps, min(args.warmup, 10))
+        f32 = bench_gqa_f32_dropin(args.f32_steps, min(args.warmup, 10), traffic)
     i8 = None
     if args.only in ("all", "int8"):
-        i8 = bench_gqa_int8(args.int8_steps, 2, cpu_s)
+        i8 = bench_gqa_int8(args.int8_steps, 2, cpu_s, traffic)
     b = None
     if args.only in ("all", "batched"):
         b = bench_mla_batched(args.batched_steps, min(args.warmup, 5),
