@@ -284,8 +284,9 @@ __global__ __launch_bounds__(kBatchWaves * kWave) void mla_batch_screen_kernel(
 //    [64 w, 64 w + 64) and has SIMD w to itself, so its 512 registers hold
 //    the queries, two sets of accumulators and A fragments four K-steps
 //    ahead.  The MFMAs of tile s and the reductions of tile s - 1 form one
-//    straight-line region, interleaved (sched_group_barrier): the matrix
-//    core and the VALU work side by side within the wavefront.
+//    straight-line region, each MFMA followed by its share of the
+//    reductions and a scheduling barrier: the matrix core and the VALU work
+//    side by side within the wavefront.
 //  * Block b is sub-stream b of W = blocks and walks tiles
 //    [b * n_tiles32 / W, (b + 1) * n_tiles32 / W), one per step, so the
 //    merge decodes its slot codes as for the wavefront sub-streams of
