@@ -56,6 +56,26 @@ def pct(xs, p):
     return float(np.percentile(np.asarray(xs, dtype=np.float64), p))
 
 
+class route_events:
+    """Timed routes inside keep HIP events around their kernels on the
+    route's stream (GRM_HIP_ROUTE_TIMING=events, read by the library at
+    each route); by default a timed route that completes through flags
+    takes its device time from the device's constant clock instead.  The
+    kernel times behind every roofline figure are taken in here."""
+
+    def __enter__(self):
+        self._old = os.environ.get("GRM_HIP_ROUTE_TIMING")
+        os.environ["GRM_HIP_ROUTE_TIMING"] = "events"
+        return self
+
+    def __exit__(self, *exc):
+        if self._old is None:
+            os.environ.pop("GRM_HIP_ROUTE_TIMING", None)
+        else:
+            os.environ["GRM_HIP_ROUTE_TIMING"] = self._old
+        return False
+
+
 def host_cpu() -> dict:
     """What the CPU baselines ran on: core counts and the CPU model."""
     model = None
@@ -195,10 +215,15 @@ def bench_mla(steps: int, warmup: int):
         r = bank.route(dq, k, on_device=True, query_count=1, timed=False)
         calls_1000.append(r.wall_ms)
     assert np.array_equal(r.ids[0], ids) and np.array_equal(r.scores[0], scores)
+    with route_events():
+        for _ in range(min(steps, 300)):
+            r = bank.route(dq, k, on_device=True, query_count=1)
+            assert np.array_equal(r.ids[0], ids) and np.array_equal(r.scores[0], scores)
+            devs.append(r.device_ms)
+    # what a caller that asks for device time waits (device clock, flags)
     for _ in range(min(steps, 300)):
         r = bank.route(dq, k, on_device=True, query_count=1)
         assert np.array_equal(r.ids[0], ids) and np.array_equal(r.scores[0], scores)
-        devs.append(r.device_ms)
         timed_walls.append(r.wall_ms)
     dq.close()
     latent = bench_latent_entry(bank, d, k, max(20, steps // 10))
@@ -241,9 +266,10 @@ def bench_mla_small(steps: int, warmup: int, cpu_seconds: float, skip_cpu: bool)
     walls, devs = [], []
     for _ in range(steps):
         walls.append(bank.route(dq, k, on_device=True, query_count=1, timed=False).wall_ms)
-    for _ in range(min(steps, 300)):
-        r = bank.route(dq, k, on_device=True, query_count=1)
-        devs.append(r.device_ms)
+    with route_events():
+        for _ in range(min(steps, 300)):
+            r = bank.route(dq, k, on_device=True, query_count=1)
+            devs.append(r.device_ms)
     host_r = bank.route(q, k, timed=False)
     host_walls = [bank.route(q, k, timed=False).wall_ms for _ in range(min(steps, 300))]
     dq.close()
@@ -462,19 +488,25 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
                    query_shape=shape)
     # latency: routes that ask for no device time, as a caller makes them
     # (completion seen through the finalize blocks' flags); device time:
-    # the same routes with stream events around the kernels
+    # the same routes with stream events around the kernels; and the
+    # latency of routes that ask for device time (device clock, flags)
     walls, devs = [], []
     for _ in range(steps):
         r = bank.route(dq, cfg["topk"], on_device=True, query_dtype="bf16",
                        query_shape=shape, timed=False)
         walls.append(r.wall_ms)
         ids0, sc0 = r.ids, r.scores
+    with route_events():
+        for _ in range(min(steps, 300)):
+            r = bank.route(dq, cfg["topk"], on_device=True, query_dtype="bf16",
+                           query_shape=shape)
+            assert np.array_equal(r.ids, ids0) and np.array_equal(r.scores, sc0)
+            devs.append(r.device_ms)
     timed_walls = []
     for _ in range(min(steps, 300)):
         r = bank.route(dq, cfg["topk"], on_device=True, query_dtype="bf16",
                        query_shape=shape)
         assert np.array_equal(r.ids, ids0) and np.array_equal(r.scores, sc0)
-        devs.append(r.device_ms)
         timed_walls.append(r.wall_ms)
     dq.close()
     # the same query handed over from host memory (one H2D copy per call,
@@ -493,9 +525,10 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
     walls4 = [bank.route(dq4, cfg["topk"], on_device=True, query_dtype="bf16",
                          query_shape=q4.shape, timed=False).wall_ms
               for _ in range(max(1, steps // 2))]
-    devs4 = [bank.route(dq4, cfg["topk"], on_device=True, query_dtype="bf16",
-                        query_shape=q4.shape).device_ms
-             for _ in range(min(steps, 100))]
+    with route_events():
+        devs4 = [bank.route(dq4, cfg["topk"], on_device=True, query_dtype="bf16",
+                            query_shape=q4.shape).device_ms
+                 for _ in range(min(steps, 100))]
     dq4.close()
     # a 64-token query (a prompt-length probe key): 256 query columns per
     # kv head, routed in four passes of 64
@@ -506,9 +539,10 @@ def bench_gqa(steps: int, warmup: int, cpu_seconds: float = 0.0):
     walls64 = [bank.route(dq64, cfg["topk"], on_device=True, query_dtype="bf16",
                           query_shape=q64.shape, timed=False).wall_ms
                for _ in range(max(1, steps // 4))]
-    devs64 = [bank.route(dq64, cfg["topk"], on_device=True, query_dtype="bf16",
-                         query_shape=q64.shape).device_ms
-              for _ in range(min(steps, 50))]
+    with route_events():
+        devs64 = [bank.route(dq64, cfg["topk"], on_device=True, query_dtype="bf16",
+                             query_shape=q64.shape).device_ms
+                  for _ in range(min(steps, 50))]
     dq64.close()
     bank.close()
     sum_l = int(offs[-1])
@@ -578,11 +612,17 @@ def bench_gqa_f32_dropin(steps: int, warmup: int, traffic: dict | None = None):
     bank = sidecar.create_bank(dense)
     for _ in range(warmup):
         bank.route_topk(q, topk=cfg["topk"])
+    # the caller's latency (every call asks for device time: device clock,
+    # flags), then the device time with HIP events around the kernels
     walls, devs = [], []
     for _ in range(steps):
         mapped, rec = bank.route_topk(q, topk=cfg["topk"])
         walls.append(rec.route_wall_ms)
-        devs.append(rec.device_route_ms_total)
+    with route_events():
+        for _ in range(steps):
+            mapped_ev, rec = bank.route_topk(q, topk=cfg["topk"])
+            assert np.array_equal(mapped_ev, mapped)
+            devs.append(rec.device_route_ms_total)
     setup_ms = bank.setup_wall_ms
     bank.close()
     # parity: the oracle's fp64 law on the dense bank (checker only)

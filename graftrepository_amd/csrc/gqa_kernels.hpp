@@ -371,13 +371,14 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
 // Query qb's maxima are hmax[qb*hstride + h*cap + slot].  All waves of the
 // block stage the group's maxima in LDS -- every load of a group is in
 // flight at once, since the atomics that produced them leave them outside
-// the cache -- and re-zero them; wave 0 sums each slot's heads in order,
-// keeps the block's k best and writes them to
-// block_out[(qb*gridDim.x + blockIdx.x)*k ..).  qbad[qb*kv + g] are the
-// query's non-finite flags.  With done (host-mapped memory) the block then
-// stores seq at done[qb*gridDim.x + blockIdx.x] once all of its stores are
-// complete, so a host that sees every flag of a launch holds its lists
-// without waiting for the stream.
+// the cache; wave 0 sums each slot's heads in order, keeps the block's k
+// best and writes them to block_out[(qb*gridDim.x + blockIdx.x)*k ..).
+// qbad[qb*kv + g] are the query's non-finite flags.  With done
+// (host-mapped memory) wave 0 then stores seq at done[qb*gridDim.x +
+// blockIdx.x] once its list is complete (after its end tick at the same
+// index of stamps, when given), so a host that sees every flag of a launch
+// holds its lists without waiting for the stream; the maxima are re-zeroed
+// last.
 constexpr int kFinSlots = 64;    // slots per finalize group (one per lane)
 constexpr int kFinHeads = 128;   // heads staged per pass
 
@@ -387,7 +388,7 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
     const uint64_t* __restrict__ ids, const unsigned* __restrict__ qbad, int kv,
     int k, Cand* __restrict__ block_out, const uint32_t* __restrict__ slot_list,
     const uint32_t* __restrict__ list_count, size_t list_stride, unsigned* __restrict__ done,
-    unsigned seq) {
+    unsigned seq, unsigned long long* __restrict__ stamps) {
   __shared__ double s_h[kFinHeads][kFinSlots];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -432,15 +433,6 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
         const int h = wave + kFinWaves * i;
         if (h < nh) s_h[h][lane] = v[i];
       }
-      // The re-zeroing stores go after every LDS write: a store in between
-      // would make each later write wait for it (stores and loads share
-      // one counter).
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const int h = wave + kFinWaves * i;
-        if (h < nh && in) hmax[(h0 + h) * cap + slot] = 0ull;
-      }
       __syncthreads();
       if (wave == 0) {
         // h ascending; LDS reads go out 16 at a time ahead of the adds
@@ -476,12 +468,22 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
   if (wave == 0 && lane < k) {
     block_out[(static_cast<size_t>(qb) * gridDim.x + blockIdx.x) * k + lane] = wl_entry(L);
   }
-  if (done) {
-    // every wave's stores (the list, the re-zeroed maxima) are complete
-    // before the flag
+  if (done && wave == 0) {
+    // wave 0's list stores are complete before the end tick and the flag
+    const size_t fi = static_cast<size_t>(qb) * gridDim.x + blockIdx.x;
+    if (stamps && lane == 0) stamps[fi] = wall_clock64();
     __threadfence_system();
-    __syncthreads();
-    if (threadIdx.x == 0) done[static_cast<size_t>(qb) * gridDim.x + blockIdx.x] = seq;
+    if (lane == 0) done[fi] = seq;
+  }
+  // The maxima go back to zero for the next route after the flag, so the
+  // host does not wait for these stores; the next route's kernels follow
+  // this one on the stream.
+  for (uint32_t base = blockIdx.x * kFinSlots; base < n_slots; base += gridDim.x * kFinSlots) {
+    const bool in = base + lane < n_slots;
+    const uint32_t slot = slot_list ? (in ? slot_list[base + lane] : 0u) : base + lane;
+    if (in) {
+      for (int h = wave; h < H; h += kFinWaves) hmax[h * cap + slot] = 0ull;
+    }
   }
 }
 
@@ -890,7 +892,9 @@ __global__ __launch_bounds__(kUnitWaves * kWave, (sr_waves_per_simd<KDT, KS, NT,
     const void* __restrict__ query, int q_dtype, size_t q_elems, int Qb, int emax,
     double gamma, double delta, double sigma_q, double sigma_k, double sigma_p,
     double eps_rel, double eps_abs, unsigned* __restrict__ qflags, int flags_or, const float* __restrict__ kmax, double denom,
-    unsigned long long* __restrict__ hmax, size_t hstride, size_t cap, int g_fast, int split) {
+    unsigned long long* __restrict__ hmax, size_t hstride, size_t cap, int g_fast, int split,
+    RouteStamps stamps, unsigned seq) {
+  route_start_stamp(stamps, seq);
   using KT = KeyTraits<KDT>;
   constexpr int MT = ScreenTraits<KDT>::kMfma;
   constexpr int HD = 32 * KS;

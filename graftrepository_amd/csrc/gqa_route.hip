@@ -118,6 +118,10 @@ struct GqaDeviceArena {
   // number the last route stored there
   grm::MappedBuf done_flags;
   unsigned route_seq = 0;
+  // device-clock stamps of timed routes on the flag path (host mapped),
+  // and the clock's ticks per ms (0: timed routes use stream events)
+  grm::MappedBuf stamps;
+  double ticks_per_ms = 0.0;
   unsigned* d_qbad = nullptr;   // per (query, kv head): non-finite query value
   size_t d_qbad_count = 0;
   // exact path
@@ -252,6 +256,7 @@ void destroy_arena(GqaDeviceArena* a) {
   }
   grm::release_mapped(&a->blocks_out);
   grm::release_mapped_bytes(&a->done_flags);
+  grm::release_mapped_bytes(&a->stamps);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
   grm::release_mapped_bytes(&a->q_map);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
@@ -483,6 +488,7 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
   if (const char* env = getenv("GRM_HIP_QUERY_COPY")) a->query_dma = strcmp(env, "dma") == 0;
   if (const char* env = getenv("GRM_HIP_GQA_SPLIT")) a->query_split = env[0] != '0';
+  a->ticks_per_ms = grm::wall_ticks_per_ms(a->device);
   if (const char* env = getenv("GRM_HIP_GQA_SR_ORDER")) {
     a->sr_order = strcmp(env, "slot") == 0 ? 0 : (strcmp(env, "size") == 0 ? 1 : -1);
   }
@@ -672,14 +678,14 @@ int ensure_hmax(GqaDeviceArena* a, int H, int qb) {
 // the listed candidate slots of each query.
 int launch_finalize(GqaDeviceArena* a, int H, int qb, int topk, uint32_t fin_blocks, Cand* bout,
                     const uint32_t* slot_list = nullptr, const uint32_t* list_count = nullptr,
-                    unsigned* done = nullptr) {
+                    unsigned* done = nullptr, unsigned long long* end_stamps = nullptr) {
   const uint32_t per_block = grm::gqa::kFinWaves * grm::kWave;
   grm::gqa::gqa_finalize_kernel<<<dim3(fin_blocks, qb), per_block, 0, a->stream>>>(
       a->d_hmax, a->cap_nodes * static_cast<size_t>(H), a->cap_nodes, H,
       static_cast<uint32_t>(a->high_water), a->d_len,
       a->route_flags ? a->route_flags : a->d_flags, a->d_ids, a->d_qbad,
       static_cast<int>(a->kv), topk, bout, slot_list, list_count, a->cap_nodes, done,
-      a->route_seq);
+      a->route_seq, end_stamps);
   GRM_HIP_CHECK(hipGetLastError());
   return 0;
 }
@@ -866,7 +872,8 @@ ScreenBound screen_bound(const GqaDeviceArena* a, const SrPlan& p, int q_dtype) 
 // (the queries' start) against every (item, kv head), folding into the
 // maxima; the first pass writes the query flags, later ones raise them.
 int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
-                   const unsigned char* qptr, int q_dtype, int qb, size_t pi) {
+                   const unsigned char* qptr, int q_dtype, int qb, size_t pi,
+                   const grm::RouteStamps& st) {
   const int kv = static_cast<int>(a->kv);
   const QPass& ps = p.passes[pi];
   if (a->n_items == 0) {
@@ -927,7 +934,7 @@ int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
       static_cast<uint32_t>(a->n_items), kv, p.R, p.Qt, ps.rc, ps.qc, qpass, q_dtype, q_elems,  \
       qb, sb.emax, sb.gamma, sb.delta, sb.sigma_q, sb.sigma_k, sb.sigma_p, sb.eps_rel,          \
       sb.eps_abs, a->d_qbad, pi > 0 ? 1 : 0, reinterpret_cast<const float*>(a->d_kmax), denom,   \
-      hpass, hstride, a->cap_nodes, g_fast, split)
+      hpass, hstride, a->cap_nodes, g_fast, split, st, a->route_seq)
 #define GRM_SR_NT(KDT, KS, XF)                 \
   switch (NT) {                                \
     case 1: GRM_SR(KDT, KS, 1, XF); break;     \
@@ -960,14 +967,18 @@ int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
 // `qstride` bytes apart): its query passes one after another, all folding
 // into the same maxima, then the finalize.  Their per-block top-k lands at
 // bout, and with `done` the finalize blocks' completion flags at
-// done[0, qb*fin_blocks).  Launches only (prepare_sr allocates).
+// done[0, qb*fin_blocks).  With st.start the first pass stores the route's
+// start tick, with st.end the finalize blocks their end ticks
+// (RouteStamps).  Launches only (prepare_sr allocates).
 int enqueue_sr(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, int q_dtype, int qb,
-               int topk, uint32_t fin_blocks, Cand* bout, unsigned* done) {
+               int topk, uint32_t fin_blocks, Cand* bout, unsigned* done,
+               const grm::RouteStamps& st) {
   const ScreenBound eb = screen_bound(a, p, q_dtype);
   for (size_t pi = 0; pi < p.passes.size(); ++pi) {
-    GRM_CHECK_RC(launch_sr_pass(a, p, eb, qptr, q_dtype, qb, pi));
+    const grm::RouteStamps sp{pi == 0 ? st.start : nullptr, nullptr};
+    GRM_CHECK_RC(launch_sr_pass(a, p, eb, qptr, q_dtype, qb, pi, sp));
   }
-  return launch_finalize(a, p.H, qb, topk, fin_blocks, bout, nullptr, nullptr, done);
+  return launch_finalize(a, p.H, qb, topk, fin_blocks, bout, nullptr, nullptr, done, st.end);
 }
 
 // ------------------------------------------------------ bound-and-verify path
@@ -1314,16 +1325,25 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   SrPlan plan;
   const bool use_sr = sr_plan(a, H, Qt, &plan);
   if (use_sr) GRM_CHECK_RC(prepare_sr(a, plan));
-  // Without a timing request, screen-and-refine routes report completion
-  // through per-block flags in host memory, which the host sees as soon as
-  // the last finalize block stores its flag (no stream event on the path).
+  // Screen-and-refine routes report completion through per-block flags in
+  // host memory, which the host sees as soon as the last finalize block
+  // stores its flag (no stream event on the path).  A timed route does too
+  // when every pass is screen and refine and the device reports its
+  // constant clock: its device time is then the clock's ticks from the
+  // first timed kernel's start to the last flag (RouteStamps) instead of
+  // stream events around the kernels (GRM_HIP_ROUTE_TIMING=events keeps
+  // the events).
   const size_t n_flags = static_cast<size_t>(q_count) * fin_blocks;
-  bool flags = !elapsed_ms && use_sr && n_flags <= kMaxDoneFlags && !grm::blocking_sync();
+  const bool flaggable = use_sr && n_flags <= kMaxDoneFlags && !grm::blocking_sync();
+  const bool clocked = elapsed_ms && flaggable && a->ticks_per_ms > 0.0 && !grm::event_timing() &&
+                       a->n_items > 0 && !use_bound(a, plan, std::min(plan.qb_max, q_count));
+  bool flags = flaggable && (!elapsed_ms || clocked);
   unsigned* d_done = nullptr;
   if (flags) {
     GRM_CHECK_RC(grm::begin_flags(&a->done_flags, kMaxDoneFlags, &a->route_seq));
     d_done = static_cast<unsigned*>(a->done_flags.dev);
   }
+  if (clocked) GRM_CHECK_RC(grm::reserve_stamps(&a->stamps, kMaxDoneFlags));
   // where each query's per-block lists are, and how many entries they hold
   std::vector<uint32_t> q_entries(q_count, static_cast<uint32_t>(per_q));
   std::vector<size_t> q_off(q_count);
@@ -1333,7 +1353,7 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   const int segments[2][2] = {{0, warmup}, {warmup, q_count}};
   for (int si = 0; si < 2; ++si) {
     const auto& seg = segments[si];
-    if (si == 1 && elapsed_ms) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+    if (si == 1 && elapsed_ms && !clocked) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
     if (use_sr) {
       for (int q0 = seg[0]; q0 < seg[1]; q0 += plan.qb_max) {
         const int qb = std::min(plan.qb_max, seg[1] - q0);
@@ -1354,9 +1374,15 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
           }
           a->bv_routes += 1;
         } else {
+          // the timed segment's first launch stores the start tick
+          grm::RouteStamps st{nullptr, nullptr};
+          if (clocked) {
+            st = grm::route_stamps(a->stamps, static_cast<size_t>(q0) * fin_blocks);
+            if (si == 0 || q0 != seg[0]) st.start = nullptr;
+          }
           GRM_CHECK_RC(enqueue_sr(a, plan, qbase + static_cast<size_t>(q0) * qstride, q_dtype, qb, topk,
                                   fin_blocks, a->blocks_out.dev + static_cast<size_t>(q0) * per_q,
-                                  d_done ? d_done + static_cast<size_t>(q0) * fin_blocks : nullptr));
+                                  d_done ? d_done + static_cast<size_t>(q0) * fin_blocks : nullptr, st));
           a->sr_routes += 1;
         }
       }
@@ -1379,7 +1405,12 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
     write_result(a->merged.data(), topk, out_ids + static_cast<size_t>(qi) * topk,
                  out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
   }
-  if (elapsed_ms) GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
+  if (clocked) {
+    GRM_CHECK_RC(grm::stamps_elapsed(a->stamps, a->route_seq, n_flags, a->ev_stop, a->ticks_per_ms,
+                                     elapsed_ms));
+  } else if (elapsed_ms) {
+    GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
+  }
   grm::clear_error();
   return 0;
 }

@@ -118,6 +118,54 @@ int wait_flags(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev) {
   return 0;
 }
 
+constexpr size_t kStampHead = 2;  // start tick, route number
+
+int reserve_stamps(MappedBuf* buf, size_t max) {
+  const size_t bytes = (kStampHead + max) * sizeof(unsigned long long);
+  if (buf->bytes < bytes) {
+    GRM_CHECK_RC(reserve_mapped_bytes(buf, bytes));
+    memset(buf->host, 0, bytes);
+  }
+  return 0;
+}
+
+RouteStamps route_stamps(const MappedBuf& buf, size_t first) {
+  unsigned long long* d = static_cast<unsigned long long*>(buf.dev);
+  return RouteStamps{d, d + kStampHead + first};
+}
+
+int stamps_elapsed(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev,
+                   double ticks_per_ms, float* ms) {
+  const volatile unsigned long long* st = static_cast<const volatile unsigned long long*>(buf.host);
+  if (st[1] != seq) {
+    GRM_CHECK_RC(wait_event(ev));
+    if (st[1] != seq) return fail(-1, "route finished without its start stamp");
+  }
+  std::atomic_thread_fence(std::memory_order_acquire);
+  const unsigned long long t0 = st[0];
+  unsigned long long t1 = t0;
+  for (size_t i = 0; i < n; ++i) {
+    const unsigned long long e = st[kStampHead + i];
+    if (e > t1) t1 = e;
+  }
+  *ms = static_cast<float>(static_cast<double>(t1 - t0) / ticks_per_ms);
+  return 0;
+}
+
+bool event_timing() {
+  const char* env = getenv("GRM_HIP_ROUTE_TIMING");
+  return env && strcmp(env, "events") == 0;
+}
+
+double wall_ticks_per_ms(int device) {
+  int khz = 0;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0.0;
+  }
+  return khz > 0 ? static_cast<double>(khz) : 0.0;
+}
+
 int reserve_mapped_bytes(MappedBuf* m, size_t bytes) {
   if (bytes <= m->bytes && m->host) return 0;
   release_mapped_bytes(m);

@@ -105,6 +105,36 @@ __device__ inline void wl_refresh(WaveList& L, int k) {
   L.th_id = lane_u64(L.id, k - 1);
 }
 
+// Cross-lane moves through the VALU's data-parallel primitives (gfx9 DPP
+// encodings) instead of LDS permutes: a lane whose source row is masked
+// off keeps its own value.  Every lane of the wavefront must be active.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), kCtrl, kRowMask, 0xf, false));
+}
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<kCtrl, kRowMask>(__float_as_uint(v)));
+}
+
+// Largest v over the wavefront (wave-uniform): quad swaps (lanes ^1, ^2),
+// rotations by 4 and 8 within each row of 16, then rows 0 -> 1 and 2 -> 3
+// (row broadcast of lane 15) and rows 0-1 -> 2-3 (of lane 31), so lane
+// 63 ends with the maximum.
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, dpp_f32<0xb1>(v));        // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4e>(v));        // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x124>(v));       // row_ror:4
+  v = fmaxf(v, dpp_f32<0x128>(v));       // row_ror:8
+  v = fmaxf(v, dpp_f32<0x142, 0xa>(v));  // row_bcast:15 into rows 1, 3
+  v = fmaxf(v, dpp_f32<0x143, 0xc>(v));  // row_bcast:31 into rows 2, 3
+  return lane_f32(v, kWave - 1);
+}
+
+// Lane l gets v of lane l - 1 (wave_shr:1; lane 0 keeps its own).
+__device__ __forceinline__ uint32_t wave_shr1_u32(uint32_t v) { return dpp_u32<0x138>(v); }
+
 // Offer one candidate per lane (`valid` lanes only) and keep the best k of
 // list + candidates.  Each iteration extracts the best remaining candidate
 // (a max-reduction of the scores, then the lowest id among lanes holding
@@ -120,9 +150,7 @@ __device__ inline void wl_consume(WaveList& L, int k, float s, uint64_t id,
     if (__popcll(mask) == 1) {
       bl = __ffsll(static_cast<long long>(mask)) - 1;
     } else {
-      float bs = cand ? s : -INFINITY;
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) bs = fmaxf(bs, __shfl_xor(bs, off));
+      const float bs = wave_max_f32(cand ? s : -INFINITY);
       const uint64_t tie = __ballot(cand && s == bs);
       if (__popcll(tie) == 1) {
         bl = __ffsll(static_cast<long long>(tie)) - 1;
@@ -142,9 +170,10 @@ __device__ inline void wl_consume(WaveList& L, int k, float s, uint64_t id,
     // Entries ahead of the winner form a prefix of the sorted list.
     const bool ahead = lane < k && better(L.s, L.id, ws, wid);
     const int pos = __popcll(__ballot(ahead));
-    const float ps = __shfl_up(L.s, 1);
-    const uint64_t pid = __shfl_up(L.id, 1);
-    const uint32_t pslot = __shfl_up(L.slot, 1);
+    const float ps = __uint_as_float(wave_shr1_u32(__float_as_uint(L.s)));
+    const uint64_t pid = (static_cast<uint64_t>(wave_shr1_u32(static_cast<uint32_t>(L.id >> 32))) << 32) |
+                         wave_shr1_u32(static_cast<uint32_t>(L.id));
+    const uint32_t pslot = wave_shr1_u32(L.slot);
     if (lane == pos) {
       L.s = ws;
       L.id = wid;
@@ -240,11 +269,36 @@ __device__ inline void block_topk_write(WaveList& L, int k,
   }
 }
 
+// Device-clock stamps of a timed route that reports completion through
+// flags, in host-mapped memory (null pointers when the route is untimed
+// or timed by stream events): the route's first timed kernel stores its
+// start tick and the route's number at start[0], start[1]
+// (route_start_stamp); each block that stores a completion flag first
+// stores its end tick at end[flag index].  The clock is the device's
+// constant-rate one (wall_clock64), so the difference is device time
+// whatever the shader clock does.
+struct RouteStamps {
+  unsigned long long* start;
+  unsigned long long* end;
+};
+
+// Start tick of a route: the grid's first block (blocks start in index
+// order) stores it as the kernel begins.
+__device__ inline void route_start_stamp(const RouteStamps& st, unsigned seq) {
+  if (st.start && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+    st.start[0] = wall_clock64();
+    st.start[1] = seq;
+  }
+}
+
 // Completion flag of a block whose list went to host-mapped memory (after
 // block_topk_write, where wave 0 wrote the list): once wave 0's stores are
-// complete it stores seq at done[blockIdx.x].  No-op when done is null.
-__device__ inline void block_done_flag(unsigned* __restrict__ done, unsigned seq) {
+// complete it stores seq at done[blockIdx.x], after its end tick at
+// end[blockIdx.x] when `end` is given.  No-op when done is null.
+__device__ inline void block_done_flag(unsigned* __restrict__ done, unsigned seq,
+                                       unsigned long long* __restrict__ end = nullptr) {
   if (done && threadIdx.x < kWave) {
+    if (end && threadIdx.x == 0) end[blockIdx.x] = wall_clock64();
     __threadfence_system();
     if (threadIdx.x == 0) done[blockIdx.x] = seq;
   }
@@ -284,6 +338,26 @@ void release_mapped_bytes(MappedBuf* m);
 // flags returns an error instead of spinning.
 int begin_flags(MappedBuf* buf, size_t max, unsigned* seq);
 int wait_flags(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev);
+
+// Device-clock timing of a flagged route (RouteStamps).  reserve_stamps
+// puts a buffer in place for `max` flags: two start words, then one end
+// tick per flag; route_stamps gives the device pointers, with the end
+// ticks from flag `first` on.  stamps_elapsed, once wait_flags has seen
+// flags [0, n) hold seq, gives the route's device time in ms: the latest
+// end tick less the start tick, at `ticks_per_ms`.  A start stamp of
+// another route (never expected: it is stored before any flag) is waited
+// for through `ev` and is an error if the kernels end without it.
+// wall_ticks_per_ms: the constant clock's rate on `device` (0 when the
+// device does not report it; such routes keep stream events).
+int reserve_stamps(MappedBuf* buf, size_t max);
+RouteStamps route_stamps(const MappedBuf& buf, size_t first);
+int stamps_elapsed(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev,
+                   double ticks_per_ms, float* ms);
+double wall_ticks_per_ms(int device);
+// True when GRM_HIP_ROUTE_TIMING=events asks timed routes to keep stream
+// events (and their wait) instead of flags and the device clock; read at
+// each route.
+bool event_timing();
 
 // Pinned host buffer the device writes directly (mapped, coherent): the
 // route kernels leave their per-block results there so the final merge

@@ -102,14 +102,16 @@ __device__ inline double tile_dot(const u32x4* __restrict__ p, uint32_t chunks,
 }
 
 // One query against every slot; each block writes its k best entries to
-// block_out[blockIdx.x*k ..), then (with done) seq to done[blockIdx.x].
+// block_out[blockIdx.x*k ..), then (with done) seq to done[blockIdx.x];
+// with stamps a timed route's start and end ticks (RouteStamps).
 template <int DT, int NW>
 __global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
     const u32x4* __restrict__ tiles, const float* __restrict__ norms,
     const uint64_t* __restrict__ ids, uint32_t num_tiles, uint32_t chunks,
     size_t plane, uint32_t dim, uint32_t dim_pad,
     const void* __restrict__ query, int query_dtype, int k,
-    Cand* __restrict__ block_out, unsigned* __restrict__ done, unsigned seq) {
+    Cand* __restrict__ block_out, unsigned* __restrict__ done, unsigned seq, RouteStamps stamps) {
+  route_start_stamp(stamps, seq);
   extern __shared__ double qd[];
   __shared__ double s_qnorm;
   __shared__ Cand s_lists[NW][kMaxTopK];
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
   }
 
   block_topk_write<NW>(L, k, s_lists, block_out);
-  block_done_flag(done, seq);
+  block_done_flag(done, seq, stamps.end);
 }
 
 // Stage the query as doubles in LDS (zero beyond dim).
@@ -189,7 +191,8 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_pipe_kernel(
     const uint64_t* __restrict__ ids, uint32_t num_tiles, uint32_t chunks,
     size_t plane, uint32_t dim, uint32_t dim_pad,
     const void* __restrict__ query, int query_dtype, int k,
-    Cand* __restrict__ block_out, unsigned* __restrict__ done, unsigned seq) {
+    Cand* __restrict__ block_out, unsigned* __restrict__ done, unsigned seq, RouteStamps stamps) {
+  route_start_stamp(stamps, seq);
   constexpr int EPC = DT == kF32 ? 4 : 8;
   extern __shared__ double qd[];
   __shared__ double s_qnorm;
@@ -275,7 +278,7 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_pipe_kernel(
     b = bn;
   }
   block_topk_write<NW>(L, k, s_lists, block_out);
-  block_done_flag(done, seq);
+  block_done_flag(done, seq, stamps.end);
 }
 
 // Place staged row-major rows into their tile slots and compute row norms
@@ -406,6 +409,10 @@ struct MlaDeviceArena {
   // last flag-waiting route stored there
   grm::MappedBuf done_flags;
   unsigned route_seq = 0;
+  // device-clock stamps of timed single-query routes on the flag path
+  // (host mapped), and the clock's ticks per ms (0: stream events)
+  grm::MappedBuf stamps;
+  double ticks_per_ms = 0.0;
   std::vector<Cand> merged;
   void* h_stage = nullptr;
   size_t h_stage_bytes = 0;
@@ -479,6 +486,7 @@ void destroy_arena(MlaDeviceArena* a) {
   grm::release_mapped_bytes(&a->q_map);
   grm::release_mapped(&a->blocks_out);
   grm::release_mapped_bytes(&a->done_flags);
+  grm::release_mapped_bytes(&a->stamps);
   if (a->h_stage) (void)hipHostFree(a->h_stage);
   if (a->ev_start) (void)hipEventDestroy(a->ev_start);
   if (a->ev_stop) (void)hipEventDestroy(a->ev_stop);
@@ -600,6 +608,7 @@ int create_arena(const void* rows, int dtype, uint64_t nodes, int dim,
   if (const char* env = getenv("GRM_HIP_MLA_PIPELINE")) a->pipeline = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_BATCH_RING")) a->ring = env[0] != '0';
   if (const char* env = getenv("GRM_HIP_QUERY_COPY")) a->query_dma = strcmp(env, "dma") == 0;
+  a->ticks_per_ms = grm::wall_ticks_per_ms(a->device);
   if (const char* env = getenv("GRM_HIP_MLA_BATCH_MIN")) {
     const long v = strtol(env, nullptr, 10);
     if (v >= 1) a->batch_min = static_cast<int>(std::min<long>(v, 1l << 30));
@@ -720,13 +729,14 @@ SingleGeom single_geom(const MlaDeviceArena* a) {
 // per-block top-k lands at bout (g.blocks * topk entries), and with done
 // its blocks' completion flags at done[0, g.blocks).
 int launch_single(MlaDeviceArena* a, const SingleGeom& g, const void* q, int q_dtype, int topk,
-                  Cand* bout, unsigned* done = nullptr) {
+                  Cand* bout, unsigned* done = nullptr,
+                  const grm::RouteStamps& st = grm::RouteStamps{nullptr, nullptr}) {
   const size_t lds = static_cast<size_t>(a->dim_pad) * sizeof(double);
   const dim3 grid(g.blocks), block(g.nw * grm::kWave);
   const float* nrm = a->route_norms ? a->route_norms : a->d_norms;
 #define GRM_MLA_ARGS                                                                  \
   a->d_tiles, nrm, a->d_ids, g.num_tiles, a->chunks, a->capacity, a->dim, a->dim_pad, q, \
-      q_dtype, topk, bout, done, a->route_seq
+      q_dtype, topk, bout, done, a->route_seq, st
   constexpr int PW = grm::mla::kPipeWaves;
   constexpr int RW = grm::mla::kRouteWaves;
   if (a->dtype == kF32) {
@@ -1021,27 +1031,38 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
   if (!redo.empty()) {
     a->single_queries += redo.size();
     GRM_CHECK_RC(grm::reserve_mapped(&a->blocks_out, per_q * redo.size()));
-    // Without a timing request the host sees completion through per-block
-    // flags in host memory, as soon as the last block stores its flag (no
-    // stream event on the path).
+    // The host sees completion through per-block flags in host memory, as
+    // soon as the last block stores its flag (no stream event on the
+    // path).  A timed route without a batched pass does too when the
+    // device reports its constant clock: its device time is then the
+    // clock's ticks from the first timed launch's start to the last flag
+    // (RouteStamps; GRM_HIP_ROUTE_TIMING=events keeps stream events).
     const size_t n_flags = static_cast<size_t>(g.blocks) * redo.size();
-    const bool flags = !elapsed_ms && n_flags <= kMaxDoneFlags && !grm::blocking_sync();
+    const bool flaggable = n_flags <= kMaxDoneFlags && !grm::blocking_sync();
+    const bool clocked =
+        elapsed_ms && !batched && flaggable && a->ticks_per_ms > 0.0 && !grm::event_timing();
+    const bool flags = flaggable && (!elapsed_ms || clocked);
     unsigned* d_done = nullptr;
     if (flags) {
       GRM_CHECK_RC(grm::begin_flags(&a->done_flags, kMaxDoneFlags, &a->route_seq));
       d_done = static_cast<unsigned*>(a->done_flags.dev);
     }
+    if (clocked) GRM_CHECK_RC(grm::reserve_stamps(&a->stamps, kMaxDoneFlags));
     // Uncertified batched queries add their time to the timed segment.
     bool started = false;
     for (size_t j = 0; j < redo.size(); ++j) {
       const int qi = redo[j];
+      grm::RouteStamps st{nullptr, nullptr};
+      if (clocked) st = grm::route_stamps(a->stamps, j * g.blocks);
       if (!started && elapsed_ms && (batched || qi == warmup)) {
-        GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
+        if (!clocked) GRM_HIP_CHECK(hipEventRecord(a->ev_start, a->stream));
         started = true;
+      } else {
+        st.start = nullptr;
       }
       GRM_CHECK_RC(launch_single(a, g, qbase + qi * qstride, q_dtype, topk,
                                  a->blocks_out.dev + j * per_q,
-                                 d_done ? d_done + j * g.blocks : nullptr));
+                                 d_done ? d_done + j * g.blocks : nullptr, st));
     }
     GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
     if (flags) {
@@ -1049,7 +1070,10 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
     } else {
       GRM_CHECK_RC(grm::wait_event(a->ev_stop));
     }
-    if (elapsed_ms) {
+    if (clocked) {
+      GRM_CHECK_RC(grm::stamps_elapsed(a->stamps, a->route_seq, n_flags, a->ev_stop, a->ticks_per_ms,
+                                       elapsed_ms));
+    } else if (elapsed_ms) {
       float ms = 0.0f;
       GRM_HIP_CHECK(hipEventElapsedTime(&ms, a->ev_start, a->ev_stop));
       *elapsed_ms = batched ? *elapsed_ms + ms : ms;
