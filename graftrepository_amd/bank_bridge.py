@@ -47,10 +47,20 @@ both on the device:
   length (:813-837).  The reference leaves its native and CUDA routes for
   its Python path when it is on (:686-687).  Here every eligible node is
   scored exactly on the device and the ranking applies the factor.
+
+Route receipts follow the reference's route profile (core/graft_arena.py:
+161-256): with ``route_profile=True`` or ``GRM_ROUTE_SEAMS_PROFILE`` set to
+1 / true / yes / on, every ``route_order`` leaves a JSON-ready dict in
+``last_route_receipt`` (and appends it to ``route_receipt_history``): the
+time of each phase in ``terms_ms``, the bank's refresh event under
+``rebuilds``, the reasons a route fell back to the caller's CPU path under
+``fallbacks``, and the ranking's length and first 16 graft indices.  An
+unprofiled route leaves ``last_route_receipt`` None.
 """
 
 from __future__ import annotations
 
+import os
 import time
 from typing import NamedTuple
 
@@ -59,6 +69,14 @@ import numpy as np
 from .node_bank import GqaNodeBank, MlaNodeBank
 
 MAX_TOPK = 16  # reference ABI cap (scripts/grm_mla_cuda_probe.py:355-358)
+ROUTE_RECEIPT_SCHEMA = "grm_route_seams_route_v1"
+
+
+def route_profile_env() -> bool:
+    """GRM_ROUTE_SEAMS_PROFILE asks for route receipts
+    (core/graft_arena.py:161-165)."""
+    return os.environ.get("GRM_ROUTE_SEAMS_PROFILE", "").strip().lower() in (
+        "1", "true", "yes", "on")
 
 
 class RowSet(NamedTuple):
@@ -320,12 +338,17 @@ class _Bridge:
     _full_walk = None
 
     def __init__(self, *, dtype: str = "f32", headroom: float = 1.25,
-                 length_debias: bool = False):
+                 length_debias: bool = False, route_profile: bool = False):
         if headroom < 1.0:
             raise ValueError("headroom must be >= 1")
         self.dtype = dtype
         self.headroom = float(headroom)
         self.length_debias = bool(length_debias)
+        self.route_profile = bool(route_profile)
+        self.last_route_receipt = None
+        self.route_receipt_history: list = []
+        self._receipt = None           # the route being profiled
+        self._refresh_ms = 0.0         # refresh time since the last route
         self.bank = None               # single-key nodes
         self.side = None               # digest nodes' keys, ids 0..keys-1
         self._epoch = None
@@ -388,6 +411,12 @@ class _Bridge:
         Returns the event (also ``last_event``).
         """
         t0 = time.perf_counter()
+        try:
+            return self._refresh(grafts, epoch, t0)
+        finally:
+            self._refresh_ms += (time.perf_counter() - t0) * 1.0e3
+
+    def _refresh(self, grafts, epoch: int, t0: float) -> dict:
         if self._epoch is not None and epoch == self._epoch:
             self.last_event = {
                 "status": "reused" if self._eligible_bank else "ineligible_reused",
@@ -525,15 +554,18 @@ class _Bridge:
         if not self._eligible_bank or topk <= 0:
             return ids_out, sc_out
         main_n = int(self._resident.node_ids.size)
+        t = self._clock()
         if self.length_debias:
             ids = self._resident.node_ids
             sc = (self._score_main(query, ids) if main_n
                   else np.empty(0, dtype=np.float32))
             kl = self._klen_main
+            t = self._term("device_score_all_ms", t)
             if self._digest is not None:
                 ids = np.concatenate([ids, self._digest.node_ids])
                 sc = np.concatenate([sc, self._digest_scores(query)])
                 kl = np.concatenate([kl, self._klen_digest])
+                t = self._term("device_digest_score_ms", t)
             score = apply_length_debias(sc, kl)
         else:
             ids = np.empty(0, dtype=np.uint64)
@@ -542,15 +574,18 @@ class _Bridge:
                 ids, sc = self._route_main(query, min(topk, main_n, MAX_TOPK))
                 keep = ids != np.iinfo(np.uint64).max
                 ids, sc = ids[keep], sc[keep]
+                t = self._term("device_route_call_ms", t)
             if self._digest is not None:
                 ids = np.concatenate([ids, self._digest.node_ids])
                 sc = np.concatenate([sc, self._digest_scores(query)])
+                t = self._term("device_digest_score_ms", t)
             score = sc.astype(np.float64)
         fin = np.isfinite(score)
         ids, score = ids[fin], score[fin]
         order = np.lexsort((ids, -score))[:topk]
         ids_out[:order.size] = ids[order]
         sc_out[:order.size] = score[order]
+        self._term("ranking_ms", t)
         return ids_out, sc_out
 
     def _graft_index(self, nid) -> int | None:
@@ -559,7 +594,60 @@ class _Bridge:
             return int(self._sorted_gidx[i])
         return None
 
+    # ----------------------------------------------------------- receipts
+    def _profiling(self) -> bool:
+        return self.route_profile or route_profile_env()
+
+    def _clock(self):
+        return time.perf_counter_ns() if self._receipt is not None else None
+
+    def _term(self, name: str, started):
+        """Add the time since ``started`` to term ``name`` of the receipt
+        being built; returns a new start (None when not profiling)."""
+        if started is None or self._receipt is None:
+            return None
+        now = time.perf_counter_ns()
+        terms = self._receipt["terms_ms"]
+        terms[name] = terms.get(name, 0.0) + (now - started) / 1.0e6
+        return now
+
+    def _fallback(self, reason: str) -> None:
+        if self._receipt is not None and reason not in self._receipt["fallbacks"]:
+            self._receipt["fallbacks"].append(reason)
+
     def route_order(self, query, limit: int, exclude=(), cand_count=None):
+        """Graft indices of the best ``limit`` nodes, or None (the caller's
+        CPU path); with route profiling on, the route's receipt goes to
+        ``last_route_receipt`` (module docstring)."""
+        refresh_ms, self._refresh_ms = self._refresh_ms, 0.0
+        if not self._profiling():
+            self.last_route_receipt = None
+            return self._route_order(query, limit, exclude, cand_count)
+        receipt = {
+            "schema": ROUTE_RECEIPT_SCHEMA,
+            "epoch": None if self._epoch is None else int(self._epoch),
+            "terms_ms": {"bank_refresh_ms": refresh_ms},
+            "rebuilds": {"device_bank": dict(self.last_event)},
+            "parity": {"checked": False, "ok": None},
+            "fallbacks": [],
+        }
+        self._receipt = receipt
+        t0 = time.perf_counter_ns()
+        try:
+            out = self._route_order(query, limit, exclude, cand_count)
+        finally:
+            self._receipt = None
+        receipt["route_backend"] = "hip" if out is not None else None
+        receipt["candidate_count"] = self.bank_size
+        if out is not None:
+            receipt["ranking_count"] = len(out)
+            receipt["ranking_prefix"] = [int(i) for i in out[:16]]
+        receipt["terms_ms"]["route_wall_ms"] = (time.perf_counter_ns() - t0) / 1.0e6
+        self.last_route_receipt = receipt
+        self.route_receipt_history.append(receipt)
+        return out
+
+    def _route_order(self, query, limit: int, exclude=(), cand_count=None):
         """Graft indices of the best ``limit`` nodes, excluded indices
         dropped.  Follows core/graft_arena.py:1282-1364:
 
@@ -573,7 +661,11 @@ class _Bridge:
         excludes in the bank, else None (the reference's fail-closed
         candidate check).
         """
-        if limit is None or not self._eligible_bank:
+        if limit is None:
+            self._fallback("requires_limited_route")
+            return None
+        if not self._eligible_bank:
+            self._fallback("bank_ineligible")
             return None
         size = self.bank_size
         exclude_set = set(exclude) if exclude else None
@@ -581,15 +673,19 @@ class _Bridge:
         in_bank = (sum(1 for i in exclude_set if 0 <= i < n_g and self._in_bank[i])
                    if exclude_set else 0)
         if cand_count is not None and int(cand_count) != size - in_bank:
+            self._fallback("candidate_subset_mismatch")
             return None
         want = min(max(0, int(limit)), size - in_bank)
         if want <= 0:
             return []
         topk = min(MAX_TOPK, size, want + in_bank)
         if topk < want:
+            self._fallback("topk_cap")
             return None
+        ranked = self.route_scored(query, topk)[0]
+        t = self._clock()
         out = []
-        for nid in self.route_scored(query, topk)[0]:
+        for nid in ranked:
             if nid == np.iinfo(np.uint64).max:
                 continue
             gi = self._graft_index(nid)
@@ -598,7 +694,11 @@ class _Bridge:
             out.append(gi)
             if len(out) >= want:
                 break
-        return out if len(out) >= want else None
+        self._term("result_remap_ms", t)
+        if len(out) < want:
+            self._fallback("short_result")
+            return None
+        return out
 
 
 class MlaRouteBankBridge(_Bridge):

@@ -361,3 +361,64 @@ def test_digest_and_debias_routes_follow_the_law(debias):
             w_ids, w_sc = expected_order(gs, q, 9, debias=debias)
             np.testing.assert_array_equal(ids, w_ids)
             np.testing.assert_array_equal(sc, w_sc)
+
+
+def test_route_receipts_follow_the_route_profile(monkeypatch):
+    # core/graft_arena.py:161-256: a receipt per profiled route (phase
+    # times, the bank's event, fallback reasons, the ranking's prefix);
+    # none for an unprofiled route
+    monkeypatch.delenv("GRM_ROUTE_SEAMS_PROFILE", raising=False)
+    rng = np.random.default_rng(17)
+    gs = [graft(300 + i, rng.standard_normal(8).astype(np.float32)) for i in range(30)]
+    q = rng.standard_normal(8).astype(np.float32)
+    br = CpuMlaBridge()
+    br.refresh(gs, 1)
+    want = br.route_order(q, 5)
+    assert want is not None and br.last_route_receipt is None
+    assert br.route_receipt_history == []
+
+    monkeypatch.setenv("GRM_ROUTE_SEAMS_PROFILE", "on")
+    gs[2]["cent"] = rng.standard_normal(8).astype(np.float32)
+    br.refresh(gs, 2)
+    got = br.route_order(q, 5)
+    r = br.last_route_receipt
+    assert r["schema"] == bb.ROUTE_RECEIPT_SCHEMA and r["epoch"] == 2
+    assert r["route_backend"] == "hip" and r["fallbacks"] == []
+    assert r["rebuilds"]["device_bank"]["status"] == "updated"
+    assert r["ranking_count"] == 5 and r["ranking_prefix"] == got
+    assert r["candidate_count"] == 30
+    t = r["terms_ms"]
+    for name in ("bank_refresh_ms", "device_route_call_ms", "ranking_ms",
+                 "result_remap_ms", "route_wall_ms"):
+        assert t[name] >= 0.0, name
+    assert t["bank_refresh_ms"] > 0.0
+    assert t["route_wall_ms"] >= t["device_route_call_ms"]
+    # the refresh time goes to the next route only
+    br.route_order(q, 5)
+    assert br.last_route_receipt["terms_ms"]["bank_refresh_ms"] == 0.0
+    assert len(br.route_receipt_history) == 2
+
+    # fallbacks, each with its reason
+    assert br.route_order(q, None) is None
+    assert br.last_route_receipt["fallbacks"] == ["requires_limited_route"]
+    assert br.last_route_receipt["route_backend"] is None
+    assert br.route_order(q, 5, cand_count=7) is None
+    assert br.last_route_receipt["fallbacks"] == ["candidate_subset_mismatch"]
+    order = br.route_order(q, 16)
+    assert br.route_order(q, 16, exclude={order[0], order[1]}) is None
+    assert br.last_route_receipt["fallbacks"] == ["short_result"]
+    gs.append(graft(999, np.full(9, 1.0, np.float32)))  # a dim the bank cannot hold
+    br.refresh(gs, 3)
+    assert br.route_order(q, 5) is None
+    assert br.last_route_receipt["fallbacks"] == ["bank_ineligible"]
+    assert br.last_route_receipt["rebuilds"]["device_bank"]["status"] == "ineligible"
+
+    # the constructor flag asks for receipts without the environment
+    monkeypatch.delenv("GRM_ROUTE_SEAMS_PROFILE")
+    gs.pop()
+    br2 = CpuMlaBridge(route_profile=True, length_debias=True)
+    gs.append(graft(800, gs[0]["cent"], child_cents=[gs[1]["cent"]]))
+    br2.refresh(gs, 1)
+    assert br2.route_order(q, 4) is not None
+    t2 = br2.last_route_receipt["terms_ms"]
+    assert "device_score_all_ms" in t2 and "device_digest_score_ms" in t2

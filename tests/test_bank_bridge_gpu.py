@@ -219,3 +219,30 @@ def test_gqa_bridge_digests_and_debias(hip_lib, debias):
                 w_ids, w_sc = law_order(gs, score_keys, q, 6, debias)
                 np.testing.assert_array_equal(ids, w_ids)
                 np.testing.assert_array_equal(sc, w_sc)
+
+
+def test_gqa_bridge_route_receipts(hip_lib):
+    # a profiled route over a device bank: the ranking is the oracle's and
+    # the receipt names the device phases (core/graft_arena.py:161-256)
+    rng = np.random.default_rng(25)
+    kv, hd = 2, 64
+    make = lambda: rng.standard_normal((kv, int(rng.integers(4, 40)), hd)).astype(np.float32)
+    gs = [{"native_node_id": 100 + i, "cent": make()} for i in range(60)]
+    q = rng.standard_normal((8, 2, hd)).astype(np.float32)
+    with GqaRouteBankBridge(route_profile=True) as br:
+        br.refresh(gs, 1)
+        got = br.route_order(q, 6)
+        r = br.last_route_receipt
+    ids = np.asarray([g["native_node_id"] for g in gs], np.uint64)
+    offs = np.zeros(len(gs) + 1, np.uint64)
+    offs[1:] = np.cumsum([g["cent"].shape[1] for g in gs])
+    keys = np.concatenate([g["cent"].reshape(-1) for g in gs])
+    want, _, _ = oracle.gqa_route(keys, oracle.F32, offs, kv, hd, q[None], 6, node_ids=ids)
+    by_id = {int(g["native_node_id"]): i for i, g in enumerate(gs)}
+    assert got == [by_id[int(n)] for n in want[0]]
+    assert r["route_backend"] == "hip" and r["fallbacks"] == []
+    assert r["rebuilds"]["device_bank"]["status"] == "created"
+    assert r["ranking_prefix"] == got
+    t = r["terms_ms"]
+    assert t["device_route_call_ms"] > 0.0 and t["bank_refresh_ms"] > 0.0
+    assert t["route_wall_ms"] >= t["device_route_call_ms"]
