@@ -374,7 +374,8 @@ __global__ __launch_bounds__(kUnitWaves * kWave) void gqa_exact_kernel(
 // the cache; wave 0 sums each slot's heads in order, keeps the block's k
 // best and writes them to block_out[(qb*gridDim.x + blockIdx.x)*k ..).
 // qbad[qb*kv + g] are the query's non-finite flags.  With done
-// (host-mapped memory) wave 0 then stores seq at done[qb*gridDim.x +
+// (host-mapped memory) the entries carry route_tag(seq) in their slot
+// field (store_entry) and wave 0 then stores seq at done[qb*gridDim.x +
 // blockIdx.x] once its list is complete (after its end tick at the same
 // index of stamps, when given), so a host that sees every flag of a launch
 // holds its lists without waiting for the stream; the maxima are re-zeroed
@@ -466,7 +467,8 @@ __global__ __launch_bounds__(kFinWaves * kWave) void gqa_finalize_kernel(
     }
   }
   if (wave == 0 && lane < k) {
-    block_out[(static_cast<size_t>(qb) * gridDim.x + blockIdx.x) * k + lane] = wl_entry(L);
+    store_entry(block_out + (static_cast<size_t>(qb) * gridDim.x + blockIdx.x) * k + lane, wl_entry(L),
+                done ? route_tag(seq) : kNoSlot);
   }
   if (done && wave == 0) {
     // wave 0's list stores are complete before the end tick and the flag

@@ -1397,6 +1397,9 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
   GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
   if (flags) {
     GRM_CHECK_RC(grm::wait_flags(a->done_flags, a->route_seq, n_flags, a->ev_stop));
+    for (int qi = 0; qi < q_count; ++qi) {
+      GRM_CHECK_RC(grm::wait_tagged(a->blocks_out.host + q_off[qi], q_entries[qi], a->route_seq, a->ev_stop));
+    }
   } else {
     GRM_CHECK_RC(grm::wait_event(a->ev_stop));
   }
@@ -1406,8 +1409,8 @@ int route_impl(GqaDeviceArena* a, const void* queries, int q_dtype, bool on_devi
                  out_scores ? out_scores + static_cast<size_t>(qi) * topk : nullptr);
   }
   if (clocked) {
-    GRM_CHECK_RC(grm::stamps_elapsed(a->stamps, a->route_seq, n_flags, a->ev_stop, a->ticks_per_ms,
-                                     elapsed_ms));
+    GRM_CHECK_RC(grm::stamps_elapsed(a->stamps, a->route_seq, static_cast<size_t>(warmup) * fin_blocks, n_flags,
+                                     a->ev_stop, a->ticks_per_ms, elapsed_ms));
   } else if (elapsed_ms) {
     GRM_HIP_CHECK(hipEventElapsedTime(elapsed_ms, a->ev_start, a->ev_stop));
   }

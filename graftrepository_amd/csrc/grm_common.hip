@@ -118,6 +118,26 @@ int wait_flags(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev) {
   return 0;
 }
 
+int wait_tagged(const Cand* entries, size_t n, unsigned seq, hipEvent_t ev) {
+  const volatile uint32_t* tags = reinterpret_cast<const volatile uint32_t*>(entries);
+  const uint32_t tag = route_tag(seq);
+  // the slot field is the second word of each 16-byte entry
+  for (size_t i = 0; i < n; ++i) {
+    for (uint64_t spin = 1; tags[4 * i + 1] != tag; ++spin) {
+      if (spin % 256 == 0) {
+        const hipError_t e = hipEventQuery(ev);
+        if (e == hipSuccess) {
+          if (tags[4 * i + 1] == tag) break;
+          return fail(-1, "route finished without its list entries");
+        }
+        if (e != hipErrorNotReady) return fail_hip(e, "hipEventQuery");
+      }
+    }
+  }
+  std::atomic_thread_fence(std::memory_order_acquire);
+  return 0;
+}
+
 constexpr size_t kStampHead = 2;  // start tick, route number
 
 int reserve_stamps(MappedBuf* buf, size_t max) {
@@ -134,7 +154,7 @@ RouteStamps route_stamps(const MappedBuf& buf, size_t first) {
   return RouteStamps{d, d + kStampHead + first};
 }
 
-int stamps_elapsed(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev,
+int stamps_elapsed(const MappedBuf& buf, unsigned seq, size_t first, size_t n, hipEvent_t ev,
                    double ticks_per_ms, float* ms) {
   const volatile unsigned long long* st = static_cast<const volatile unsigned long long*>(buf.host);
   if (st[1] != seq) {
@@ -144,8 +164,18 @@ int stamps_elapsed(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev,
   std::atomic_thread_fence(std::memory_order_acquire);
   const unsigned long long t0 = st[0];
   unsigned long long t1 = t0;
-  for (size_t i = 0; i < n; ++i) {
+  // A timed block's end tick below t0 is an earlier route's (the stream
+  // ran those kernels before this route's first timed one started); it is
+  // replaced before the route's event completes.
+  bool stale = false;
+  for (size_t i = first; i < n; ++i) stale |= st[kStampHead + i] < t0;
+  if (stale) {
+    GRM_CHECK_RC(wait_event(ev));
+    std::atomic_thread_fence(std::memory_order_acquire);
+  }
+  for (size_t i = first; i < n; ++i) {
     const unsigned long long e = st[kStampHead + i];
+    if (e < t0) return fail(-1, "route finished without its end stamps");
     if (e > t1) t1 = e;
   }
   *ms = static_cast<float>(static_cast<double>(t1 - t0) / ticks_per_ms);

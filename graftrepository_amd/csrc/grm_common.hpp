@@ -248,16 +248,43 @@ __device__ inline void wl_consume_global(WaveList& L, int k,
 }
 
 
+// Tag of route number `seq` in the slot field of a host-bound list entry
+// (store_entry): the high bit keeps it apart from every real slot (all
+// below 2^31) and from kNoSlot, so an entry of an earlier route, tagged or
+// not, never carries the current route's tag (for 2^30 routes in a row).
+__host__ __device__ constexpr uint32_t route_tag(unsigned seq) {
+  return 0x80000000u | (seq & 0x3FFFFFFFu);
+}
+
+// A list entry bound for host memory on the completion-flag path, as one
+// 16-byte store, its slot field replaced by `tag` (route_tag): the host
+// takes an entry only once it carries the tag (wait_tagged), as it may see
+// a block's flag before that block's earlier stores to other lines.  Host
+// code never reads the slot of such an entry.  With tag kNoSlot the entry
+// is stored as it is.
+__device__ inline void store_entry(Cand* __restrict__ dst, Cand c, uint32_t tag) {
+  if (tag != kNoSlot) c.slot = tag;
+  typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+  u32x4_t v;
+  v.x = __float_as_uint(c.score);
+  v.y = c.slot;
+  v.z = static_cast<uint32_t>(c.id);
+  v.w = static_cast<uint32_t>(c.id >> 32);
+  *reinterpret_cast<u32x4_t*>(dst) = v;
+}
+
 // Block epilogue shared by the route kernels: merge the block's wave lists
-// in LDS and write the block's k best entries to block_out[blockIdx.x*k ..).
-// Must be reached by every thread of the block.  The entries of all blocks
-// are merged by topk_merge_kernel, launched next on the same stream; the
-// kernel boundary orders the writes, so no device-scope fence (an L2
-// write-back on gfx950) is paid per block.
+// in LDS and write the block's k best entries to block_out[blockIdx.x*k ..)
+// (tagged with `tag` unless it is kNoSlot, store_entry).  Must be reached
+// by every thread of the block.  Device-side lists are merged by
+// topk_merge_kernel, launched next on the same stream; the kernel boundary
+// orders the writes, so no device-scope fence (an L2 write-back on gfx950)
+// is paid per block.
 template <int NW, int CAP>
 __device__ inline void block_topk_write(WaveList& L, int k,
                                         Cand (*s_lists)[CAP],
-                                        Cand* __restrict__ block_out) {
+                                        Cand* __restrict__ block_out,
+                                        uint32_t tag = kNoSlot) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   if (lane < CAP) s_lists[wave][lane] = wl_entry(L);
@@ -265,7 +292,7 @@ __device__ inline void block_topk_write(WaveList& L, int k,
   if (wave == 0) {
     WaveList B;
     block_merge<NW>(s_lists, k, B);
-    if (lane < k) block_out[static_cast<size_t>(blockIdx.x) * k + lane] = wl_entry(B);
+    if (lane < k) store_entry(block_out + static_cast<size_t>(blockIdx.x) * k + lane, wl_entry(B), tag);
   }
 }
 
@@ -283,11 +310,15 @@ struct RouteStamps {
 };
 
 // Start tick of a route: the grid's first block (blocks start in index
-// order) stores it as the kernel begins.
+// order) stores it as the kernel begins, with the route's number in the
+// same 16-byte store, so a host that reads the number reads the tick.
 __device__ inline void route_start_stamp(const RouteStamps& st, unsigned seq) {
   if (st.start && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
-    st.start[0] = wall_clock64();
-    st.start[1] = seq;
+    typedef unsigned long long u64x2_t __attribute__((ext_vector_type(2)));
+    u64x2_t v;
+    v.x = wall_clock64();
+    v.y = seq;
+    *reinterpret_cast<u64x2_t*>(st.start) = v;
   }
 }
 
@@ -338,20 +369,27 @@ void release_mapped_bytes(MappedBuf* m);
 // flags returns an error instead of spinning.
 int begin_flags(MappedBuf* buf, size_t max, unsigned* seq);
 int wait_flags(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev);
+// After wait_flags: wait until each of the n host-mapped list entries at
+// `entries` carries route_tag(seq) in its slot field (store_entry), so no
+// entry of an earlier route is read; an error if `ev` (recorded after the
+// route's kernels) completes and an entry still lacks the tag.
+int wait_tagged(const Cand* entries, size_t n, unsigned seq, hipEvent_t ev);
 
 // Device-clock timing of a flagged route (RouteStamps).  reserve_stamps
 // puts a buffer in place for `max` flags: two start words, then one end
 // tick per flag; route_stamps gives the device pointers, with the end
 // ticks from flag `first` on.  stamps_elapsed, once wait_flags has seen
 // flags [0, n) hold seq, gives the route's device time in ms: the latest
-// end tick less the start tick, at `ticks_per_ms`.  A start stamp of
-// another route (never expected: it is stored before any flag) is waited
-// for through `ev` and is an error if the kernels end without it.
+// end tick of the timed flags [first, n) less the start tick, at
+// `ticks_per_ms`.  As with list entries, the host may see a flag before
+// the stores ahead of it: a start stamp of another route, or a timed end
+// tick below the start tick (an earlier route's), is waited for through
+// `ev` and is an error if the kernels end without the new one.
 // wall_ticks_per_ms: the constant clock's rate on `device` (0 when the
 // device does not report it; such routes keep stream events).
 int reserve_stamps(MappedBuf* buf, size_t max);
 RouteStamps route_stamps(const MappedBuf& buf, size_t first);
-int stamps_elapsed(const MappedBuf& buf, unsigned seq, size_t n, hipEvent_t ev,
+int stamps_elapsed(const MappedBuf& buf, unsigned seq, size_t first, size_t n, hipEvent_t ev,
                    double ticks_per_ms, float* ms);
 double wall_ticks_per_ms(int device);
 // True when GRM_HIP_ROUTE_TIMING=events asks timed routes to keep stream

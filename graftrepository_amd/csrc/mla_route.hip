@@ -152,7 +152,7 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_kernel(
     wl_consume(L, k, s, id, slot, need);
   }
 
-  block_topk_write<NW>(L, k, s_lists, block_out);
+  block_topk_write<NW>(L, k, s_lists, block_out, done ? route_tag(seq) : kNoSlot);
   block_done_flag(done, seq, stamps.end);
 }
 
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(NW * kWave) void mla_route_pipe_kernel(
     t = tn;
     b = bn;
   }
-  block_topk_write<NW>(L, k, s_lists, block_out);
+  block_topk_write<NW>(L, k, s_lists, block_out, done ? route_tag(seq) : kNoSlot);
   block_done_flag(done, seq, stamps.end);
 }
 
@@ -1067,12 +1067,13 @@ int route_impl(MlaDeviceArena* a, const void* queries, int q_dtype,
     GRM_HIP_CHECK(hipEventRecord(a->ev_stop, a->stream));
     if (flags) {
       GRM_CHECK_RC(grm::wait_flags(a->done_flags, a->route_seq, n_flags, a->ev_stop));
+      GRM_CHECK_RC(grm::wait_tagged(a->blocks_out.host, per_q * redo.size(), a->route_seq, a->ev_stop));
     } else {
       GRM_CHECK_RC(grm::wait_event(a->ev_stop));
     }
     if (clocked) {
-      GRM_CHECK_RC(grm::stamps_elapsed(a->stamps, a->route_seq, n_flags, a->ev_stop, a->ticks_per_ms,
-                                       elapsed_ms));
+      GRM_CHECK_RC(grm::stamps_elapsed(a->stamps, a->route_seq, static_cast<size_t>(warmup) * g.blocks, n_flags,
+                                       a->ev_stop, a->ticks_per_ms, elapsed_ms));
     } else if (elapsed_ms) {
       float ms = 0.0f;
       GRM_HIP_CHECK(hipEventElapsedTime(&ms, a->ev_start, a->ev_stop));
