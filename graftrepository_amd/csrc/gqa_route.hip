@@ -95,7 +95,17 @@ struct GqaDeviceArena {
   std::unordered_map<uint64_t, uint64_t> slot_of;
   std::set<uint64_t> free_slots;
   // route work list, rebuilt when the epoch moves
-  uint32_t chunk = 256;  // key tokens per work item
+  // Key tokens per work item of the route passes (screen and refine, the
+  // exact path): a screen-and-refine item refines its columns' best rows
+  // once at its end, so longer items read fewer rows again -- 512 for
+  // banks the screen reads exactly (4-token route 0.229 -> 0.214 ms p50 on
+  // the 512-node bf16 bank), 256 for fp32 banks screened through their
+  // fp16 copy, whose refine gathers fp32 rows per wavefront (fp32
+  // hand-over 0.205 against 0.207 ms device at 512); and per candidate
+  // item of the bound-and-verify exact step, which is set by the
+  // candidates' tokens and measured best at 256.
+  uint32_t chunk = 512;
+  uint32_t cand_chunk = 256;
   Item* d_items = nullptr;
   size_t d_items_count = 0;
   // the same items by decreasing token count in 64-token classes, address
@@ -103,6 +113,7 @@ struct GqaDeviceArena {
   Item* d_items_sized = nullptr;
   size_t d_items_sized_count = 0;
   uint64_t n_items = 0;
+  uint64_t n_cand_items = 0;  // the live nodes' items at cand_chunk tokens
   // one item per live node with key tokens (all of them), for the
   // screen-only pass of the bound-and-verify path
   Item* d_units = nullptr;
@@ -481,9 +492,14 @@ int create_arena(const void* keys, int key_dtype, const void* scales, int scale_
   a->tok_off.assign(cap_nodes, 0);
   a->len.assign(cap_nodes, 0);
   a->slot_id.assign(cap_nodes, kNoId);
+  a->chunk = key_dtype == kF32 ? 256 : 512;
   if (const char* env = getenv("GRM_HIP_GQA_CHUNK")) {
     const long v = strtol(env, nullptr, 10);
     if (v >= 16 && v <= 4096 && v % 16 == 0) a->chunk = static_cast<uint32_t>(v);
+  }
+  if (const char* env = getenv("GRM_HIP_GQA_CAND_CHUNK")) {
+    const long v = strtol(env, nullptr, 10);
+    if (v >= 16 && v <= 4096 && v % 16 == 0) a->cand_chunk = static_cast<uint32_t>(v);
   }
   if (const char* env = getenv("GRM_HIP_GQA_SCREEN")) a->screen_mode = env[0] != '0' ? -1 : 0;
   if (const char* env = getenv("GRM_HIP_QUERY_COPY")) a->query_dma = strcmp(env, "dma") == 0;
@@ -584,9 +600,11 @@ int ensure_items(GqaDeviceArena* a) {
   items.reserve(a->live * 2);
   units.reserve(a->live);
   uint32_t max_len = 0;
+  uint64_t n_cand_items = 0;
   for (uint64_t s = 0; s < a->high_water; ++s) {
     if (a->slot_id[s] == kNoId) continue;
     append_items(items, static_cast<uint32_t>(s), a->tok_off[s] * a->kv, a->len[s], a->chunk);
+    n_cand_items += (a->len[s] + a->cand_chunk - 1) / a->cand_chunk;
     if (a->len[s] > 0) {
       append_items(units, static_cast<uint32_t>(s), a->tok_off[s] * a->kv, a->len[s], a->len[s]);
     }
@@ -625,6 +643,7 @@ int ensure_items(GqaDeviceArena* a) {
     GRM_HIP_CHECK(hipStreamSynchronize(a->stream));
   }
   a->n_items = items.size();
+  a->n_cand_items = n_cand_items;
   a->n_units = units.size();
   a->max_len = max_len;
   a->items_epoch = a->epoch;
@@ -1047,7 +1066,7 @@ int prepare_bv(GqaDeviceArena* a, const SrPlan& p, int topk, uint32_t fin_blocks
   GRM_CHECK_RC(reserve_device(&a->d_cslots, &a->d_cslots_count, qbm * cap));
   GRM_CHECK_RC(reserve_device(&a->d_ccount, &a->d_ccount_count, qbm + 1));
   GRM_CHECK_RC(reserve_device(&a->d_citems, &a->d_citems_count,
-                              std::max<size_t>(1, qbm * a->n_items)));
+                              std::max<size_t>(1, qbm * a->n_cand_items)));
   GRM_CHECK_RC(reserve_device(&a->d_q64, &a->d_q64_count,
                               qbm * a->kv * a->hd * rq_pad_of(p.R * p.Qt)));
   return 0;
@@ -1233,7 +1252,7 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
                                     (4 * grm::gqa::kCandWaves * grm::kWave)));
   grm::gqa::gqa_cands_kernel<<<dim3(qb, cblocks), grm::gqa::kCandWaves * grm::kWave, 0, a->stream>>>(
       a->d_blists, bblocks, topk, a->d_lbub, a->cap_nodes, static_cast<uint32_t>(a->high_water),
-      a->d_tok_off, a->d_len, kv, a->chunk, a->d_cslots, a->d_ccount, a->d_citems,
+      a->d_tok_off, a->d_len, kv, a->cand_chunk, a->d_cslots, a->d_ccount, a->d_citems,
       a->d_ccount + p.qb_max);
   GRM_HIP_CHECK(hipGetLastError());
   // 5. the law on the candidates, then their exact scores and top-k: one
@@ -1267,7 +1286,7 @@ int enqueue_bv(GqaDeviceArena* a, const SrPlan& p, const unsigned char* qptr, in
     for (size_t i = 0; i < xpasses.size(); ++i) {
       if (xpasses.size() > 1) GRM_CHECK_RC(launch_q64(a, qptr, q_dtype, qb, H, p.Qt, xpasses[i], true));
       GRM_CHECK_RC(launch_exact(a, H, xpasses[i], a->d_citems,
-                                static_cast<uint64_t>(qb) * a->n_items, a->d_ccount + p.qb_max));
+                                static_cast<uint64_t>(qb) * a->n_cand_items, a->d_ccount + p.qb_max));
     }
   }
   (void)per_q;
