@@ -915,14 +915,16 @@ int launch_sr_pass(GqaDeviceArena* a, const SrPlan& p, const ScreenBound& eb,
   const unsigned threads = grm::gqa::kUnitWaves * grm::kWave;
   const size_t hstride = a->cap_nodes * static_cast<size_t>(p.H);
   const double denom = sqrt(static_cast<double>(a->hd));
-  // Item order: with a light refine (at most 4 query columns per kv head,
-  // keys exact in the screen) address order streams best (C4 shape, one
-  // query token: 192 us against 198 us by size); with a heavier refine
-  // (more columns, or an fp32 bank's rows read again in fp32) the waves of
-  // short items at the launch's end even out the refines' cost (4 tokens:
-  // 221 us against 252 us; fp32 bank: 215 us against 227 us).
+  // Item order: address order streams best (C4 shape, one query token:
+  // 192 us against 198 us by size), and with items of 512 tokens (whole
+  // nodes there) also for 4 query tokens (207 against 209 us).  Items of
+  // 256 tokens with a heavier refine (more columns, or an fp32 bank's rows
+  // read again in fp32) go by decreasing size: the waves of short items at
+  // the launch's end even out the refines' cost (4 tokens: 221 us against
+  // 252 us; fp32 bank: 215 us against 227 us).
   // GRM_HIP_GQA_SR_ORDER=slot / size fixes either.
-  const bool by_size = a->sr_order >= 0 ? a->sr_order == 1 : (cols > 4 || a->d_skeys != nullptr);
+  const bool by_size = a->sr_order >= 0 ? a->sr_order == 1
+                                        : (a->d_skeys != nullptr || (cols > 4 && a->chunk <= 256));
   // fp32 queries over at most 8 columns: each column's remainder after its
   // rounding to the MFMA type rides in an idle column slot (gqa_sr_kernel,
   // query_frags), so the query's rounding leaves the bound: per value
