@@ -388,3 +388,35 @@ def test_untimed_routes_wait_on_completion_flags(hip_lib, monkeypatch, bound):
             if step == 0:
                 bank.evict(node_ids[10:40])
                 live = live[:10] + live[40:]
+
+
+@pytest.mark.parametrize("chunk", [None, "256"])
+@pytest.mark.parametrize("Qt", [1, 4])
+def test_long_nodes_span_several_work_items(hip_lib, monkeypatch, Qt, chunk):
+    # Screen and refine over nodes longer than one work item (512 tokens by
+    # default for bf16 banks, 256 when set): each item refines its own
+    # candidates and the per-(node, head) maxima combine across the items.
+    monkeypatch.setenv("GRM_HIP_GQA_SCREEN", "1")
+    monkeypatch.setenv("GRM_HIP_GQA_BOUND", "0")
+    if chunk is None:
+        monkeypatch.delenv("GRM_HIP_GQA_CHUNK", raising=False)
+    else:
+        monkeypatch.setenv("GRM_HIP_GQA_CHUNK", chunk)
+    rng = np.random.default_rng(900 + Qt)
+    kv, hd, H = 4, 128, 16
+    keys, offs = ragged(rng, 60, kv, hd, 1, 1500)
+    lens = np.diff(offs)
+    # the best token of some nodes sits in a late item
+    for i in range(0, 60, 7):
+        if lens[i] > 1100:
+            blk = keys[int(offs[i]) * kv * hd:int(offs[i + 1]) * kv * hd].reshape(kv, int(lens[i]), hd)
+            blk[:, 1050] *= 3.0
+    qs = rng.standard_normal((2, H, Qt, hd)).astype(np.float32)
+    with GqaNodeBank(keys, offs, kv_heads=kv, head_dim=hd, dtype="bf16") as bank:
+        res = bank.route(qs, 7)
+        one = bank.route(qs[:1], 7, timed=False)
+        stats = bank.route_stats()
+    ids, sc, _ = oracle.gqa_route(oracle.bf16_bits(keys), oracle.BF16, offs, kv, hd, qs, 7)
+    assert_same(res, ids, sc)
+    assert_same(one, ids[:1], sc[:1])
+    assert stats["screen_refine"] > 0 and stats["exact"] == 0
