@@ -47,7 +47,7 @@ def bound_mode(request, monkeypatch):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_half_banks_batched(hip_lib, bound_mode, dtype):
-    # nodes up to 600 tokens: several 256-token items per node
+    # nodes up to 600 tokens: several work items per node
     lens = wl.gqa_lengths(500, seed=101, lo=1, hi=600)
     keys, offs = wl.gqa_bank(lens, 8, 128, seed=101, dtype=dtype)
     qs = wl.gqa_queries(16, 32, 1, 128, seed=101, dtype="bf16")
@@ -195,3 +195,22 @@ def test_after_evict_append_compact(hip_lib, bound_mode):
                                             scale_dtype="f16", group_size=hd,
                                             node_ids=np.asarray(order, np.uint64))
             assert_same(res, want, wsc)
+
+
+@pytest.mark.parametrize("route_chunk,cand_chunk", [("512", "64"), ("64", "512"), ("256", "16")])
+def test_candidate_items_apart_from_route_items(hip_lib, monkeypatch, route_chunk, cand_chunk):
+    # The bound-and-verify exact step cuts its candidates into items of its
+    # own length (GRM_HIP_GQA_CAND_CHUNK), sized apart from the route's
+    # items (GRM_HIP_GQA_CHUNK): shorter, longer, and the shortest allowed.
+    monkeypatch.setenv("GRM_HIP_GQA_BOUND", "1")
+    monkeypatch.setenv("GRM_HIP_GQA_CHUNK", route_chunk)
+    monkeypatch.setenv("GRM_HIP_GQA_CAND_CHUNK", cand_chunk)
+    rng = np.random.default_rng(int(route_chunk) + int(cand_chunk))
+    keys, offs = ragged(rng, 120, 8, 128, 1, 700)
+    qs = rng.standard_normal((8, 32, 1, 128)).astype(np.float32)  # 32 columns per kv head
+    with GqaNodeBank(keys, offs, kv_heads=8, head_dim=128, dtype="bf16") as bank:
+        res = bank.route(qs, 6)
+        stats = bank.route_stats()
+    ids, sc, _ = oracle.gqa_route(oracle.bf16_bits(keys), oracle.BF16, offs, 8, 128, qs, 6)
+    assert_same(res, ids, sc)
+    assert stats["bound_verify"] > 0
