@@ -1487,22 +1487,12 @@ __global__ __launch_bounds__((NP == 1 ? kUnitWaves : 8) * kWave,
       key_frags(b, h, bk);
       sc[h] = 1.0f;
       if constexpr (FACT) sc[h] = scale_of(b.s[h][0]);
-      // The wavefront's priority is raised while it issues its MFMAs, so
-      // the SIMD's arbiter keeps the matrix core fed from it and fills the
-      // gaps with the other wavefront's decode and maxima: MFMA and VALU
-      // work overlap across wavefronts, not within one (INT8 100k-node
-      // route after a churn step: device 7.03 / 7.01 ms against 7.12 /
-      // 7.10 ms, one box).
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         c[h][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) c[h][nt] = mfma16x16x32<MT>(bq[nt][ks], bk[ks], c[h][nt]);
       }
-      __builtin_amdgcn_s_setprio(0);
-      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
