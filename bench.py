@@ -1294,7 +1294,11 @@ def main() -> int:
             "device_ms_mean": round(g["mean_dev"], 5),
             "timed_calls_p50_ms": round(g["timed_p50"], 5),
             "host_query_p50_ms": round(g["host_p50"], 5),
-            "query_tokens_4": g["qt4"],
+            "query_tokens_4": dict(g["qt4"], roofline={
+                "bound": "hbm", "achieved": g["qt4"]["achieved_gbs"], "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(g["qt4"]["achieved_gbs"] / HBM_PEAK_GBS, 4),
+                "traffic": traffic.get("gqa_sr_qt4", {}).get("bytes_per_launch"),
+                "kernel": "gqa_sr_kernel<bf16, 4, 1>", "bytes_per_call": g["bytes"]}),
             "query_tokens_64": g["qt64"],
             "cpu_baseline": g["cpu"],
             "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1),
