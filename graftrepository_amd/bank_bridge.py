@@ -55,7 +55,9 @@ Route receipts follow the reference's route profile (core/graft_arena.py:
 time of each phase in ``terms_ms``, the bank's refresh event under
 ``rebuilds``, the reasons a route fell back to the caller's CPU path under
 ``fallbacks``, and the ranking's length and first 16 graft indices.  An
-unprofiled route leaves ``last_route_receipt`` None.
+unprofiled route leaves ``last_route_receipt`` None.  The history keeps
+every profiled route's receipt, as the reference's does (:249-254); a
+long-running caller that profiles clears it when it has read it.
 """
 
 from __future__ import annotations
