@@ -390,13 +390,15 @@ def test_untimed_routes_wait_on_completion_flags(hip_lib, monkeypatch, bound):
                 live = live[:10] + live[40:]
 
 
+@pytest.mark.parametrize("path", ["screen", "exact"])
 @pytest.mark.parametrize("chunk", [None, "256"])
 @pytest.mark.parametrize("Qt", [1, 4])
-def test_long_nodes_span_several_work_items(hip_lib, monkeypatch, Qt, chunk):
-    # Screen and refine over nodes longer than one work item (512 tokens by
-    # default for bf16 banks, 256 when set): each item refines its own
-    # candidates and the per-(node, head) maxima combine across the items.
-    monkeypatch.setenv("GRM_HIP_GQA_SCREEN", "1")
+def test_long_nodes_span_several_work_items(hip_lib, monkeypatch, Qt, chunk, path):
+    # Screen and refine, and the exact fp64 path, over nodes longer than one
+    # work item (512 tokens by default for bf16 banks, 256 when set): each
+    # item yields its own per-(node, head) maxima, which combine across the
+    # node's items.
+    monkeypatch.setenv("GRM_HIP_GQA_SCREEN", "1" if path == "screen" else "0")
     monkeypatch.setenv("GRM_HIP_GQA_BOUND", "0")
     if chunk is None:
         monkeypatch.delenv("GRM_HIP_GQA_CHUNK", raising=False)
@@ -419,4 +421,7 @@ def test_long_nodes_span_several_work_items(hip_lib, monkeypatch, Qt, chunk):
     ids, sc, _ = oracle.gqa_route(oracle.bf16_bits(keys), oracle.BF16, offs, kv, hd, qs, 7)
     assert_same(res, ids, sc)
     assert_same(one, ids[:1], sc[:1])
-    assert stats["screen_refine"] > 0 and stats["exact"] == 0
+    if path == "screen":
+        assert stats["screen_refine"] > 0 and stats["exact"] == 0
+    else:
+        assert stats["exact"] > 0 and stats["screen_refine"] == 0
